@@ -1,0 +1,176 @@
+#!/usr/bin/env python3
+"""GDN megakernel fwd+bwd throughput on one MI355X (tjev's mega2, BASELINE.json's metric).
+
+A step is one forward and one backward pass of the GDN core over one batch of synthetic
+inputs already resident in HBM (the HIP library called through its C ABI, no autograd): out
+and the chunk states, then d(qkv), d(a), d(b), d(A_log), d(dt_bias) under a fixed upstream
+gradient. W untimed warm-up steps, then K timed steps between device synchronizations;
+``value`` = B*T / (seconds per step). A second, event-profiled pass of K steps gives every
+kernel's average duration (HIP events on the launch stream) for the dominant kernel's
+roofline. The CPU baseline is the oracle (a CPU restatement of tjev's XLA chunked path, fp32,
+torch autograd) on a bounded sample of the same workload.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 0.8B|9B|varlen|tiny]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+METRIC = "GDN layer fwd+bwd tokens/sec at 0.8B/9B shapes; MFMA util % and HBM GB/s"
+
+
+def _args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="0.8B")
+    ap.add_argument("--precision", default=None, help="override the config's precision")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-length", type=int, default=1024)
+    ap.add_argument("--details", default=None, help="also write the full report to this JSON file")
+    return ap.parse_args(argv)
+
+
+def _cpu_baseline(cfg, precision_dtype, sample_length: int) -> dict:
+    """The oracle's fwd+bwd on the CPU: one row of ``sample_length`` tokens at the config's
+    heads and dims (its per-token cost does not depend on T); 1 warm-up, median of 3."""
+    import torch
+
+    from oracle.gdn_oracle import reference_with_grads
+    from tjev_amd.testing import cotangent, gdn_inputs
+
+    threads = torch.get_num_threads()
+    inputs = gdn_inputs(batch=1, length=sample_length, key_heads=cfg["key_heads"],
+                        value_heads=cfg["value_heads"], dim=cfg["dim"], dtype=precision_dtype)
+    cot = cotangent(1, sample_length, cfg["value_heads"], cfg["dim"])
+    kw = dict(key_heads=cfg["key_heads"], key_dim=cfg["dim"], value_heads=cfg["value_heads"],
+              value_dim=cfg["dim"], chunk=cfg["chunk"])
+    times = []
+    for rep in range(4):
+        t0 = time.perf_counter()
+        reference_with_grads(inputs, cot, **kw)
+        if rep:
+            times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    return {"value": sample_length / sec, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle (CPU restatement of tjev's XLA chunked path, fp32, torch autograd) fwd+bwd "
+                       f"on B=1 T={sample_length} at the config's heads/dims, median of 3 after 1 warm-up, "
+                       f"{threads} threads, {sec:.2f} s per pass")}
+
+
+def main(argv=None) -> int:
+    args = _args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "the operator would shard by batch rows, one process per GPU, with no exchange", file=sys.stderr)
+        return 2
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import torch
+
+    from tjev_amd import _lib
+    from tjev_amd.gdn import GdnPlan
+    from tjev_amd.roofline import PEAK_BF16_TFLOPS, PEAK_FP32_TFLOPS, PEAK_HBM_GBS, kernel_work, operator_work
+    from tjev_amd.testing import CONFIGS, cotangent, gdn_inputs
+
+    cfg = dict(CONFIGS[args.config])
+    precision = args.precision or cfg["precision"]
+    dtype = cfg["dtype"]
+    dev = torch.device("cuda", 0)
+    B, T, Hk, H, D, C = (cfg[k] for k in ("batch", "length", "key_heads", "value_heads", "dim", "chunk"))
+    qkv, a, b, a_log, dt_bias, w, seg = gdn_inputs(batch=B, length=T, key_heads=Hk, value_heads=H, dim=D,
+                                                  dtype=dtype, segments=cfg["segments"], device=dev)
+    d_out = cotangent(B, T, H, D).to(dtype).to(dev)
+    plan = GdnPlan(batch=B, length=T, key_heads=Hk, key_dim=D, value_heads=H, value_dim=D, taps=w.shape[0],
+                   chunk=C, io_dtype=dtype, gate_dtype=dtype, precision=precision)
+    ws = torch.empty(max(plan.fwd_bytes, plan.bwd_bytes), dtype=torch.uint8, device=dev)
+    out = torch.empty((B, T, H, D), dtype=dtype, device=dev)
+    states = torch.empty(plan.states_shape, dtype=torch.float32, device=dev)
+    d_qkv, d_a, d_b = torch.empty_like(qkv), torch.empty_like(a), torch.empty_like(b)
+    d_alog, d_dtb = torch.empty_like(a_log), torch.empty_like(dt_bias)
+
+    def step():
+        plan.forward(qkv, a, b, a_log, dt_bias, w, seg, out, states, ws)
+        plan.backward(qkv, a, b, a_log, dt_bias, w, seg, states, d_out, d_qkv, d_a, d_b, d_alog, d_dtb, None, ws)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_wall = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t_wall
+    ms = start.elapsed_time(end) / args.steps
+    finite = bool(torch.isfinite(out.float()).all()) and bool(torch.isfinite(d_qkv.float()).all())
+
+    with _lib.KernelTimer() as kt:  # the same steps again, each kernel between HIP events
+        for _ in range(args.steps):
+            step()
+    per_kernel = {k: kt.ms[k] / kt.launches[k] for k in kt.ms if kt.launches[k]}
+    io_bytes = 2 if dtype == torch.bfloat16 else 4
+    shape = dict(batch=B, length=T, key_heads=Hk, value_heads=H, dim=D, chunk=C, io_bytes=io_bytes)
+    work = kernel_work(**shape)
+    peak_mfma = PEAK_FP32_TFLOPS if precision == "highest" else PEAK_BF16_TFLOPS
+    kernels = {}
+    for name, avg_ms in per_kernel.items():
+        wk = work[name]
+        if wk["bound"] == "mfma":
+            ach = wk["flops"] / (avg_ms * 1e-3) / 1e12
+            kernels[name] = {"ms": avg_ms, "bound": "mfma", "achieved": ach, "unit": "TFLOP/s", "peak": peak_mfma,
+                             "frac": ach / peak_mfma, "algorithmic": wk["flops"]}
+        else:
+            ach = wk["bytes"] / (avg_ms * 1e-3) / 1e9
+            kernels[name] = {"ms": avg_ms, "bound": "hbm", "achieved": ach, "unit": "GB/s", "peak": PEAK_HBM_GBS,
+                             "frac": ach / PEAK_HBM_GBS, "algorithmic": wk["bytes"]}
+    dominant = max(kernels, key=lambda k: kernels[k]["ms"])
+    dk = kernels[dominant]
+    op = operator_work(**shape)
+    value = B * T / (ms * 1e-3)
+    report = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if dtype == torch.bfloat16 else "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{args.config} GDN layer core (mega2) fwd+bwd", "batch": B, "seq_len": T,
+                   "key_heads": Hk, "value_heads": H, "head_dim": D, "chunk": C, "conv_taps": int(w.shape[0]),
+                   "precision": precision, "segments": cfg["segments"]},
+        "roofline": {"kernel": dominant, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
+                     "unit": dk["unit"], "frac": dk["frac"], "traffic": None},
+        "operator_roofline": {"algorithmic_gflop": op["flops"] / 1e9, "algorithmic_mb": op["bytes"] / 1e6,
+                              "ceiling_tokens_per_s": op["ceiling_tokens_per_s"],
+                              "frac": value / op["ceiling_tokens_per_s"],
+                              "achieved_tflops": op["flops"] / (ms * 1e-3) / 1e12},
+        "kernels": {k: {kk: (round(vv, 6) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for k, v in kernels.items()},
+        "finite": finite,
+        "wall_s_timed": t_wall,
+    }
+    if not args.no_cpu_baseline:
+        report["cpu_baseline"] = _cpu_baseline(cfg, dtype, args.cpu_sample_length)
+    if args.details:
+        with open(args.details, "w") as f:
+            json.dump(report, f, indent=1)
+    print(json.dumps(report), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,118 @@
+/* C ABI of the MI355X (gfx950) Gated DeltaNet megakernel library, libtjev_gdn.so.
+ *
+ * Drop-in for the two Pallas calls behind tjev's `gdn_megakernel`
+ * (src/tjev/kernels/gated_delta_rule/pallas_tpu_mega.py:585-639): the forward kernel
+ * `gdn_mega2_fwd` (:429-468) and the backward kernel `gdn_mega2_bwd` (:471-524) with the XLA
+ * sums of `_core_bwd` (:554-572). The caller (a jax.ffi handler, ctypes, torch) passes plain
+ * device pointers and the stream; every entry point is asynchronous on that stream, validates
+ * its arguments before any launch and returns 0 or a nonzero tjev_gdn_status
+ * (tjev_gdn_last_error() then describes it). No torch or HIP types appear here.
+ *
+ * Layouts (row-major, as the reference's arrays):
+ *   qkv        [B, T, 2*Hk*Dk + H*Dv]  io_dtype   raw in_proj_qkv output (taps > 0, mega2)
+ *                                                 or the post-conv activations (taps == 0, mega1)
+ *   a, b       [B, T, H]               gate_dtype raw gate projections
+ *   a_log      [H] fp32, dt_bias [H] fp32
+ *   conv_w     [K, 2*Hk*Dk + H*Dv]     fp32       (K = taps; ignored when taps == 0)
+ *   seg        [B, T] int32            segment ids, 0 = padding
+ *   out        [B, T, H, Dv]           io_dtype
+ *   states     [B, H, ceil(T/C), Dk, Dv] fp32     the state before each chunk: the only
+ *                                                 residual the backward needs besides the inputs
+ * T need not be a multiple of the chunk: the tail is treated as segment-0 padding with zero
+ * qkv, a and b, as the reference pads (pallas_tpu_mega.py:616-621).
+ */
+#ifndef TJEV_GDN_H
+#define TJEV_GDN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum tjev_gdn_dtype { TJEV_GDN_F32 = 0, TJEV_GDN_BF16 = 1 };
+
+/* the reference's `precision` (xla.py:23): highest = fp32 products; high = bf16x3; bf16 = one
+ * bf16 pass; mixed = bf16x3 intra-chunk products, one bf16 pass for products with the state */
+enum tjev_gdn_precision {
+  TJEV_GDN_HIGHEST = 0,
+  TJEV_GDN_HIGH = 1,
+  TJEV_GDN_ONE_PASS_BF16 = 2,
+  TJEV_GDN_MIXED = 3
+};
+
+/* the reference's `inverse` (pallas_tpu_v2.py:141) */
+enum tjev_gdn_inverse { TJEV_GDN_DOUBLING = 0, TJEV_GDN_BLOCKED = 1 };
+
+enum tjev_gdn_status {
+  TJEV_GDN_OK = 0,
+  TJEV_GDN_EINVAL = 1,       /* bad shape or parameter (the reference raises ValueError) */
+  TJEV_GDN_EUNSUPPORTED = 2, /* valid for the reference, no kernel instantiated for it here */
+  TJEV_GDN_EWORKSPACE = 3,   /* workspace missing or too small */
+  TJEV_GDN_EHIP = 4          /* a HIP launch or runtime error */
+};
+
+typedef struct tjev_gdn_params {
+  int32_t batch;          /* B */
+  int32_t length;         /* T */
+  int32_t key_heads;      /* Hk */
+  int32_t key_dim;        /* Dk */
+  int32_t value_heads;    /* H (a multiple of Hk) */
+  int32_t value_dim;      /* Dv */
+  int32_t taps;           /* conv taps K in 1..5 (mega2), 0 for mega1 (conv_weight=None) */
+  int32_t chunk;          /* C, a power of two >= 8 */
+  int32_t io_dtype;       /* tjev_gdn_dtype of qkv, out, d_out, d_qkv */
+  int32_t gate_dtype;     /* tjev_gdn_dtype of a, b, d_a, d_b */
+  int32_t precision;      /* tjev_gdn_precision */
+  int32_t inverse;        /* tjev_gdn_inverse */
+  int32_t heads_per_step; /* accepted for the reference's signature (0 = default) */
+} tjev_gdn_params;
+
+/* 0 if the library has kernels for these parameters, else a status (and the message). */
+int tjev_gdn_check(const tjev_gdn_params* p);
+
+/* bytes of the states residual, and of the scratch the forward / backward need */
+size_t tjev_gdn_states_bytes(const tjev_gdn_params* p);
+size_t tjev_gdn_workspace_bytes(const tjev_gdn_params* p, int backward);
+
+/* forward: replaces pallas_call "gdn_mega2_fwd" (pallas_tpu_mega.py:429-468); writes out and
+ * states. `stream` is a hipStream_t. */
+int tjev_gdn_mega2_fwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a,
+                       const void* b, const float* a_log, const float* dt_bias,
+                       const float* conv_w, const int32_t* seg, void* out, float* states,
+                       void* workspace, size_t workspace_bytes);
+
+/* backward: replaces pallas_call "gdn_mega2_bwd" (pallas_tpu_mega.py:471-524) plus the XLA sums
+ * of _core_bwd (:563-571): d_qkv (io_dtype), d_a, d_b (gate_dtype), d_a_log and d_dt_bias ([H] fp32), and,
+ * when d_conv_w is not null, the conv weight's gradient [K, W] fp32 (the reference's
+ * gdn_mega2_bwd_dw variant, computed only when requested). */
+int tjev_gdn_mega2_bwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a,
+                       const void* b, const float* a_log, const float* dt_bias,
+                       const float* conv_w, const int32_t* seg, const float* states,
+                       const void* d_out, void* d_qkv, void* d_a, void* d_b, float* d_a_log,
+                       float* d_dt_bias, float* d_conv_w, void* workspace,
+                       size_t workspace_bytes);
+
+/* Per-kernel timing (no counterpart in the reference, whose kernels are timed by xprof):
+ * between tjev_gdn_profile_begin() and tjev_gdn_profile_end(), every launch of the fwd / bwd
+ * calls is bracketed by a hipEvent pair on the call's stream. _end synchronizes those events
+ * and writes, for kernel ids 0..n-1, the summed milliseconds and the launch count.
+ * TJEV_GDN_KERNELS is the number of ids; tjev_gdn_kernel_name(id) names them. Not thread-safe:
+ * profile from one host thread. */
+#define TJEV_GDN_KERNELS 11
+int tjev_gdn_profile_begin(void);
+int tjev_gdn_profile_end(float* ms, int* launches, int n);
+const char* tjev_gdn_kernel_name(int kernel);
+
+/* message of the last nonzero status on this thread */
+const char* tjev_gdn_last_error(void);
+
+/* (major << 16) | minor */
+int tjev_gdn_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TJEV_GDN_H */

@@ -1,0 +1,331 @@
+"""CPU restatement of tjev's XLA Gated DeltaNet path (the megakernel's parity oracle).
+
+TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()`` (as the
+checker) and ``bench.py``'s CPU-baseline leg, never by the product path.
+
+Each function follows a reference file (paths relative to the tjev repository root):
+
+- ``tap_masks`` / ``segmented_causal_conv1d``  src/tjev/kernels/causal_conv1d.py:10-46
+- ``l2norm``                                   src/tjev/kernels/gated_delta_rule/xla.py:42-53
+- ``unit_lower_inverse``                       xla.py:66-100 (doubling) and
+                                               pallas_tpu_v2.py:144-193 (16x16 diagonal
+                                               blocks by substitution, then doubling)
+- ``recurrent_gated_delta_rule``               xla.py:141-167
+- ``chunk_gated_delta_rule``                   xla.py:170-262 (precision "highest",
+                                               inverse "solve")
+- ``masks``                                    pallas_tpu_mega.py:349-361 with
+                                               pallas_tpu_v2.py:505-515 (integer logic)
+- ``heads_per_block``                          pallas_tpu_v2.py:518-525
+- ``reference_core``                           tests/kernels/test_gdn_mega.py:44-58
+                                               (``_reference``), the recurrent variant
+                                               tests/kernels/test_gdn_long.py:131-176
+- ``gated_rmsnorm``                            src/tjev/model/norms.py:13-15, 36-40
+
+Gradients come from torch autograd through these functions, as the reference takes
+``jax.grad`` of the same XLA program (test_gdn_mega.py:75-86). Arithmetic runs in the dtype
+of the floating inputs: float32 reproduces the reference's fp32 ("highest") numerics up to
+operation order, float64 is the truth the float32 path and the GPU kernels are judged by.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+PRECISIONS = ("highest", "high", "bf16", "mixed")  # xla.py:23
+
+
+# --------------------------------------------------------------------------- conv
+def tap_masks(segment_ids: torch.Tensor, taps: int) -> list[torch.Tensor]:
+    """keep[L] [B,T] bool: token t may read token t-L (same segment id, t-L >= 0), L = 0..K-1.
+    causal_conv1d.py:10-17 (the front is padded with id -1)."""
+    length = segment_ids.shape[1]
+    sp = torch.nn.functional.pad(segment_ids, (taps - 1, 0), value=-1)
+    return [sp[:, taps - 1 - lag : taps - 1 - lag + length] == segment_ids for lag in range(taps)]
+
+
+def _shift(x: torch.Tensor, lag: int) -> torch.Tensor:
+    """y[t] = x[t-lag], zeros before the start (causal_conv1d.py:20-23)."""
+    if lag == 0:
+        return x
+    return torch.nn.functional.pad(x, (0, 0, lag, 0))[:, : x.shape[1]]
+
+
+def segmented_causal_conv1d(x: torch.Tensor, weight: torch.Tensor,
+                            segment_ids: torch.Tensor) -> torch.Tensor:
+    """Depthwise causal conv that never mixes segments (causal_conv1d.py:32-46).
+
+    x [B,T,W], weight [K,W] (weight[K-1] multiplies the current token). Accumulates in
+    float32 (float64 when x is float64) lag 0 first, then lags 1..K-1; output in x.dtype."""
+    taps = weight.shape[0]
+    acc = torch.float64 if x.dtype == torch.float64 else torch.float32
+    keeps = tap_masks(segment_ids, taps)
+    out = torch.zeros(x.shape, dtype=acc)
+    for lag in range(taps):
+        w = weight[taps - 1 - lag].to(acc)
+        out = out + torch.where(keeps[lag][..., None], _shift(x, lag).to(acc), 0.0) * w
+    return out.to(x.dtype)
+
+
+# --------------------------------------------------------------------------- norms
+def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """x / sqrt(||x||^2 + eps) over the last axis; all-zero rows map to 0 with a zero
+    gradient (the double select of xla.py:49-53)."""
+    sq = torch.sum(x * x, dim=-1, keepdim=True)
+    zero = sq == 0
+    safe = torch.where(zero, torch.ones_like(x), x)
+    out = safe * torch.rsqrt(torch.where(zero, torch.ones_like(sq), sq) + eps)
+    return torch.where(zero, torch.zeros_like(x), out)
+
+
+def gated_rmsnorm(x: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor,
+                  eps: float = 1e-6) -> torch.Tensor:
+    """GDN output norm (norms.py:13-15, 36-40): w * (x*rsqrt(mean x^2 + eps)) rounded to
+    x.dtype and back, times silu(gate), in float32, cast to x.dtype. x, gate [..., H, D]."""
+    dtype = x.dtype
+    acc = torch.float64 if dtype == torch.float64 else torch.float32
+    xf = x.to(acc)
+    normed = (xf * torch.rsqrt(torch.mean(xf * xf, dim=-1, keepdim=True) + eps))
+    normed = normed.to(dtype).to(acc)
+    g = gate.to(acc)
+    return (weight.to(acc) * normed * (g * torch.sigmoid(g))).to(dtype)
+
+
+# --------------------------------------------------------------------------- inverse
+def doubling_masks(size: int) -> list[np.ndarray]:
+    """xla.py:66-79: per level s = 1, 2, 4, ...: the lower-left s x s block of every
+    2s x 2s diagonal block."""
+    row = np.arange(size)[:, None]
+    col = np.arange(size)[None, :]
+    out, s = [], 1
+    while s < size:
+        out.append((row // (2 * s) == col // (2 * s)) & (row // s == 2 * (row // (2 * s)) + 1)
+                   & (col // s == 2 * (col // (2 * s))))
+        s *= 2
+    return out
+
+
+def unit_lower_inverse(lower: torch.Tensor, block: int = 0) -> torch.Tensor:
+    """(I + L)^-1 for strictly lower-triangular L [..., C, C] (C a power of two).
+
+    ``block`` 0: recursive doubling from T = I (xla.py:82-100). ``block`` > 1: the exact
+    block x block diagonal inverse by forward substitution first, then the remaining
+    doubling levels (pallas_tpu_v2.py:144-193, ``inverse="blocked"``)."""
+    c = lower.shape[-1]
+    row = torch.arange(c)[:, None]
+    col = torch.arange(c)[None, :]
+    eye = (row == col).to(lower.dtype)
+    block = min(block, c)
+    if block > 1:
+        same = (row // block) == (col // block)
+        ld = torch.where(same, lower, 0.0)
+        x = eye.expand(lower.shape).clone()
+        for r in range(block - 1):
+            l_col = torch.sum(torch.where(col == (row // block) * block + r, ld, 0.0), -1,
+                              keepdim=True)
+            x_row = torch.sum(torch.where(row == (col // block) * block + r, x, 0.0), -2,
+                              keepdim=True)
+            x = x - torch.where(same, l_col * x_row, 0.0)
+        tinv, s = x, block
+    else:
+        tinv, s = eye.expand(lower.shape).clone(), 1
+    while s < c:
+        mask = ((row // (2 * s)) == (col // (2 * s))) & ((row // s) % 2 == 1) & ((col // s) % 2 == 0)
+        off = torch.where(mask, lower, 0.0)
+        tinv = tinv - (tinv @ off) @ tinv
+        s *= 2
+    return tinv
+
+
+# --------------------------------------------------------------------------- delta rule
+def recurrent_gated_delta_rule(q, k, v, g, beta, segment_ids=None, initial_state=None):
+    """Token-by-token reference (xla.py:141-167). q,k [B,T,H,Dk]; v [B,T,H,Dv]; g, beta
+    [B,T,H]. The state restarts where the segment id changes. Returns (out, final_state)."""
+    batch, length, heads, dk = k.shape
+    dv = v.shape[-1]
+    dt = q.dtype
+    if segment_ids is None:
+        segment_ids = torch.ones((batch, length), dtype=torch.int64)
+    previous = torch.cat([segment_ids[:, :1], segment_ids[:, :-1]], dim=1)
+    restart = segment_ids != previous
+    restart[:, 0] = initial_state is None
+    s = (torch.zeros((batch, heads, dk, dv), dtype=dt) if initial_state is None
+         else initial_state.to(dt))
+    outs = []
+    for t in range(length):
+        s = torch.where(restart[:, t, None, None, None], torch.zeros_like(s), s)
+        s = s * torch.exp(g[:, t])[..., None, None]
+        memory = torch.einsum("bhkv,bhk->bhv", s, k[:, t])
+        delta = (v[:, t] - memory) * beta[:, t][..., None]
+        s = s + k[:, t][..., :, None] * delta[..., None, :]
+        outs.append(torch.einsum("bhkv,bhk->bhv", s, q[:, t]))
+    return torch.stack(outs, dim=1), s
+
+
+def chunk_gated_delta_rule(q, k, v, g, beta, segment_ids=None, initial_state=None,
+                           chunk: int = 64):
+    """Chunked WY/UT form with segment resets (xla.py:170-262) at precision "highest"
+    (the matmuls in the inputs' float dtype) with the triangular solve (``inverse="solve"``).
+
+    Pads T to a multiple of ``chunk`` with zero q/k/v/beta, g = 0 and the edge segment id
+    (xla.py:198-204). Returns (out [B,T,H,Dv], final state [B,H,Dk,Dv])."""
+    batch, length, heads, dk = k.shape
+    dv = v.shape[-1]
+    dt = q.dtype
+    if segment_ids is None:
+        segment_ids = torch.ones((batch, length), dtype=torch.int64)
+    segment_ids = segment_ids.to(torch.int64)
+    pad = (-length) % chunk
+    if pad:
+        q, k, v = (torch.nn.functional.pad(x, (0, 0, 0, 0, 0, pad)) for x in (q, k, v))
+        g, beta = (torch.nn.functional.pad(x, (0, 0, 0, pad)) for x in (g, beta))
+        segment_ids = torch.cat([segment_ids, segment_ids[:, -1:].expand(batch, pad)], dim=1)
+    n = (length + pad) // chunk
+
+    def chunked(x):  # [B,T,H,...] -> [B,H,N,C,...]
+        x = x.reshape(batch, n, chunk, heads, *x.shape[3:])
+        return torch.movedim(x, 3, 1)
+
+    q, k, v, g, beta = (chunked(x) for x in (q, k, v, g, beta))
+    seg = segment_ids.reshape(batch, n, chunk)
+    first = (seg[:, :1, 0] if initial_state is not None
+             else torch.full((batch, 1), -2, dtype=seg.dtype))
+    before = torch.cat([first, seg[:, :-1, -1]], dim=1)
+    continues = (seg == before[..., None])[:, None]  # [B,1,N,C]
+    in_last = (seg == seg[..., -1:])[:, None]
+    carry_keep = continues[..., -1]
+    causal = torch.tril(torch.ones((chunk, chunk), dtype=torch.bool))
+    same = ((seg[..., :, None] == seg[..., None, :]) & causal)[:, None]  # [B,1,N,C,C]
+
+    cum = torch.cumsum(g, dim=-1)  # [B,H,N,C]
+    diff = cum[..., :, None] - cum[..., None, :]
+    decay = torch.exp(torch.where(same, diff, torch.full_like(diff, -torch.inf)))
+    k_beta = k * beta[..., None]
+    v_beta = v * beta[..., None]
+    strict = torch.tril(torch.ones((chunk, chunk), dtype=torch.bool), -1)
+    lower = torch.where(strict, (k_beta @ k.transpose(-1, -2)) * decay, 0.0)
+    grow = torch.exp(cum) * continues
+    rhs = torch.cat([v_beta, k_beta * grow[..., None]], dim=-1)
+    eye = torch.eye(chunk, dtype=dt)
+    solved = torch.linalg.solve_triangular(lower + eye, rhs, upper=False, unitriangular=True)
+    u, w = solved[..., :dv], solved[..., dv:]
+    intra = (q @ k.transpose(-1, -2)) * decay
+    q_read = q * grow[..., None]
+    k_write = k * (torch.exp(cum[..., -1:] - cum) * in_last)[..., None]
+    carry = torch.exp(cum[..., -1]) * carry_keep  # [B,H,N]
+
+    s = (torch.zeros((batch, heads, dk, dv), dtype=dt) if initial_state is None
+         else initial_state.to(dt))
+    outs = []
+    for i in range(n):
+        v_new = u[:, :, i] - w[:, :, i] @ s
+        outs.append(q_read[:, :, i] @ s + intra[:, :, i] @ v_new)
+        s = s * carry[:, :, i, None, None] + k_write[:, :, i].transpose(-1, -2) @ v_new
+    out = torch.stack(outs, dim=2).reshape(batch, heads, n * chunk, dv)
+    return out.transpose(1, 2)[:, :length], s
+
+
+# --------------------------------------------------------------------------- masks
+def masks(segment_ids, chunk: int, taps: int) -> dict[str, np.ndarray]:
+    """The megakernel's per-token integer masks (pallas_tpu_mega.py:349-361,
+    pallas_tpu_v2.py:505-515) on ids [B,T] with T a multiple of ``chunk``:
+
+    cont[t]    token t reads the incoming state: seg[t] == id of the previous chunk's last
+               token (-2 before chunk 0)
+    in_last[t] token t writes the outgoing state: seg[t] == id of its chunk's last token
+    keep_L[t]  (L = 1..K-1) token t's conv reads t-L: t-L >= 0 and seg[t-L] == seg[t]
+    valid[t]   seg[t] > 0
+    The reference carries them as float32 (exact for |id| < 2**24); here they are ints."""
+    seg = np.asarray(segment_ids, dtype=np.int64)
+    batch, length = seg.shape
+    if length % chunk:
+        raise ValueError("masks: T must be a multiple of chunk (the megakernel pads first)")
+    n = length // chunk
+    s = seg.reshape(batch, n, chunk)
+    before = np.concatenate([np.full((batch, 1), -2, np.int64), s[:, :-1, -1]], axis=1)
+    out = {
+        "seg": seg.copy(),
+        "cont": (s == before[..., None]).reshape(batch, length).astype(np.int32),
+        "in_last": (s == s[..., -1:]).reshape(batch, length).astype(np.int32),
+        "valid": (seg > 0).astype(np.int32),
+    }
+    padded = np.pad(seg, ((0, 0), (taps - 1, 0)), constant_values=-1)
+    for lag in range(1, taps):
+        out[f"keep_{lag}"] = (padded[:, taps - 1 - lag: taps - 1 - lag + length] == seg
+                              ).astype(np.int32)
+    return out
+
+
+def heads_per_block(heads: int, ratio: int, preferred: int = 8) -> int:
+    """Value heads per program (pallas_tpu_v2.py:518-525): the largest multiple of the GQA
+    ratio dividing H, up to ``preferred``."""
+    if heads % ratio:
+        raise ValueError(f"{heads} value heads are not groups of {ratio}")
+    sizes = range(ratio, max(preferred, ratio) + 1, ratio)
+    return max(size for size in sizes if heads % size == 0)
+
+
+# --------------------------------------------------------------------------- the core
+def reference_core(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_heads: int,
+                   key_dim: int, value_heads: int, value_dim: int, conv: bool = True,
+                   rule: str = "chunked", chunk: int = 64, dtype=torch.float32):
+    """The XLA path the megakernel replaces (test_gdn_mega.py:44-58, ``_reference``):
+    segmented causal conv -> SiLU -> padding mask (``conv``), l2norm(q) * Dk^-1/2, l2norm(k),
+    beta = sigmoid(b), g = -exp(A_log) * softplus(a + dt_bias), key heads repeated for GQA,
+    then the chunked delta rule at fp32 ("highest", triangular solve) or, with
+    ``rule="recurrent"``, the token recurrence (the fp64 truth of test_gdn_long.py:131-176).
+
+    Every floating input is cast to ``dtype`` first (bf16 projections are judged against
+    the reference on the same values in fp32, test_gdn_mega.py:281-297). Returns
+    [B,T,H,Dv] in ``dtype``; differentiable by autograd."""
+    qkv, a, b, a_log, dt_bias = (x.to(dtype) for x in (qkv, a, b, a_log, dt_bias))
+    seg = segment_ids.to(torch.int64)
+    batch, length, _ = qkv.shape
+    hk, h, dk, dv = key_heads, value_heads, key_dim, value_dim
+    if conv:
+        x = segmented_causal_conv1d(qkv, conv_weight.to(dtype), seg)
+        x = torch.where((seg > 0)[..., None], x * torch.sigmoid(x), 0.0)
+    else:
+        x = qkv
+    q, k, v = torch.split(x, [hk * dk, hk * dk, h * dv], dim=-1)
+    q = l2norm(q.reshape(batch, length, hk, dk)) * dk ** -0.5
+    k = l2norm(k.reshape(batch, length, hk, dk))
+    v = v.reshape(batch, length, h, dv)
+    beta = torch.sigmoid(b)
+    xg = a + dt_bias
+    g = -torch.exp(a_log) * torch.logaddexp(xg, torch.zeros_like(xg))  # jax.nn.softplus
+    ratio = h // hk
+    q, k = q.repeat_interleave(ratio, dim=2), k.repeat_interleave(ratio, dim=2)
+    if rule == "chunked":
+        return chunk_gated_delta_rule(q, k, v, g, beta, seg, chunk=chunk)[0]
+    if rule == "recurrent":
+        return recurrent_gated_delta_rule(q, k, v, g, beta, seg)[0]
+    raise ValueError(f"rule in (chunked, recurrent), not {rule!r}")
+
+
+def reference_with_grads(inputs, cotangent, *, key_heads, key_dim, value_heads, value_dim,
+                         conv=True, rule="chunked", chunk=64, dtype=torch.float32,
+                         want_conv_grad=True):
+    """out and the gradients of sum(out * cotangent) w.r.t. qkv, a, b, A_log, dt_bias and the
+    conv weight (test_gdn_mega.py:75-86), all as ``dtype`` tensors.
+    ``inputs`` = (qkv, a, b, a_log, dt_bias, conv_weight, segment_ids)."""
+    qkv, a, b, a_log, dt_bias, w, seg = inputs
+    leaves = [x.detach().to(dtype).requires_grad_(True) for x in (qkv, a, b, a_log, dt_bias)]
+    wl = w.detach().to(dtype).requires_grad_(want_conv_grad and conv) if w is not None else None
+    out = reference_core(*leaves, wl, seg, key_heads=key_heads, key_dim=key_dim,
+                         value_heads=value_heads, value_dim=value_dim, conv=conv, rule=rule,
+                         chunk=chunk, dtype=dtype)
+    loss = torch.sum(out * cotangent.to(dtype))
+    targets = leaves + ([wl] if (wl is not None and wl.requires_grad) else [])
+    grads = torch.autograd.grad(loss, targets)
+    names = ["qkv", "a", "b", "A_log", "dt_bias", "w"]
+    result = {"out": out.detach()}
+    result.update({n: g.detach() for n, g in zip(names, grads)})
+    return result
+
+
+def fp64_truth(inputs, cotangent, **kw):
+    """The same math in float64, token by token (test_gdn_long.py:131-176)."""
+    kw = dict(kw)
+    kw.update(rule="recurrent", dtype=torch.float64)
+    return reference_with_grads(inputs, cotangent, **kw)

@@ -1,0 +1,9 @@
+"""tjev_amd: tjev's Gated DeltaNet megakernel (mega2) on MI355X (gfx950).
+
+``gdn_megakernel`` / ``gdn_core_mega`` keep the reference's operator signature; the work runs
+in hand-written HIP kernels behind the C ABI of ``libtjev_gdn.so`` (include/tjev_gdn.h).
+"""
+
+from .gdn import GdnPlan, gdn_core_mega, gdn_megakernel, heads_per_block, kernel_inverse  # noqa: F401
+
+__all__ = ["GdnPlan", "gdn_core_mega", "gdn_megakernel", "heads_per_block", "kernel_inverse"]

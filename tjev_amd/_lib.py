@@ -1,0 +1,114 @@
+"""ctypes binding of libtjev_gdn.so (include/tjev_gdn.h).
+
+The library is built in-tree by ``python -m tjev_amd.build``. Loading never falls back to
+anything: a missing or broken library raises, so no GDN call can silently run elsewhere.
+torch is imported first so that the library shares torch's HIP runtime (same soname).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch  # noqa: F401  (loads the HIP runtime the library binds to)
+
+LIB_PATH = Path(__file__).resolve().parent / "libtjev_gdn.so"
+
+F32, BF16 = 0, 1
+PRECISION = {"highest": 0, "high": 1, "bf16": 2, "mixed": 3}
+INVERSE = {"doubling": 0, "blocked": 1}
+STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported", 3: "workspace", 4: "HIP error"}
+
+EXPORTS = (
+    "tjev_gdn_check",
+    "tjev_gdn_states_bytes",
+    "tjev_gdn_workspace_bytes",
+    "tjev_gdn_mega2_fwd",
+    "tjev_gdn_mega2_bwd",
+    "tjev_gdn_profile_begin",
+    "tjev_gdn_profile_end",
+    "tjev_gdn_kernel_name",
+    "tjev_gdn_last_error",
+    "tjev_gdn_version",
+)
+N_KERNELS = 11  # TJEV_GDN_KERNELS
+
+
+class Params(ctypes.Structure):
+    """tjev_gdn_params"""
+
+    _fields_ = [(name, ctypes.c_int32) for name in (
+        "batch", "length", "key_heads", "key_dim", "value_heads", "value_dim", "taps", "chunk",
+        "io_dtype", "gate_dtype", "precision", "inverse", "heads_per_step",
+    )]
+
+
+class GdnLibraryError(RuntimeError):
+    """A nonzero status from the library (the message is tjev_gdn_last_error())."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{message} (status {status}: {STATUS.get(status, '?')})")
+        self.status = status
+
+
+_LIB: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library (raises if it is not built)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is not built: run `python -m tjev_amd.build` (hipcc, gfx950)")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    vp, sz, i32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+    pp = ctypes.POINTER(Params)
+    lib.tjev_gdn_check.argtypes = [pp]
+    lib.tjev_gdn_check.restype = i32
+    lib.tjev_gdn_states_bytes.argtypes = [pp]
+    lib.tjev_gdn_states_bytes.restype = sz
+    lib.tjev_gdn_workspace_bytes.argtypes = [pp, i32]
+    lib.tjev_gdn_workspace_bytes.restype = sz
+    lib.tjev_gdn_mega2_fwd.argtypes = [pp, vp] + [vp] * 10 + [sz]
+    lib.tjev_gdn_mega2_fwd.restype = i32
+    lib.tjev_gdn_mega2_bwd.argtypes = [pp, vp] + [vp] * 16 + [sz]
+    lib.tjev_gdn_mega2_bwd.restype = i32
+    lib.tjev_gdn_profile_begin.argtypes = []
+    lib.tjev_gdn_profile_begin.restype = i32
+    lib.tjev_gdn_profile_end.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_int), i32]
+    lib.tjev_gdn_profile_end.restype = i32
+    lib.tjev_gdn_kernel_name.argtypes = [i32]
+    lib.tjev_gdn_kernel_name.restype = ctypes.c_char_p
+    lib.tjev_gdn_last_error.argtypes = []
+    lib.tjev_gdn_last_error.restype = ctypes.c_char_p
+    lib.tjev_gdn_version.argtypes = []
+    lib.tjev_gdn_version.restype = i32
+    _LIB = lib
+    return lib
+
+
+def check_status(status: int) -> None:
+    if status != 0:
+        raise GdnLibraryError(status, load().tjev_gdn_last_error().decode())
+
+
+class KernelTimer:
+    """Per-kernel HIP-event timing of the library's launches (tjev_gdn_profile_*):
+    ``with KernelTimer() as kt: ...`` then ``kt.ms`` / ``kt.launches`` keyed by kernel name."""
+
+    def __enter__(self):
+        check_status(load().tjev_gdn_profile_begin())
+        return self
+
+    def __exit__(self, *exc):
+        lib = load()
+        ms = (ctypes.c_float * N_KERNELS)()
+        launches = (ctypes.c_int * N_KERNELS)()
+        status = lib.tjev_gdn_profile_end(ms, launches, N_KERNELS)
+        names = [lib.tjev_gdn_kernel_name(k).decode() for k in range(N_KERNELS)]
+        self.ms = {n: float(ms[k]) for k, n in enumerate(names)}
+        self.launches = {n: int(launches[k]) for k, n in enumerate(names)}
+        if exc[0] is None:
+            check_status(status)
+        return False

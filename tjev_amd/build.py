@@ -1,0 +1,83 @@
+"""Build libtjev_gdn.so for gfx950 in-tree: one hipcc job per (chunk, head dim) pair of
+csrc/gdn_shapes.def plus the C ABI, linked with ``hipcc -shared``.
+
+    python -m tjev_amd.build [-j JOBS]
+"""
+
+from __future__ import annotations
+
+import argparse
+import os
+import re
+import shutil
+import subprocess
+import sys
+import time
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / "csrc"
+OUT = HERE / "_build"
+LIB = HERE / "libtjev_gdn.so"
+ARCH = "gfx950"
+FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    # packed fp32 instructions stay off in every GPU build of this library
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def shapes() -> list[tuple[int, int]]:
+    text = (CSRC / "gdn_shapes.def").read_text()
+    return [(int(c), int(d)) for c, d in re.findall(r"GDN_SHAPE\((\d+),\s*(\d+)\)", text)]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: the GDN library needs ROCm's hipcc")
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        noise = "is not a recognized feature for this target"
+        err = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{err}")
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    """Compile every kernel unit and link the library (always rebuilds)."""
+    hipcc = _hipcc()
+    OUT.mkdir(exist_ok=True)
+    units = []
+    for c, d in shapes():
+        obj = OUT / f"gdn_inst_c{c}_d{d}.o"
+        units.append([hipcc, *FLAGS, f"-DGDN_C={c}", f"-DGDN_D={d}", "-c", str(CSRC / "gdn_inst.hip"),
+                      "-o", str(obj)])
+    api_obj = OUT / "gdn_api.o"
+    units.append([hipcc, *FLAGS, "-c", str(CSRC / "gdn_api.hip"), "-o", str(api_obj)])
+    t0 = time.time()
+    with ThreadPoolExecutor(max_workers=jobs or min(len(units), os.cpu_count() or 4)) as pool:
+        list(pool.map(_run, units))
+    objs = [u[-1] for u in units]
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([hipcc, *FLAGS, "-shared", "-o", str(tmp), *objs])
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB} in {time.time() - t0:.1f}s ({len(units)} units)")
+    return LIB
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("-j", "--jobs", type=int, default=None)
+    args = ap.parse_args(argv)
+    build(args.jobs, verbose=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,338 @@
+// C ABI of libtjev_gdn.so (declared in include/tjev_gdn.h): argument validation with the
+// reference's error conventions, the workspace layout, and dispatch to the compiled
+// (chunk, head dim, precision, dtype) kernel sequences.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "../../include/tjev_gdn.h"
+#include "gdn_launch.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int status, const std::string& msg) {
+  g_error = msg;
+  return status;
+}
+
+bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+
+const gdn::ShapeTable* lookup(int c, int d) {
+#define GDN_SHAPE(cc, dd) \
+  if (c == cc && d == dd) return gdn::table_##cc##_##dd();
+#include "gdn_shapes.def"
+#undef GDN_SHAPE
+  return nullptr;
+}
+
+std::string supported_shapes() {
+  std::string s;
+#define GDN_SHAPE(cc, dd) s += "(chunk " #cc ", dim " #dd ") ";
+#include "gdn_shapes.def"
+#undef GDN_SHAPE
+  return s;
+}
+
+// The chunk the kernels run: the requested one, or 16 for chunks below 16 (the chunked form is
+// exact for any chunk, so only fp32 rounding depends on it).
+int kernel_chunk(const tjev_gdn_params* p) { return p->chunk < 16 ? 16 : p->chunk; }
+
+// Validation in the order of gdn_megakernel (pallas_tpu_mega.py:597-615) and
+// heads_per_block (pallas_tpu_v2.py:518-525).
+int validate(const tjev_gdn_params* p) {
+  if (!p) return fail(TJEV_GDN_EINVAL, "null params");
+  if (p->precision < 0 || p->precision > 3)
+    return fail(TJEV_GDN_EINVAL, "precision in (highest, high, bf16, mixed)");
+  if (p->inverse < 0 || p->inverse > 1)
+    return fail(TJEV_GDN_EINVAL, "the GDN megakernel's inverse in (doubling, blocked)");
+  if (!pow2(p->chunk) || p->chunk < 8)
+    return fail(TJEV_GDN_EINVAL, "the GDN megakernel needs a power-of-two chunk >= 8, not " +
+                                     std::to_string(p->chunk));
+  if (p->batch <= 0 || p->length <= 0 || p->key_heads <= 0 || p->value_heads <= 0 ||
+      p->key_dim <= 0 || p->value_dim <= 0)
+    return fail(TJEV_GDN_EINVAL, "batch, length, heads and dims must be positive");
+  if (p->value_heads % p->key_heads)
+    return fail(TJEV_GDN_EINVAL, std::to_string(p->value_heads) + " value heads are not groups of " +
+                                     std::to_string(p->key_heads) + " key heads");
+  if (p->taps < 0 || p->taps > 5)
+    return fail(TJEV_GDN_EINVAL, "conv kernel of " + std::to_string(p->taps) +
+                                     " taps: the megakernel supports 1..5");
+  if (p->io_dtype < 0 || p->io_dtype > 1 || p->gate_dtype < 0 || p->gate_dtype > 1)
+    return fail(TJEV_GDN_EINVAL, "dtypes must be TJEV_GDN_F32 or TJEV_GDN_BF16");
+  if (p->heads_per_step < 0) return fail(TJEV_GDN_EINVAL, "heads_per_step must be >= 0");
+  if (p->key_dim != p->value_dim)
+    return fail(TJEV_GDN_EUNSUPPORTED, "this build's kernels need key_dim == value_dim");
+  if (!lookup(kernel_chunk(p), p->key_dim))
+    return fail(TJEV_GDN_EUNSUPPORTED, "no kernels for chunk " + std::to_string(p->chunk) + ", head dim " +
+                                           std::to_string(p->key_dim) + "; compiled: " + supported_shapes());
+  const long w = 2L * p->key_heads * p->key_dim + (long)p->value_heads * p->value_dim;
+  if (w > (1L << 30) || (long)p->batch * p->length * w > (1L << 40))
+    return fail(TJEV_GDN_EINVAL, "problem too large");
+  return 0;
+}
+
+struct Layout {
+  size_t segp, qn, kn, vv, gam, gaml, bet, uu, ww, vnew, tt, xl, kt, gg, gsp, dqh, dkh, dgam, dbet, pa, pd, dwp;
+  size_t total;
+};
+
+size_t up(size_t x) { return (x + 255) & ~size_t(255); }
+
+Layout layout(const tjev_gdn_params* p, int backward) {
+  const size_t C = kernel_chunk(p), D = p->key_dim;
+  const size_t B = p->batch, H = p->value_heads, Hk = p->key_heads;
+  const size_t N = (p->length + C - 1) / C, Tp = N * C;
+  const size_t W = 2 * Hk * D + H * D;
+  const size_t ntiles = D / (D < 32 ? D : 32);
+  const size_t hv = B * H * Tp * D * 4, hkv = B * Hk * Tp * D * 4, tok = B * H * Tp * 4;
+  Layout L{};
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += up(bytes);
+    return at;
+  };
+  const size_t none = ~size_t(0);
+  L.segp = take(B * Tp * 4);
+  L.qn = take(hkv);
+  L.kn = take(hkv);
+  L.vv = take(hv);
+  L.gam = take(tok);
+  L.gaml = take(tok);
+  L.bet = take(tok);
+  L.vnew = take(hv);
+  if (!backward) {
+    L.uu = take(hv);
+    L.ww = take(hv);
+    L.tt = L.xl = L.kt = L.gg = L.gsp = L.dqh = L.dkh = L.dgam = L.dbet = L.pa = L.pd = L.dwp = none;
+  } else {
+    L.uu = L.ww = none;
+    L.tt = take(B * H * N * C * C * 4);
+    L.xl = take(hv);
+    L.kt = take(hv);
+    L.gg = take(B * H * N * D * D * 4);
+    L.gsp = take(B * H * N * ntiles * 4);
+    L.dqh = take(hv);
+    L.dkh = take(hv);
+    L.dgam = take(tok);
+    L.dbet = take(tok);
+    L.pa = take(B * N * H * 8);
+    L.pd = take(B * N * H * 8);
+    L.dwp = take(B * N * (p->taps > 0 ? p->taps : 1) * W * 4);
+  }
+  L.total = o;
+  return L;
+}
+
+template <class T>
+T* at(void* ws, size_t off) {
+  return off == ~size_t(0) ? nullptr : reinterpret_cast<T*>(static_cast<char*>(ws) + off);
+}
+
+gdn::GdnArgs base_args(const tjev_gdn_params* p, void* ws, const Layout& L) {
+  gdn::GdnArgs A{};
+  const int C = kernel_chunk(p), D = p->key_dim;
+  A.B = p->batch;
+  A.T = p->length;
+  A.N = (p->length + C - 1) / C;
+  A.Tp = A.N * C;
+  A.Hk = p->key_heads;
+  A.H = p->value_heads;
+  A.ratio = p->value_heads / p->key_heads;
+  A.taps = p->taps;
+  A.W = 2 * p->key_heads * D + p->value_heads * D;
+  A.ntiles = D / (D < 32 ? D : 32);
+  A.scale = 1.0f / sqrtf((float)D);
+  A.segp = at<int32_t>(ws, L.segp);
+  A.qn = at<float>(ws, L.qn);
+  A.kn = at<float>(ws, L.kn);
+  A.vv = at<float>(ws, L.vv);
+  A.gam = at<float>(ws, L.gam);
+  A.gaml = at<float>(ws, L.gaml);
+  A.bet = at<float>(ws, L.bet);
+  A.uu = at<float>(ws, L.uu);
+  A.ww = at<float>(ws, L.ww);
+  A.vnew = at<float>(ws, L.vnew);
+  A.tt = at<float>(ws, L.tt);
+  A.xl = at<float>(ws, L.xl);
+  A.kt = at<float>(ws, L.kt);
+  A.gg = at<float>(ws, L.gg);
+  A.gsp = at<float>(ws, L.gsp);
+  A.dqh = at<float>(ws, L.dqh);
+  A.dkh = at<float>(ws, L.dkh);
+  A.dgam = at<float>(ws, L.dgam);
+  A.dbet = at<float>(ws, L.dbet);
+  A.pa = at<double>(ws, L.pa);
+  A.pd = at<double>(ws, L.pd);
+  A.dwp = at<float>(ws, L.dwp);
+  return A;
+}
+
+int aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// ---- per-kernel timing: an event pair around each launch while profiling is on
+const char* const kKernelNames[gdn::K_COUNT] = {
+    "gdn_prep_fwd", "gdn_chunk_fwd", "gdn_scan_fwd", "gdn_out",     "gdn_prep_bwd", "gdn_chunk_bwd",
+    "gdn_bwd_local", "gdn_scan_bwd", "gdn_bwd_grads", "gdn_post", "gdn_reduce"};
+
+struct Profiler {
+  bool on = false;
+  std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> marks;
+  std::vector<hipEvent_t> pool;
+  hipEvent_t pending = nullptr;
+  hipError_t err = hipSuccess;
+  hipEvent_t take() {
+    if (!pool.empty()) {
+      hipEvent_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    const hipError_t r = hipEventCreate(&e);
+    if (r != hipSuccess) err = r;
+    return e;
+  }
+};
+Profiler g_prof;
+
+void prof_mark(void*, int kernel, int end, hipStream_t st) {
+  hipEvent_t e = g_prof.take();
+  if (!e) return;
+  const hipError_t r = hipEventRecord(e, st);
+  if (r != hipSuccess) g_prof.err = r;
+  if (!end) {
+    g_prof.pending = e;
+  } else {
+    g_prof.marks.push_back({kernel, {g_prof.pending, e}});
+    g_prof.pending = nullptr;
+  }
+}
+
+int run(const tjev_gdn_params* p, void* stream, gdn::GdnArgs& A, int backward) {
+  const gdn::ShapeTable* t = lookup(kernel_chunk(p), p->key_dim);
+  const gdn::GdnFn fn = t->fn[p->precision][p->io_dtype][p->gate_dtype];
+  const gdn::Timer timer{prof_mark, nullptr};
+  const hipError_t e = fn(A, static_cast<hipStream_t>(stream), backward, g_prof.on ? &timer : nullptr);
+  if (e != hipSuccess) return fail(TJEV_GDN_EHIP, std::string("HIP launch failed: ") + hipGetErrorString(e));
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tjev_gdn_check(const tjev_gdn_params* p) { return validate(p); }
+
+size_t tjev_gdn_states_bytes(const tjev_gdn_params* p) {
+  if (validate(p)) return 0;
+  const size_t C = kernel_chunk(p);
+  const size_t N = (p->length + C - 1) / C;
+  return (size_t)p->batch * p->value_heads * N * p->key_dim * p->value_dim * 4;
+}
+
+size_t tjev_gdn_workspace_bytes(const tjev_gdn_params* p, int backward) {
+  if (validate(p)) return 0;
+  return layout(p, backward).total;
+}
+
+int tjev_gdn_mega2_fwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
+                       const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg, void* out,
+                       float* states, void* workspace, size_t workspace_bytes) {
+  if (int s = validate(p)) return s;
+  if (!qkv || !a || !b || !a_log || !dt_bias || !seg || !out || !states || (p->taps > 0 && !conv_w))
+    return fail(TJEV_GDN_EINVAL, "null tensor argument");
+  if (!aligned(qkv, 16) || !aligned(out, 16) || !aligned(states, 16) || !aligned(workspace, 256))
+    return fail(TJEV_GDN_EINVAL, "qkv, out and states must be 16-byte aligned, the workspace 256-byte aligned");
+  const Layout L = layout(p, 0);
+  if (!workspace || workspace_bytes < L.total)
+    return fail(TJEV_GDN_EWORKSPACE, "forward workspace needs " + std::to_string(L.total) + " bytes");
+  gdn::GdnArgs A = base_args(p, workspace, L);
+  A.qkv = qkv;
+  A.ga = a;
+  A.gb = b;
+  A.a_log = a_log;
+  A.dt_bias = dt_bias;
+  A.conv_w = conv_w;
+  A.seg = seg;
+  A.out = out;
+  A.states = states;
+  return run(p, stream, A, 0);
+}
+
+int tjev_gdn_mega2_bwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
+                       const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg,
+                       const float* states, const void* d_out, void* d_qkv, void* d_a, void* d_b, float* d_a_log,
+                       float* d_dt_bias, float* d_conv_w, void* workspace, size_t workspace_bytes) {
+  if (int s = validate(p)) return s;
+  if (!qkv || !a || !b || !a_log || !dt_bias || !seg || !states || !d_out || !d_qkv || !d_a || !d_b || !d_a_log ||
+      !d_dt_bias || (p->taps > 0 && !conv_w))
+    return fail(TJEV_GDN_EINVAL, "null tensor argument");
+  if (p->taps == 0 && d_conv_w) return fail(TJEV_GDN_EINVAL, "no conv weight gradient without a conv (taps == 0)");
+  if (!aligned(qkv, 16) || !aligned(d_out, 16) || !aligned(d_qkv, 16) || !aligned(states, 16) ||
+      !aligned(workspace, 256))
+    return fail(TJEV_GDN_EINVAL, "tensors must be 16-byte aligned, the workspace 256-byte aligned");
+  const Layout L = layout(p, 1);
+  if (!workspace || workspace_bytes < L.total)
+    return fail(TJEV_GDN_EWORKSPACE, "backward workspace needs " + std::to_string(L.total) + " bytes");
+  gdn::GdnArgs A = base_args(p, workspace, L);
+  A.qkv = qkv;
+  A.ga = a;
+  A.gb = b;
+  A.a_log = a_log;
+  A.dt_bias = dt_bias;
+  A.conv_w = conv_w;
+  A.seg = seg;
+  A.states = const_cast<float*>(states);
+  A.d_out = d_out;
+  A.d_qkv = d_qkv;
+  A.d_a = d_a;
+  A.d_b = d_b;
+  A.d_a_log = d_a_log;
+  A.d_dt_bias = d_dt_bias;
+  A.d_conv_w = d_conv_w;
+  return run(p, stream, A, 1);
+}
+
+int tjev_gdn_profile_begin(void) {
+  g_prof.on = true;
+  return 0;
+}
+
+int tjev_gdn_profile_end(float* ms, int* launches, int n) {
+  g_prof.on = false;
+  for (int k = 0; k < n; ++k) {
+    ms[k] = 0.f;
+    launches[k] = 0;
+  }
+  int status = 0;
+  if (g_prof.err != hipSuccess) status = fail(TJEV_GDN_EHIP, std::string("profiling: ") + hipGetErrorString(g_prof.err));
+  for (auto& m : g_prof.marks) {
+    float t = 0.f;
+    if (hipEventSynchronize(m.second.second) == hipSuccess &&
+        hipEventElapsedTime(&t, m.second.first, m.second.second) == hipSuccess && m.first < n) {
+      ms[m.first] += t;
+      launches[m.first] += 1;
+    }
+    g_prof.pool.push_back(m.second.first);
+    g_prof.pool.push_back(m.second.second);
+  }
+  g_prof.marks.clear();
+  g_prof.err = hipSuccess;
+  return status;
+}
+
+const char* tjev_gdn_kernel_name(int kernel) {
+  return (kernel >= 0 && kernel < gdn::K_COUNT) ? kKernelNames[kernel] : "";
+}
+
+const char* tjev_gdn_last_error(void) { return g_error.c_str(); }
+
+int tjev_gdn_version(void) { return (0 << 16) | 1; }
+
+}  // extern "C"

@@ -1,0 +1,57 @@
+// Kernel arguments of the GDN kernel sequences: shapes, tensors and workspace slices.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace gdn {
+
+struct GdnArgs {
+  int B, T, Tp, N, Hk, H, ratio, taps, W;
+  int ntiles;  // Dv tiles of the scans
+  float scale; // Dk^-1/2
+  // inputs
+  const void* qkv;
+  const void* ga;
+  const void* gb;
+  const float* a_log;
+  const float* dt_bias;
+  const float* conv_w;
+  const int32_t* seg;
+  // forward outputs
+  void* out;
+  float* states;  // [B, H, N, Dk, Dv]
+  // backward
+  const void* d_out;
+  void* d_qkv;
+  void* d_a;
+  void* d_b;
+  float* d_a_log;
+  float* d_dt_bias;
+  float* d_conv_w;
+  // workspace
+  int32_t* segp;  // [B, Tp]
+  float* qn;      // [B, Hk, Tp, D]  l2norm(q) * Dk^-1/2
+  float* kn;      // [B, Hk, Tp, D]  l2norm(k)
+  float* vv;      // [B, H, Tp, D]   post-conv v
+  float* gam;     // [B, H, Tp]      in-chunk cumulative log decay (fp32 high part)
+  float* gaml;    // [B, H, Tp]      its low part: gamma = gam + gaml to fp64 accuracy
+  float* bet;     // [B, H, Tp]      beta
+  float* uu;      // [B, H, Tp, D]   u = T v beta            (forward)
+  float* ww;      // [B, H, Tp, D]   w = T kbe               (forward)
+  float* vnew;    // [B, H, Tp, D]   v_new
+  float* tt;      // [B, H, N, C, C] T = (I+L)^-1           (backward)
+  float* xl;      // [B, H, Tp, D]   X_loc, then X
+  float* kt;      // [B, H, Tp, D]   T^T k_write
+  float* gg;      // [B, H, N, D, D] G after each chunk
+  float* gsp;     // [B, H, N, ntiles] <G_after, S_after> per Dv tile
+  float* dqh;     // [B, H, Tp, D]   dq per value head
+  float* dkh;     // [B, H, Tp, D]   dk per value head
+  float* dgam;    // [B, H, Tp]
+  float* dbet;    // [B, H, Tp]
+  double* pa;     // [B, N, H] partial d A_log (fp64)
+  double* pd;     // [B, N, H] partial d dt_bias (fp64)
+  float* dwp;     // [B*N, K, W] partial d conv weight (or null)
+};
+
+}  // namespace gdn

@@ -1,0 +1,235 @@
+// Device building blocks of the GDN megakernel for gfx950 (MI355X, CDNA4).
+//
+// Matrix products run on 16x16 MFMA tiles, one wave (64 lanes) per tile strip. A lane's
+// operand fragment is 8 consecutive contraction values: A(i, k0 + 8*(lane/16) + e) and
+// B(k0 + 8*(lane/16) + e, j) for e = 0..7, with i = i0 + lane%16 and j = j0 + lane%16.
+// The accumulator of a tile holds D[4*(lane/16) + r][lane%16], r = 0..3.
+//
+// Three arithmetic modes (the reference's "precision", xla.py:23-36):
+//   P_F32    fp32 operands on v_mfma_f32_16x16x4_f32 (8 instructions per 32 k-values)
+//   P_BF16X3 each fp32 operand split into bf16 hi + lo, hi*hi + hi*lo + lo*hi on
+//            v_mfma_f32_16x16x32_bf16, fp32 accumulation (the TPU's bf16_3x "high")
+//   P_BF16   one bf16 pass with fp32 accumulation
+// Operands are "views": small structs whose load(r, k, out) fills out[e] = V(r, k + e).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gdn {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+enum : int { P_F32 = 0, P_BF16X3 = 1, P_BF16 = 2 };
+
+__device__ __forceinline__ int lane() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave() { return threadIdx.x >> 6; }
+
+// ---------------------------------------------------------------- bf16 storage
+// bf16 tensors are held as uint16_t; conversion rounds to nearest even (as torch does).
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float ldf(const float* p) { return *p; }
+__device__ __forceinline__ float ldf(const uint16_t* p) { return bf2f(*p); }
+__device__ __forceinline__ void stf(float* p, float v) { *p = v; }
+__device__ __forceinline__ void stf(uint16_t* p, float v) { *p = f2bf(v); }
+
+// 8 consecutive elements (16-byte aligned for bf16, 32-byte for fp32) as floats
+__device__ __forceinline__ void ld8(const float* p, float (&o)[8]) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0];
+  const float4 b = reinterpret_cast<const float4*>(p)[1];
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+  o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+__device__ __forceinline__ void ld8(const uint16_t* p, float (&o)[8]) {
+  const uint4 a = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    o[2 * e] = __uint_as_float(w[e] << 16);
+    o[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+  }
+}
+
+// ---------------------------------------------------------------- numerics
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+// jax.nn.softplus = logaddexp(x, 0) = max(x, 0) + log1p(exp(-|x|))
+__device__ __forceinline__ float softplusf_(float x) {
+  return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
+}
+
+// ---------------------------------------------------------------- MFMA fragments
+template <int P> struct Frag;
+template <> struct Frag<P_F32> { float v[8]; };
+template <> struct Frag<P_BF16> { bf16x8 hi; };
+template <> struct Frag<P_BF16X3> { bf16x8 hi, lo; };
+
+template <int P>
+__device__ __forceinline__ Frag<P> make_frag(const float (&x)[8]) {
+  Frag<P> f;
+  if constexpr (P == P_F32) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f.v[e] = x[e];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f.hi[e] = (__bf16)x[e];
+    if constexpr (P == P_BF16X3) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f.lo[e] = (__bf16)(x[e] - (float)f.hi[e]);
+    }
+  }
+  return f;
+}
+
+template <int P>
+__device__ __forceinline__ void mma(f32x4& acc, const Frag<P>& a, const Frag<P>& b) {
+  if constexpr (P == P_F32) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[e], b.v[e], acc, 0, 0, 0);
+  } else if constexpr (P == P_BF16) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.hi, acc, 0, 0, 0);
+  } else {  // the small cross terms first, then hi*hi
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, b.hi, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.lo, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.hi, acc, 0, 0, 0);
+  }
+}
+
+// ---------------------------------------------------------------- operand views
+// V(r, k) = p[r*ld + k]: the contraction index is contiguous (vector loads).
+template <class T>
+struct KRow {
+  const T* p;
+  int ld;
+  __device__ __forceinline__ void load(int r, int k, float (&o)[8]) const { ld8(p + r * ld + k, o); }
+};
+// V(r, k) = p[k*ld + r]: the contraction index is the row (strided loads; LDS operands).
+template <class T>
+struct KCol {
+  const T* p;
+  int ld;
+  __device__ __forceinline__ void load(int r, int k, float (&o)[8]) const {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = ldf(p + (k + e) * ld + r);
+  }
+};
+// V'(r, k) = c * s[r] * V(r, k)
+template <class V>
+struct ScaleR {
+  V v;
+  const float* s;
+  float c;
+  __device__ __forceinline__ void load(int r, int k, float (&o)[8]) const {
+    v.load(r, k, o);
+    const float f = c * s[r];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] *= f;
+  }
+};
+// V'(r, k) = c * s[k] * V(r, k)
+template <class V>
+struct ScaleK {
+  V v;
+  const float* s;
+  float c;
+  __device__ __forceinline__ void load(int r, int k, float (&o)[8]) const {
+    v.load(r, k, o);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] *= c * s[k + e];
+  }
+};
+template <class T> __device__ __forceinline__ KRow<T> krow(const T* p, int ld) { return {p, ld}; }
+template <class T> __device__ __forceinline__ KCol<T> kcol(const T* p, int ld) { return {p, ld}; }
+template <class V> __device__ __forceinline__ ScaleR<V> scale_r(V v, const float* s, float c = 1.f) { return {v, s, c}; }
+template <class V> __device__ __forceinline__ ScaleK<V> scale_k(V v, const float* s, float c = 1.f) { return {v, s, c}; }
+
+// ---------------------------------------------------------------- strip product
+// acc[t] += sum over k in [kb, ke) of A(i0 + lane%16, k) * B(k, j0 + 16t + lane%16).
+// kb is a multiple of 32; ke <= K. K is a multiple of 16; when K is 16 the lanes of the
+// upper contraction half feed zeros.
+template <int P, int K, int TN, class AV, class BV>
+__device__ __forceinline__ void strip_mma(f32x4 (&acc)[TN], const AV& A, int i0, const BV& B, int j0,
+                                          int kb = 0, int ke = K) {
+  const int l = lane();
+  const int r = l & 15;
+  const int kg = (l >> 4) << 3;
+  for (int k = kb; k < ke; k += 32) {
+    const bool ok = (K % 32 == 0) || (k + kg < K);
+    float x[8];
+    if (ok) {
+      A.load(i0 + r, k + kg, x);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = 0.f;
+    }
+    const Frag<P> fa = make_frag<P>(x);
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      float y[8];
+      if (ok) {
+        B.load(j0 + 16 * t + r, k + kg, y);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = 0.f;
+      }
+      mma<P>(acc[t], fa, make_frag<P>(y));
+    }
+  }
+}
+
+template <int TN>
+__device__ __forceinline__ void zero(f32x4 (&acc)[TN]) {
+#pragma unroll
+  for (int t = 0; t < TN; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+// Row (within a 16-row strip) of accumulator element rr, and column within a tile.
+__device__ __forceinline__ int acc_row(int rr) { return ((lane() >> 4) << 2) + rr; }
+__device__ __forceinline__ int acc_col() { return lane() & 15; }
+
+// contraction range of a lower-triangular left operand for rows [i0, i0+16): k <= i0+15
+template <int K> __device__ __forceinline__ int tri_end(int i0) { return min(K, ((i0 + 16 + 31) / 32) * 32); }
+// ... and of an upper-triangular one (a transposed lower-triangular): k >= i0
+__device__ __forceinline__ int tri_begin(int i0) { return (i0 / 32) * 32; }
+
+// sum over the 16 lanes that share lane/16 (one accumulator row across a tile's columns)
+__device__ __forceinline__ float sum16(float v) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 4);
+  v += __shfl_xor(v, 8);
+  return v;
+}
+__device__ __forceinline__ float sum64(float v) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 4);
+  v += __shfl_xor(v, 8);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+__device__ __forceinline__ double sum64d(double v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
+// ---------------------------------------------------------------- launch mapping
+// Workgroups go to the 8 XCDs round-robin (id % 8). This remap gives each XCD a contiguous
+// range of logical ids, so work items that share inputs (the Dv tiles of one head) land on
+// the same XCD and its L2. Identity when the grid is not a multiple of 8.
+__device__ __forceinline__ int xcd_remap(int bid, int grid) {
+  if (grid % 8) return bid;
+  return (bid % 8) * (grid / 8) + bid / 8;
+}
+
+}  // namespace gdn

@@ -1,0 +1,76 @@
+// One (chunk, head dim) instantiation of the kernel sequences, built once per GDN_SHAPE in
+// gdn_shapes.def with -DGDN_C=<chunk> -DGDN_D=<head dim>.
+#include "gdn_kernels.h"
+#include "gdn_launch.h"
+
+#ifndef GDN_C
+#error "build with -DGDN_C=<chunk> -DGDN_D=<head dim>"
+#endif
+
+namespace gdn {
+namespace {
+
+template <int C, int D, int PI, int PS, class TIO, class TG>
+hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) {
+  constexpr int DVT = D < 32 ? D : 32;
+  constexpr int NS = (C > D ? C : D) * 4;
+  const dim3 prep(A.B * A.N, 2 * A.Hk + A.H);
+  const dim3 chunks(A.B * A.H * A.N);
+  const dim3 tiles(A.B * A.H * (D / DVT));
+  auto mark = [&](int k, int end) {
+    if (tm) tm->mark(tm->self, k, end, st);
+  };
+#define GDN_LAUNCH(id, kern, grid, block)                  \
+  do {                                                     \
+    mark(id, 0);                                           \
+    hipLaunchKernelGGL(kern, grid, block, 0, st, A);       \
+    mark(id, 1);                                           \
+  } while (0)
+  if (!backward) {
+    GDN_LAUNCH(K_PREP_FWD, (k_prep<C, D, TIO, TG>), prep, dim3(256));
+    GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0>), chunks, dim3(C * 4));
+    GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd<C, D, DVT, PI, PS>), tiles, dim3(NS));
+    GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO>), chunks, dim3(C * 4));
+  } else {
+    const int outs = A.H + (A.d_conv_w ? A.taps * A.W : 0);
+    GDN_LAUNCH(K_PREP_BWD, (k_prep<C, D, TIO, TG>), prep, dim3(256));
+    GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 1>), chunks, dim3(C * 4));
+    GDN_LAUNCH(K_BWD_LOCAL, (k_bwd_local<C, D, PI, TIO>), chunks, dim3(C * 4));
+    GDN_LAUNCH(K_SCAN_BWD, (k_scan_bwd<C, D, DVT, PI, PS, TIO>), tiles, dim3(NS));
+    GDN_LAUNCH(K_BWD_GRADS, (k_bwd_grads<C, D, PI, PS, TIO>), chunks, dim3(C * 4));
+    GDN_LAUNCH(K_POST, (k_post<C, D, TIO, TG>), prep, dim3(256));
+    GDN_LAUNCH(K_REDUCE, (k_reduce<C>), dim3((outs + 255) / 256), dim3(256));
+  }
+#undef GDN_LAUNCH
+  return hipGetLastError();
+}
+
+template <int PI, int PS>
+void fill(GdnFn (&f)[2][2]) {
+  f[0][0] = run<GDN_C, GDN_D, PI, PS, float, float>;
+  f[0][1] = run<GDN_C, GDN_D, PI, PS, float, uint16_t>;
+  f[1][0] = run<GDN_C, GDN_D, PI, PS, uint16_t, float>;
+  f[1][1] = run<GDN_C, GDN_D, PI, PS, uint16_t, uint16_t>;
+}
+
+ShapeTable make() {
+  ShapeTable t{};
+  t.C = GDN_C;
+  t.D = GDN_D;
+  fill<P_F32, P_F32>(t.fn[0]);       // highest
+  fill<P_BF16X3, P_BF16X3>(t.fn[1]); // high
+  fill<P_BF16, P_BF16>(t.fn[2]);     // bf16
+  fill<P_BF16X3, P_BF16>(t.fn[3]);   // mixed
+  return t;
+}
+
+}  // namespace
+
+#define GDN_CAT_(a, b, c) a##b##_##c
+#define GDN_CAT(a, b, c) GDN_CAT_(a, b, c)
+const ShapeTable* GDN_CAT(table_, GDN_C, GDN_D)() {
+  static const ShapeTable t = make();
+  return &t;
+}
+
+}  // namespace gdn

@@ -1,0 +1,1025 @@
+// The GDN megakernel's HIP kernels for gfx950, as templates over the chunk C, the head dim
+// D (= Dk = Dv), the arithmetic of the intra-chunk products PI and of the state-path
+// products PS, and the storage type of the activations (float or bf16 as uint16_t).
+//
+// Forward (reference: pallas_tpu_mega.py:216-249 with pallas_tpu_v2.py:212-269):
+//   k_prep      conv + SiLU + padding mask, l2norm(q, k), q * Dk^-1/2, gates beta, g and the
+//               in-chunk cumulative decay gamma; head-major fp32 tiles      (HBM-bound)
+//   k_chunk     per (row, head, chunk): L = strict(beta k k^T . D), T = (I+L)^-1 (16x16
+//               diagonal blocks by substitution, then doubling levels on MFMA),
+//               w = T kbe, u = T v beta                                       (MFMA)
+//   k_scan_fwd  per (row, head, Dv tile): the recurrent state S (Dk x Dv tile, fp32), chunks
+//               in order: S_before stored, v_new = u - w S, S = carry S + k_write^T v_new
+//   k_out       per chunk: o = q_read S_before + ((q k^T) . D) v_new        (MFMA)
+// Backward (reference: pallas_tpu_mega.py:252-319 with pallas_tpu_v2.py:272-318):
+//   k_prep (recomputed), k_chunk (mode 1: T kept, v_new = u - w S_before recomputed from the
+//   saved chunk-boundary states), k_bwd_local (X_loc = T^T intra^T do, Kt = T^T k_write),
+//   k_scan_bwd (chunks reversed: X = X_loc + Kt G, G = carry G + q_read^T do - kbe^T X),
+//   k_bwd_grads (dq, dk per value head, d gamma, d beta), k_post (GQA sums, l2norm, SiLU and
+//   conv backward, gate backward), k_reduce (d A_log, d dt_bias, d conv weight).
+#pragma once
+
+#include "gdn_args.h"
+#include "gdn_device.h"
+
+namespace gdn {
+
+
+
+__device__ __forceinline__ size_t hoff(const GdnArgs& A, int b, int head, int heads, int n, int C, int D) {
+  return ((size_t)(b * heads + head) * A.Tp + (size_t)n * C) * D;
+}
+
+// ---------------------------------------------------------------- chunk context
+// Segment semantics (pallas_tpu_v2.py:226-241, pallas_tpu_mega.py:349-361): cont_i: token i
+// reads the incoming state (same id as the previous chunk's last token; -2 before chunk 0);
+// in_last_i: token i writes the outgoing state (same id as the chunk's last token).
+template <int C>
+struct Ctx {
+  int seg[C];
+  float gam[C], gaml[C], beta[C], grow[C], kws[C], bg[C];
+  int before;
+  float carry;
+};
+
+// gamma_i - gamma_j from the (high, low) pairs: the high parts of nearby tokens subtract
+// exactly, so the decays keep the accuracy of the fp64 prefix sum
+template <int C>
+__device__ __forceinline__ float gdiff(const Ctx<C>& cx, int i, int j) {
+  return (cx.gam[i] - cx.gam[j]) + (cx.gaml[i] - cx.gaml[j]);
+}
+
+template <int C, int NT>
+__device__ void load_ctx(Ctx<C>& cx, const GdnArgs& A, int b, int h, int n) {
+  const size_t tok = (size_t)(b * A.H + h) * A.Tp + (size_t)n * C;
+  for (int i = threadIdx.x; i < C; i += NT) {
+    cx.seg[i] = A.segp[(size_t)b * A.Tp + (size_t)n * C + i];
+    cx.gam[i] = A.gam[tok + i];
+    cx.gaml[i] = A.gaml[tok + i];
+    cx.beta[i] = A.bet[tok + i];
+  }
+  if (threadIdx.x == 0) cx.before = n == 0 ? -2 : A.segp[(size_t)b * A.Tp + (size_t)n * C - 1];
+  __syncthreads();
+  for (int i = threadIdx.x; i < C; i += NT) {
+    const bool cont = cx.seg[i] == cx.before;
+    const bool in_last = cx.seg[i] == cx.seg[C - 1];
+    cx.grow[i] = cont ? expf(cx.gam[i] + cx.gaml[i]) : 0.f;        // e^gamma . cont
+    cx.kws[i] = in_last ? expf(gdiff(cx, C - 1, i)) : 0.f;          // e^(gamma_C - gamma) . in_last
+    cx.bg[i] = cx.beta[i] * cx.grow[i];                              // kbe = k . beta . grow
+  }
+  if (threadIdx.x == 0) cx.carry = (cx.seg[C - 1] == cx.before) ? expf(cx.gam[C - 1] + cx.gaml[C - 1]) : 0.f;
+  __syncthreads();
+}
+
+// D_ij = e^(gamma_i - gamma_j) on same-segment i >= j, else 0 (the exp taken only there)
+template <int C>
+__device__ __forceinline__ float decay(const Ctx<C>& cx, int i, int j) {
+  return (i >= j && cx.seg[i] == cx.seg[j]) ? expf(gdiff(cx, i, j)) : 0.f;
+}
+
+// rows x D fp32 tile from global (row stride D) into LDS (row stride LD)
+template <int R, int D, int NT>
+__device__ __forceinline__ void load_tile(float* s, int LD, const float* g) {
+  constexpr int V = D / 4;
+  for (int idx = threadIdx.x; idx < R * V; idx += NT) {
+    const int r = idx / V, c = idx % V;
+    *reinterpret_cast<float4*>(s + r * LD + 4 * c) = reinterpret_cast<const float4*>(g)[idx];
+  }
+}
+
+// row view of a token-major activation tensor with rows past the valid count read as 0
+template <class T>
+struct KRowLim {
+  const T* p;
+  int ld;
+  int rows;
+  __device__ __forceinline__ void load(int r, int k, float (&o)[8]) const {
+    if (r < rows) {
+      ld8(p + (size_t)r * ld + k, o);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = 0.f;
+    }
+  }
+};
+
+// ---------------------------------------------------------------- inverse
+// (I + L)^-1 in place for the strictly lower-triangular L in sT (C x C, row stride LT):
+// exact 16x16 diagonal blocks by forward substitution (one wave per block, on the VALU),
+// then doubling levels s = 16 .. C/2: T_LL = -T_BR (L_LL T_TL) on MFMA
+// (pallas_tpu_v2.py:144-193; xla.py:82-100). tmp holds C*(C/2+4)/2 floats.
+template <int C, int P, int S>
+__device__ void doubling_level(float* sT, int LT, float* tmp) {
+  if constexpr (S < C) {
+    constexpr int NW = C / 16;
+    constexpr int TPS = S / 16;
+    constexpr int NB = C / (2 * S);
+    constexpr int LP = S + 4;
+    const int w = wave();
+    for (int q = w; q < NB * TPS * TPS; q += NW) {
+      const int p = q / (TPS * TPS), ti = (q / TPS) % TPS, tj = q % TPS;
+      const int r0 = 2 * S * p;
+      f32x4 acc[1];
+      zero(acc);
+      strip_mma<P, S, 1>(acc, krow(sT + (r0 + S) * LT + r0, LT), 16 * ti, kcol(sT + r0 * LT + r0, LT), 16 * tj);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        tmp[p * S * LP + (16 * ti + acc_row(rr)) * LP + 16 * tj + acc_col()] = acc[0][rr];
+    }
+    __syncthreads();
+    for (int q = w; q < NB * TPS * TPS; q += NW) {
+      const int p = q / (TPS * TPS), ti = (q / TPS) % TPS, tj = q % TPS;
+      const int r0 = 2 * S * p;
+      f32x4 acc[1];
+      zero(acc);
+      strip_mma<P, S, 1>(acc, krow(sT + (r0 + S) * LT + r0 + S, LT), 16 * ti, kcol(tmp + p * S * LP, LP), 16 * tj, 0,
+                         tri_end<S>(16 * ti));
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        sT[(r0 + S + 16 * ti + acc_row(rr)) * LT + r0 + 16 * tj + acc_col()] = -acc[0][rr];
+    }
+    __syncthreads();
+    doubling_level<C, P, 2 * S>(sT, LT, tmp);
+  }
+}
+
+template <int C, int P>
+__device__ void invert_unit_lower(float* sT, int LT, float* tmp) {
+  const int w = wave(), l = lane(), j = l & 15, rb = (l >> 4) << 2;
+  {  // diagonal block w
+    const int base = 16 * w;
+    float x[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = (rb + e == j) ? 1.f : 0.f;
+#pragma unroll
+    for (int r = 0; r < 15; ++r) {
+      const float xr = __shfl(x[r & 3], j + 16 * (r >> 2));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = rb + e;
+        if (i > r) x[e] -= sT[(base + i) * LT + base + r] * xr;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sT[(base + rb + e) * LT + base + j] = x[e];
+  }
+  __syncthreads();
+  doubling_level<C, P, 16>(sT, LT, tmp);
+}
+
+// ---------------------------------------------------------------- k_prep
+// grid (B*N, 2*Hk + H), 256 threads. Slot y: q head y (< Hk), k head y - Hk, v head y - 2Hk.
+// Conv sum order of causal_conv1d.py:42-45 (lag 0, then 1..K-1); l2norm of xla.py:42-53.
+template <int C, int D, class TIO, class TG>
+__global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
+  constexpr int CG = D / 8;
+  constexpr int NTG = 256 / CG;
+  constexpr int TPT = (C >= NTG) ? C / NTG : 1;
+  const int b = blockIdx.x / A.N, n = blockIdx.x % A.N;
+  const int slot = blockIdx.y;
+  const int cg = threadIdx.x % CG, tg = threadIdx.x / CG;
+  int kind, head, c0;
+  if (slot < A.Hk) { kind = 0; head = slot; c0 = slot * D; }
+  else if (slot < 2 * A.Hk) { kind = 1; head = slot - A.Hk; c0 = A.Hk * D + head * D; }
+  else { kind = 2; head = slot - 2 * A.Hk; c0 = 2 * A.Hk * D + head * D; }
+  const int cc = c0 + cg * 8;
+  const TIO* x = reinterpret_cast<const TIO*>(A.qkv);
+  float* dst = kind == 0 ? A.qn + hoff(A, b, head, A.Hk, n, C, D)
+             : kind == 1 ? A.kn + hoff(A, b, head, A.Hk, n, C, D)
+                         : A.vv + hoff(A, b, head, A.H, n, C, D);
+  const int taps = A.taps;
+  float wt[5][8];
+#pragma unroll
+  for (int L = 0; L < 5; ++L)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wt[L][e] = (L < taps) ? A.conv_w[(size_t)L * A.W + cc + e] : 0.f;
+
+  const int t_lo = tg * TPT;
+  if (t_lo < C) {
+    // history of raw rows t-1 .. t-4 and their ids
+    float xh[4][8];
+    int sh[4];
+#pragma unroll
+    for (int L = 1; L <= 4; ++L) {
+      const int t = n * C + t_lo - L;
+      const bool in = t >= 0 && t < A.T;
+      sh[L - 1] = in ? A.seg[(size_t)b * A.T + t] : 0;
+      if (in && L < taps) {
+        ld8(x + ((size_t)b * A.T + t) * A.W + cc, xh[L - 1]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xh[L - 1][e] = 0.f;
+      }
+    }
+    for (int q = 0; q < TPT; ++q) {
+      const int tl = t_lo + q, t = n * C + tl;
+      const bool in = t < A.T;
+      float xt[8];
+      if (in) {
+        ld8(x + ((size_t)b * A.T + t) * A.W + cc, xt);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xt[e] = 0.f;
+      }
+      const int st = in ? A.seg[(size_t)b * A.T + t] : 0;
+      float act[8];
+      if (taps == 0) {  // mega1: qkv is already the activation
+#pragma unroll
+        for (int e = 0; e < 8; ++e) act[e] = xt[e];
+      } else {
+        bool keep[4];
+#pragma unroll
+        for (int L = 1; L <= 4; ++L) keep[L - 1] = (L < taps) && (t - L >= 0) && (sh[L - 1] == st);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float z = xt[e] * wt[taps - 1][e];
+#pragma unroll
+          for (int L = 1; L <= 4; ++L)
+            if (keep[L - 1]) z += xh[L - 1][e] * wt[taps - 1 - L][e];
+          act[e] = st > 0 ? z * sigmoidf_(z) : 0.f;
+        }
+      }
+#pragma unroll
+      for (int L = 3; L >= 1; --L) {
+        sh[L] = sh[L - 1];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xh[L][e] = xh[L - 1][e];
+      }
+      sh[0] = st;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xh[0][e] = xt[e];
+      if (kind < 2) {  // l2norm over the head's D channels (CG lanes)
+        float sq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sq += act[e] * act[e];
+#pragma unroll
+        for (int m = 1; m < CG; m <<= 1) sq += __shfl_xor(sq, m);
+        float r = sq == 0.f ? 0.f : 1.0f / sqrtf(sq + 1e-6f);
+        if (kind == 0) r *= A.scale;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) act[e] *= r;
+      }
+      float4* o = reinterpret_cast<float4*>(dst + (size_t)tl * D + cg * 8);
+      o[0] = make_float4(act[0], act[1], act[2], act[3]);
+      o[1] = make_float4(act[4], act[5], act[6], act[7]);
+    }
+  }
+  if (slot == 0) {
+    for (int i = threadIdx.x; i < C; i += 256) {
+      const int t = n * C + i;
+      A.segp[(size_t)b * A.Tp + t] = t < A.T ? A.seg[(size_t)b * A.T + t] : 0;
+    }
+  }
+  if (kind == 2 && threadIdx.x < 64) {  // gates of value head `head` (pallas_tpu_mega.py:106-127)
+    constexpr int E = (C + 63) / 64;
+    const int l = threadIdx.x;
+    const TG* ga = reinterpret_cast<const TG*>(A.ga);
+    const TG* gb = reinterpret_cast<const TG*>(A.gb);
+    const float alog = expf(A.a_log[head]), dtb = A.dt_bias[head];
+    // gamma = in-chunk inclusive prefix sum of g, accumulated in fp64 and kept as fp32 hi + lo
+    double g[E], run = 0.0;
+    float bt[E];
+#pragma unroll
+    for (int q = 0; q < E; ++q) {
+      const int i = l * E + q, t = n * C + i;
+      const bool in = i < C && t < A.T;
+      const float av = in ? ldf(ga + ((size_t)b * A.T + t) * A.H + head) : 0.f;
+      const float bv = in ? ldf(gb + ((size_t)b * A.T + t) * A.H + head) : 0.f;
+      run += i < C ? (double)(-alog * softplusf_(av + dtb)) : 0.0;
+      g[q] = run;  // inclusive within the lane
+      bt[q] = sigmoidf_(bv);
+    }
+    double inc = run;  // inclusive scan of lane totals
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const double up = __shfl_up(inc, d);
+      if (l >= d) inc += up;
+    }
+    const double excl = inc - run;
+    const size_t tok = (size_t)(b * A.H + head) * A.Tp + (size_t)n * C;
+#pragma unroll
+    for (int q = 0; q < E; ++q) {
+      const int i = l * E + q;
+      if (i < C) {
+        const double gm = excl + g[q];
+        const float hi = (float)gm;
+        A.gam[tok + i] = hi;
+        A.gaml[tok + i] = (float)(gm - (double)hi);
+        A.bet[tok + i] = bt[q];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- k_chunk
+// grid B*H*N, C/16 waves (one 16-row strip each). MODE 0 (forward): writes w and u.
+// MODE 1 (backward recompute): writes T and v_new = u - w S_before.
+template <int C, int D, int PI, int PS, int MODE>
+__global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
+  constexpr int NT = C * 4;
+  constexpr int LT = (C > D ? C : D) + 4;
+  constexpr int LX = D + 4;
+  constexpr int XR = C > D ? C : D;
+  constexpr int TMP = C * (C / 2 + 4) / 2;  // doubling scratch, shared with the operand tile
+  constexpr int SX = XR * LX > TMP ? XR * LX : TMP;
+  __shared__ float sT[C * LT];
+  __shared__ float sX[SX];
+  __shared__ Ctx<C> cx;
+  const int id = blockIdx.x;
+  const int n = id % A.N, bh = id / A.N, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
+  load_ctx<C, NT>(cx, A, b, h, n);
+  const float* kg = A.kn + hoff(A, b, hk, A.Hk, n, C, D);
+  const float* vg = A.vv + hoff(A, b, h, A.H, n, C, D);
+  const size_t off = hoff(A, b, h, A.H, n, C, D);
+  const int i0 = 16 * wave();
+  {  // L = strict(beta_i (k k^T)_ij D_ij)
+    f32x4 acc[C / 16];
+    zero(acc);
+    strip_mma<PI, D, C / 16>(acc, krow(kg, D), i0, krow(kg, D), 0);
+#pragma unroll
+    for (int t = 0; t < C / 16; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
+        sT[i * LT + j] = (i > j) ? cx.beta[i] * acc[t][rr] * decay(cx, i, j) : 0.f;
+      }
+  }
+  __syncthreads();
+  invert_unit_lower<C, PI>(sT, LT, sX);
+  if constexpr (MODE == 0) {
+    load_tile<C, D, NT>(sX, LX, kg);
+    __syncthreads();
+    {
+      f32x4 acc[D / 16];
+      zero(acc);
+      strip_mma<PI, C, D / 16>(acc, krow(sT, LT), i0, scale_k(kcol(sX, LX), cx.bg), 0, 0, tri_end<C>(i0));
+#pragma unroll
+      for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) A.ww[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = acc[t][rr];
+    }
+    __syncthreads();
+    load_tile<C, D, NT>(sX, LX, vg);
+    __syncthreads();
+    {
+      f32x4 acc[D / 16];
+      zero(acc);
+      strip_mma<PI, C, D / 16>(acc, krow(sT, LT), i0, scale_k(kcol(sX, LX), cx.beta), 0, 0, tri_end<C>(i0));
+#pragma unroll
+      for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) A.uu[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = acc[t][rr];
+    }
+  } else {
+    float* tg = A.tt + ((size_t)bh * A.N + n) * C * C;
+    for (int idx = threadIdx.x; idx < C * C; idx += NT) tg[idx] = sT[(idx / C) * LT + idx % C];
+    load_tile<C, D, NT>(sX, LX, kg);
+    __syncthreads();
+    f32x4 aw[D / 16], au[D / 16];
+    zero(aw);
+    zero(au);
+    strip_mma<PI, C, D / 16>(aw, krow(sT, LT), i0, scale_k(kcol(sX, LX), cx.bg), 0, 0, tri_end<C>(i0));
+    __syncthreads();
+    load_tile<C, D, NT>(sX, LX, vg);
+    __syncthreads();
+    strip_mma<PI, C, D / 16>(au, krow(sT, LT), i0, scale_k(kcol(sX, LX), cx.beta), 0, 0, tri_end<C>(i0));
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) sT[(i0 + acc_row(rr)) * LT + 16 * t + acc_col()] = aw[t][rr];
+    load_tile<D, D, NT>(sX, LX, A.states + ((size_t)bh * A.N + n) * D * D);
+    __syncthreads();
+    f32x4 ws[D / 16];
+    zero(ws);
+    strip_mma<PS, D, D / 16>(ws, krow(sT, LT), i0, kcol(sX, LX), 0);
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        A.vnew[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = au[t][rr] - ws[t][rr];
+  }
+}
+
+// ---------------------------------------------------------------- k_scan_fwd
+// grid B*H*(D/DVT) (XCD-remapped), max(C,D)/16 waves. The state tile S [D x DVT] lives in
+// the accumulators of waves < D/16; chunks in order (pallas_tpu_v2.py:254-269).
+template <int C, int D, int DVT, int PI, int PS>
+__global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
+  constexpr int NT = (C > D ? C : D) * 4;
+  constexpr int LS = DVT + 4, LK = D + 4;
+  __shared__ float sS[D * LS];
+  __shared__ float sV[C * LS];
+  __shared__ float sK[C * LK];
+  __shared__ Ctx<C> cx;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = id % A.ntiles, bh = id / A.ntiles, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
+  const int j0 = tile * DVT;
+  const int w = wave();
+  f32x4 accS[DVT / 16];
+  zero(accS);
+  for (int n = 0; n < A.N; ++n) {
+    float* sg = A.states + ((size_t)bh * A.N + n) * D * D;
+    if (w < D / 16) {
+#pragma unroll
+      for (int t = 0; t < DVT / 16; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
+          sS[i * LS + j] = accS[t][rr];
+          sg[i * D + j0 + j] = accS[t][rr];
+        }
+    }
+    load_ctx<C, NT>(cx, A, b, h, n);
+    load_tile<C, D, NT>(sK, LK, A.kn + hoff(A, b, hk, A.Hk, n, C, D));
+    __syncthreads();
+    const size_t off = hoff(A, b, h, A.H, n, C, D);
+    if (w < C / 16) {  // v_new = u - w S
+      f32x4 acc[DVT / 16];
+      zero(acc);
+      strip_mma<PS, D, DVT / 16>(acc, krow(A.ww + off, D), 16 * w, kcol(sS, LS), 0);
+#pragma unroll
+      for (int t = 0; t < DVT / 16; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
+          const size_t g = off + (size_t)i * D + j0 + j;
+          const float vn = A.uu[g] - acc[t][rr];
+          sV[i * LS + j] = vn;
+          A.vnew[g] = vn;
+        }
+    }
+    __syncthreads();
+    if (w < D / 16) {  // S = carry S + k_write^T v_new
+#pragma unroll
+      for (int t = 0; t < DVT / 16; ++t) accS[t] *= cx.carry;
+      strip_mma<PI, C, DVT / 16>(accS, scale_k(kcol(sK, LK), cx.kws), 16 * w, kcol(sV, LS), 0);
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- k_out
+// grid B*H*N, C/16 waves: o = ((q k^T) . D) v_new + q_read S_before, token-major output.
+template <int C, int D, int PI, int PS, class TIO>
+__global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
+  constexpr int NT = C * 4;
+  constexpr int LI = C + 4, LX = D + 4;
+  constexpr int XR = C > D ? C : D;
+  __shared__ float sI[C * LI];
+  __shared__ float sX[XR * LX];
+  __shared__ Ctx<C> cx;
+  const int id = blockIdx.x;
+  const int n = id % A.N, bh = id / A.N, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
+  load_ctx<C, NT>(cx, A, b, h, n);
+  const float* qg = A.qn + hoff(A, b, hk, A.Hk, n, C, D);
+  const float* kg = A.kn + hoff(A, b, hk, A.Hk, n, C, D);
+  const size_t off = hoff(A, b, h, A.H, n, C, D);
+  const int i0 = 16 * wave();
+  {
+    f32x4 acc[C / 16];
+    zero(acc);
+    strip_mma<PI, D, C / 16>(acc, krow(qg, D), i0, krow(kg, D), 0);
+#pragma unroll
+    for (int t = 0; t < C / 16; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
+        sI[i * LI + j] = acc[t][rr] * decay(cx, i, j);
+      }
+  }
+  load_tile<C, D, NT>(sX, LX, A.vnew + off);
+  __syncthreads();
+  f32x4 o[D / 16];
+  zero(o);
+  strip_mma<PI, C, D / 16>(o, krow(sI, LI), i0, kcol(sX, LX), 0, 0, tri_end<C>(i0));
+  __syncthreads();
+  load_tile<D, D, NT>(sX, LX, A.states + ((size_t)bh * A.N + n) * D * D);
+  __syncthreads();
+  strip_mma<PS, D, D / 16>(o, scale_r(krow(qg, D), cx.grow), i0, kcol(sX, LX), 0);
+  TIO* out = reinterpret_cast<TIO*>(A.out);
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int tok = n * C + i0 + acc_row(rr);
+      if (tok < A.T) stf(out + (((size_t)b * A.T + tok) * A.H + h) * D + 16 * t + acc_col(), o[t][rr]);
+    }
+}
+
+// ---------------------------------------------------------------- k_bwd_local
+// grid B*H*N, C/16 waves: X_loc = T^T (intra^T do), Kt = T^T k_write.
+template <int C, int D, int PI, class TIO>
+__global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
+  constexpr int NT = C * 4;
+  constexpr int LA = C + 4, LX = D + 4;
+  __shared__ float sA[C * LA];
+  __shared__ float sX[C * LX];
+  __shared__ Ctx<C> cx;
+  const int id = blockIdx.x;
+  const int n = id % A.N, bh = id / A.N, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
+  load_ctx<C, NT>(cx, A, b, h, n);
+  const float* qg = A.qn + hoff(A, b, hk, A.Hk, n, C, D);
+  const float* kg = A.kn + hoff(A, b, hk, A.Hk, n, C, D);
+  const size_t off = hoff(A, b, h, A.H, n, C, D);
+  const int i0 = 16 * wave();
+  {
+    f32x4 acc[C / 16];
+    zero(acc);
+    strip_mma<PI, D, C / 16>(acc, krow(qg, D), i0, krow(kg, D), 0);
+#pragma unroll
+    for (int t = 0; t < C / 16; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
+        sA[i * LA + j] = acc[t][rr] * decay(cx, i, j);
+      }
+  }
+  const TIO* dout = reinterpret_cast<const TIO*>(A.d_out);
+  for (int idx = threadIdx.x; idx < C * D; idx += NT) {
+    const int r = idx / D, c = idx % D, tok = n * C + r;
+    sX[r * LX + c] = tok < A.T ? ldf(dout + (((size_t)b * A.T + tok) * A.H + h) * D + c) : 0.f;
+  }
+  __syncthreads();
+  f32x4 acc[D / 16];
+  zero(acc);
+  strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, kcol(sX, LX), 0, tri_begin(i0), C);  // intra^T do
+  __syncthreads();
+  load_tile<C, C, NT>(sA, LA, A.tt + ((size_t)bh * A.N + n) * C * C);
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) sX[(i0 + acc_row(rr)) * LX + 16 * t + acc_col()] = acc[t][rr];
+  __syncthreads();
+  zero(acc);
+  strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, kcol(sX, LX), 0, tri_begin(i0), C);  // T^T dv_loc
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) A.xl[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = acc[t][rr];
+  __syncthreads();
+  load_tile<C, D, NT>(sX, LX, kg);
+  __syncthreads();
+  zero(acc);
+  strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, scale_k(kcol(sX, LX), cx.kws), 0, tri_begin(i0), C);  // T^T k_write
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) A.kt[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = acc[t][rr];
+}
+
+// ---------------------------------------------------------------- k_scan_bwd
+// grid B*H*(D/DVT) (XCD-remapped), max(C,D)/16 waves. G [D x DVT] in the accumulators of
+// waves < D/16, chunks reversed (pallas_tpu_v2.py:272-291). Also writes, per chunk and tile,
+// <G_after, S_after> (the last token's d gamma term: sum d_kws kws + d_carry carry).
+template <int C, int D, int DVT, int PI, int PS, class TIO>
+__global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
+  constexpr int NT = (C > D ? C : D) * 4;
+  constexpr int NW = NT / 64;
+  constexpr int LS = DVT + 4, LK = D + 4;
+  __shared__ float sG[D * LS];
+  __shared__ float sXt[C * LS];
+  __shared__ float sDo[C * LS];
+  __shared__ float sQK[C * LK];
+  __shared__ float red[NW];
+  __shared__ Ctx<C> cx;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int tile = id % A.ntiles, bh = id / A.ntiles, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
+  const int j0 = tile * DVT;
+  const int w = wave();
+  const TIO* dout = reinterpret_cast<const TIO*>(A.d_out);
+  f32x4 accG[DVT / 16];
+  zero(accG);
+  for (int n = A.N - 1; n >= 0; --n) {
+    float part = 0.f;
+    if (w < D / 16) {
+      float* gdst = A.gg + ((size_t)bh * A.N + n) * D * D;
+      const float* snext = A.states + ((size_t)bh * A.N + n + 1) * D * D;
+#pragma unroll
+      for (int t = 0; t < DVT / 16; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
+          const float g = accG[t][rr];
+          sG[i * LS + j] = g;
+          gdst[i * D + j0 + j] = g;
+          if (n + 1 < A.N) part += g * snext[i * D + j0 + j];
+        }
+    }
+    part = sum64(part);
+    if (lane() == 0) red[w] = part;
+    load_ctx<C, NT>(cx, A, b, h, n);
+    if (threadIdx.x == 0) {
+      float s = 0.f;
+      for (int q = 0; q < NW; ++q) s += red[q];
+      A.gsp[((size_t)bh * A.N + n) * A.ntiles + tile] = s;
+    }
+    for (int idx = threadIdx.x; idx < C * DVT; idx += NT) {
+      const int r = idx / DVT, c = idx % DVT, tok = n * C + r;
+      sDo[r * LS + c] = tok < A.T ? ldf(dout + (((size_t)b * A.T + tok) * A.H + h) * D + j0 + c) : 0.f;
+    }
+    load_tile<C, D, NT>(sQK, LK, A.qn + hoff(A, b, hk, A.Hk, n, C, D));
+    __syncthreads();
+    const size_t off = hoff(A, b, h, A.H, n, C, D);
+    if (w < C / 16) {  // X = X_loc + Kt G
+      f32x4 acc[DVT / 16];
+      zero(acc);
+      strip_mma<PS, D, DVT / 16>(acc, krow(A.kt + off, D), 16 * w, kcol(sG, LS), 0);
+#pragma unroll
+      for (int t = 0; t < DVT / 16; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
+          const size_t g = off + (size_t)i * D + j0 + j;
+          const float xv = A.xl[g] + acc[t][rr];
+          sXt[i * LS + j] = xv;
+          A.xl[g] = xv;
+        }
+    }
+    __syncthreads();
+    if (w < D / 16) {  // G = carry G + q_read^T do
+#pragma unroll
+      for (int t = 0; t < DVT / 16; ++t) accG[t] *= cx.carry;
+      strip_mma<PI, C, DVT / 16>(accG, scale_k(kcol(sQK, LK), cx.grow), 16 * w, kcol(sDo, LS), 0);
+    }
+    __syncthreads();
+    load_tile<C, D, NT>(sQK, LK, A.kn + hoff(A, b, hk, A.Hk, n, C, D));
+    __syncthreads();
+    if (w < D / 16)  // ... - kbe^T X
+      strip_mma<PI, C, DVT / 16>(accG, scale_k(kcol(sQK, LK), cx.bg, -1.f), 16 * w, kcol(sXt, LS), 0);
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- k_bwd_grads
+// grid B*H*N, C/16 waves. With m1 = strict(-X v_new^T) . D and m2 = (do v_new^T) . D:
+//   dkb = m1 k - (grow . X) S^T                    dq  = m2 k + (grow . do) S^T
+//   dk' = m1^T (beta k) + m2^T q + (kws . v_new) G^T
+//   dk  = dk' + beta dkb    d beta = rows(dkb, k) + rows(X, v)
+//   d gamma = rows(beta k, dkb) + rows(q, dq) - rows(k, dk')  (+ <G_after, S_after> at the
+//   chunk's last token) -- pallas_tpu_v2.py:272-318 regrouped by shared operands.
+template <int C, int D, int PI, int PS, class TIO>
+__global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
+  constexpr int NT = C * 4;
+  constexpr int LA = C + 4, LB = D + 4;
+  __shared__ float sA[C * LA];
+  __shared__ float sB[C * LB];
+  __shared__ Ctx<C> cx;
+  const int id = blockIdx.x;
+  const int n = id % A.N, bh = id / A.N, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
+  load_ctx<C, NT>(cx, A, b, h, n);
+  const float* qg = A.qn + hoff(A, b, hk, A.Hk, n, C, D);
+  const float* kg = A.kn + hoff(A, b, hk, A.Hk, n, C, D);
+  const size_t off = hoff(A, b, h, A.H, n, C, D);
+  const float* xg = A.xl + off;
+  const float* vng = A.vnew + off;
+  const float* vg = A.vv + off;
+  const float* Sg = A.states + ((size_t)bh * A.N + n) * D * D;
+  const float* Gg = A.gg + ((size_t)bh * A.N + n) * D * D;
+  const TIO* dout = reinterpret_cast<const TIO*>(A.d_out);
+  const KRowLim<TIO> dov{dout + (((size_t)b * A.T + (size_t)n * C) * A.H + h) * D, A.H * D, A.T - n * C};
+  const int i0 = 16 * wave();
+  {  // m1
+    f32x4 acc[C / 16];
+    zero(acc);
+    strip_mma<PI, D, C / 16>(acc, krow(xg, D), i0, krow(vng, D), 0);
+#pragma unroll
+    for (int t = 0; t < C / 16; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
+        sA[i * LA + j] = (i > j) ? -acc[t][rr] * decay(cx, i, j) : 0.f;
+      }
+  }
+  load_tile<C, D, NT>(sB, LB, kg);
+  __syncthreads();
+  f32x4 dkb[D / 16], dk[D / 16], dq[D / 16];
+  zero(dkb);
+  zero(dk);
+  zero(dq);
+  strip_mma<PI, C, D / 16>(dkb, krow(sA, LA), i0, kcol(sB, LB), 0, 0, tri_end<C>(i0));
+  strip_mma<PS, D, D / 16>(dkb, scale_r(krow(xg, D), cx.grow, -1.f), i0, krow(Sg, D), 0);
+  strip_mma<PI, C, D / 16>(dk, kcol(sA, LA), i0, scale_k(kcol(sB, LB), cx.beta), 0, tri_begin(i0), C);
+  __syncthreads();
+  {  // m2
+    f32x4 acc[C / 16];
+    zero(acc);
+    strip_mma<PI, D, C / 16>(acc, dov, i0, krow(vng, D), 0);
+#pragma unroll
+    for (int t = 0; t < C / 16; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
+        sA[i * LA + j] = acc[t][rr] * decay(cx, i, j);
+      }
+  }
+  __syncthreads();
+  strip_mma<PI, C, D / 16>(dq, krow(sA, LA), i0, kcol(sB, LB), 0, 0, tri_end<C>(i0));
+  strip_mma<PS, D, D / 16>(dq, scale_r(dov, cx.grow), i0, krow(Sg, D), 0);
+  __syncthreads();
+  load_tile<C, D, NT>(sB, LB, qg);
+  __syncthreads();
+  strip_mma<PI, C, D / 16>(dk, kcol(sA, LA), i0, kcol(sB, LB), 0, tri_begin(i0), C);
+  strip_mma<PS, D, D / 16>(dk, scale_r(krow(vng, D), cx.kws), i0, krow(Gg, D), 0);
+  // epilogue: row sums and the per-value-head dq, dk
+  float r2[4] = {0.f, 0.f, 0.f, 0.f}, r3[4] = {0.f, 0.f, 0.f, 0.f}, r4[4] = {0.f, 0.f, 0.f, 0.f};
+  float rxv[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
+      const float kv = kg[i * D + j], qv = sB[i * LB + j];
+      r4[rr] += dkb[t][rr] * kv;
+      r2[rr] += qv * dq[t][rr];
+      r3[rr] += kv * dk[t][rr];
+      rxv[rr] += xg[i * D + j] * vg[i * D + j];
+      A.dqh[off + i * D + j] = dq[t][rr];
+      A.dkh[off + i * D + j] = dk[t][rr] + cx.beta[i] * dkb[t][rr];
+    }
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    r2[rr] = sum16(r2[rr]);
+    r3[rr] = sum16(r3[rr]);
+    r4[rr] = sum16(r4[rr]);
+    rxv[rr] = sum16(rxv[rr]);
+  }
+  if (acc_col() == 0) {
+    const size_t tok = (size_t)bh * A.Tp + (size_t)n * C;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int i = i0 + acc_row(rr);
+      float dgm = cx.beta[i] * r4[rr] + r2[rr] - r3[rr];
+      if (i == C - 1) {
+        float s = 0.f;
+        for (int q = 0; q < A.ntiles; ++q) s += A.gsp[((size_t)bh * A.N + n) * A.ntiles + q];
+        dgm += s;
+      }
+      A.dgam[tok + i] = dgm;
+      A.dbet[tok + i] = r4[rr] + rxv[rr];
+    }
+  }
+}
+
+// ---------------------------------------------------------------- k_post
+// grid (B*N, 2*Hk + H), 256 threads: the activations' gradients back to d(qkv) -- GQA sums,
+// l2norm backward (pallas_tpu_mega.py:101-103), SiLU and the anti-causal conv backward with
+// segment masks (pallas_tpu_mega.py:161-179, 306-319) -- and, for the value heads, the gate
+// backward (pallas_tpu_mega.py:129-145): dg = reverse in-chunk cumsum of d gamma.
+template <int C, int D, class TIO, class TG>
+__global__ __launch_bounds__(256) void k_post(GdnArgs A) {
+  constexpr int CG = D / 8;
+  constexpr int NTG = 256 / CG;
+  constexpr int TPT = (C >= NTG) ? C / NTG : 1;
+  __shared__ float sdw[256 * 5 * 8];  // per-thread d(conv weight) partials [tg][tap][D]
+  const int b = blockIdx.x / A.N, n = blockIdx.x % A.N;
+  const int slot = blockIdx.y;
+  const int cg = threadIdx.x % CG, tg = threadIdx.x / CG;
+  int kind, head, c0;
+  if (slot < A.Hk) { kind = 0; head = slot; c0 = slot * D; }
+  else if (slot < 2 * A.Hk) { kind = 1; head = slot - A.Hk; c0 = A.Hk * D + head * D; }
+  else { kind = 2; head = slot - 2 * A.Hk; c0 = 2 * A.Hk * D + head * D; }
+  const int cc = c0 + cg * 8;
+  const int taps = A.taps;
+  const TIO* x = reinterpret_cast<const TIO*>(A.qkv);
+  TIO* dx = reinterpret_cast<TIO*>(A.d_qkv);
+  const int32_t* sp = A.segp + (size_t)b * A.Tp;
+  float wt[5][8];
+#pragma unroll
+  for (int L = 0; L < 5; ++L)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wt[L][e] = (L < taps) ? A.conv_w[(size_t)L * A.W + cc + e] : 0.f;
+  float dwa[5][8];
+#pragma unroll
+  for (int L = 0; L < 5; ++L)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dwa[L][e] = 0.f;
+  const int t_lo = tg * TPT;
+  if (t_lo < C) {
+    float dzw[4][8];  // dz of tokens t+1 .. t+4
+    int sw[4];
+#pragma unroll
+    for (int L = 0; L < 4; ++L) {
+      sw[L] = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dzw[L][e] = 0.f;
+    }
+    const int ahead = taps > 1 ? taps - 1 : 0;
+    for (int q = TPT - 1 + ahead; q >= 0; --q) {
+      const int t = n * C + t_lo + q;
+      float dz[8], xs[5][8];
+      int st = 0;
+      if (t < A.Tp) {  // uniform over the CG lanes of this token
+        st = sp[t];
+#pragma unroll
+        for (int L = 0; L < 5; ++L) {
+          const int tt = t - L;
+          if (L < (taps > 0 ? taps : 1) && tt >= 0 && tt < A.T) {
+            ld8(x + ((size_t)b * A.T + tt) * A.W + cc, xs[L]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xs[L][e] = 0.f;
+          }
+        }
+        float z[8], act[8];
+        if (taps == 0) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) { z[e] = 0.f; act[e] = xs[0][e]; }
+        } else {
+          bool keep[5];
+#pragma unroll
+          for (int L = 0; L < 5; ++L) keep[L] = (L < taps) && (L == 0 || (t - L >= 0 && sp[t - L] == st));
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float s = xs[0][e] * wt[taps - 1][e];
+#pragma unroll
+            for (int L = 1; L < 5; ++L)
+              if (keep[L]) s += xs[L][e] * wt[taps - 1 - L][e];
+            z[e] = s;
+            act[e] = st > 0 ? s * sigmoidf_(s) : 0.f;
+          }
+        }
+        float dy[8];
+        if (kind < 2) {
+          const float* src = (kind == 0 ? A.dqh : A.dkh);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dy[e] = 0.f;
+          for (int v = 0; v < A.ratio; ++v) {
+            float y[8];
+            ld8(src + ((size_t)(b * A.H + head * A.ratio + v) * A.Tp + t) * D + cg * 8, y);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) dy[e] += y[e];
+          }
+          if (kind == 0) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) dy[e] *= A.scale;
+          }
+          float sq = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sq += act[e] * act[e];
+#pragma unroll
+          for (int m = 1; m < CG; m <<= 1) sq += __shfl_xor(sq, m);
+          const float r = sq == 0.f ? 0.f : 1.0f / sqrtf(sq + 1e-6f);
+          float dot = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dot += act[e] * r * dy[e];
+#pragma unroll
+          for (int m = 1; m < CG; m <<= 1) dot += __shfl_xor(dot, m);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dy[e] = r * (dy[e] - act[e] * r * dot);
+        } else {
+          const float bt = A.bet[(size_t)(b * A.H + head) * A.Tp + t];
+          ld8(A.xl + ((size_t)(b * A.H + head) * A.Tp + t) * D + cg * 8, dy);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dy[e] *= bt;
+        }
+        if (taps == 0) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dz[e] = dy[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float s = sigmoidf_(z[e]);
+            dz[e] = st > 0 ? dy[e] * s * (1.f + z[e] * (1.f - s)) : 0.f;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dz[e] = 0.f;
+#pragma unroll
+        for (int L = 0; L < 5; ++L)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) xs[L][e] = 0.f;
+      }
+      if (q < TPT && t < A.Tp) {
+        float o[8];
+        if (taps == 0) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = dz[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float s = dz[e] * wt[taps - 1][e];
+#pragma unroll
+            for (int L = 1; L < 5; ++L)
+              if (L < taps && sw[L - 1] == st) s += wt[taps - 1 - L][e] * dzw[L - 1][e];
+            o[e] = s;
+          }
+          if (A.d_conv_w) {
+#pragma unroll
+            for (int L = 0; L < 5; ++L)
+              if (L < taps && (L == 0 || (t - L >= 0 && sp[t - L] == st))) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) dwa[L][e] += dz[e] * xs[L][e];
+              }
+          }
+        }
+        if (t < A.T) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) stf(dx + ((size_t)b * A.T + t) * A.W + cc + e, o[e]);
+        }
+      }
+#pragma unroll
+      for (int L = 3; L >= 1; --L) {
+        sw[L] = sw[L - 1];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dzw[L][e] = dzw[L - 1][e];
+      }
+      sw[0] = st;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dzw[0][e] = dz[e];
+    }
+  }
+  if (A.d_conv_w && taps > 0) {  // per-workgroup partial of d(conv weight), fixed sum order
+#pragma unroll
+    for (int L = 0; L < 5; ++L)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sdw[(tg * 5 + L) * 8 * CG + cg * 8 + e] = dwa[L][e];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < taps * D; idx += 256) {
+      const int L = idx / D, c = idx % D;
+      float s = 0.f;
+      for (int q = 0; q < NTG; ++q) s += sdw[(q * 5 + L) * 8 * CG + c];
+      A.dwp[(((size_t)b * A.N + n) * taps + (taps - 1 - L)) * A.W + c0 + c] = s;
+    }
+  }
+  if (kind == 2 && threadIdx.x < 64) {  // gate backward of value head `head`
+    constexpr int E = (C + 63) / 64;
+    const int l = threadIdx.x;
+    const TG* ga = reinterpret_cast<const TG*>(A.ga);
+    const TG* gb = reinterpret_cast<const TG*>(A.gb);
+    TG* da = reinterpret_cast<TG*>(A.d_a);
+    TG* db = reinterpret_cast<TG*>(A.d_b);
+    const float ea = expf(A.a_log[head]), dtb = A.dt_bias[head];
+    const size_t tok = (size_t)(b * A.H + head) * A.Tp + (size_t)n * C;
+    // dg = reverse in-chunk cumsum of d gamma, and the A_log / dt_bias partial sums, in fp64
+    double dgv[E], run = 0.0;
+#pragma unroll
+    for (int q = E - 1; q >= 0; --q) {
+      const int i = l * E + q;
+      run += i < C ? (double)A.dgam[tok + i] : 0.0;
+      dgv[q] = run;  // inclusive suffix within the lane
+    }
+    double inc = run;  // inclusive suffix scan of lane totals
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const double dn = __shfl_down(inc, d);
+      if (l + d < 64) inc += dn;
+    }
+    const double excl = inc - run;
+    double sa = 0.0, sd = 0.0;
+#pragma unroll
+    for (int q = 0; q < E; ++q) {
+      const int i = l * E + q, t = n * C + i;
+      if (i < C) {
+        const bool in = t < A.T;
+        const float av = in ? ldf(ga + ((size_t)b * A.T + t) * A.H + head) : 0.f;
+        const float bv = in ? ldf(gb + ((size_t)b * A.T + t) * A.H + head) : 0.f;
+        const double dg = excl + dgv[q];
+        const float xg = av + dtb;
+        const float g = -ea * softplusf_(xg);
+        const double dad = dg * (double)(-ea * sigmoidf_(xg));
+        const float dav = (float)dad;
+        const float bt = sigmoidf_(bv);
+        const float dbv = A.dbet[tok + i] * bt * (1.f - bt);
+        sa += dg * (double)g;
+        sd += dad;
+        if (in) {
+          stf(da + ((size_t)b * A.T + t) * A.H + head, dav);
+          stf(db + ((size_t)b * A.T + t) * A.H + head, dbv);
+        }
+      }
+    }
+    sa = sum64d(sa);
+    sd = sum64d(sd);
+    if (l == 0) {
+      A.pa[((size_t)b * A.N + n) * A.H + head] = sa;
+      A.pd[((size_t)b * A.N + n) * A.H + head] = sd;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- k_reduce
+// d A_log[h] = sum over rows and chunks of the per-chunk partials, likewise d dt_bias and
+// the conv weight (pallas_tpu_mega.py:527-535, 563-568); fixed order, no atomics.
+template <int C>
+__global__ __launch_bounds__(256) void k_reduce(GdnArgs A) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  const int bn = A.B * A.N;
+  if (idx < A.H) {
+    double sa = 0.0, sd = 0.0;
+    for (int q = 0; q < bn; ++q) {
+      sa += A.pa[(size_t)q * A.H + idx];
+      sd += A.pd[(size_t)q * A.H + idx];
+    }
+    A.d_a_log[idx] = (float)sa;
+    A.d_dt_bias[idx] = (float)sd;
+  } else if (A.d_conv_w && A.taps > 0 && idx - A.H < A.taps * A.W) {
+    const int j = idx - A.H;
+    float s = 0.f;
+    for (int q = 0; q < bn; ++q) s += A.dwp[(size_t)q * A.taps * A.W + j];
+    A.d_conv_w[j] = s;
+  }
+}
+
+}  // namespace gdn

@@ -1,0 +1,198 @@
+"""The GDN megakernel operator on MI355X: tjev's ``gdn_megakernel`` signature and semantics,
+computed by the HIP library through its C ABI.
+
+Mirrors ``gdn_megakernel`` (src/tjev/kernels/gated_delta_rule/pallas_tpu_mega.py:585-639) and
+its dispatcher form ``gdn_core_mega`` (src/tjev/kernels/gated_delta_rule/__init__.py:112-149):
+same arguments, same ValueErrors before any launch, same segment-packing semantics, output
+[B, T, H, Dv] in qkv's dtype. The custom VJP of ``_core`` (pallas_tpu_mega.py:538-575) is a
+torch.autograd.Function whose only residual besides the inputs is the fp32 state before each
+chunk (the reference's ``gdn_states``); the backward recomputes everything else. The conv
+weight's gradient is computed only when the weight requires grad (the reference's
+``gdn_mega2_bwd_dw`` variant, :549-551). There is no fallback: without the HIP library, or on a
+CPU tensor, the operator raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+
+PRECISIONS = ("highest", "high", "bf16", "mixed")  # xla.py:23
+INVERSE_BLOCKS = {"doubling": 0, "blocked": 16}    # pallas_tpu_v2.py:141
+HALO = 8                                           # pallas_tpu_mega.py:71
+LANES = 128                                        # pallas_tpu_mega.py:72
+
+
+def heads_per_block(heads: int, ratio: int, preferred: int = 8) -> int:
+    """Value heads per grid step of the reference kernels (pallas_tpu_v2.py:518-525): the
+    largest multiple of the GQA ratio dividing H, up to ``preferred``. The HIP kernels run one
+    value head per work item; this is kept for the reference's argument checks."""
+    if heads % ratio:
+        raise ValueError(f"{heads} value heads are not groups of {ratio}")
+    sizes = range(ratio, max(preferred, ratio) + 1, ratio)
+    return max(size for size in sizes if heads % size == 0)
+
+
+def kernel_inverse(inverse: str) -> str:
+    """``compute.gdn_inverse`` -> the in-kernel inverse (__init__.py:38-45)."""
+    if inverse in ("default", "doubling"):
+        return "doubling"
+    if inverse == "blocked":
+        return "blocked"
+    raise ValueError(f"gdn_inverse={inverse} has no in-kernel form: default, doubling, blocked")
+
+
+_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+class GdnPlan:
+    """The library's view of one problem shape: parameters, residual and workspace sizes,
+    and raw forward / backward launches on the current stream (no autograd)."""
+
+    def __init__(self, *, batch: int, length: int, key_heads: int, key_dim: int, value_heads: int,
+                 value_dim: int, taps: int, chunk: int, io_dtype: torch.dtype,
+                 gate_dtype: torch.dtype, precision: str = "high", inverse: str = "doubling",
+                 heads_per_step: int = 0):
+        self.lib = _lib.load()
+        if io_dtype not in _DTYPES or gate_dtype not in _DTYPES:
+            raise ValueError(f"the GDN megakernel takes float32 or bfloat16 tensors, not {io_dtype}/{gate_dtype}")
+        self.params = _lib.Params(batch, length, key_heads, key_dim, value_heads, value_dim, taps, chunk,
+                                  _DTYPES[io_dtype], _DTYPES[gate_dtype], _lib.PRECISION[precision],
+                                  _lib.INVERSE[inverse], heads_per_step)
+        status = self.lib.tjev_gdn_check(ctypes.byref(self.params))
+        if status == 1:
+            raise ValueError(self.lib.tjev_gdn_last_error().decode())
+        _lib.check_status(status)
+        self.chunk_run = max(chunk, 16)
+        self.n_chunks = math.ceil(length / self.chunk_run)
+        self.states_shape = (batch, value_heads, self.n_chunks, key_dim, value_dim)
+        self.fwd_bytes = self.lib.tjev_gdn_workspace_bytes(ctypes.byref(self.params), 0)
+        self.bwd_bytes = self.lib.tjev_gdn_workspace_bytes(ctypes.byref(self.params), 1)
+
+    @staticmethod
+    def _stream(device: torch.device) -> int:
+        return torch.cuda.current_stream(device).cuda_stream
+
+    def workspace(self, backward: bool, device) -> torch.Tensor:
+        return torch.empty(self.bwd_bytes if backward else self.fwd_bytes, dtype=torch.uint8, device=device)
+
+    def forward(self, qkv, a, b, a_log, dt_bias, conv_w, seg, out, states, workspace) -> None:
+        status = self.lib.tjev_gdn_mega2_fwd(
+            ctypes.byref(self.params), self._stream(qkv.device), _ptr(qkv), _ptr(a), _ptr(b), _ptr(a_log),
+            _ptr(dt_bias), _ptr(conv_w), _ptr(seg), _ptr(out), _ptr(states), _ptr(workspace), workspace.numel())
+        _lib.check_status(status)
+
+    def backward(self, qkv, a, b, a_log, dt_bias, conv_w, seg, states, d_out, d_qkv, d_a, d_b, d_a_log,
+                 d_dt_bias, d_conv_w, workspace) -> None:
+        status = self.lib.tjev_gdn_mega2_bwd(
+            ctypes.byref(self.params), self._stream(qkv.device), _ptr(qkv), _ptr(a), _ptr(b), _ptr(a_log),
+            _ptr(dt_bias), _ptr(conv_w), _ptr(seg), _ptr(states), _ptr(d_out), _ptr(d_qkv), _ptr(d_a), _ptr(d_b),
+            _ptr(d_a_log), _ptr(d_dt_bias), _ptr(d_conv_w), _ptr(workspace), workspace.numel())
+        _lib.check_status(status)
+
+
+class _Core(torch.autograd.Function):
+    """The custom VJP of the reference's ``_core`` (pallas_tpu_mega.py:538-575)."""
+
+    @staticmethod
+    def forward(ctx, plan: GdnPlan, qkv, a, b, a_log, dt_bias, conv_w, seg, out_shape):
+        out = torch.empty(out_shape, dtype=qkv.dtype, device=qkv.device)
+        states = torch.empty(plan.states_shape, dtype=torch.float32, device=qkv.device)
+        ws = plan.workspace(False, qkv.device)
+        plan.forward(qkv, a, b, a_log, dt_bias, conv_w, seg, out, states, ws)
+        ctx.plan = plan
+        ctx.save_for_backward(qkv, a, b, a_log, dt_bias, conv_w, seg, states)
+        ctx.mark_non_differentiable(states)
+        return out, states
+
+    @staticmethod
+    def backward(ctx, d_out, _d_states):
+        plan: GdnPlan = ctx.plan
+        qkv, a, b, a_log, dt_bias, conv_w, seg, states = ctx.saved_tensors
+        if d_out is None:
+            d_out = torch.zeros((qkv.shape[0], qkv.shape[1], plan.params.value_heads, plan.params.value_dim),
+                                dtype=qkv.dtype, device=qkv.device)
+        d_out = d_out.to(qkv.dtype).contiguous()
+        d_qkv = torch.empty_like(qkv)
+        d_a = torch.empty_like(a)
+        d_b = torch.empty_like(b)
+        d_a_log = torch.empty_like(a_log)
+        d_dt_bias = torch.empty_like(dt_bias)
+        want_dw = conv_w is not None and ctx.needs_input_grad[6]
+        d_w = torch.empty_like(conv_w) if want_dw else None
+        ws = plan.workspace(True, qkv.device)
+        plan.backward(qkv, a, b, a_log, dt_bias, conv_w, seg, states, d_out, d_qkv, d_a, d_b, d_a_log, d_dt_bias,
+                      d_w, ws)
+        return None, d_qkv, d_a, d_b, d_a_log, d_dt_bias, d_w, None, None
+
+
+def _check(precision, inverse, chunk, width, key_heads, key_dim, value_heads, value_dim, heads_per_step,
+           conv_weight):
+    """gdn_megakernel's checks, in its order and wording (pallas_tpu_mega.py:597-615)."""
+    if precision not in PRECISIONS:
+        raise ValueError(f"precision in {PRECISIONS}")
+    if inverse not in INVERSE_BLOCKS:
+        raise ValueError(f"the GDN megakernel's inverse in {tuple(INVERSE_BLOCKS)}")
+    if chunk & (chunk - 1) or chunk < HALO:
+        raise ValueError(f"the GDN megakernel needs a power-of-two chunk ≥ {HALO}, not {chunk}")
+    if width != 2 * key_heads * key_dim + value_heads * value_dim:
+        raise ValueError(f"qkv width {width} is not 2·{key_heads}·{key_dim} + {value_heads}·{value_dim}")
+    ratio = value_heads // key_heads
+    if ratio < 1 or value_heads % key_heads:
+        raise ValueError(f"{value_heads} value heads are not groups of {key_heads} key heads")
+    hb = heads_per_block(value_heads, ratio, heads_per_step or 8)
+    if 3 * hb > LANES:
+        raise ValueError(f"at most 42 heads per step, not {hb}")
+    taps = 1 if conv_weight is None else conv_weight.shape[0]
+    if not 1 <= taps <= 5:
+        raise ValueError(f"conv kernel of {taps} taps: the megakernel supports 1..5")
+    return taps
+
+
+def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: torch.Tensor,
+                   dt_bias: torch.Tensor, conv_weight: torch.Tensor | None, segment_ids: torch.Tensor, *,
+                   key_heads: int, key_dim: int, value_heads: int, value_dim: int, chunk: int = 64,
+                   precision: str = "high", inverse: str = "doubling", heads_per_step: int = 0,
+                   vmem_fraction: float = 0.0) -> torch.Tensor:
+    """The GDN core from the projection outputs (pallas_tpu_mega.py:585-596).
+
+    qkv [B, T, 2·Hk·Dk + H·Dv]: with ``conv_weight`` [K, 2·Hk·Dk + H·Dv] (mega2) the raw
+    in_proj_qkv output, the conv + SiLU + padding mask in the kernel; with ``conv_weight``
+    None (mega1) the post-conv, post-SiLU, masked activations. a, b [B, T, H] raw gate
+    projections, a_log, dt_bias [H]; segment_ids [B, T] (0 = padding). Returns the delta
+    rule's output [B, T, H, Dv] in qkv's dtype. ``vmem_fraction`` is TPU-only and ignored;
+    ``heads_per_step`` is checked as the reference does and otherwise ignored."""
+    batch, length, width = qkv.shape
+    taps = _check(precision, inverse, chunk, width, key_heads, key_dim, value_heads, value_dim, heads_per_step,
+                  conv_weight)
+    if not qkv.is_cuda:
+        raise RuntimeError("gdn_megakernel runs on the GPU (HIP); got a CPU tensor")
+    plan = GdnPlan(batch=batch, length=length, key_heads=key_heads, key_dim=key_dim, value_heads=value_heads,
+                   value_dim=value_dim, taps=0 if conv_weight is None else taps, chunk=chunk,
+                   io_dtype=qkv.dtype, gate_dtype=a.dtype, precision=precision, inverse=inverse,
+                   heads_per_step=heads_per_step)
+    b = b.to(a.dtype)
+    conv_w = None if conv_weight is None else conv_weight.to(torch.float32).contiguous()
+    out, _ = _Core.apply(plan, qkv.contiguous(), a.contiguous(), b.contiguous(),
+                         a_log.to(torch.float32).contiguous(), dt_bias.to(torch.float32).contiguous(), conv_w,
+                         segment_ids.to(torch.int32).contiguous(), (batch, length, value_heads, value_dim))
+    return out
+
+
+def gdn_core_mega(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_heads: int, key_dim: int,
+                  value_heads: int, value_dim: int, chunk: int = 64, precision: str = "high",
+                  inverse: str = "default", heads_per_step: int = 0, vmem_fraction: float = 0.0):
+    """The dispatcher form (__init__.py:112-149): ``inverse`` "default" -> doubling. On one
+    GPU there is no row sharding; see the design notes for the multi-GPU split."""
+    return gdn_megakernel(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, key_heads=key_heads,
+                          key_dim=key_dim, value_heads=value_heads, value_dim=value_dim, chunk=chunk,
+                          precision=precision, inverse=kernel_inverse(inverse),
+                          heads_per_step=heads_per_step, vmem_fraction=vmem_fraction)

@@ -1,0 +1,76 @@
+"""Algorithmic work of the GDN megakernel: FLOPs of the dense chunk contractions and minimal
+HBM bytes, per kernel launch and for the whole operator, against MI355X's published peaks.
+
+Per value head and chunk (C tokens, Dk = Dv = D), counting 2*m*n*k per product as in the
+reference's cost model (pallas_tpu_v2.py:126-138) and the operator count of the build notes:
+  forward:  6 C^2 D + C^3/3 + 6 C D^2       (k k^T, the inverse, T [v beta | kbe], q k^T,
+                                             intra v_new, [w; q_read] S, k_write^T v_new)
+  backward: recompute k k^T, the inverse, T [v beta | kbe], w S_before, then the products of
+            the reverse chunk step (intra^T do, T^T(.), T^T k_write, Kt G, q_read^T do, kbe^T X,
+            the m1 / m2 products and the state-gradient products).
+Elementwise work (conv, gates, l2norm, exps) is not counted in FLOPs.
+"""
+
+from __future__ import annotations
+
+# MI355X published peaks (dense): bf16 MFMA 2.5 PFLOP/s, fp32 MFMA 157.3 TFLOP/s, HBM 8 TB/s
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+
+def kernel_work(*, batch: int, length: int, key_heads: int, value_heads: int, dim: int, chunk: int,
+                io_bytes: int) -> dict[str, dict]:
+    """Per-launch algorithmic work of each kernel: {"flops": F} for the MFMA kernels,
+    {"bytes": B} for the HBM-bound ones, with the bound they are judged on."""
+    C, D = chunk, dim
+    n = -(-length // C)
+    tp = n * C
+    units = batch * value_heads * n            # (row, value head, chunk) work items
+    tok_h = batch * value_heads * tp           # token-heads
+    tok_k = batch * key_heads * tp
+    tokens = batch * length
+    width = 2 * key_heads * D + value_heads * D
+    sq = 2 * C * C * D                         # one C x C x D product
+    sd = 2 * C * D * D                         # one C x D x D product
+    inv = C ** 3 / 3
+    f32 = 4
+    w = {
+        # conv + gates + l2norm: read qkv, a, b; write q, k (key heads), v, gamma (hi, lo), beta
+        "gdn_prep_fwd": {"bound": "hbm", "bytes": tokens * (width + 2 * value_heads) * io_bytes
+                         + (2 * tok_k + tok_h) * D * f32 + 3 * tok_h * f32},
+        "gdn_chunk_fwd": {"bound": "mfma", "flops": units * (3 * sq + inv)},
+        "gdn_scan_fwd": {"bound": "hbm", "bytes": tok_h * D * f32 * 4 + units * D * D * f32},
+        "gdn_out": {"bound": "mfma", "flops": units * (2 * sq + sd)},
+        "gdn_prep_bwd": {"bound": "hbm", "bytes": tokens * (width + 2 * value_heads) * io_bytes
+                         + (2 * tok_k + tok_h) * D * f32 + 3 * tok_h * f32},
+        "gdn_chunk_bwd": {"bound": "mfma", "flops": units * (3 * sq + inv + sd)},
+        "gdn_bwd_local": {"bound": "mfma", "flops": units * 4 * sq},
+        "gdn_scan_bwd": {"bound": "hbm", "bytes": tok_h * D * f32 * 5 + units * D * D * f32 * 2},
+        "gdn_bwd_grads": {"bound": "mfma", "flops": units * (6 * sq + 3 * sd)},
+        # GQA sums, l2norm / SiLU / conv backward: read qkv, dq, dk, X, beta; write d_qkv, da, db
+        "gdn_post": {"bound": "hbm", "bytes": tokens * width * io_bytes * 2 + 3 * tok_h * D * f32
+                     + 2 * tokens * value_heads * io_bytes},
+        "gdn_reduce": {"bound": "hbm", "bytes": batch * n * value_heads * 16},
+    }
+    return w
+
+
+def operator_work(*, batch: int, length: int, key_heads: int, value_heads: int, dim: int, chunk: int,
+                  io_bytes: int) -> dict:
+    """Whole fwd+bwd: algorithmic FLOPs (per token-head 18 C Dk + 14 C Dv + 2/3 C^2 + 20 Dk Dv)
+    and minimal HBM bytes at the operator boundary (inputs, output, fp32 chunk states, the
+    gradients), and the roofline time max(t_mfma, t_hbm) at the bf16 / HBM peaks."""
+    C, D = chunk, dim
+    tokens = batch * length
+    th = tokens * value_heads
+    flops = th * (18 * C * D + 14 * C * D + (2 / 3) * C * C + 20 * D * D)
+    width = 2 * key_heads * D + value_heads * D
+    s = io_bytes
+    state = value_heads * D * D * 4 / C
+    fwd = tokens * (width * s + 2 * value_heads * s + value_heads * D * s + state)
+    bwd = tokens * (2 * width * s + 2 * value_heads * s + state + value_heads * D * s + 2 * value_heads * 4)
+    t_mfma = flops / (PEAK_BF16_TFLOPS * 1e12)
+    t_hbm = (fwd + bwd) / (PEAK_HBM_GBS * 1e9)
+    return {"flops": flops, "bytes": fwd + bwd, "t_mfma_s": t_mfma, "t_hbm_s": t_hbm,
+            "ceiling_tokens_per_s": tokens / max(t_mfma, t_hbm)}
