@@ -1,0 +1,161 @@
+"""Host-side checks of the drop-in boundary (CPU only, no kernel launches): the library loads and
+exports every entry point its header declares; argument validation follows the reference's
+ValueError conventions (pallas_tpu_mega.py:597-615) before anything is launched; the operator
+never falls back to a CPU path."""
+
+import ctypes
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared():
+    text = (ROOT / "include" / "tjev_gdn.h").read_text()
+    return sorted(set(re.findall(r"\b(tjev_gdn_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from tjev_amd import _lib
+
+    lib = _lib.load()
+    declared = _declared()
+    assert set(declared) == set(_lib.EXPORTS), (declared, _lib.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.tjev_gdn_version() >> 16 == 0
+    assert lib.tjev_gdn_kernel_name(0) == b"gdn_prep_fwd"
+
+
+def _params(**kw):
+    from tjev_amd import _lib
+
+    base = dict(batch=1, length=100, key_heads=2, key_dim=16, value_heads=4, value_dim=16, taps=4, chunk=16,
+                io_dtype=0, gate_dtype=0, precision=1, inverse=0, heads_per_step=0)
+    base.update(kw)
+    return _lib.Params(**base)
+
+
+@pytest.mark.parametrize("bad,status,msg", [
+    (dict(precision=7), 1, "precision"),
+    (dict(inverse=2), 1, "inverse"),
+    (dict(chunk=96), 1, "power-of-two chunk"),
+    (dict(chunk=4), 1, "power-of-two chunk"),
+    (dict(value_heads=5), 1, "groups of"),
+    (dict(taps=6), 1, "taps"),
+    (dict(key_dim=48, value_dim=48), 2, "no kernels"),
+    (dict(value_dim=32), 2, "key_dim == value_dim"),
+])
+def test_c_abi_validation(bad, status, msg):
+    from tjev_amd import _lib
+
+    lib = _lib.load()
+    p = _params(**bad)
+    assert lib.tjev_gdn_check(ctypes.byref(p)) == status
+    assert msg in lib.tjev_gdn_last_error().decode()
+    assert lib.tjev_gdn_workspace_bytes(ctypes.byref(p), 0) == 0
+
+
+def test_c_abi_sizes():
+    from tjev_amd import _lib
+
+    lib = _lib.load()
+    p = _params(batch=4, length=4096, key_heads=16, key_dim=128, value_heads=16, value_dim=128, chunk=128, io_dtype=1,
+                gate_dtype=1)
+    assert lib.tjev_gdn_check(ctypes.byref(p)) == 0
+    assert lib.tjev_gdn_states_bytes(ctypes.byref(p)) == 4 * 16 * 32 * 128 * 128 * 4
+    fwd, bwd = (lib.tjev_gdn_workspace_bytes(ctypes.byref(p), k) for k in (0, 1))
+    assert 0 < fwd < bwd < (2 << 30)
+    # a ragged T is padded to whole chunks (segment-0 padding, as the reference pads)
+    p = _params(length=100, chunk=16)
+    assert lib.tjev_gdn_states_bytes(ctypes.byref(p)) == 1 * 4 * 7 * 16 * 16 * 4
+
+
+def test_null_pointers_are_rejected_before_launch():
+    from tjev_amd import _lib
+
+    lib = _lib.load()
+    p = _params()
+    status = lib.tjev_gdn_mega2_fwd(ctypes.byref(p), None, *([None] * 10), 0)
+    assert status == 1 and "null" in lib.tjev_gdn_last_error().decode()
+
+
+def _args(**kw):
+    base = dict(key_heads=2, key_dim=16, value_heads=4, value_dim=16, chunk=16)
+    base.update(kw)
+    return base
+
+
+@pytest.mark.parametrize("kw,match", [
+    (dict(precision="fp8"), "precision in"),
+    (dict(inverse="solve"), "inverse in"),
+    (dict(chunk=24), "power-of-two chunk"),
+    (dict(chunk=4), "power-of-two chunk"),
+    (dict(key_heads=3), "qkv width"),
+])
+def test_operator_raises_value_errors_like_the_reference(kw, match):
+    from tjev_amd import gdn_megakernel
+
+    qkv = torch.zeros((1, 64, 2 * 2 * 16 + 4 * 16))
+    g = torch.zeros((1, 64, 4))
+    h = torch.zeros(4)
+    w = torch.zeros((4, qkv.shape[-1]))
+    seg = torch.ones((1, 64), dtype=torch.int32)
+    with pytest.raises(ValueError, match=match):
+        gdn_megakernel(qkv, g, g, h, h, w, seg, **_args(**kw))
+
+
+def test_operator_rejects_taps_and_head_groups():
+    from tjev_amd import gdn_megakernel
+
+    qkv = torch.zeros((1, 64, 2 * 2 * 16 + 4 * 16))
+    g = torch.zeros((1, 64, 4))
+    h = torch.zeros(4)
+    seg = torch.ones((1, 64), dtype=torch.int32)
+    with pytest.raises(ValueError, match="taps"):
+        gdn_megakernel(qkv, g, g, h, h, torch.zeros((6, qkv.shape[-1])), seg, **_args())
+    with pytest.raises(ValueError, match="42 heads"):
+        big = torch.zeros((1, 64, 2 * 1 * 16 + 48 * 16))
+        gdn_megakernel(big, torch.zeros((1, 64, 48)), torch.zeros((1, 64, 48)), torch.zeros(48), torch.zeros(48),
+                       None, seg, key_heads=1, key_dim=16, value_heads=48, value_dim=16, chunk=16, heads_per_step=48)
+
+
+def test_operator_has_no_cpu_fallback():
+    from tjev_amd import gdn_megakernel
+
+    qkv = torch.zeros((1, 64, 2 * 2 * 16 + 4 * 16))
+    g = torch.zeros((1, 64, 4))
+    h = torch.zeros(4)
+    with pytest.raises(RuntimeError, match="GPU"):
+        gdn_megakernel(qkv, g, g, h, h, None, torch.ones((1, 64), dtype=torch.int32), **_args())
+
+
+def test_kernel_inverse_and_heads_per_block():
+    from tjev_amd import heads_per_block, kernel_inverse
+
+    assert [kernel_inverse(x) for x in ("default", "doubling", "blocked")] == ["doubling", "doubling", "blocked"]
+    with pytest.raises(ValueError):
+        kernel_inverse("solve")
+    assert [heads_per_block(h, r) for h, r in ((16, 1), (32, 2), (4, 2), (3, 1), (48, 3))] == [8, 8, 4, 3, 6]
+
+
+def test_bench_refuses_more_than_one_gpu():
+    proc = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True)
+    assert proc.returncode == 2 and "one GPU" in proc.stderr
+
+
+def test_varlen_segments_follow_the_config():
+    import numpy as np
+
+    from tjev_amd.testing import geometric_segments
+
+    ids = geometric_segments(16384, np.random.default_rng(0))
+    assert ids.shape == (16384,) and ids[0] == 1 and np.all(np.diff(ids) >= 0)
+    lengths = np.bincount(ids)[1:]
+    assert np.all(lengths[:-1] >= 16) and np.all(lengths <= 4096)
+    assert 30 <= len(lengths) <= 90  # mean 300 over 16384 tokens

@@ -1,0 +1,330 @@
+"""Pinning the CPU oracle (CPU only).
+
+The reference ships no GDN golden arrays, so the oracle is pinned by what the mathematics and
+the reference's own tests fix: the token recurrence (chunked == recurrent for any chunk, with
+segments and states), packed rows == segments alone, state continuation, gradients, the
+triangular inverse against a dense inverse, the l2norm known answer, the conv against a
+textbook padded conv and torch's F.conv1d, HF transformers' independent GDN implementation
+(transformers 5.15.0, single segment), and the known answers of heads_per_block. Each check
+is chosen so that a plausible slip (a dropped reset, a wrong sign or index, a transposed
+operand) fails it; the planted-mistake tests at the end show that they do.
+"""
+
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.gdn_oracle as O
+
+F64 = torch.float64
+
+
+def _qkvgb(seed, batch=2, length=45, heads=3, dk=8, dv=6, dtype=F64):
+    """tests/kernels/test_gated_delta_rule.py:18-25 (numpy streams)."""
+    rng = np.random.default_rng(seed)
+    t = lambda *s: torch.from_numpy(rng.standard_normal(s)).to(dtype)  # noqa: E731
+    q = O.l2norm(t(batch, length, heads, dk)) * dk ** -0.5
+    k = O.l2norm(t(batch, length, heads, dk))
+    v = t(batch, length, heads, dv)
+    g = -torch.nn.functional.softplus(t(batch, length, heads))
+    beta = torch.sigmoid(t(batch, length, heads))
+    return q, k, v, g, beta
+
+
+def _segments(batch, length, seed):
+    """test_gated_delta_rule.py:28-35: 4 random cuts per row."""
+    rng = np.random.default_rng(seed)
+    rows = []
+    for _ in range(batch):
+        cuts = np.sort(rng.choice(np.arange(1, length), size=4, replace=False))
+        rows.append(np.searchsorted(cuts, np.arange(length), side="right") + 1)
+    return torch.from_numpy(np.stack(rows)).to(torch.int64)
+
+
+# ------------------------------------------------------------------ delta rule
+@pytest.mark.parametrize("chunk", [4, 8, 16, 64])
+def test_chunked_matches_recurrence(chunk):
+    q, k, v, g, beta = _qkvgb(0)
+    seg = _segments(2, 45, 0)
+    ref, ref_state = O.recurrent_gated_delta_rule(q, k, v, g, beta, seg)
+    out, state = O.chunk_gated_delta_rule(q, k, v, g, beta, seg, chunk=chunk)
+    assert torch.allclose(out, ref, atol=1e-12, rtol=1e-10)
+    assert torch.allclose(state, ref_state, atol=1e-12, rtol=1e-10)
+
+
+def test_packed_segments_equal_runs_alone():
+    """test_gated_delta_rule.py:47-58: each segment of a packed row alone."""
+    q, k, v, g, beta = _qkvgb(1)
+    seg = _segments(2, 45, 1)
+    out, _ = O.chunk_gated_delta_rule(q, k, v, g, beta, seg, chunk=16)
+    for b in range(2):
+        for s in torch.unique(seg[b]):
+            idx = torch.nonzero(seg[b] == s).ravel()
+            alone, _ = O.recurrent_gated_delta_rule(*(x[b: b + 1, idx] for x in (q, k, v, g, beta)))
+            assert torch.allclose(out[b, idx], alone[0], atol=1e-12)
+
+
+def test_initial_state_continuation():
+    """test_gated_delta_rule.py:61-73."""
+    q, k, v, g, beta = _qkvgb(2, length=40)
+    full, full_state = O.chunk_gated_delta_rule(q, k, v, g, beta, chunk=8)
+    first, state = O.chunk_gated_delta_rule(*(x[:, :24] for x in (q, k, v, g, beta)), chunk=8)
+    second, end = O.chunk_gated_delta_rule(*(x[:, 24:] for x in (q, k, v, g, beta)), initial_state=state,
+                                           chunk=8)
+    assert torch.allclose(torch.cat([first, second], 1), full, atol=1e-12)
+    assert torch.allclose(end, full_state, atol=1e-12)
+    step, _ = O.recurrent_gated_delta_rule(*(x[:, 24:25] for x in (q, k, v, g, beta)), initial_state=state)
+    assert torch.allclose(step[:, 0], full[:, 24], atol=1e-12)
+
+
+def test_gradients_chunked_match_recurrence():
+    """test_gated_delta_rule.py:76-92, in float64."""
+    xs = [x.requires_grad_(True) for x in _qkvgb(3, length=33)]
+    seg = _segments(2, 33, 3)
+    w = torch.from_numpy(np.random.default_rng(9).standard_normal((2, 33, 3, 6)))
+    gc = torch.autograd.grad((O.chunk_gated_delta_rule(*xs, seg, chunk=8)[0] * w).sum(), xs)
+    gr = torch.autograd.grad((O.recurrent_gated_delta_rule(*xs, seg)[0] * w).sum(), xs)
+    for a, b in zip(gc, gr):
+        assert torch.allclose(a, b, atol=1e-11, rtol=1e-9)
+
+
+def test_hf_transformers_single_segment():
+    """HF ``torch_chunk_gated_delta_rule`` / ``torch_recurrent_gated_delta_rule`` (the functions
+    the reference's xla.py follows) on one segment, including their in-kernel l2norm and
+    q scale: an implementation independent of this repository."""
+    hf = pytest.importorskip("transformers.models.qwen3_5.modeling_qwen3_5")
+    rng = np.random.default_rng(4)
+    B, T, H, D = 1, 100, 2, 16
+    q, k, v = (torch.from_numpy(rng.standard_normal((B, T, H, D))) for _ in range(3))
+    g = -torch.nn.functional.softplus(torch.from_numpy(rng.standard_normal((B, T, H))))
+    beta = torch.sigmoid(torch.from_numpy(rng.standard_normal((B, T, H))))
+    want_c, _ = hf.torch_chunk_gated_delta_rule(q, k, v, g, beta, chunk_size=32, use_qk_l2norm_in_kernel=True)
+    want_r, _ = hf.torch_recurrent_gated_delta_rule(q, k, v, g, beta, None, False, use_qk_l2norm_in_kernel=True)
+    qn, kn = O.l2norm(q) * D ** -0.5, O.l2norm(k)
+    got, _ = O.chunk_gated_delta_rule(qn, kn, v, g, beta, chunk=32)
+    # HF computes in float32 (its inputs are cast) and its l2norm has no zero-row guard (the
+    # rows here are nonzero): agreement to fp32 rounding
+    scale = float(got.abs().max())
+    assert float((got - want_r.double()).abs().max()) < 2e-6 * scale
+    assert float((got - want_c.double()).abs().max()) < 2e-6 * scale
+
+
+# ------------------------------------------------------------------ inverse
+@pytest.mark.parametrize("size", [16, 64, 128])
+@pytest.mark.parametrize("block", [0, 16])
+def test_inverse_matches_dense_inverse_correlated_keys(size, block):
+    """test_pallas_tpu.py:194-207 / test_gated_delta_rule.py:137-147: correlated keys (L ~ beta
+    on the whole strict lower triangle), doubling and blocked, against an fp64 dense inverse."""
+    rng = np.random.default_rng(size)
+    kk = torch.from_numpy(rng.standard_normal((3, size, 32))) + 2.0
+    kk = kk / kk.norm(dim=-1, keepdim=True)
+    lower = torch.tril(0.9 * kk @ kk.transpose(-1, -2), -1)
+    exact = torch.linalg.inv(torch.eye(size, dtype=F64) + lower)
+    got = O.unit_lower_inverse(lower, block)
+    assert float((got - exact).abs().max()) < 1e-9 * float(exact.abs().max())
+
+
+# ------------------------------------------------------------------ l2norm, conv, norms
+def test_l2norm_known_answer():
+    """test_gated_delta_rule.py:172-183: a zero row maps to 0 with zero gradient; elsewhere the
+    plain formula."""
+    x = torch.tensor([[0.0, 0.0, 0.0, 0.0], [3.0, 0.0, 4.0, 0.0]], dtype=F64, requires_grad=True)
+    cot = torch.tensor([[1.0, -2.0, 0.5, 3.0], [1.0, 2.0, -1.0, 0.5]], dtype=F64)
+    out = O.l2norm(x)
+    (grad,) = torch.autograd.grad((out * cot).sum(), x)
+    assert torch.all(out[0] == 0) and torch.all(grad[0] == 0)
+    row = torch.tensor([3.0, 0.0, 4.0, 0.0], dtype=F64, requires_grad=True)
+    plain = row * torch.rsqrt((row * row).sum() + 1e-6)
+    (pg,) = torch.autograd.grad((plain * cot[1]).sum(), row)
+    assert torch.allclose(out[1], plain.detach(), rtol=1e-12)
+    assert torch.allclose(grad[1], pg, rtol=1e-12)
+    assert torch.allclose(out[1], torch.tensor([0.6, 0.0, 0.8, 0.0], dtype=F64), atol=1e-7)
+
+
+def _conv_textbook(x, w, seg):
+    """test_causal_conv1d.py:34-44: zero-padded causal conv with per-tap segment masks."""
+    taps, length = w.shape[0], x.shape[1]
+    xp = torch.nn.functional.pad(x, (0, 0, taps - 1, 0))
+    sp = torch.nn.functional.pad(seg, (taps - 1, 0), value=-1)
+    out = torch.zeros_like(x)
+    for i in range(taps):
+        keep = (sp[:, i: i + length] == seg)[..., None]
+        out = out + torch.where(keep, xp[:, i: i + length], 0.0) * w[i]
+    return out
+
+
+def test_conv_matches_textbook_and_never_mixes_segments():
+    rng = np.random.default_rng(7)
+    x = torch.from_numpy(rng.standard_normal((2, 30, 7)))
+    w = torch.from_numpy(rng.standard_normal((4, 7)))
+    seg = _segments(2, 30, 3)
+    got = O.segmented_causal_conv1d(x, w, seg)
+    assert torch.allclose(got, _conv_textbook(x, w, seg), atol=1e-12)
+    for b in range(2):
+        for s in torch.unique(seg[b]):
+            idx = torch.nonzero(seg[b] == s).ravel()
+            alone = O.segmented_causal_conv1d(x[b: b + 1, idx], w, torch.ones((1, len(idx)), dtype=torch.int64))
+            assert torch.allclose(got[b, idx], alone[0], atol=1e-12)
+
+
+def test_conv_single_segment_is_torch_conv1d():
+    """HF's causal_conv1d_fn: F.conv1d with padding K-1, depthwise, weight [C, 1, K] (w[K-1]
+    multiplies the current token)."""
+    rng = np.random.default_rng(8)
+    x = torch.from_numpy(rng.standard_normal((1, 25, 5)))
+    w = torch.from_numpy(rng.standard_normal((4, 5)))
+    want = torch.nn.functional.conv1d(x.transpose(1, 2), w.T[:, None, :], padding=3, groups=5)[..., :25]
+    got = O.segmented_causal_conv1d(x, w, torch.ones((1, 25), dtype=torch.int64))
+    assert torch.allclose(got, want.transpose(1, 2), atol=1e-12)
+
+
+def test_gated_rmsnorm_matches_hf():
+    hf = pytest.importorskip("transformers.models.qwen3_5.modeling_qwen3_5")
+    rng = np.random.default_rng(5)
+    x = torch.from_numpy(rng.standard_normal((2, 7, 3, 16)).astype(np.float32)).to(torch.bfloat16)
+    z = torch.from_numpy(rng.standard_normal((2, 7, 3, 16)).astype(np.float32)).to(torch.bfloat16)
+    w = torch.from_numpy(rng.standard_normal(16).astype(np.float32))
+    norm = hf.Qwen3_5RMSNormGated(16, eps=1e-6)
+    with torch.no_grad():
+        norm.weight.copy_(w)
+        want = norm(x, z)
+    got = O.gated_rmsnorm(x, z, w)
+    assert got.dtype == torch.bfloat16
+    assert torch.equal(got, want)
+
+
+# ------------------------------------------------------------------ gates
+def test_gates_closed_forms():
+    """beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias) with jax.nn.softplus =
+    logaddexp(x, 0): against the formulas evaluated in Python's math at a few points,
+    including large |x| where a naive log(1 + exp(x)) overflows."""
+    import math
+
+    xs = [-50.0, -3.0, -1e-3, 0.0, 0.7, 20.0, 80.0]
+    for x in xs:
+        sp = float(torch.logaddexp(torch.tensor(x, dtype=F64), torch.tensor(0.0, dtype=F64)))
+        want = x + math.log1p(math.exp(-x)) if x > 0 else math.log1p(math.exp(x))
+        assert abs(sp - want) <= 1e-15 * max(1.0, abs(want))
+    seg = torch.ones((1, 3), dtype=torch.int64)
+    qkv = torch.zeros((1, 3, 2 * 1 * 2 + 1 * 2), dtype=F64)
+    a = torch.tensor([[[0.3], [-2.0], [5.0]]], dtype=F64)
+    b = torch.tensor([[[0.1], [0.2], [-0.3]]], dtype=F64)
+    a_log, dt = torch.tensor([0.4], dtype=F64), torch.tensor([-0.5], dtype=F64)
+    a.requires_grad_(True)
+    out = O.reference_core(qkv, a, b, a_log, dt, None, seg, key_heads=1, key_dim=2, value_heads=1, value_dim=2,
+                           conv=False, dtype=F64)
+    assert torch.all(out == 0)  # zero q, k, v: nothing to read or write
+
+
+# ------------------------------------------------------------------ masks
+def test_masks_brute_force():
+    """The integer masks against their per-token definitions on random rows with repeated,
+    zero and negative ids (pallas_tpu_mega.py:349-361, pallas_tpu_v2.py:505-515)."""
+    rng = np.random.default_rng(11)
+    for trial in range(20):
+        chunk, taps = [8, 16][trial % 2], 1 + trial % 5
+        n = 1 + trial % 4
+        seg = rng.integers(-1, 4, size=(2, n * chunk))
+        m = O.masks(seg, chunk, taps)
+        for b in range(2):
+            for t in range(n * chunk):
+                c0 = (t // chunk) * chunk
+                before = -2 if c0 == 0 else seg[b, c0 - 1]
+                assert m["cont"][b, t] == int(seg[b, t] == before)
+                assert m["in_last"][b, t] == int(seg[b, t] == seg[b, c0 + chunk - 1])
+                assert m["valid"][b, t] == int(seg[b, t] > 0)
+                for lag in range(1, taps):
+                    # ids are padded with -1 in front (causal_conv1d.py:12): an id of -1 "keeps"
+                    # the taps before the row start, which read the conv's zero padding
+                    prev = seg[b, t - lag] if t - lag >= 0 else -1
+                    assert m[f"keep_{lag}"][b, t] == int(prev == seg[b, t])
+
+
+def test_masks_known_answer():
+    seg = np.array([[1, 1, 1, 2, 2, 2, 0, 0]])
+    m = O.masks(seg, 4, 3)
+    assert m["cont"].tolist() == [[0, 0, 0, 0, 1, 1, 0, 0]]
+    assert m["in_last"].tolist() == [[0, 0, 0, 1, 0, 0, 1, 1]]
+    assert m["keep_1"].tolist() == [[0, 1, 1, 0, 1, 1, 0, 1]]
+    assert m["keep_2"].tolist() == [[0, 0, 1, 0, 0, 1, 0, 0]]
+    assert m["valid"].tolist() == [[1, 1, 1, 1, 1, 1, 0, 0]]
+    m = O.masks(np.array([[3, 3, 3, 3, 3, 3, 3, 3]]), 4, 2)
+    assert m["cont"].tolist() == [[0, 0, 0, 0, 1, 1, 1, 1]]
+
+
+def test_heads_per_block_known_answers():
+    """test_pallas_tpu.py:276-282."""
+    got = [O.heads_per_block(h, r) for h, r in ((16, 1), (32, 2), (4, 2), (3, 1), (48, 3))]
+    assert got == [8, 8, 4, 3, 6]
+    with pytest.raises(ValueError):
+        O.heads_per_block(5, 2)
+
+
+# ------------------------------------------------------------------ the core
+def test_reference_core_packed_rows_equal_segments_alone():
+    """test_gdn_mega.py:135-147: conv taps and the state never cross a boundary."""
+    from tjev_amd.testing import gdn_inputs
+
+    qkv, a, b, a_log, dt_bias, w, _ = gdn_inputs(batch=1, length=96, key_heads=2, value_heads=4, dim=16,
+                                                 style="reference", dtype=F64)
+    spans = list(itertools.pairwise([0, 16, 33, 71, 96]))
+    seg = torch.cat([torch.full((e - s,), i + 1) for i, (s, e) in enumerate(spans)])[None]
+    kw = dict(key_heads=2, key_dim=16, value_heads=4, value_dim=16, chunk=16, dtype=F64)
+    packed = O.reference_core(qkv, a, b, a_log, dt_bias, w, seg, **kw)
+    for s, e in spans:
+        alone = O.reference_core(qkv[:, s:e], a[:, s:e], b[:, s:e], a_log, dt_bias, w,
+                                 torch.ones((1, e - s), dtype=torch.int64), **kw)
+        assert torch.allclose(packed[:, s:e], alone, atol=1e-12)
+
+
+def test_reference_core_chunked_equals_recurrent_with_grads():
+    """The whole core (conv, norms, gates, rule) chunked vs token-recurrent in float64, forward
+    and every input gradient, with packed segments and trailing padding."""
+    import sys
+    from pathlib import Path
+
+    sys.path.insert(0, str(Path(__file__).parent))
+    from gdn_cases import case_inputs
+
+    inputs, cot = case_inputs(1, 120, 2, 4, 16, cuts=[16, 33, 50, 67, 95])
+    kw = dict(key_heads=2, key_dim=16, value_heads=4, value_dim=16)
+    a = O.reference_with_grads(inputs, cot, rule="chunked", dtype=F64, **kw)
+    b = O.reference_with_grads(inputs, cot, rule="recurrent", dtype=F64, **kw)
+    for k in a:
+        assert torch.allclose(a[k], b[k], atol=1e-10, rtol=1e-9), k
+
+
+# ------------------------------------------------------------------ planted mistakes
+def test_planted_mistakes_are_caught(monkeypatch):
+    """Each check above has teeth: a broken oracle (no reset across a chunk boundary, a wrong
+    decay sign, reversed conv taps, no zero-row guard) fails the corresponding check."""
+    q, k, v, g, beta = _qkvgb(0)
+    seg = _segments(2, 45, 0)
+    ref, _ = O.recurrent_gated_delta_rule(q, k, v, g, beta, seg)
+
+    # 1. the carried state never resets (cont forced true): chunked != recurrence
+    orig_cat = torch.cat
+
+    def no_reset(q_, k_, v_, g_, b_, s_, chunk):
+        return O.chunk_gated_delta_rule(q_, k_, v_, g_, b_, torch.ones_like(s_), chunk=chunk)[0]
+    assert not torch.allclose(no_reset(q, k, v, g, beta, seg, 16), ref, atol=1e-6)
+
+    # 2. a sign slip in the decay (e^{+g}): chunked != recurrence
+    bad, _ = O.chunk_gated_delta_rule(q, k, v, -g, beta, seg, chunk=16)
+    assert not torch.allclose(bad, ref, atol=1e-6)
+
+    # 3. reversed conv taps: textbook conv disagrees
+    rng = np.random.default_rng(7)
+    x = torch.from_numpy(rng.standard_normal((1, 20, 3)))
+    w = torch.from_numpy(rng.standard_normal((4, 3)))
+    s1 = torch.ones((1, 20), dtype=torch.int64)
+    assert not torch.allclose(O.segmented_causal_conv1d(x, w.flip(0), s1), _conv_textbook(x, w, s1), atol=1e-6)
+
+    # 4. l2norm without the zero-row guard: the known answer's zero gradient fails
+    monkeypatch.setattr(O, "l2norm", lambda x, eps=1e-6: x * torch.rsqrt((x * x).sum(-1, keepdim=True) + eps))
+    xx = torch.zeros((1, 4), dtype=F64, requires_grad=True)
+    (gr,) = torch.autograd.grad((O.l2norm(xx) * torch.ones(1, 4, dtype=F64)).sum(), xx)
+    assert not torch.all(gr == 0)
+    assert orig_cat is torch.cat
