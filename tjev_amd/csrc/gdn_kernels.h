@@ -167,107 +167,108 @@ __device__ void invert_unit_lower(float* sT, int LT, float* tmp) {
   doubling_level<C, P, 16>(sT, LT, tmp);
 }
 
+// ---------------------------------------------------------------- conv helpers
+// Per-lag conv weights of 8 channels: wl[L] multiplies token t-L (w[K-1-L]), zero past the taps.
+// Static lag indices keep them in registers.
+__device__ __forceinline__ void lag_weights(const GdnArgs& A, int cc, float (&wl)[5][8]) {
+#pragma unroll
+  for (int L = 0; L < 5; ++L)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wl[L][e] = (L < A.taps) ? A.conv_w[(size_t)(A.taps - 1 - L) * A.W + cc + e] : 0.f;
+}
+
+// Raw rows t, t-1, .. t-4 of 8 channels (zeros outside [0, T) and past the taps) and whether
+// each tap stays in token t's segment (causal_conv1d.py:10-17).
+template <class TIO>
+__device__ __forceinline__ void conv_rows(const GdnArgs& A, const TIO* x, const int32_t* sp, int b, int t, int cc,
+                                          int st, float (&xs)[5][8], bool (&keep)[5]) {
+  const int taps = A.taps > 0 ? A.taps : 1;
+#pragma unroll
+  for (int L = 0; L < 5; ++L) {
+    const int tt = t - L;
+    keep[L] = L < taps && tt >= 0 && (L == 0 || sp[tt] == st);
+    if (L < taps && tt >= 0 && tt < A.T) {
+      ld8(x + ((size_t)b * A.T + tt) * A.W + cc, xs[L]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xs[L][e] = 0.f;
+    }
+  }
+}
+
+// z = sum over lags of keep * x[t-L] * w[K-1-L], lag 0 first (causal_conv1d.py:42-45)
+__device__ __forceinline__ void conv_z(const float (&xs)[5][8], const bool (&keep)[5], const float (&wl)[5][8],
+                                       float (&z)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float v = xs[0][e] * wl[0][e];
+#pragma unroll
+    for (int L = 1; L < 5; ++L)
+      if (keep[L]) v += xs[L][e] * wl[L][e];
+    z[e] = v;
+  }
+}
+
 // ---------------------------------------------------------------- k_prep
 // grid (B*N, 2*Hk + H), 256 threads. Slot y: q head y (< Hk), k head y - Hk, v head y - 2Hk.
-// Conv sum order of causal_conv1d.py:42-45 (lag 0, then 1..K-1); l2norm of xla.py:42-53.
+// Every (token, 8 channels) is independent: D/8 lanes per token row. l2norm of xla.py:42-53.
+// Slot 0 first writes the padded segment ids of the chunk (read by every later kernel).
 template <int C, int D, class TIO, class TG>
 __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
   constexpr int CG = D / 8;
-  constexpr int NTG = 256 / CG;
-  constexpr int TPT = (C >= NTG) ? C / NTG : 1;
+  constexpr int RPP = 256 / CG;
   const int b = blockIdx.x / A.N, n = blockIdx.x % A.N;
   const int slot = blockIdx.y;
-  const int cg = threadIdx.x % CG, tg = threadIdx.x / CG;
+  const int cg = threadIdx.x % CG;
   int kind, head, c0;
   if (slot < A.Hk) { kind = 0; head = slot; c0 = slot * D; }
   else if (slot < 2 * A.Hk) { kind = 1; head = slot - A.Hk; c0 = A.Hk * D + head * D; }
   else { kind = 2; head = slot - 2 * A.Hk; c0 = 2 * A.Hk * D + head * D; }
   const int cc = c0 + cg * 8;
   const TIO* x = reinterpret_cast<const TIO*>(A.qkv);
+  const int32_t* sg = A.seg + (size_t)b * A.T;
   float* dst = kind == 0 ? A.qn + hoff(A, b, head, A.Hk, n, C, D)
              : kind == 1 ? A.kn + hoff(A, b, head, A.Hk, n, C, D)
                          : A.vv + hoff(A, b, head, A.H, n, C, D);
-  const int taps = A.taps;
-  float wt[5][8];
+  float wl[5][8];
+  lag_weights(A, cc, wl);
+#pragma unroll 2
+  for (int r = threadIdx.x / CG; r < C; r += RPP) {
+    const int t = n * C + r;
+    const int st = t < A.T ? sg[t] : 0;
+    float act[8];
+    if (t >= A.T) {  // the padded tail: zero qkv, segment 0
 #pragma unroll
-  for (int L = 0; L < 5; ++L)
+      for (int e = 0; e < 8; ++e) act[e] = 0.f;
+    } else if (A.taps == 0) {  // mega1: qkv is already the activation
+      ld8(x + ((size_t)b * A.T + t) * A.W + cc, act);
+    } else {  // every tap index t-L < T reads a real segment id
+      float xs[5][8], z[8];
+      bool keep[5];
+      conv_rows(A, x, sg, b, t, cc, st, xs, keep);
+      conv_z(xs, keep, wl, z);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) wt[L][e] = (L < taps) ? A.conv_w[(size_t)L * A.W + cc + e] : 0.f;
-
-  const int t_lo = tg * TPT;
-  if (t_lo < C) {
-    // history of raw rows t-1 .. t-4 and their ids
-    float xh[4][8];
-    int sh[4];
-#pragma unroll
-    for (int L = 1; L <= 4; ++L) {
-      const int t = n * C + t_lo - L;
-      const bool in = t >= 0 && t < A.T;
-      sh[L - 1] = in ? A.seg[(size_t)b * A.T + t] : 0;
-      if (in && L < taps) {
-        ld8(x + ((size_t)b * A.T + t) * A.W + cc, xh[L - 1]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xh[L - 1][e] = 0.f;
-      }
+      for (int e = 0; e < 8; ++e) act[e] = st > 0 ? z[e] * sigmoidf_(z[e]) : 0.f;
     }
-    for (int q = 0; q < TPT; ++q) {
-      const int tl = t_lo + q, t = n * C + tl;
-      const bool in = t < A.T;
-      float xt[8];
-      if (in) {
-        ld8(x + ((size_t)b * A.T + t) * A.W + cc, xt);
-      } else {
+    if (kind < 2) {  // l2norm over the head's D channels (CG lanes)
+      float sq = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xt[e] = 0.f;
-      }
-      const int st = in ? A.seg[(size_t)b * A.T + t] : 0;
-      float act[8];
-      if (taps == 0) {  // mega1: qkv is already the activation
+      for (int e = 0; e < 8; ++e) sq += act[e] * act[e];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) act[e] = xt[e];
-      } else {
-        bool keep[4];
+      for (int m = 1; m < CG; m <<= 1) sq += __shfl_xor(sq, m);
+      float rn = sq == 0.f ? 0.f : 1.0f / sqrtf(sq + 1e-6f);
+      if (kind == 0) rn *= A.scale;
 #pragma unroll
-        for (int L = 1; L <= 4; ++L) keep[L - 1] = (L < taps) && (t - L >= 0) && (sh[L - 1] == st);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float z = xt[e] * wt[taps - 1][e];
-#pragma unroll
-          for (int L = 1; L <= 4; ++L)
-            if (keep[L - 1]) z += xh[L - 1][e] * wt[taps - 1 - L][e];
-          act[e] = st > 0 ? z * sigmoidf_(z) : 0.f;
-        }
-      }
-#pragma unroll
-      for (int L = 3; L >= 1; --L) {
-        sh[L] = sh[L - 1];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xh[L][e] = xh[L - 1][e];
-      }
-      sh[0] = st;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xh[0][e] = xt[e];
-      if (kind < 2) {  // l2norm over the head's D channels (CG lanes)
-        float sq = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sq += act[e] * act[e];
-#pragma unroll
-        for (int m = 1; m < CG; m <<= 1) sq += __shfl_xor(sq, m);
-        float r = sq == 0.f ? 0.f : 1.0f / sqrtf(sq + 1e-6f);
-        if (kind == 0) r *= A.scale;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) act[e] *= r;
-      }
-      float4* o = reinterpret_cast<float4*>(dst + (size_t)tl * D + cg * 8);
-      o[0] = make_float4(act[0], act[1], act[2], act[3]);
-      o[1] = make_float4(act[4], act[5], act[6], act[7]);
+      for (int e = 0; e < 8; ++e) act[e] *= rn;
     }
+    float4* o = reinterpret_cast<float4*>(dst + (size_t)r * D + cg * 8);
+    o[0] = make_float4(act[0], act[1], act[2], act[3]);
+    o[1] = make_float4(act[4], act[5], act[6], act[7]);
   }
   if (slot == 0) {
     for (int i = threadIdx.x; i < C; i += 256) {
       const int t = n * C + i;
-      A.segp[(size_t)b * A.Tp + t] = t < A.T ? A.seg[(size_t)b * A.T + t] : 0;
+      A.segp[(size_t)b * A.Tp + t] = t < A.T ? sg[t] : 0;
     }
   }
   if (kind == 2 && threadIdx.x < 64) {  // gates of value head `head` (pallas_tpu_mega.py:106-127)
@@ -769,12 +770,15 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
 template <int C, int D, class TIO, class TG>
 __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
   constexpr int CG = D / 8;
-  constexpr int NTG = 256 / CG;
-  constexpr int TPT = (C >= NTG) ? C / NTG : 1;
-  __shared__ float sdw[256 * 5 * 8];  // per-thread d(conv weight) partials [tg][tap][D]
+  constexpr int RPP = 256 / CG;
+  constexpr int R = C + 4;  // the chunk's rows and 4 look-ahead rows (taps <= 5)
+  constexpr int LZ = D + 4;
+  constexpr int SZ = R * LZ > 256 * 5 * 8 ? R * LZ : 256 * 5 * 8;  // also the d(conv w) scratch
+  __shared__ float sdz[SZ];
+  __shared__ int sseg[R];
   const int b = blockIdx.x / A.N, n = blockIdx.x % A.N;
   const int slot = blockIdx.y;
-  const int cg = threadIdx.x % CG, tg = threadIdx.x / CG;
+  const int cg = threadIdx.x % CG;
   int kind, head, c0;
   if (slot < A.Hk) { kind = 0; head = slot; c0 = slot * D; }
   else if (slot < 2 * A.Hk) { kind = 1; head = slot - A.Hk; c0 = A.Hk * D + head * D; }
@@ -784,162 +788,156 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
   const TIO* x = reinterpret_cast<const TIO*>(A.qkv);
   TIO* dx = reinterpret_cast<TIO*>(A.d_qkv);
   const int32_t* sp = A.segp + (size_t)b * A.Tp;
-  float wt[5][8];
+  float wl[5][8];
+  lag_weights(A, cc, wl);
+  const int rows = C + (taps > 1 ? taps - 1 : 0);
+  // phase 1: dz for the chunk and the look-ahead rows, into LDS
+#pragma unroll 2
+  for (int r = threadIdx.x / CG; r < R; r += RPP) {
+    const int t = n * C + r;
+    float dz[8];
+    int st = -3;
+    if (r < rows && t < A.Tp) {  // uniform over the CG lanes of the row
+      st = sp[t];
+      float xs[5][8], z[8], act[8];
+      bool keep[5];
+      if (taps == 0) {
+        if (t < A.T) {
+          ld8(x + ((size_t)b * A.T + t) * A.W + cc, act);
+        } else {
 #pragma unroll
-  for (int L = 0; L < 5; ++L)
+          for (int e = 0; e < 8; ++e) act[e] = 0.f;
+        }
+      } else {
+        conv_rows(A, x, sp, b, t, cc, st, xs, keep);
+        conv_z(xs, keep, wl, z);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) wt[L][e] = (L < taps) ? A.conv_w[(size_t)L * A.W + cc + e] : 0.f;
+        for (int e = 0; e < 8; ++e) act[e] = st > 0 ? z[e] * sigmoidf_(z[e]) : 0.f;
+      }
+      float dy[8];
+      if (kind < 2) {  // GQA sum over the value heads of this key head, then l2norm backward
+        const float* src = kind == 0 ? A.dqh : A.dkh;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dy[e] = 0.f;
+        for (int v = 0; v < A.ratio; ++v) {
+          float y[8];
+          ld8(src + ((size_t)(b * A.H + head * A.ratio + v) * A.Tp + t) * D + cg * 8, y);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dy[e] += y[e];
+        }
+        if (kind == 0) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dy[e] *= A.scale;
+        }
+        float sq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sq += act[e] * act[e];
+#pragma unroll
+        for (int m = 1; m < CG; m <<= 1) sq += __shfl_xor(sq, m);
+        const float rn = sq == 0.f ? 0.f : 1.0f / sqrtf(sq + 1e-6f);
+        float dot = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dot += act[e] * rn * dy[e];
+#pragma unroll
+        for (int m = 1; m < CG; m <<= 1) dot += __shfl_xor(dot, m);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dy[e] = rn * (dy[e] - act[e] * rn * dot);
+      } else {  // dv = X beta
+        const float bt = A.bet[(size_t)(b * A.H + head) * A.Tp + t];
+        ld8(A.xl + ((size_t)(b * A.H + head) * A.Tp + t) * D + cg * 8, dy);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dy[e] *= bt;
+      }
+      if (taps == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dz[e] = dy[e];
+      } else {  // SiLU backward on valid tokens
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float sgm = sigmoidf_(z[e]);
+          dz[e] = st > 0 ? dy[e] * sgm * (1.f + z[e] * (1.f - sgm)) : 0.f;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dz[e] = 0.f;
+    }
+    float4* o = reinterpret_cast<float4*>(sdz + r * LZ + cg * 8);
+    o[0] = make_float4(dz[0], dz[1], dz[2], dz[3]);
+    o[1] = make_float4(dz[4], dz[5], dz[6], dz[7]);
+    if (cg == 0) sseg[r] = st;
+  }
+  __syncthreads();
+  // phase 2: the anti-causal conv, dx[t] = sum over lags of w[K-1-L] keep_L[t+L] dz[t+L]
   float dwa[5][8];
 #pragma unroll
   for (int L = 0; L < 5; ++L)
 #pragma unroll
     for (int e = 0; e < 8; ++e) dwa[L][e] = 0.f;
-  const int t_lo = tg * TPT;
-  if (t_lo < C) {
-    float dzw[4][8];  // dz of tokens t+1 .. t+4
-    int sw[4];
+  const bool want_dw = A.d_conv_w && taps > 0;
+#pragma unroll 2
+  for (int r = threadIdx.x / CG; r < C; r += RPP) {
+    const int t = n * C + r;
+    const int st = sseg[r];
+    float o[8], dz[8];
+    const float4* d0 = reinterpret_cast<const float4*>(sdz + r * LZ + cg * 8);
+    const float4 p0 = d0[0], p1 = d0[1];
+    dz[0] = p0.x; dz[1] = p0.y; dz[2] = p0.z; dz[3] = p0.w;
+    dz[4] = p1.x; dz[5] = p1.y; dz[6] = p1.z; dz[7] = p1.w;
+    if (taps == 0) {
 #pragma unroll
-    for (int L = 0; L < 4; ++L) {
-      sw[L] = 0;
+      for (int e = 0; e < 8; ++e) o[e] = dz[e];
+    } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dzw[L][e] = 0.f;
-    }
-    const int ahead = taps > 1 ? taps - 1 : 0;
-    for (int q = TPT - 1 + ahead; q >= 0; --q) {
-      const int t = n * C + t_lo + q;
-      float dz[8], xs[5][8];
-      int st = 0;
-      if (t < A.Tp) {  // uniform over the CG lanes of this token
-        st = sp[t];
+      for (int e = 0; e < 8; ++e) o[e] = dz[e] * wl[0][e];
 #pragma unroll
-        for (int L = 0; L < 5; ++L) {
-          const int tt = t - L;
-          if (L < (taps > 0 ? taps : 1) && tt >= 0 && tt < A.T) {
-            ld8(x + ((size_t)b * A.T + tt) * A.W + cc, xs[L]);
-          } else {
+      for (int L = 1; L < 5; ++L) {
+        if (L < taps && sseg[r + L] == st) {
+          const float* dl = sdz + (r + L) * LZ + cg * 8;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) xs[L][e] = 0.f;
-          }
+          for (int e = 0; e < 8; ++e) o[e] += wl[L][e] * dl[e];
         }
-        float z[8], act[8];
-        if (taps == 0) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) { z[e] = 0.f; act[e] = xs[0][e]; }
-        } else {
-          bool keep[5];
-#pragma unroll
-          for (int L = 0; L < 5; ++L) keep[L] = (L < taps) && (L == 0 || (t - L >= 0 && sp[t - L] == st));
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            float s = xs[0][e] * wt[taps - 1][e];
-#pragma unroll
-            for (int L = 1; L < 5; ++L)
-              if (keep[L]) s += xs[L][e] * wt[taps - 1 - L][e];
-            z[e] = s;
-            act[e] = st > 0 ? s * sigmoidf_(s) : 0.f;
-          }
-        }
-        float dy[8];
-        if (kind < 2) {
-          const float* src = (kind == 0 ? A.dqh : A.dkh);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) dy[e] = 0.f;
-          for (int v = 0; v < A.ratio; ++v) {
-            float y[8];
-            ld8(src + ((size_t)(b * A.H + head * A.ratio + v) * A.Tp + t) * D + cg * 8, y);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) dy[e] += y[e];
-          }
-          if (kind == 0) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) dy[e] *= A.scale;
-          }
-          float sq = 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) sq += act[e] * act[e];
-#pragma unroll
-          for (int m = 1; m < CG; m <<= 1) sq += __shfl_xor(sq, m);
-          const float r = sq == 0.f ? 0.f : 1.0f / sqrtf(sq + 1e-6f);
-          float dot = 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) dot += act[e] * r * dy[e];
-#pragma unroll
-          for (int m = 1; m < CG; m <<= 1) dot += __shfl_xor(dot, m);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) dy[e] = r * (dy[e] - act[e] * r * dot);
-        } else {
-          const float bt = A.bet[(size_t)(b * A.H + head) * A.Tp + t];
-          ld8(A.xl + ((size_t)(b * A.H + head) * A.Tp + t) * D + cg * 8, dy);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) dy[e] *= bt;
-        }
-        if (taps == 0) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) dz[e] = dy[e];
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float s = sigmoidf_(z[e]);
-            dz[e] = st > 0 ? dy[e] * s * (1.f + z[e] * (1.f - s)) : 0.f;
-          }
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dz[e] = 0.f;
+      }
+      if (want_dw) {  // d w[K-1-L] += keep_L[t] dz[t] x[t-L]
+        float xs[5][8];
+        bool keep[5];
+        conv_rows(A, x, sp, b, t, cc, st, xs, keep);
 #pragma unroll
         for (int L = 0; L < 5; ++L)
+          if (keep[L]) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) xs[L][e] = 0.f;
-      }
-      if (q < TPT && t < A.Tp) {
-        float o[8];
-        if (taps == 0) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[e] = dz[e];
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            float s = dz[e] * wt[taps - 1][e];
-#pragma unroll
-            for (int L = 1; L < 5; ++L)
-              if (L < taps && sw[L - 1] == st) s += wt[taps - 1 - L][e] * dzw[L - 1][e];
-            o[e] = s;
+            for (int e = 0; e < 8; ++e) dwa[L][e] += dz[e] * xs[L][e];
           }
-          if (A.d_conv_w) {
-#pragma unroll
-            for (int L = 0; L < 5; ++L)
-              if (L < taps && (L == 0 || (t - L >= 0 && sp[t - L] == st))) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) dwa[L][e] += dz[e] * xs[L][e];
-              }
-          }
-        }
-        if (t < A.T) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) stf(dx + ((size_t)b * A.T + t) * A.W + cc + e, o[e]);
-        }
       }
-#pragma unroll
-      for (int L = 3; L >= 1; --L) {
-        sw[L] = sw[L - 1];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dzw[L][e] = dzw[L - 1][e];
+    }
+    if (t < A.T) {
+      TIO* dst = dx + ((size_t)b * A.T + t) * A.W + cc;
+      if constexpr (sizeof(TIO) == 2) {
+        uint4 pk;
+        pk.x = (uint32_t)f2bf(o[0]) | ((uint32_t)f2bf(o[1]) << 16);
+        pk.y = (uint32_t)f2bf(o[2]) | ((uint32_t)f2bf(o[3]) << 16);
+        pk.z = (uint32_t)f2bf(o[4]) | ((uint32_t)f2bf(o[5]) << 16);
+        pk.w = (uint32_t)f2bf(o[6]) | ((uint32_t)f2bf(o[7]) << 16);
+        *reinterpret_cast<uint4*>(dst) = pk;
+      } else {
+        float4* q = reinterpret_cast<float4*>(dst);
+        q[0] = make_float4(o[0], o[1], o[2], o[3]);
+        q[1] = make_float4(o[4], o[5], o[6], o[7]);
       }
-      sw[0] = st;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dzw[0][e] = dz[e];
     }
   }
-  if (A.d_conv_w && taps > 0) {  // per-workgroup partial of d(conv weight), fixed sum order
+  if (want_dw) {  // per-workgroup partial of d(conv weight), fixed sum order
+    __syncthreads();
+    float* sdw = sdz;  // [thread][lag][8]
 #pragma unroll
     for (int L = 0; L < 5; ++L)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sdw[(tg * 5 + L) * 8 * CG + cg * 8 + e] = dwa[L][e];
+      for (int e = 0; e < 8; ++e) sdw[(threadIdx.x * 5 + L) * 8 + e] = dwa[L][e];
     __syncthreads();
     for (int idx = threadIdx.x; idx < taps * D; idx += 256) {
-      const int L = idx / D, c = idx % D;
+      const int L = idx / D, c = idx % D, g = c / 8, e = c % 8;
       float s = 0.f;
-      for (int q = 0; q < NTG; ++q) s += sdw[(q * 5 + L) * 8 * CG + c];
+      for (int q = 0; q < RPP; ++q) s += sdw[((q * CG + g) * 5 + L) * 8 + e];
       A.dwp[(((size_t)b * A.N + n) * taps + (taps - 1 - L)) * A.W + c0 + c] = s;
     }
   }
