@@ -48,8 +48,10 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"build failed: {' '.join(cmd)}\n{err}")
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> Path:
-    """Compile every kernel unit and link the library (always rebuilds)."""
+def build(jobs: int | None = None, verbose: bool = False, verify: bool = True) -> Path:
+    """Compile every kernel unit and link the library (always rebuilds). ``verify`` also runs
+    the merged-LDS-access check of ds_check.py on every unit and fails the build if any
+    access was miscompiled."""
     hipcc = _hipcc()
     OUT.mkdir(exist_ok=True)
     units = []
@@ -61,7 +63,15 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     units.append([hipcc, *FLAGS, "-c", str(CSRC / "gdn_api.hip"), "-o", str(api_obj)])
     t0 = time.time()
     with ThreadPoolExecutor(max_workers=jobs or min(len(units), os.cpu_count() or 4)) as pool:
+        checks = []
+        if verify:
+            from .ds_check import check_unit
+
+            checks = [pool.submit(check_unit, c, d) for c, d in shapes()]
         list(pool.map(_run, units))
+        bad = [line for f in checks for line in f.result()]
+    if bad:
+        raise RuntimeError("miscompiled merged LDS accesses (ds_check):\n" + "\n".join(bad[:10]))
     objs = [u[-1] for u in units]
     tmp = LIB.with_suffix(".so.tmp")
     _run([hipcc, *FLAGS, "-shared", "-o", str(tmp), *objs])
@@ -74,8 +84,9 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("-j", "--jobs", type=int, default=None)
+    ap.add_argument("--no-verify", action="store_true", help="skip the merged-LDS-access check")
     args = ap.parse_args(argv)
-    build(args.jobs, verbose=True)
+    build(args.jobs, verbose=True, verify=not args.no_verify)
     return 0
 
 

@@ -36,6 +36,16 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
   return (uint16_t)(u >> 16);
 }
 
+// A single fp32 store into LDS that the backend may not pair with its neighbours. ROCm 7.2's
+// SI load/store optimizer can merge two such stores into one ds_write2_b32 with a wrongly
+// scaled first offset (seen for 272/336-byte offsets: emitted as 17/84 dwords); the empty asm
+// with a memory clobber keeps every store single. build.py checks the merged DS accesses of
+// every kernel for this.
+__device__ __forceinline__ void lds_st(float* p, float v) {
+  *p = v;
+  asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ float ldf(const float* p) { return *p; }
 __device__ __forceinline__ float ldf(const uint16_t* p) { return bf2f(*p); }
 __device__ __forceinline__ void stf(float* p, float v) { *p = v; }
@@ -145,41 +155,125 @@ struct ScaleK {
     for (int e = 0; e < 8; ++e) o[e] *= c * s[k + e];
   }
 };
-template <class T> __device__ __forceinline__ KRow<T> krow(const T* p, int ld) { return {p, ld}; }
-template <class T> __device__ __forceinline__ KCol<T> kcol(const T* p, int ld) { return {p, ld}; }
-template <class V> __device__ __forceinline__ ScaleR<V> scale_r(V v, const float* s, float c = 1.f) { return {v, s, c}; }
-template <class V> __device__ __forceinline__ ScaleK<V> scale_k(V v, const float* s, float c = 1.f) { return {v, s, c}; }
+// Every view also yields a converted fragment: frag<Q>(r, k) = make_frag<Q>(load(r, k)).
+#define GDN_VIEW_FRAG                                                            \
+  template <int Q>                                                               \
+  __device__ __forceinline__ Frag<Q> frag(int r, int k) const {                  \
+    float x_[8];                                                                 \
+    this->load(r, k, x_);                                                        \
+    return make_frag<Q>(x_);                                                     \
+  }
+template <class T> struct KRowF : KRow<T> { GDN_VIEW_FRAG };
+template <class T> struct KColF : KCol<T> { GDN_VIEW_FRAG };
+template <class V> struct ScaleRF : ScaleR<V> { GDN_VIEW_FRAG };
+template <class V> struct ScaleKF : ScaleK<V> { GDN_VIEW_FRAG };
+
+template <class T> __device__ __forceinline__ KRowF<T> krow(const T* p, int ld) { return {{p, ld}}; }
+template <class T> __device__ __forceinline__ KColF<T> kcol(const T* p, int ld) { return {{p, ld}}; }
+template <class V> __device__ __forceinline__ ScaleRF<V> scale_r(V v, const float* s, float c = 1.f) { return {{v, s, c}}; }
+template <class V> __device__ __forceinline__ ScaleKF<V> scale_k(V v, const float* s, float c = 1.f) { return {{v, s, c}}; }
+
+
+// ---------------------------------------------------------------- pre-converted LDS operands
+// Op<P>: an operand tile in LDS, converted once when it is staged. Element (r, k) sits at
+// r*ld + k with the contraction index k contiguous (r: the M index of an A operand, the N index
+// of a B operand), so a fragment is one 16-byte read per plane. P_F32 keeps fp32; P_BF16 one bf16
+// plane; P_BF16X3 the bf16 hi and lo planes of each value. A P_BF16X3 tile also serves one-pass
+// products (its hi plane), as the state-path products of "mixed" need.
+template <int P> struct Op;
+template <>
+struct Op<P_F32> {
+  float* p;
+  int ld;
+  __device__ __forceinline__ void put(int r, int k, float v) const { lds_st(p + r * ld + k, v); }
+  template <int Q>
+  __device__ __forceinline__ Frag<Q> frag(int r, int k) const {
+    static_assert(Q == P_F32, "an fp32 tile feeds fp32 products");
+    float x[8];
+    ld8(p + r * ld + k, x);
+    Frag<P_F32> f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f.v[e] = x[e];
+    return f;
+  }
+};
+template <>
+struct Op<P_BF16> {
+  uint16_t* hi;
+  int ld;
+  __device__ __forceinline__ void put(int r, int k, float v) const {
+    hi[r * ld + k] = __builtin_bit_cast(uint16_t, (__bf16)v);
+  }
+  template <int Q>
+  __device__ __forceinline__ Frag<Q> frag(int r, int k) const {
+    static_assert(Q == P_BF16, "a bf16 tile feeds one-pass products");
+    Frag<P_BF16> f;
+    f.hi = *reinterpret_cast<const bf16x8*>(hi + r * ld + k);
+    return f;
+  }
+};
+template <>
+struct Op<P_BF16X3> {
+  uint16_t* hi;
+  uint16_t* lo;
+  int ld;
+  __device__ __forceinline__ void put(int r, int k, float v) const {
+    const __bf16 h = (__bf16)v;
+    hi[r * ld + k] = __builtin_bit_cast(uint16_t, h);
+    lo[r * ld + k] = __builtin_bit_cast(uint16_t, (__bf16)(v - (float)h));
+  }
+  template <int Q>
+  __device__ __forceinline__ Frag<Q> frag(int r, int k) const {
+    static_assert(Q == P_BF16X3 || Q == P_BF16, "a split tile feeds bf16x3 or one-pass products");
+    Frag<Q> f;
+    f.hi = *reinterpret_cast<const bf16x8*>(hi + r * ld + k);
+    if constexpr (Q == P_BF16X3) f.lo = *reinterpret_cast<const bf16x8*>(lo + r * ld + k);
+    return f;
+  }
+};
+
+// LDS bytes and carving of an R x K operand tile (16 bytes of padding per row)
+template <int P, int R, int K>
+struct OpTile {
+  static constexpr int LD = K + 8;
+  static constexpr int BYTES = R * LD * (P == P_BF16 ? 2 : 4);
+  __device__ __forceinline__ static Op<P> at(char* base) {
+    if constexpr (P == P_F32) {
+      return Op<P_F32>{reinterpret_cast<float*>(base), LD};
+    } else if constexpr (P == P_BF16) {
+      return Op<P_BF16>{reinterpret_cast<uint16_t*>(base), LD};
+    } else {
+      return Op<P_BF16X3>{reinterpret_cast<uint16_t*>(base), reinterpret_cast<uint16_t*>(base + R * LD * 2), LD};
+    }
+  }
+};
+
+template <int P>
+__device__ __forceinline__ Frag<P> zero_frag() {
+  float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  return make_frag<P>(x);
+}
 
 // ---------------------------------------------------------------- strip product
-// acc[t] += sum over k in [kb, ke) of A(i0 + lane%16, k) * B(k, j0 + 16t + lane%16).
-// kb is a multiple of 32; ke <= K. K is a multiple of 16; when K is 16 the lanes of the
-// upper contraction half feed zeros.
+// acc[t] += sum over k in [kb, ke) of A(i0 + lane%16, k) * B(k, j0 + 16t + lane%16) for the
+// tiles t < tn (wave-uniform; the rest are skipped). kb is a multiple of 32; ke <= K. K is a
+// multiple of 16; when K is 16 the lanes of the upper contraction half feed zeros. A and B are
+// views (converted on use) or Op tiles (pre-converted).
 template <int P, int K, int TN, class AV, class BV>
 __device__ __forceinline__ void strip_mma(f32x4 (&acc)[TN], const AV& A, int i0, const BV& B, int j0,
-                                          int kb = 0, int ke = K) {
+                                          int kb = 0, int ke = K, int tn = TN) {
   const int l = lane();
   const int r = l & 15;
   const int kg = (l >> 4) << 3;
   for (int k = kb; k < ke; k += 32) {
     const bool ok = (K % 32 == 0) || (k + kg < K);
-    float x[8];
-    if (ok) {
-      A.load(i0 + r, k + kg, x);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = 0.f;
-    }
-    const Frag<P> fa = make_frag<P>(x);
+    const Frag<P> fa = ok ? A.template frag<P>(i0 + r, k + kg) : zero_frag<P>();
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
-      float y[8];
-      if (ok) {
-        B.load(j0 + 16 * t + r, k + kg, y);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] = 0.f;
+      if (t < tn) {
+        const Frag<P> fb = ok ? B.template frag<P>(j0 + 16 * t + r, k + kg) : zero_frag<P>();
+        mma<P>(acc[t], fa, fb);
       }
-      mma<P>(acc[t], fa, make_frag<P>(y));
     }
   }
 }

@@ -101,6 +101,7 @@ struct KRowLim {
       for (int e = 0; e < 8; ++e) o[e] = 0.f;
     }
   }
+  GDN_VIEW_FRAG
 };
 
 // ---------------------------------------------------------------- inverse
@@ -124,7 +125,7 @@ __device__ void doubling_level(float* sT, int LT, float* tmp) {
       strip_mma<P, S, 1>(acc, krow(sT + (r0 + S) * LT + r0, LT), 16 * ti, kcol(sT + r0 * LT + r0, LT), 16 * tj);
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr)
-        tmp[p * S * LP + (16 * ti + acc_row(rr)) * LP + 16 * tj + acc_col()] = acc[0][rr];
+        lds_st(tmp + p * S * LP + (16 * ti + acc_row(rr)) * LP + 16 * tj + acc_col(), acc[0][rr]);
     }
     __syncthreads();
     for (int q = w; q < NB * TPS * TPS; q += NW) {
@@ -136,7 +137,7 @@ __device__ void doubling_level(float* sT, int LT, float* tmp) {
                          tri_end<S>(16 * ti));
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr)
-        sT[(r0 + S + 16 * ti + acc_row(rr)) * LT + r0 + 16 * tj + acc_col()] = -acc[0][rr];
+        lds_st(sT + (r0 + S + 16 * ti + acc_row(rr)) * LT + r0 + 16 * tj + acc_col(), -acc[0][rr]);
     }
     __syncthreads();
     doubling_level<C, P, 2 * S>(sT, LT, tmp);
@@ -161,7 +162,7 @@ __device__ void invert_unit_lower(float* sT, int LT, float* tmp) {
       }
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) sT[(base + rb + e) * LT + base + j] = x[e];
+    for (int e = 0; e < 4; ++e) lds_st(sT + (base + rb + e) * LT + base + j, x[e]);
   }
   __syncthreads();
   doubling_level<C, P, 16>(sT, LT, tmp);
@@ -312,19 +313,60 @@ __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
   }
 }
 
+// ---------------------------------------------------------------- operand staging
+// fp32 global R x K tile (row stride ldg) into an operand tile as stored: op(r, k) = g[r][k] * rs[r]
+template <int R, int K, int NT, int P>
+__device__ __forceinline__ void stage_rows(const Op<P>& op, const float* g, int ldg, const float* rs = nullptr) {
+  constexpr int V = K / 4;
+  for (int idx = threadIdx.x; idx < R * V; idx += NT) {
+    const int r = idx / V, c = 4 * (idx % V);
+    const float4 x = *reinterpret_cast<const float4*>(g + (size_t)r * ldg + c);
+    const float f = rs ? rs[r] : 1.f;
+    op.put(r, c, x.x * f);
+    op.put(r, c + 1, x.y * f);
+    op.put(r, c + 2, x.z * f);
+    op.put(r, c + 3, x.w * f);
+  }
+}
+// ... transposed: op(c, r) = g[r][c] * ks[r] * cst (the source rows become the contraction index)
+template <int R, int K, int NT, int P>
+__device__ __forceinline__ void stage_cols(const Op<P>& op, const float* g, int ldg, const float* ks = nullptr,
+                                           float cst = 1.f) {
+  constexpr int V = K / 4;
+  for (int idx = threadIdx.x; idx < R * V; idx += NT) {
+    const int r = idx / V, c = 4 * (idx % V);
+    const float4 x = *reinterpret_cast<const float4*>(g + (size_t)r * ldg + c);
+    const float f = (ks ? ks[r] : 1.f) * cst;
+    op.put(c, r, x.x * f);
+    op.put(c + 1, r, x.y * f);
+    op.put(c + 2, r, x.z * f);
+    op.put(c + 3, r, x.w * f);
+  }
+}
+// ... transposed from a token-major activation (rows past `rows` read as 0)
+template <int R, int K, int NT, int P, class T>
+__device__ __forceinline__ void stage_cols_io(const Op<P>& op, const T* g, int ldg, int rows) {
+  for (int idx = threadIdx.x; idx < R * K; idx += NT) {
+    const int r = idx / K, c = idx % K;
+    op.put(c, r, r < rows ? ldf(g + (size_t)r * ldg + c) : 0.f);
+  }
+}
+
 // ---------------------------------------------------------------- k_chunk
 // grid B*H*N, C/16 waves (one 16-row strip each). MODE 0 (forward): writes w and u.
 // MODE 1 (backward recompute): writes T and v_new = u - w S_before.
+// LDS: T in fp32 (the inverse runs in place), one operand region reused for k, kbe^T, (v beta)^T
+// and S^T (the doubling scratch borrows it too).
 template <int C, int D, int PI, int PS, int MODE>
 __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
   constexpr int NT = C * 4;
-  constexpr int LT = (C > D ? C : D) + 4;
-  constexpr int LX = D + 4;
-  constexpr int XR = C > D ? C : D;
-  constexpr int TMP = C * (C / 2 + 4) / 2;  // doubling scratch, shared with the operand tile
-  constexpr int SX = XR * LX > TMP ? XR * LX : TMP;
+  constexpr int M = C > D ? C : D;
+  constexpr int LT = M + 4;
+  using TB = OpTile<PI, M, M>;
+  constexpr int TMP = C * (C / 2 + 4) / 2;
+  constexpr int RB = TB::BYTES > TMP * 4 ? TB::BYTES : TMP * 4;
   __shared__ float sT[C * LT];
-  __shared__ float sX[SX];
+  __shared__ __align__(16) char sB[RB];
   __shared__ Ctx<C> cx;
   const int id = blockIdx.x;
   const int n = id % A.N, bh = id / A.N, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
@@ -332,68 +374,56 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
   const float* kg = A.kn + hoff(A, b, hk, A.Hk, n, C, D);
   const float* vg = A.vv + hoff(A, b, h, A.H, n, C, D);
   const size_t off = hoff(A, b, h, A.H, n, C, D);
-  const int i0 = 16 * wave();
-  {  // L = strict(beta_i (k k^T)_ij D_ij)
+  const int w = wave(), i0 = 16 * w;
+  const Op<PI> ob = TB::at(sB);
+  stage_rows<C, D, NT>(ob, kg, D);
+  __syncthreads();
+  {  // L = strict(beta_i (k k^T)_ij D_ij): tiles on and below the diagonal only
     f32x4 acc[C / 16];
     zero(acc);
-    strip_mma<PI, D, C / 16>(acc, krow(kg, D), i0, krow(kg, D), 0);
+    strip_mma<PI, D, C / 16>(acc, ob, i0, ob, 0, 0, D, w + 1);
 #pragma unroll
     for (int t = 0; t < C / 16; ++t)
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-        sT[i * LT + j] = (i > j) ? cx.beta[i] * acc[t][rr] * decay(cx, i, j) : 0.f;
+        lds_st(sT + i * LT + j, (i > j && t <= w) ? cx.beta[i] * acc[t][rr] * decay(cx, i, j) : 0.f);
       }
   }
   __syncthreads();
-  invert_unit_lower<C, PI>(sT, LT, sX);
+  invert_unit_lower<C, PI>(sT, LT, reinterpret_cast<float*>(sB));
+  f32x4 aw[D / 16], au[D / 16];
+  zero(aw);
+  zero(au);
+  stage_cols<C, D, NT>(ob, kg, D, cx.bg);  // kbe^T
+  __syncthreads();
+  strip_mma<PI, C, D / 16>(aw, krow(sT, LT), i0, ob, 0, 0, tri_end<C>(i0));
+  __syncthreads();
+  stage_cols<C, D, NT>(ob, vg, D, cx.beta);  // (v beta)^T
+  __syncthreads();
+  strip_mma<PI, C, D / 16>(au, krow(sT, LT), i0, ob, 0, 0, tri_end<C>(i0));
   if constexpr (MODE == 0) {
-    load_tile<C, D, NT>(sX, LX, kg);
-    __syncthreads();
-    {
-      f32x4 acc[D / 16];
-      zero(acc);
-      strip_mma<PI, C, D / 16>(acc, krow(sT, LT), i0, scale_k(kcol(sX, LX), cx.bg), 0, 0, tri_end<C>(i0));
 #pragma unroll
-      for (int t = 0; t < D / 16; ++t)
+    for (int t = 0; t < D / 16; ++t)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) A.ww[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = acc[t][rr];
-    }
-    __syncthreads();
-    load_tile<C, D, NT>(sX, LX, vg);
-    __syncthreads();
-    {
-      f32x4 acc[D / 16];
-      zero(acc);
-      strip_mma<PI, C, D / 16>(acc, krow(sT, LT), i0, scale_k(kcol(sX, LX), cx.beta), 0, 0, tri_end<C>(i0));
-#pragma unroll
-      for (int t = 0; t < D / 16; ++t)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) A.uu[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = acc[t][rr];
-    }
+      for (int rr = 0; rr < 4; ++rr) {
+        const size_t g = off + (size_t)(i0 + acc_row(rr)) * D + 16 * t + acc_col();
+        A.ww[g] = aw[t][rr];
+        A.uu[g] = au[t][rr];
+      }
   } else {
     float* tg = A.tt + ((size_t)bh * A.N + n) * C * C;
     for (int idx = threadIdx.x; idx < C * C; idx += NT) tg[idx] = sT[(idx / C) * LT + idx % C];
-    load_tile<C, D, NT>(sX, LX, kg);
-    __syncthreads();
-    f32x4 aw[D / 16], au[D / 16];
-    zero(aw);
-    zero(au);
-    strip_mma<PI, C, D / 16>(aw, krow(sT, LT), i0, scale_k(kcol(sX, LX), cx.bg), 0, 0, tri_end<C>(i0));
-    __syncthreads();
-    load_tile<C, D, NT>(sX, LX, vg);
-    __syncthreads();
-    strip_mma<PI, C, D / 16>(au, krow(sT, LT), i0, scale_k(kcol(sX, LX), cx.beta), 0, 0, tri_end<C>(i0));
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < D / 16; ++t)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) sT[(i0 + acc_row(rr)) * LT + 16 * t + acc_col()] = aw[t][rr];
-    load_tile<D, D, NT>(sX, LX, A.states + ((size_t)bh * A.N + n) * D * D);
+      for (int rr = 0; rr < 4; ++rr) lds_st(sT + (i0 + acc_row(rr)) * LT + 16 * t + acc_col(), aw[t][rr]);
+    stage_cols<D, D, NT>(ob, A.states + ((size_t)bh * A.N + n) * D * D, D);  // S^T
     __syncthreads();
     f32x4 ws[D / 16];
     zero(ws);
-    strip_mma<PS, D, D / 16>(ws, krow(sT, LT), i0, kcol(sX, LX), 0);
+    strip_mma<PS, D, D / 16>(ws, krow(sT, LT), i0, ob, 0);
 #pragma unroll
     for (int t = 0; t < D / 16; ++t)
 #pragma unroll
@@ -404,15 +434,19 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
 
 // ---------------------------------------------------------------- k_scan_fwd
 // grid B*H*(D/DVT) (XCD-remapped), max(C,D)/16 waves. The state tile S [D x DVT] lives in
-// the accumulators of waves < D/16; chunks in order (pallas_tpu_v2.py:254-269).
+// the accumulators of waves < D/16; chunks in order (pallas_tpu_v2.py:254-269). Operands of
+// each chunk step are staged once: S^T, (k kws)^T and v_new^T.
 template <int C, int D, int DVT, int PI, int PS>
 __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
   constexpr int NT = (C > D ? C : D) * 4;
-  constexpr int LS = DVT + 4, LK = D + 4;
-  __shared__ float sS[D * LS];
-  __shared__ float sV[C * LS];
-  __shared__ float sK[C * LK];
+  using TS = OpTile<PI, DVT, D>;   // S^T: B(k=dk, j) = S[dk][j]
+  using TK = OpTile<PI, D, C>;     // (k kws)^T: A(i=dk, k=c)
+  using TV = OpTile<PI, DVT, C>;   // v_new^T: B(k=c, j)
+  __shared__ __align__(16) char sS[TS::BYTES];
+  __shared__ __align__(16) char sK[TK::BYTES];
+  __shared__ __align__(16) char sV[TV::BYTES];
   __shared__ Ctx<C> cx;
+  const Op<PI> os = TS::at(sS), ok = TK::at(sK), ov = TV::at(sV);
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int tile = id % A.ntiles, bh = id / A.ntiles, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
   const int j0 = tile * DVT;
@@ -427,18 +461,18 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
-          sS[i * LS + j] = accS[t][rr];
+          os.put(j, i, accS[t][rr]);
           sg[i * D + j0 + j] = accS[t][rr];
         }
     }
     load_ctx<C, NT>(cx, A, b, h, n);
-    load_tile<C, D, NT>(sK, LK, A.kn + hoff(A, b, hk, A.Hk, n, C, D));
+    stage_cols<C, D, NT>(ok, A.kn + hoff(A, b, hk, A.Hk, n, C, D), D, cx.kws);
     __syncthreads();
     const size_t off = hoff(A, b, h, A.H, n, C, D);
     if (w < C / 16) {  // v_new = u - w S
       f32x4 acc[DVT / 16];
       zero(acc);
-      strip_mma<PS, D, DVT / 16>(acc, krow(A.ww + off, D), 16 * w, kcol(sS, LS), 0);
+      strip_mma<PS, D, DVT / 16>(acc, krow(A.ww + off, D), 16 * w, os, 0);
 #pragma unroll
       for (int t = 0; t < DVT / 16; ++t)
 #pragma unroll
@@ -446,7 +480,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
           const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
           const size_t g = off + (size_t)i * D + j0 + j;
           const float vn = A.uu[g] - acc[t][rr];
-          sV[i * LS + j] = vn;
+          ov.put(j, i, vn);
           A.vnew[g] = vn;
         }
     }
@@ -454,7 +488,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
     if (w < D / 16) {  // S = carry S + k_write^T v_new
 #pragma unroll
       for (int t = 0; t < DVT / 16; ++t) accS[t] *= cx.carry;
-      strip_mma<PI, C, DVT / 16>(accS, scale_k(kcol(sK, LK), cx.kws), 16 * w, kcol(sV, LS), 0);
+      strip_mma<PI, C, DVT / 16>(accS, ok, 16 * w, ov, 0);
     }
     __syncthreads();
   }
@@ -465,39 +499,44 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
 template <int C, int D, int PI, int PS, class TIO>
 __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
   constexpr int NT = C * 4;
-  constexpr int LI = C + 4, LX = D + 4;
-  constexpr int XR = C > D ? C : D;
+  constexpr int LI = C + 4;
+  constexpr int M = C > D ? C : D;
+  using TB = OpTile<PI, M, M>;
   __shared__ float sI[C * LI];
-  __shared__ float sX[XR * LX];
+  __shared__ __align__(16) char sB[TB::BYTES];
   __shared__ Ctx<C> cx;
+  const Op<PI> ob = TB::at(sB);
   const int id = blockIdx.x;
   const int n = id % A.N, bh = id / A.N, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
   load_ctx<C, NT>(cx, A, b, h, n);
   const float* qg = A.qn + hoff(A, b, hk, A.Hk, n, C, D);
   const float* kg = A.kn + hoff(A, b, hk, A.Hk, n, C, D);
   const size_t off = hoff(A, b, h, A.H, n, C, D);
-  const int i0 = 16 * wave();
+  const int w = wave(), i0 = 16 * w;
+  stage_rows<C, D, NT>(ob, kg, D);  // k: B(d, j) = k[j][d]
+  __syncthreads();
   {
     f32x4 acc[C / 16];
     zero(acc);
-    strip_mma<PI, D, C / 16>(acc, krow(qg, D), i0, krow(kg, D), 0);
+    strip_mma<PI, D, C / 16>(acc, krow(qg, D), i0, ob, 0, 0, D, w + 1);
 #pragma unroll
     for (int t = 0; t < C / 16; ++t)
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-        sI[i * LI + j] = acc[t][rr] * decay(cx, i, j);
+        lds_st(sI + i * LI + j, t <= w ? acc[t][rr] * decay(cx, i, j) : 0.f);
       }
   }
-  load_tile<C, D, NT>(sX, LX, A.vnew + off);
+  __syncthreads();
+  stage_cols<C, D, NT>(ob, A.vnew + off, D);  // v_new^T
   __syncthreads();
   f32x4 o[D / 16];
   zero(o);
-  strip_mma<PI, C, D / 16>(o, krow(sI, LI), i0, kcol(sX, LX), 0, 0, tri_end<C>(i0));
+  strip_mma<PI, C, D / 16>(o, krow(sI, LI), i0, ob, 0, 0, tri_end<C>(i0));
   __syncthreads();
-  load_tile<D, D, NT>(sX, LX, A.states + ((size_t)bh * A.N + n) * D * D);
+  stage_cols<D, D, NT>(ob, A.states + ((size_t)bh * A.N + n) * D * D, D);  // S^T
   __syncthreads();
-  strip_mma<PS, D, D / 16>(o, scale_r(krow(qg, D), cx.grow), i0, kcol(sX, LX), 0);
+  strip_mma<PS, D, D / 16>(o, scale_r(krow(qg, D), cx.grow), i0, ob, 0);
   TIO* out = reinterpret_cast<TIO*>(A.out);
 #pragma unroll
   for (int t = 0; t < D / 16; ++t)
@@ -513,56 +552,59 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
 template <int C, int D, int PI, class TIO>
 __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
   constexpr int NT = C * 4;
-  constexpr int LA = C + 4, LX = D + 4;
+  constexpr int LA = C + 4;
+  constexpr int M = C > D ? C : D;
+  using TB = OpTile<PI, M, M>;
   __shared__ float sA[C * LA];
-  __shared__ float sX[C * LX];
+  __shared__ __align__(16) char sB[TB::BYTES];
   __shared__ Ctx<C> cx;
+  const Op<PI> ob = TB::at(sB);
   const int id = blockIdx.x;
   const int n = id % A.N, bh = id / A.N, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
   load_ctx<C, NT>(cx, A, b, h, n);
   const float* qg = A.qn + hoff(A, b, hk, A.Hk, n, C, D);
   const float* kg = A.kn + hoff(A, b, hk, A.Hk, n, C, D);
   const size_t off = hoff(A, b, h, A.H, n, C, D);
-  const int i0 = 16 * wave();
+  const int w = wave(), i0 = 16 * w;
+  stage_rows<C, D, NT>(ob, kg, D);
+  __syncthreads();
   {
     f32x4 acc[C / 16];
     zero(acc);
-    strip_mma<PI, D, C / 16>(acc, krow(qg, D), i0, krow(kg, D), 0);
+    strip_mma<PI, D, C / 16>(acc, krow(qg, D), i0, ob, 0, 0, D, w + 1);
 #pragma unroll
     for (int t = 0; t < C / 16; ++t)
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-        sA[i * LA + j] = acc[t][rr] * decay(cx, i, j);
+        lds_st(sA + i * LA + j, t <= w ? acc[t][rr] * decay(cx, i, j) : 0.f);
       }
   }
+  __syncthreads();
   const TIO* dout = reinterpret_cast<const TIO*>(A.d_out);
-  for (int idx = threadIdx.x; idx < C * D; idx += NT) {
-    const int r = idx / D, c = idx % D, tok = n * C + r;
-    sX[r * LX + c] = tok < A.T ? ldf(dout + (((size_t)b * A.T + tok) * A.H + h) * D + c) : 0.f;
-  }
+  stage_cols_io<C, D, NT>(ob, dout + (((size_t)b * A.T + (size_t)n * C) * A.H + h) * D, A.H * D, A.T - n * C);
   __syncthreads();
   f32x4 acc[D / 16];
   zero(acc);
-  strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, kcol(sX, LX), 0, tri_begin(i0), C);  // intra^T do
+  strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // intra^T do
   __syncthreads();
   load_tile<C, C, NT>(sA, LA, A.tt + ((size_t)bh * A.N + n) * C * C);
 #pragma unroll
   for (int t = 0; t < D / 16; ++t)
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) sX[(i0 + acc_row(rr)) * LX + 16 * t + acc_col()] = acc[t][rr];
+    for (int rr = 0; rr < 4; ++rr) ob.put(16 * t + acc_col(), i0 + acc_row(rr), acc[t][rr]);  // dv_loc^T
   __syncthreads();
   zero(acc);
-  strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, kcol(sX, LX), 0, tri_begin(i0), C);  // T^T dv_loc
+  strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // T^T dv_loc
 #pragma unroll
   for (int t = 0; t < D / 16; ++t)
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) A.xl[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = acc[t][rr];
   __syncthreads();
-  load_tile<C, D, NT>(sX, LX, kg);
+  stage_cols<C, D, NT>(ob, kg, D, cx.kws);  // k_write^T
   __syncthreads();
   zero(acc);
-  strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, scale_k(kcol(sX, LX), cx.kws), 0, tri_begin(i0), C);  // T^T k_write
+  strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // T^T k_write
 #pragma unroll
   for (int t = 0; t < D / 16; ++t)
 #pragma unroll
@@ -577,13 +619,16 @@ template <int C, int D, int DVT, int PI, int PS, class TIO>
 __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
   constexpr int NT = (C > D ? C : D) * 4;
   constexpr int NW = NT / 64;
-  constexpr int LS = DVT + 4, LK = D + 4;
-  __shared__ float sG[D * LS];
-  __shared__ float sXt[C * LS];
-  __shared__ float sDo[C * LS];
-  __shared__ float sQK[C * LK];
+  using TG_ = OpTile<PI, DVT, D>;  // G^T: B(k=dk, j)
+  using TQ = OpTile<PI, D, C>;     // (q grow)^T, then (-k beta grow)^T: A(i=dk, k=c)
+  using TD = OpTile<PI, DVT, C>;   // do^T and X^T: B(k=c, j)
+  __shared__ __align__(16) char sG[TG_::BYTES];
+  __shared__ __align__(16) char sQ[TQ::BYTES];
+  __shared__ __align__(16) char sDo[TD::BYTES];
+  __shared__ __align__(16) char sX[TD::BYTES];
   __shared__ float red[NW];
   __shared__ Ctx<C> cx;
+  const Op<PI> og = TG_::at(sG), oq = TQ::at(sQ), odo = TD::at(sDo), ox = TD::at(sX);
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int tile = id % A.ntiles, bh = id / A.ntiles, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
   const int j0 = tile * DVT;
@@ -602,7 +647,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
         for (int rr = 0; rr < 4; ++rr) {
           const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
           const float g = accG[t][rr];
-          sG[i * LS + j] = g;
+          og.put(j, i, g);
           gdst[i * D + j0 + j] = g;
           if (n + 1 < A.N) part += g * snext[i * D + j0 + j];
         }
@@ -615,17 +660,15 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
       for (int q = 0; q < NW; ++q) s += red[q];
       A.gsp[((size_t)bh * A.N + n) * A.ntiles + tile] = s;
     }
-    for (int idx = threadIdx.x; idx < C * DVT; idx += NT) {
-      const int r = idx / DVT, c = idx % DVT, tok = n * C + r;
-      sDo[r * LS + c] = tok < A.T ? ldf(dout + (((size_t)b * A.T + tok) * A.H + h) * D + j0 + c) : 0.f;
-    }
-    load_tile<C, D, NT>(sQK, LK, A.qn + hoff(A, b, hk, A.Hk, n, C, D));
+    stage_cols_io<C, DVT, NT>(odo, dout + (((size_t)b * A.T + (size_t)n * C) * A.H + h) * D + j0, A.H * D,
+                              A.T - n * C);
+    stage_cols<C, D, NT>(oq, A.qn + hoff(A, b, hk, A.Hk, n, C, D), D, cx.grow);
     __syncthreads();
     const size_t off = hoff(A, b, h, A.H, n, C, D);
     if (w < C / 16) {  // X = X_loc + Kt G
       f32x4 acc[DVT / 16];
       zero(acc);
-      strip_mma<PS, D, DVT / 16>(acc, krow(A.kt + off, D), 16 * w, kcol(sG, LS), 0);
+      strip_mma<PS, D, DVT / 16>(acc, krow(A.kt + off, D), 16 * w, og, 0);
 #pragma unroll
       for (int t = 0; t < DVT / 16; ++t)
 #pragma unroll
@@ -633,21 +676,20 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
           const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
           const size_t g = off + (size_t)i * D + j0 + j;
           const float xv = A.xl[g] + acc[t][rr];
-          sXt[i * LS + j] = xv;
+          ox.put(j, i, xv);
           A.xl[g] = xv;
         }
     }
-    __syncthreads();
     if (w < D / 16) {  // G = carry G + q_read^T do
 #pragma unroll
       for (int t = 0; t < DVT / 16; ++t) accG[t] *= cx.carry;
-      strip_mma<PI, C, DVT / 16>(accG, scale_k(kcol(sQK, LK), cx.grow), 16 * w, kcol(sDo, LS), 0);
+      strip_mma<PI, C, DVT / 16>(accG, oq, 16 * w, odo, 0);
     }
     __syncthreads();
-    load_tile<C, D, NT>(sQK, LK, A.kn + hoff(A, b, hk, A.Hk, n, C, D));
+    stage_cols<C, D, NT>(oq, A.kn + hoff(A, b, hk, A.Hk, n, C, D), D, cx.bg, -1.f);
     __syncthreads();
     if (w < D / 16)  // ... - kbe^T X
-      strip_mma<PI, C, DVT / 16>(accG, scale_k(kcol(sQK, LK), cx.bg, -1.f), 16 * w, kcol(sXt, LS), 0);
+      strip_mma<PI, C, DVT / 16>(accG, oq, 16 * w, ox, 0);
     __syncthreads();
   }
 }
@@ -659,13 +701,18 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
 //   dk  = dk' + beta dkb    d beta = rows(dkb, k) + rows(X, v)
 //   d gamma = rows(beta k, dkb) + rows(q, dq) - rows(k, dk')  (+ <G_after, S_after> at the
 //   chunk's last token) -- pallas_tpu_v2.py:272-318 regrouped by shared operands.
+// LDS: m1, then m2, in fp32 (read by rows and by columns); one operand region reused for v_new,
+// k^T, q^T, S and G.
 template <int C, int D, int PI, int PS, class TIO>
 __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
   constexpr int NT = C * 4;
-  constexpr int LA = C + 4, LB = D + 4;
+  constexpr int LA = C + 4;
+  constexpr int M = C > D ? C : D;
+  using TB = OpTile<PI, M, M>;
   __shared__ float sA[C * LA];
-  __shared__ float sB[C * LB];
+  __shared__ __align__(16) char sB[TB::BYTES];
   __shared__ Ctx<C> cx;
+  const Op<PI> ob = TB::at(sB);
   const int id = blockIdx.x;
   const int n = id % A.N, bh = id / A.N, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
   load_ctx<C, NT>(cx, A, b, h, n);
@@ -679,49 +726,60 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
   const float* Gg = A.gg + ((size_t)bh * A.N + n) * D * D;
   const TIO* dout = reinterpret_cast<const TIO*>(A.d_out);
   const KRowLim<TIO> dov{dout + (((size_t)b * A.T + (size_t)n * C) * A.H + h) * D, A.H * D, A.T - n * C};
-  const int i0 = 16 * wave();
-  {  // m1
+  const int w = wave(), i0 = 16 * w;
+  stage_rows<C, D, NT>(ob, vng, D);  // v_new: B(dv, j) = v_new[j][dv]
+  __syncthreads();
+  f32x4 m2[C / 16];
+  {  // m1 -> LDS, m2 -> registers
     f32x4 acc[C / 16];
     zero(acc);
-    strip_mma<PI, D, C / 16>(acc, krow(xg, D), i0, krow(vng, D), 0);
+    strip_mma<PI, D, C / 16>(acc, krow(xg, D), i0, ob, 0, 0, D, w + 1);
 #pragma unroll
     for (int t = 0; t < C / 16; ++t)
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-        sA[i * LA + j] = (i > j) ? -acc[t][rr] * decay(cx, i, j) : 0.f;
+        lds_st(sA + i * LA + j, (i > j && t <= w) ? -acc[t][rr] * decay(cx, i, j) : 0.f);
+      }
+    zero(m2);
+    strip_mma<PI, D, C / 16>(m2, dov, i0, ob, 0, 0, D, w + 1);
+#pragma unroll
+    for (int t = 0; t < C / 16; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
+        m2[t][rr] = t <= w ? m2[t][rr] * decay(cx, i, j) : 0.f;
       }
   }
-  load_tile<C, D, NT>(sB, LB, kg);
+  __syncthreads();
+  stage_cols<C, D, NT>(ob, kg, D);  // k^T: B(c, j) = k[c][j]
   __syncthreads();
   f32x4 dkb[D / 16], dk[D / 16], dq[D / 16];
   zero(dkb);
   zero(dk);
   zero(dq);
-  strip_mma<PI, C, D / 16>(dkb, krow(sA, LA), i0, kcol(sB, LB), 0, 0, tri_end<C>(i0));
-  strip_mma<PS, D, D / 16>(dkb, scale_r(krow(xg, D), cx.grow, -1.f), i0, krow(Sg, D), 0);
-  strip_mma<PI, C, D / 16>(dk, kcol(sA, LA), i0, scale_k(kcol(sB, LB), cx.beta), 0, tri_begin(i0), C);
+  strip_mma<PI, C, D / 16>(dkb, krow(sA, LA), i0, ob, 0, 0, tri_end<C>(i0));                          // m1 k
+  strip_mma<PI, C, D / 16>(dk, scale_k(kcol(sA, LA), cx.beta), i0, ob, 0, tri_begin(i0), C);          // m1^T beta k
   __syncthreads();
-  {  // m2
-    f32x4 acc[C / 16];
-    zero(acc);
-    strip_mma<PI, D, C / 16>(acc, dov, i0, krow(vng, D), 0);
 #pragma unroll
-    for (int t = 0; t < C / 16; ++t)
+  for (int t = 0; t < C / 16; ++t)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-        sA[i * LA + j] = acc[t][rr] * decay(cx, i, j);
-      }
-  }
+    for (int rr = 0; rr < 4; ++rr) lds_st(sA + (i0 + acc_row(rr)) * LA + 16 * t + acc_col(), m2[t][rr]);
   __syncthreads();
-  strip_mma<PI, C, D / 16>(dq, krow(sA, LA), i0, kcol(sB, LB), 0, 0, tri_end<C>(i0));
-  strip_mma<PS, D, D / 16>(dq, scale_r(dov, cx.grow), i0, krow(Sg, D), 0);
+  strip_mma<PI, C, D / 16>(dq, krow(sA, LA), i0, ob, 0, 0, tri_end<C>(i0));                           // m2 k
   __syncthreads();
-  load_tile<C, D, NT>(sB, LB, qg);
+  stage_cols<C, D, NT>(ob, qg, D);  // q^T
   __syncthreads();
-  strip_mma<PI, C, D / 16>(dk, kcol(sA, LA), i0, kcol(sB, LB), 0, tri_begin(i0), C);
-  strip_mma<PS, D, D / 16>(dk, scale_r(krow(vng, D), cx.kws), i0, krow(Gg, D), 0);
+  strip_mma<PI, C, D / 16>(dk, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);                            // m2^T q
+  __syncthreads();
+  stage_rows<D, D, NT>(ob, Sg, D);  // S: B(dv, j=dk) = S[dk][dv]
+  __syncthreads();
+  strip_mma<PS, D, D / 16>(dkb, scale_r(krow(xg, D), cx.grow, -1.f), i0, ob, 0);                       // -(grow X) S^T
+  strip_mma<PS, D, D / 16>(dq, scale_r(dov, cx.grow), i0, ob, 0);                                      // (grow do) S^T
+  __syncthreads();
+  stage_rows<D, D, NT>(ob, Gg, D);  // G
+  __syncthreads();
+  strip_mma<PS, D, D / 16>(dk, scale_r(krow(vng, D), cx.kws), i0, ob, 0);                             // (kws v_new) G^T
   // epilogue: row sums and the per-value-head dq, dk
   float r2[4] = {0.f, 0.f, 0.f, 0.f}, r3[4] = {0.f, 0.f, 0.f, 0.f}, r4[4] = {0.f, 0.f, 0.f, 0.f};
   float rxv[4] = {0.f, 0.f, 0.f, 0.f};
@@ -730,7 +788,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-      const float kv = kg[i * D + j], qv = sB[i * LB + j];
+      const float kv = kg[i * D + j], qv = qg[i * D + j];
       r4[rr] += dkb[t][rr] * kv;
       r2[rr] += qv * dq[t][rr];
       r3[rr] += kv * dk[t][rr];
