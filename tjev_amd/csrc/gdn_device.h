@@ -175,6 +175,13 @@ template <class V> __device__ __forceinline__ ScaleKF<V> scale_k(V v, const floa
 
 
 // ---------------------------------------------------------------- pre-converted LDS operands
+// two values as bf16 (round to nearest even) in one 32-bit word, the first in the low half
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)a) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)b) << 16);
+}
+// v - bf16(v): the part a bf16 pass drops (exact in fp32)
+__device__ __forceinline__ float lo_part(float v) { return v - (float)(__bf16)v; }
+
 // Op<P>: an operand tile in LDS, converted once when it is staged. Element (r, k) sits at
 // r*ld + k with the contraction index k contiguous (r: the M index of an A operand, the N index
 // of a B operand), so a fragment is one 16-byte read per plane. P_F32 keeps fp32; P_BF16 one bf16
@@ -186,6 +193,14 @@ struct Op<P_F32> {
   float* p;
   int ld;
   __device__ __forceinline__ void put(int r, int k, float v) const { lds_st(p + r * ld + k, v); }
+  // two consecutive k (k even), four consecutive k (k a multiple of 4)
+  __device__ __forceinline__ void put2(int r, int k, float v0, float v1) const {
+    *reinterpret_cast<float2*>(p + r * ld + k) = make_float2(v0, v1);
+    asm volatile("" ::: "memory");
+  }
+  __device__ __forceinline__ void put4(int r, int k, float v0, float v1, float v2, float v3) const {
+    *reinterpret_cast<float4*>(p + r * ld + k) = make_float4(v0, v1, v2, v3);
+  }
   template <int Q>
   __device__ __forceinline__ Frag<Q> frag(int r, int k) const {
     static_assert(Q == P_F32, "an fp32 tile feeds fp32 products");
@@ -204,6 +219,12 @@ struct Op<P_BF16> {
   __device__ __forceinline__ void put(int r, int k, float v) const {
     hi[r * ld + k] = __builtin_bit_cast(uint16_t, (__bf16)v);
   }
+  __device__ __forceinline__ void put2(int r, int k, float v0, float v1) const {
+    *reinterpret_cast<uint32_t*>(hi + r * ld + k) = pack2(v0, v1);
+  }
+  __device__ __forceinline__ void put4(int r, int k, float v0, float v1, float v2, float v3) const {
+    *reinterpret_cast<uint2*>(hi + r * ld + k) = make_uint2(pack2(v0, v1), pack2(v2, v3));
+  }
   template <int Q>
   __device__ __forceinline__ Frag<Q> frag(int r, int k) const {
     static_assert(Q == P_BF16, "a bf16 tile feeds one-pass products");
@@ -221,6 +242,15 @@ struct Op<P_BF16X3> {
     const __bf16 h = (__bf16)v;
     hi[r * ld + k] = __builtin_bit_cast(uint16_t, h);
     lo[r * ld + k] = __builtin_bit_cast(uint16_t, (__bf16)(v - (float)h));
+  }
+  __device__ __forceinline__ void put2(int r, int k, float v0, float v1) const {
+    *reinterpret_cast<uint32_t*>(hi + r * ld + k) = pack2(v0, v1);
+    *reinterpret_cast<uint32_t*>(lo + r * ld + k) = pack2(lo_part(v0), lo_part(v1));
+  }
+  __device__ __forceinline__ void put4(int r, int k, float v0, float v1, float v2, float v3) const {
+    *reinterpret_cast<uint2*>(hi + r * ld + k) = make_uint2(pack2(v0, v1), pack2(v2, v3));
+    *reinterpret_cast<uint2*>(lo + r * ld + k) =
+        make_uint2(pack2(lo_part(v0), lo_part(v1)), pack2(lo_part(v2), lo_part(v3)));
   }
   template <int Q>
   __device__ __forceinline__ Frag<Q> frag(int r, int k) const {
@@ -273,6 +303,34 @@ __device__ __forceinline__ void strip_mma(f32x4 (&acc)[TN], const AV& A, int i0,
       if (t < tn) {
         const Frag<P> fb = ok ? B.template frag<P>(j0 + 16 * t + r, k + kg) : zero_frag<P>();
         mma<P>(acc[t], fa, fb);
+      }
+    }
+  }
+}
+
+// The same over the full contraction [0, K), every A fragment of the strip fetched first: for A
+// operands read from global memory, whose loads then overlap instead of each k-step waiting.
+template <int P, int K, int TN, class AV, class BV>
+__device__ __forceinline__ void strip_mma_full(f32x4 (&acc)[TN], const AV& A, int i0, const BV& B, int j0,
+                                               int tn = TN) {
+  constexpr int KS = (K + 31) / 32;
+  const int l = lane();
+  const int r = l & 15;
+  const int kg = (l >> 4) << 3;
+  Frag<P> fa[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const bool ok = (K % 32 == 0) || (32 * s + kg < K);
+    fa[s] = ok ? A.template frag<P>(i0 + r, 32 * s + kg) : zero_frag<P>();
+  }
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const bool ok = (K % 32 == 0) || (32 * s + kg < K);
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      if (t < tn) {
+        const Frag<P> fb = ok ? B.template frag<P>(j0 + 16 * t + r, 32 * s + kg) : zero_frag<P>();
+        mma<P>(acc[t], fa[s], fb);
       }
     }
   }

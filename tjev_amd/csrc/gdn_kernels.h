@@ -77,15 +77,9 @@ __device__ __forceinline__ float decay(const Ctx<C>& cx, int i, int j) {
   return (i >= j && cx.seg[i] == cx.seg[j]) ? expf(gdiff(cx, i, j)) : 0.f;
 }
 
-// rows x D fp32 tile from global (row stride D) into LDS (row stride LD)
+// R x D fp32 tile from global (row stride D) into LDS (row stride LD), every load issued first
 template <int R, int D, int NT>
-__device__ __forceinline__ void load_tile(float* s, int LD, const float* g) {
-  constexpr int V = D / 4;
-  for (int idx = threadIdx.x; idx < R * V; idx += NT) {
-    const int r = idx / V, c = idx % V;
-    *reinterpret_cast<float4*>(s + r * LD + 4 * c) = reinterpret_cast<const float4*>(g)[idx];
-  }
-}
+__device__ __forceinline__ void load_tile(float* s, int LD, const float* g);
 
 // row view of a token-major activation tensor with rows past the valid count read as 0
 template <class T>
@@ -314,42 +308,149 @@ __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
 }
 
 // ---------------------------------------------------------------- operand staging
-// fp32 global R x K tile (row stride ldg) into an operand tile as stored: op(r, k) = g[r][k] * rs[r]
+// An R x K fp32 tile held in registers, 4 consecutive values per slot: fetch() issues every
+// global load of the tile at once (one memory round trip), the put_* calls then write it to an
+// operand tile as stored (rows) or transposed (cols), scaled.
+template <int R, int K, int NT>
+struct Regs {
+  static constexpr int V = K / 4;
+  static constexpr int IT = (R * V + NT - 1) / NT;
+  float4 v[IT];
+  __device__ __forceinline__ static bool live(int it) {
+    return (R * V) % NT == 0 || (int)threadIdx.x + it * NT < R * V;
+  }
+  __device__ __forceinline__ void fetch(const float* g, int ldg) {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int idx = threadIdx.x + it * NT;
+      if (live(it)) v[it] = *reinterpret_cast<const float4*>(g + (size_t)(idx / V) * ldg + 4 * (idx % V));
+    }
+  }
+  // op(r, k) = g[r][k] * rs[r] * cst
+  template <int P>
+  __device__ __forceinline__ void put_rows(const Op<P>& op, const float* rs = nullptr, float cst = 1.f) const {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      if (!live(it)) continue;
+      const int idx = threadIdx.x + it * NT, r = idx / V, c = 4 * (idx % V);
+      const float f = (rs ? rs[r] : 1.f) * cst;
+      op.put4(r, c, v[it].x * f, v[it].y * f, v[it].z * f, v[it].w * f);
+    }
+  }
+  // plain fp32 LDS tile with row stride ld
+  __device__ __forceinline__ void put_lds(float* s, int ld) const {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      if (!live(it)) continue;
+      const int idx = threadIdx.x + it * NT;
+      *reinterpret_cast<float4*>(s + (idx / V) * ld + 4 * (idx % V)) = v[it];
+    }
+  }
+};
+
+// The transposing load: an R x K fp32 tile (R even), each slot two consecutive source rows x 4
+// columns, so that the lanes of a wave hold consecutive row pairs and write the transposed tile
+// op(c, r) = g[r][c] * ks[r] * cst as consecutive 32-bit words. (One element per lane down a
+// column of a padded tile hits only a few LDS banks.)
+template <int R, int K, int NT>
+struct RegsT {
+  static constexpr int RP = R / 2;
+  static constexpr int V = K / 4;
+  static constexpr int IT = (RP * V + NT - 1) / NT;
+  float4 a[IT], b[IT];
+  __device__ __forceinline__ static bool live(int it) {
+    return (RP * V) % NT == 0 || (int)threadIdx.x + it * NT < RP * V;
+  }
+  __device__ __forceinline__ void fetch(const float* g, int ldg) {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int idx = threadIdx.x + it * NT, j = idx % RP, c = 4 * (idx / RP);
+      if (live(it)) {
+        a[it] = *reinterpret_cast<const float4*>(g + (size_t)(2 * j) * ldg + c);
+        b[it] = *reinterpret_cast<const float4*>(g + (size_t)(2 * j + 1) * ldg + c);
+      }
+    }
+  }
+  template <int P>
+  __device__ __forceinline__ void put_cols(const Op<P>& op, const float* ks = nullptr, float cst = 1.f) const {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      if (!live(it)) continue;
+      const int idx = threadIdx.x + it * NT, j = idx % RP, c = 4 * (idx / RP);
+      const float fa = (ks ? ks[2 * j] : 1.f) * cst, fb = (ks ? ks[2 * j + 1] : 1.f) * cst;
+      op.put2(c, 2 * j, a[it].x * fa, b[it].x * fb);
+      op.put2(c + 1, 2 * j, a[it].y * fa, b[it].y * fb);
+      op.put2(c + 2, 2 * j, a[it].z * fa, b[it].z * fb);
+      op.put2(c + 3, 2 * j, a[it].w * fa, b[it].w * fb);
+    }
+  }
+};
+
 template <int R, int K, int NT, int P>
 __device__ __forceinline__ void stage_rows(const Op<P>& op, const float* g, int ldg, const float* rs = nullptr) {
-  constexpr int V = K / 4;
-  for (int idx = threadIdx.x; idx < R * V; idx += NT) {
-    const int r = idx / V, c = 4 * (idx % V);
-    const float4 x = *reinterpret_cast<const float4*>(g + (size_t)r * ldg + c);
-    const float f = rs ? rs[r] : 1.f;
-    op.put(r, c, x.x * f);
-    op.put(r, c + 1, x.y * f);
-    op.put(r, c + 2, x.z * f);
-    op.put(r, c + 3, x.w * f);
-  }
+  Regs<R, K, NT> t;
+  t.fetch(g, ldg);
+  t.put_rows(op, rs);
 }
-// ... transposed: op(c, r) = g[r][c] * ks[r] * cst (the source rows become the contraction index)
 template <int R, int K, int NT, int P>
 __device__ __forceinline__ void stage_cols(const Op<P>& op, const float* g, int ldg, const float* ks = nullptr,
                                            float cst = 1.f) {
-  constexpr int V = K / 4;
-  for (int idx = threadIdx.x; idx < R * V; idx += NT) {
-    const int r = idx / V, c = 4 * (idx % V);
-    const float4 x = *reinterpret_cast<const float4*>(g + (size_t)r * ldg + c);
-    const float f = (ks ? ks[r] : 1.f) * cst;
-    op.put(c, r, x.x * f);
-    op.put(c + 1, r, x.y * f);
-    op.put(c + 2, r, x.z * f);
-    op.put(c + 3, r, x.w * f);
-  }
+  RegsT<R, K, NT> t;
+  t.fetch(g, ldg);
+  t.put_cols(op, ks, cst);
 }
-// ... transposed from a token-major activation (rows past `rows` read as 0)
+
+// An R x K tile of a token-major activation (fp32 or bf16, rows past `rows` read as 0), 8
+// consecutive values per slot and two consecutive rows per slot, fetched at once and written
+// transposed as 32-bit row pairs: op(c, r) = g[r][c].
+template <int R, int K, int NT, class T>
+struct RegsIO {
+  static constexpr int RP = R / 2;
+  static constexpr int V = K / 8;
+  static constexpr int IT = (RP * V + NT - 1) / NT;
+  float x[IT][2][8];
+  __device__ __forceinline__ static bool live(int it) {
+    return (RP * V) % NT == 0 || (int)threadIdx.x + it * NT < RP * V;
+  }
+  __device__ __forceinline__ void fetch(const T* g, int ldg, int rows) {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int idx = threadIdx.x + it * NT, j = idx % RP, c = 8 * (idx / RP);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = 2 * j + h;
+        if (live(it) && r < rows) {
+          ld8(g + (size_t)r * ldg + c, x[it][h]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[it][h][e] = 0.f;
+        }
+      }
+    }
+  }
+  template <int P>
+  __device__ __forceinline__ void put_cols(const Op<P>& op) const {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      if (!live(it)) continue;
+      const int idx = threadIdx.x + it * NT, j = idx % RP, c = 8 * (idx / RP);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) op.put2(c + e, 2 * j, x[it][0][e], x[it][1][e]);
+    }
+  }
+};
 template <int R, int K, int NT, int P, class T>
 __device__ __forceinline__ void stage_cols_io(const Op<P>& op, const T* g, int ldg, int rows) {
-  for (int idx = threadIdx.x; idx < R * K; idx += NT) {
-    const int r = idx / K, c = idx % K;
-    op.put(c, r, r < rows ? ldf(g + (size_t)r * ldg + c) : 0.f);
-  }
+  RegsIO<R, K, NT, T> t;
+  t.fetch(g, ldg, rows);
+  t.put_cols(op);
+}
+
+template <int R, int D, int NT>
+__device__ __forceinline__ void load_tile(float* s, int LD, const float* g) {
+  Regs<R, D, NT> t;
+  t.fetch(g, D);
+  t.put_lds(s, LD);
 }
 
 // ---------------------------------------------------------------- k_chunk
@@ -472,7 +573,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
     if (w < C / 16) {  // v_new = u - w S
       f32x4 acc[DVT / 16];
       zero(acc);
-      strip_mma<PS, D, DVT / 16>(acc, krow(A.ww + off, D), 16 * w, os, 0);
+      strip_mma_full<PS, D, DVT / 16>(acc, krow(A.ww + off, D), 16 * w, os, 0);
 #pragma unroll
       for (int t = 0; t < DVT / 16; ++t)
 #pragma unroll
@@ -518,7 +619,7 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
   {
     f32x4 acc[C / 16];
     zero(acc);
-    strip_mma<PI, D, C / 16>(acc, krow(qg, D), i0, ob, 0, 0, D, w + 1);
+    strip_mma_full<PI, D, C / 16>(acc, krow(qg, D), i0, ob, 0, w + 1);
 #pragma unroll
     for (int t = 0; t < C / 16; ++t)
 #pragma unroll
@@ -536,7 +637,7 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
   __syncthreads();
   stage_cols<D, D, NT>(ob, A.states + ((size_t)bh * A.N + n) * D * D, D);  // S^T
   __syncthreads();
-  strip_mma<PS, D, D / 16>(o, scale_r(krow(qg, D), cx.grow), i0, ob, 0);
+  strip_mma_full<PS, D, D / 16>(o, scale_r(krow(qg, D), cx.grow), i0, ob, 0);
   TIO* out = reinterpret_cast<TIO*>(A.out);
 #pragma unroll
   for (int t = 0; t < D / 16; ++t)
@@ -571,7 +672,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
   {
     f32x4 acc[C / 16];
     zero(acc);
-    strip_mma<PI, D, C / 16>(acc, krow(qg, D), i0, ob, 0, 0, D, w + 1);
+    strip_mma_full<PI, D, C / 16>(acc, krow(qg, D), i0, ob, 0, w + 1);
 #pragma unroll
     for (int t = 0; t < C / 16; ++t)
 #pragma unroll
@@ -668,7 +769,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
     if (w < C / 16) {  // X = X_loc + Kt G
       f32x4 acc[DVT / 16];
       zero(acc);
-      strip_mma<PS, D, DVT / 16>(acc, krow(A.kt + off, D), 16 * w, og, 0);
+      strip_mma_full<PS, D, DVT / 16>(acc, krow(A.kt + off, D), 16 * w, og, 0);
 #pragma unroll
       for (int t = 0; t < DVT / 16; ++t)
 #pragma unroll
@@ -733,7 +834,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
   {  // m1 -> LDS, m2 -> registers
     f32x4 acc[C / 16];
     zero(acc);
-    strip_mma<PI, D, C / 16>(acc, krow(xg, D), i0, ob, 0, 0, D, w + 1);
+    strip_mma_full<PI, D, C / 16>(acc, krow(xg, D), i0, ob, 0, w + 1);
 #pragma unroll
     for (int t = 0; t < C / 16; ++t)
 #pragma unroll
@@ -742,7 +843,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
         lds_st(sA + i * LA + j, (i > j && t <= w) ? -acc[t][rr] * decay(cx, i, j) : 0.f);
       }
     zero(m2);
-    strip_mma<PI, D, C / 16>(m2, dov, i0, ob, 0, 0, D, w + 1);
+    strip_mma_full<PI, D, C / 16>(m2, dov, i0, ob, 0, w + 1);
 #pragma unroll
     for (int t = 0; t < C / 16; ++t)
 #pragma unroll
