@@ -33,36 +33,51 @@ def _args(argv=None):
     ap.add_argument("--config", default="0.8B")
     ap.add_argument("--precision", default=None, help="override the config's precision")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-length", type=int, default=1024)
+    ap.add_argument("--cpu-rows", type=int, default=1, help="rows of the workload in the CPU baseline sample")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum timed CPU work of the baseline")
     ap.add_argument("--details", default=None, help="also write the full report to this JSON file")
     return ap.parse_args(argv)
 
 
-def _cpu_baseline(cfg, precision_dtype, sample_length: int) -> dict:
-    """The oracle's fwd+bwd on the CPU: one row of ``sample_length`` tokens at the config's
-    heads and dims (its per-token cost does not depend on T); 1 warm-up, median of 3."""
+def _cpu_baseline(cfg, precision_dtype, rows: int, min_seconds: float) -> dict:
+    """The oracle's fwd+bwd on the CPU over ``rows`` full-length rows of the workload (its
+    per-token cost does not depend on the batch): one warm-up pass, then passes until at least
+    ``min_seconds`` of timed work; tokens/s over all timed passes."""
     import torch
 
     from oracle.gdn_oracle import reference_with_grads
     from tjev_amd.testing import cotangent, gdn_inputs
 
     threads = torch.get_num_threads()
-    inputs = gdn_inputs(batch=1, length=sample_length, key_heads=cfg["key_heads"],
-                        value_heads=cfg["value_heads"], dim=cfg["dim"], dtype=precision_dtype)
-    cot = cotangent(1, sample_length, cfg["value_heads"], cfg["dim"])
+    T = cfg["length"]
+    inputs = gdn_inputs(batch=rows, length=T, key_heads=cfg["key_heads"], value_heads=cfg["value_heads"],
+                        dim=cfg["dim"], dtype=precision_dtype, segments=cfg["segments"])
+    cot = cotangent(rows, T, cfg["value_heads"], cfg["dim"])
     kw = dict(key_heads=cfg["key_heads"], key_dim=cfg["dim"], value_heads=cfg["value_heads"],
               value_dim=cfg["dim"], chunk=cfg["chunk"])
-    times = []
-    for rep in range(4):
+    reference_with_grads(inputs, cot, **kw)
+    passes, total = 0, 0.0
+    while total < min_seconds or passes < 1:
         t0 = time.perf_counter()
         reference_with_grads(inputs, cot, **kw)
-        if rep:
-            times.append(time.perf_counter() - t0)
-    sec = statistics.median(times)
-    return {"value": sample_length / sec, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": (f"oracle (CPU restatement of tjev's XLA chunked path, fp32, torch autograd) fwd+bwd "
-                       f"on B=1 T={sample_length} at the config's heads/dims, median of 3 after 1 warm-up, "
-                       f"{threads} threads, {sec:.2f} s per pass")}
+        total += time.perf_counter() - t0
+        passes += 1
+    return {"value": passes * rows * T / total, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle (CPU restatement of tjev's XLA chunked path, fp32, torch autograd) fwd+bwd on "
+                       f"B={rows} T={T} rows of the same workload (its heads, dims, chunk, segments), "
+                       f"{passes} passes after 1 warm-up, {total:.1f} s timed, {threads} threads")}
+
+
+def _traffic(config: str, precision: str, kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed FETCH_SIZE / WRITE_SIZE summary of
+    this workload (profiles/hbm_traffic_<config>_<precision>.json), or None without one."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        f"hbm_traffic_{config}_{precision}.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["kernels"][kernel]["bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def main(argv=None) -> int:
@@ -134,6 +149,7 @@ def main(argv=None) -> int:
                              "frac": ach / PEAK_HBM_GBS, "algorithmic": wk["bytes"]}
     dominant = max(kernels, key=lambda k: kernels[k]["ms"])
     dk = kernels[dominant]
+    traffic = _traffic(args.config, precision, dominant)
     op = operator_work(**shape)
     value = B * T / (ms * 1e-3)
     report = {
@@ -153,7 +169,7 @@ def main(argv=None) -> int:
                    "key_heads": Hk, "value_heads": H, "head_dim": D, "chunk": C, "conv_taps": int(w.shape[0]),
                    "precision": precision, "segments": cfg["segments"]},
         "roofline": {"kernel": dominant, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
-                     "unit": dk["unit"], "frac": dk["frac"], "traffic": None},
+                     "unit": dk["unit"], "frac": dk["frac"], "traffic": traffic},
         "operator_roofline": {"algorithmic_gflop": op["flops"] / 1e9, "algorithmic_mb": op["bytes"] / 1e6,
                               "ceiling_tokens_per_s": op["ceiling_tokens_per_s"],
                               "frac": value / op["ceiling_tokens_per_s"],
@@ -164,7 +180,7 @@ def main(argv=None) -> int:
         "wall_s_timed": t_wall,
     }
     if not args.no_cpu_baseline:
-        report["cpu_baseline"] = _cpu_baseline(cfg, dtype, args.cpu_sample_length)
+        report["cpu_baseline"] = _cpu_baseline(cfg, dtype, min(args.cpu_rows, B), args.cpu_seconds)
     if args.details:
         with open(args.details, "w") as f:
             json.dump(report, f, indent=1)
