@@ -94,13 +94,43 @@ int tjev_gdn_mega2_bwd(const tjev_gdn_params* p, void* stream, const void* qkv, 
                        float* d_dt_bias, float* d_conv_w, void* workspace,
                        size_t workspace_bytes);
 
+/* The gated RMSNorm of the GDN output, replacing tjev's GatedRMSNorm (src/tjev/model/norms.py:
+ * 13-15, 36-40; its .flat form :42-62 is the same arithmetic on the same memory) and the padding
+ * select after it (src/tjev/model/gdn.py:157-163):
+ *   y = w * cast(x * rsqrt(mean_D(x^2) + eps)) * silu(gate), in fp32, stored in `dtype`
+ * where cast rounds to `dtype` and back (a no-op for fp32). x, gate, y [tokens, heads, dim];
+ * w [dim] fp32; seg [tokens] int32 or null: when given, y = 0 (and the incoming gradient is
+ * taken as 0) on tokens whose segment id is <= 0. */
+typedef struct tjev_gdn_norm_params {
+  int64_t tokens; /* B*T */
+  int32_t heads;  /* H */
+  int32_t dim;    /* D, the normalized axis: 16, 32, 64, 128 or 256 */
+  int32_t dtype;  /* tjev_gdn_dtype of x, gate, y, d_y, d_x, d_gate */
+  float eps;      /* rms_norm_eps (1e-6 in Qwen3.5) */
+} tjev_gdn_norm_params;
+
+/* scratch of the backward's weight gradient (0 if d_weight will be null) */
+size_t tjev_gdn_norm_workspace_bytes(const tjev_gdn_norm_params* p, int weight_grad);
+
+int tjev_gdn_gated_rmsnorm_fwd(const tjev_gdn_norm_params* p, void* stream, const void* x,
+                               const void* gate, const float* weight, const int32_t* seg,
+                               void* y);
+
+/* d_x and d_gate in `dtype`, as the reference's autodiff gives them (the cotangent of the
+ * rounding cast is itself rounded to `dtype`); d_weight [dim] fp32, summed over tokens and
+ * heads in a fixed order, only when not null (the reference's weight is frozen). */
+int tjev_gdn_gated_rmsnorm_bwd(const tjev_gdn_norm_params* p, void* stream, const void* x,
+                               const void* gate, const float* weight, const int32_t* seg,
+                               const void* d_y, void* d_x, void* d_gate, float* d_weight,
+                               void* workspace, size_t workspace_bytes);
+
 /* Per-kernel timing (no counterpart in the reference, whose kernels are timed by xprof):
- * between tjev_gdn_profile_begin() and tjev_gdn_profile_end(), every launch of the fwd / bwd
- * calls is bracketed by a hipEvent pair on the call's stream. _end synchronizes those events
+ * between tjev_gdn_profile_begin() and tjev_gdn_profile_end(), every launch of the megakernel
+ * and norm calls is bracketed by a hipEvent pair on the call's stream. _end synchronizes those events
  * and writes, for kernel ids 0..n-1, the summed milliseconds and the launch count.
  * TJEV_GDN_KERNELS is the number of ids; tjev_gdn_kernel_name(id) names them. Not thread-safe:
  * profile from one host thread. */
-#define TJEV_GDN_KERNELS 11
+#define TJEV_GDN_KERNELS 14
 int tjev_gdn_profile_begin(void);
 int tjev_gdn_profile_end(float* ms, int* launches, int n);
 const char* tjev_gdn_kernel_name(int kernel);

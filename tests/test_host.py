@@ -159,3 +159,56 @@ def test_varlen_segments_follow_the_config():
     lengths = np.bincount(ids)[1:]
     assert np.all(lengths[:-1] >= 16) and np.all(lengths <= 4096)
     assert 30 <= len(lengths) <= 90  # mean 300 over 16384 tokens
+
+
+def _norm_params(**kw):
+    from tjev_amd import _lib
+
+    base = dict(tokens=10, heads=2, dim=128, dtype=1, eps=1e-6)
+    base.update(kw)
+    return _lib.NormParams(**base)
+
+
+@pytest.mark.parametrize("bad,status,msg", [
+    (dict(dim=48), 2, "dim 16, 32, 64, 128 and 256"),
+    (dict(dtype=3), 1, "dtype"),
+    (dict(heads=0), 1, "heads"),
+    (dict(tokens=-1), 1, "tokens"),
+    (dict(eps=-1.0), 1, "eps"),
+])
+def test_norm_c_abi_validation(bad, status, msg):
+    from tjev_amd import _lib
+
+    lib = _lib.load()
+    p = _norm_params(**bad)
+    got = lib.tjev_gdn_gated_rmsnorm_fwd(ctypes.byref(p), None, *([None] * 5))
+    assert got == status and msg in lib.tjev_gdn_last_error().decode()
+    assert lib.tjev_gdn_norm_workspace_bytes(ctypes.byref(p), 1) == 0
+
+
+def test_norm_c_abi_nulls_and_workspace():
+    from tjev_amd import _lib
+
+    lib = _lib.load()
+    p = _norm_params(tokens=4 * 4096, heads=16, dim=128)
+    assert lib.tjev_gdn_gated_rmsnorm_fwd(ctypes.byref(p), None, *([None] * 5)) == 1
+    assert "null" in lib.tjev_gdn_last_error().decode()
+    assert lib.tjev_gdn_norm_workspace_bytes(ctypes.byref(p), 0) == 0
+    # one fp32 partial row of D per backward workgroup, at most 2048 of them
+    assert lib.tjev_gdn_norm_workspace_bytes(ctypes.byref(p), 1) == 2048 * 128 * 4
+    small = _norm_params(tokens=3, heads=2, dim=16)  # 6 rows fit one workgroup of 128 rows
+    assert lib.tjev_gdn_norm_workspace_bytes(ctypes.byref(small), 1) == 16 * 4
+
+
+def test_norm_operator_checks_and_no_cpu_fallback():
+    from tjev_amd.norm import gated_rmsnorm
+
+    x = torch.zeros(2, 3, 4, 16)
+    with pytest.raises(ValueError, match="differ"):
+        gated_rmsnorm(x, torch.zeros(2, 3, 4, 8), torch.ones(16))
+    with pytest.raises(ValueError, match="weight"):
+        gated_rmsnorm(x, x, torch.ones(8))
+    with pytest.raises(ValueError, match="heads"):
+        gated_rmsnorm(x.reshape(2, 3, 64), x.reshape(2, 3, 64), torch.ones(16), heads=5)
+    with pytest.raises(RuntimeError, match="GPU"):
+        gated_rmsnorm(x, x, torch.ones(16))

@@ -195,6 +195,30 @@ def test_gated_rmsnorm_matches_hf():
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gated_rmsnorm_backward_matches_hf(dtype):
+    """The oracle's autograd through the norm (the cotangent of the bf16 rounding cast rounded
+    to bf16, as JAX's convert_element_type transposes) equals HF's module autograd."""
+    hf = pytest.importorskip("transformers.models.qwen3_5.modeling_qwen3_5")
+    rng = np.random.default_rng(6)
+    shape = (2, 9, 3, 32)
+    x0, z0, dy = (torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).to(dtype) for _ in range(3))
+    w0 = torch.from_numpy(1 + 0.1 * rng.standard_normal(32).astype(np.float32))
+    norm = hf.Qwen3_5RMSNormGated(32, eps=1e-6)
+    with torch.no_grad():
+        norm.weight.copy_(w0)
+    x, z = x0.clone().requires_grad_(True), z0.clone().requires_grad_(True)
+    want = torch.autograd.grad((norm(x, z).float() * dy.float()).sum(), (x, z, norm.weight))
+    x, z, w = x0.clone().requires_grad_(True), z0.clone().requires_grad_(True), w0.clone().requires_grad_(True)
+    got = torch.autograd.grad((O.gated_rmsnorm(x, z, w).float() * dy.float()).sum(), (x, z, w))
+    for g, h in zip(got, want):
+        assert g.dtype == h.dtype
+        scale = float(h.double().abs().max())
+        # silu's autograd formula differs from F.silu's in the last bits: a bf16 ulp at most
+        tol = 1e-6 if dtype == torch.float32 else 8e-3
+        assert float((g.double() - h.double()).abs().max()) <= tol * scale
+
+
 # ------------------------------------------------------------------ gates
 def test_gates_closed_forms():
     """beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias) with jax.nn.softplus =

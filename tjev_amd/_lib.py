@@ -25,13 +25,16 @@ EXPORTS = (
     "tjev_gdn_workspace_bytes",
     "tjev_gdn_mega2_fwd",
     "tjev_gdn_mega2_bwd",
+    "tjev_gdn_norm_workspace_bytes",
+    "tjev_gdn_gated_rmsnorm_fwd",
+    "tjev_gdn_gated_rmsnorm_bwd",
     "tjev_gdn_profile_begin",
     "tjev_gdn_profile_end",
     "tjev_gdn_kernel_name",
     "tjev_gdn_last_error",
     "tjev_gdn_version",
 )
-N_KERNELS = 11  # TJEV_GDN_KERNELS
+N_KERNELS = 14  # TJEV_GDN_KERNELS
 
 
 class Params(ctypes.Structure):
@@ -41,6 +44,13 @@ class Params(ctypes.Structure):
         "batch", "length", "key_heads", "key_dim", "value_heads", "value_dim", "taps", "chunk",
         "io_dtype", "gate_dtype", "precision", "inverse", "heads_per_step",
     )]
+
+
+class NormParams(ctypes.Structure):
+    """tjev_gdn_norm_params"""
+
+    _fields_ = [("tokens", ctypes.c_int64), ("heads", ctypes.c_int32), ("dim", ctypes.c_int32),
+                ("dtype", ctypes.c_int32), ("eps", ctypes.c_float)]
 
 
 class GdnLibraryError(RuntimeError):
@@ -74,6 +84,13 @@ def load() -> ctypes.CDLL:
     lib.tjev_gdn_mega2_fwd.restype = i32
     lib.tjev_gdn_mega2_bwd.argtypes = [pp, vp] + [vp] * 16 + [sz]
     lib.tjev_gdn_mega2_bwd.restype = i32
+    npp = ctypes.POINTER(NormParams)
+    lib.tjev_gdn_norm_workspace_bytes.argtypes = [npp, i32]
+    lib.tjev_gdn_norm_workspace_bytes.restype = sz
+    lib.tjev_gdn_gated_rmsnorm_fwd.argtypes = [npp, vp] + [vp] * 5
+    lib.tjev_gdn_gated_rmsnorm_fwd.restype = i32
+    lib.tjev_gdn_gated_rmsnorm_bwd.argtypes = [npp, vp] + [vp] * 9 + [sz]
+    lib.tjev_gdn_gated_rmsnorm_bwd.restype = i32
     lib.tjev_gdn_profile_begin.argtypes = []
     lib.tjev_gdn_profile_begin.restype = i32
     lib.tjev_gdn_profile_end.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_int), i32]

@@ -28,6 +28,10 @@ FLAGS = [
 ]
 
 
+# units built once: the C ABI and the gated RMSNorm
+EXTRA_UNITS = ("gdn_api", "gdn_norm")
+
+
 def shapes() -> list[tuple[int, int]]:
     text = (CSRC / "gdn_shapes.def").read_text()
     return [(int(c), int(d)) for c, d in re.findall(r"GDN_SHAPE\((\d+),\s*(\d+)\)", text)]
@@ -59,15 +63,16 @@ def build(jobs: int | None = None, verbose: bool = False, verify: bool = True) -
         obj = OUT / f"gdn_inst_c{c}_d{d}.o"
         units.append([hipcc, *FLAGS, f"-DGDN_C={c}", f"-DGDN_D={d}", "-c", str(CSRC / "gdn_inst.hip"),
                       "-o", str(obj)])
-    api_obj = OUT / "gdn_api.o"
-    units.append([hipcc, *FLAGS, "-c", str(CSRC / "gdn_api.hip"), "-o", str(api_obj)])
+    for name in EXTRA_UNITS:
+        units.append([hipcc, *FLAGS, "-c", str(CSRC / f"{name}.hip"), "-o", str(OUT / f"{name}.o")])
     t0 = time.time()
     with ThreadPoolExecutor(max_workers=jobs or min(len(units), os.cpu_count() or 4)) as pool:
         checks = []
         if verify:
-            from .ds_check import check_unit
+            from .ds_check import check_source, check_unit
 
             checks = [pool.submit(check_unit, c, d) for c, d in shapes()]
+            checks += [pool.submit(check_source, CSRC / f"{name}.hip") for name in EXTRA_UNITS]
         list(pool.map(_run, units))
         bad = [line for f in checks for line in f.result()]
     if bad:

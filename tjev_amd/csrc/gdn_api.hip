@@ -178,8 +178,9 @@ int aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % 
 
 // ---- per-kernel timing: an event pair around each launch while profiling is on
 const char* const kKernelNames[gdn::K_COUNT] = {
-    "gdn_prep_fwd", "gdn_chunk_fwd", "gdn_scan_fwd", "gdn_out",     "gdn_prep_bwd", "gdn_chunk_bwd",
-    "gdn_bwd_local", "gdn_scan_bwd", "gdn_bwd_grads", "gdn_post", "gdn_reduce"};
+    "gdn_prep_fwd", "gdn_chunk_fwd", "gdn_scan_fwd", "gdn_out",       "gdn_prep_bwd",   "gdn_chunk_bwd",
+    "gdn_bwd_local", "gdn_scan_bwd", "gdn_bwd_grads", "gdn_post",     "gdn_reduce",     "gdn_norm_fwd",
+    "gdn_norm_bwd",  "gdn_norm_reduce"};
 
 struct Profiler {
   bool on = false;
@@ -214,16 +215,22 @@ void prof_mark(void*, int kernel, int end, hipStream_t st) {
   }
 }
 
+const gdn::Timer g_timer{prof_mark, nullptr};
+
 int run(const tjev_gdn_params* p, void* stream, gdn::GdnArgs& A, int backward) {
   const gdn::ShapeTable* t = lookup(kernel_chunk(p), p->key_dim);
   const gdn::GdnFn fn = t->fn[p->precision][p->io_dtype][p->gate_dtype];
-  const gdn::Timer timer{prof_mark, nullptr};
-  const hipError_t e = fn(A, static_cast<hipStream_t>(stream), backward, g_prof.on ? &timer : nullptr);
+  const hipError_t e = fn(A, static_cast<hipStream_t>(stream), backward, gdn::active_timer());
   if (e != hipSuccess) return fail(TJEV_GDN_EHIP, std::string("HIP launch failed: ") + hipGetErrorString(e));
   return 0;
 }
 
 }  // namespace
+
+namespace gdn {
+int fail(int status, const char* msg) { return ::fail(status, msg); }
+const Timer* active_timer() { return g_prof.on ? &g_timer : nullptr; }
+}  // namespace gdn
 
 extern "C" {
 

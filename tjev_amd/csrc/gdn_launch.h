@@ -11,6 +11,7 @@ namespace gdn {
 enum KernelId : int {
   K_PREP_FWD = 0, K_CHUNK_FWD, K_SCAN_FWD, K_OUT,
   K_PREP_BWD, K_CHUNK_BWD, K_BWD_LOCAL, K_SCAN_BWD, K_BWD_GRADS, K_POST, K_REDUCE,
+  K_NORM_FWD, K_NORM_BWD, K_NORM_REDUCE,
   K_COUNT
 };
 
@@ -27,6 +28,11 @@ struct ShapeTable {
   int C, D;
   GdnFn fn[4][2][2];  // [precision][io dtype][gate dtype]
 };
+
+// Shared by the C ABI's units (defined in gdn_api.hip): record the message of a nonzero status
+// for tjev_gdn_last_error(), and the timing hook while profiling is on (else null).
+int fail(int status, const char* msg);
+const Timer* active_timer();
 
 #define GDN_SHAPE(c, d) const ShapeTable* table_##c##_##d();
 #include "gdn_shapes.def"

@@ -25,9 +25,13 @@ _PAIR = re.compile(r"DS_(WRITE|READ)2(ST64)?_B(32|64)\w*\s.*?,\s*(\d+),\s*(\d+),
 
 def check_unit(c: int, d: int) -> list[str]:
     """Wrongly merged LDS accesses of the (chunk c, head dim d) kernel unit (empty if none)."""
-    cmd = [_hipcc(), *FLAGS, f"-DGDN_C={c}", f"-DGDN_D={d}", "--cuda-device-only", "-S", "-o", "/dev/null",
-           str(CSRC / "gdn_inst.hip"), "-mllvm", "-print-before=si-load-store-opt",
-           "-mllvm", "-print-after=si-load-store-opt"]
+    return check_source(CSRC / "gdn_inst.hip", [f"-DGDN_C={c}", f"-DGDN_D={d}"])
+
+
+def check_source(src, defines=()) -> list[str]:
+    """Wrongly merged LDS accesses of one HIP source's device code (empty if none)."""
+    cmd = [_hipcc(), *FLAGS, *defines, "--cuda-device-only", "-S", "-o", "/dev/null", str(src),
+           "-mllvm", "-print-before=si-load-store-opt", "-mllvm", "-print-after=si-load-store-opt"]
     text = subprocess.run(cmd, capture_output=True, text=True).stderr
     parts = re.split(r"# \*\*\* IR Dump (?:Before|After) SI Load Store Optimizer[^\n]*\n", text)[1:]
     bad = []

@@ -190,8 +190,9 @@ def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: t
 def gdn_core_mega(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_heads: int, key_dim: int,
                   value_heads: int, value_dim: int, chunk: int = 64, precision: str = "high",
                   inverse: str = "default", heads_per_step: int = 0, vmem_fraction: float = 0.0):
-    """The dispatcher form (__init__.py:112-149): ``inverse`` "default" -> doubling. On one
-    GPU there is no row sharding; see the design notes for the multi-GPU split."""
+    """The dispatcher form (__init__.py:112-149): ``inverse`` "default" -> doubling. The
+    reference shards rows over devices here (``batch_parallel_with``); this build runs one GPU,
+    where that split is the identity."""
     return gdn_megakernel(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, key_heads=key_heads,
                           key_dim=key_dim, value_heads=value_heads, value_dim=value_dim, chunk=chunk,
                           precision=precision, inverse=kernel_inverse(inverse),
