@@ -1,10 +1,11 @@
 #!/usr/bin/env python3
 """GDN megakernel fwd+bwd throughput on one MI355X (tjev's mega2, BASELINE.json's metric).
 
-A step is one forward and one backward pass of the GDN core over one batch of synthetic
-inputs already resident in HBM (the HIP library called through its C ABI, no autograd): out
-and the chunk states, then d(qkv), d(a), d(b), d(A_log), d(dt_bias) under a fixed upstream
-gradient. W untimed warm-up steps, then K timed steps between device synchronizations;
+A step is one forward and one backward pass of the GDN layer core over one batch of synthetic
+inputs already resident in HBM (the HIP library called through its C ABI, no autograd): the
+megakernel's out and chunk states, the gated RMSNorm y of out with gate z, then under a fixed
+upstream gradient of y the norm's backward (d out, d z) and the megakernel's d(qkv), d(a),
+d(b), d(A_log), d(dt_bias). ``--no-norm`` times the megakernel alone. W untimed warm-up steps, then K timed steps between device synchronizations;
 ``value`` = B*T / (seconds per step). A second, event-profiled pass of K steps gives every
 kernel's average duration (HIP events on the launch stream) for the dominant kernel's
 roofline. The CPU baseline is the oracle (a CPU restatement of tjev's XLA chunked path, fp32,
@@ -32,6 +33,7 @@ def _args(argv=None):
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="0.8B")
     ap.add_argument("--precision", default=None, help="override the config's precision")
+    ap.add_argument("--no-norm", action="store_true", help="time the GDN core alone, without the gated RMSNorm")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=1, help="rows of the workload in the CPU baseline sample")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum timed CPU work of the baseline")
@@ -39,32 +41,45 @@ def _args(argv=None):
     return ap.parse_args(argv)
 
 
-def _cpu_baseline(cfg, precision_dtype, rows: int, min_seconds: float) -> dict:
+def _cpu_baseline(cfg, precision_dtype, rows: int, min_seconds: float, norm: bool) -> dict:
     """The oracle's fwd+bwd on the CPU over ``rows`` full-length rows of the workload (its
-    per-token cost does not depend on the batch): one warm-up pass, then passes until at least
-    ``min_seconds`` of timed work; tokens/s over all timed passes."""
+    per-token cost does not depend on the batch), with the gated RMSNorm epilogue when the GPU
+    step has it: one warm-up pass, then passes until at least ``min_seconds`` of timed work;
+    tokens/s over all timed passes."""
     import torch
 
-    from oracle.gdn_oracle import reference_with_grads
+    from oracle.gdn_oracle import gated_rmsnorm, reference_core
     from tjev_amd.testing import cotangent, gdn_inputs
 
     threads = torch.get_num_threads()
-    T = cfg["length"]
-    inputs = gdn_inputs(batch=rows, length=T, key_heads=cfg["key_heads"], value_heads=cfg["value_heads"],
-                        dim=cfg["dim"], dtype=precision_dtype, segments=cfg["segments"])
-    cot = cotangent(rows, T, cfg["value_heads"], cfg["dim"])
-    kw = dict(key_heads=cfg["key_heads"], key_dim=cfg["dim"], value_heads=cfg["value_heads"],
-              value_dim=cfg["dim"], chunk=cfg["chunk"])
-    reference_with_grads(inputs, cot, **kw)
+    T, H, D = cfg["length"], cfg["value_heads"], cfg["dim"]
+    inputs = gdn_inputs(batch=rows, length=T, key_heads=cfg["key_heads"], value_heads=H, dim=D,
+                        dtype=precision_dtype, segments=cfg["segments"])
+    cot = cotangent(rows, T, H, D).float()
+    z = torch.randn((rows, T, H, D), generator=torch.Generator().manual_seed(11))
+    norm_w = torch.ones(D)
+    kw = dict(key_heads=cfg["key_heads"], key_dim=D, value_heads=H, value_dim=D, chunk=cfg["chunk"],
+              dtype=torch.float32)
+
+    def one_pass():
+        qkv, a, b, a_log, dt_bias, w, seg = inputs
+        leaves = [x.detach().float().requires_grad_(True) for x in (qkv, a, b, a_log, dt_bias)]
+        out = reference_core(*leaves, w.detach().float(), seg, **kw)
+        if norm:
+            out = gated_rmsnorm(out, z, norm_w)
+        torch.autograd.grad(torch.sum(out * cot), leaves)
+
+    one_pass()
     passes, total = 0, 0.0
     while total < min_seconds or passes < 1:
         t0 = time.perf_counter()
-        reference_with_grads(inputs, cot, **kw)
+        one_pass()
         total += time.perf_counter() - t0
         passes += 1
+    what = "GDN core + gated RMSNorm" if norm else "GDN core"
     return {"value": passes * rows * T / total, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": (f"oracle (CPU restatement of tjev's XLA chunked path, fp32, torch autograd) fwd+bwd on "
-                       f"B={rows} T={T} rows of the same workload (its heads, dims, chunk, segments), "
+            "sample": (f"oracle (CPU restatement of tjev's XLA chunked path, fp32, torch autograd) {what} "
+                       f"fwd+bwd on B={rows} T={T} rows of the same workload (its heads, dims, chunk, segments), "
                        f"{passes} passes after 1 warm-up, {total:.1f} s timed, {threads} threads")}
 
 
@@ -91,6 +106,8 @@ def main(argv=None) -> int:
 
     from tjev_amd import _lib
     from tjev_amd.gdn import GdnPlan
+    from tjev_amd.norm import _params as _norm_params
+    from tjev_amd.norm import norm_backward, norm_forward
     from tjev_amd.roofline import PEAK_BF16_TFLOPS, PEAK_FP32_TFLOPS, PEAK_HBM_GBS, kernel_work, operator_work
     from tjev_amd.testing import CONFIGS, cotangent, gdn_inputs
 
@@ -101,7 +118,17 @@ def main(argv=None) -> int:
     B, T, Hk, H, D, C = (cfg[k] for k in ("batch", "length", "key_heads", "value_heads", "dim", "chunk"))
     qkv, a, b, a_log, dt_bias, w, seg = gdn_inputs(batch=B, length=T, key_heads=Hk, value_heads=H, dim=D,
                                                   dtype=dtype, segments=cfg["segments"], device=dev)
-    d_out = cotangent(B, T, H, D).to(dtype).to(dev)
+    d_y = cotangent(B, T, H, D).to(dtype).to(dev)
+    norm = not args.no_norm
+    if norm:  # the output norm's gate z ~ N(0, 1) and weight (ones, as initialised)
+        gen = torch.Generator().manual_seed(11)
+        z = torch.randn((B, T, H, D), generator=gen).to(dtype).to(dev)
+        norm_w = torch.ones(D, dtype=torch.float32, device=dev)
+        norm_p = _norm_params(B * T, H, D, dtype, 1e-6)
+        y = torch.empty((B, T, H, D), dtype=dtype, device=dev)
+        d_out, d_z = torch.empty_like(y), torch.empty_like(y)
+    else:
+        d_out = d_y
     plan = GdnPlan(batch=B, length=T, key_heads=Hk, key_dim=D, value_heads=H, value_dim=D, taps=w.shape[0],
                    chunk=C, io_dtype=dtype, gate_dtype=dtype, precision=precision)
     ws = torch.empty(max(plan.fwd_bytes, plan.bwd_bytes), dtype=torch.uint8, device=dev)
@@ -112,6 +139,9 @@ def main(argv=None) -> int:
 
     def step():
         plan.forward(qkv, a, b, a_log, dt_bias, w, seg, out, states, ws)
+        if norm:
+            norm_forward(norm_p, out, z, norm_w, seg, y)
+            norm_backward(norm_p, out, z, norm_w, seg, d_y, d_out, d_z, None, None)
         plan.backward(qkv, a, b, a_log, dt_bias, w, seg, states, d_out, d_qkv, d_a, d_b, d_alog, d_dtb, None, ws)
 
     for _ in range(args.warmup):
@@ -126,7 +156,7 @@ def main(argv=None) -> int:
     torch.cuda.synchronize()
     t_wall = time.perf_counter() - t_wall
     ms = start.elapsed_time(end) / args.steps
-    finite = bool(torch.isfinite(out.float()).all()) and bool(torch.isfinite(d_qkv.float()).all())
+    finite = bool(torch.isfinite((y if norm else out).float()).all()) and bool(torch.isfinite(d_qkv.float()).all())
 
     with _lib.KernelTimer() as kt:  # the same steps again, each kernel between HIP events
         for _ in range(args.steps):
@@ -135,6 +165,7 @@ def main(argv=None) -> int:
     io_bytes = 2 if dtype == torch.bfloat16 else 4
     shape = dict(batch=B, length=T, key_heads=Hk, value_heads=H, dim=D, chunk=C, io_bytes=io_bytes)
     work = kernel_work(**shape)
+    shape["norm"] = norm
     peak_mfma = PEAK_FP32_TFLOPS if precision == "highest" else PEAK_BF16_TFLOPS
     kernels = {}
     for name, avg_ms in per_kernel.items():
@@ -167,7 +198,8 @@ def main(argv=None) -> int:
         "data": "synthetic",
         "config": {"workload": f"{args.config} GDN layer core (mega2) fwd+bwd", "batch": B, "seq_len": T,
                    "key_heads": Hk, "value_heads": H, "head_dim": D, "chunk": C, "conv_taps": int(w.shape[0]),
-                   "precision": precision, "segments": cfg["segments"]},
+                   "precision": precision, "segments": cfg["segments"],
+                   "epilogue": "gated_rmsnorm" if norm else None},
         "roofline": {"kernel": dominant, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
                      "unit": dk["unit"], "frac": dk["frac"], "traffic": traffic},
         "operator_roofline": {"algorithmic_gflop": op["flops"] / 1e9, "algorithmic_mb": op["bytes"] / 1e6,
@@ -180,7 +212,7 @@ def main(argv=None) -> int:
         "wall_s_timed": t_wall,
     }
     if not args.no_cpu_baseline:
-        report["cpu_baseline"] = _cpu_baseline(cfg, dtype, min(args.cpu_rows, B), args.cpu_seconds)
+        report["cpu_baseline"] = _cpu_baseline(cfg, dtype, min(args.cpu_rows, B), args.cpu_seconds, norm)
     if args.details:
         with open(args.details, "w") as f:
             json.dump(report, f, indent=1)

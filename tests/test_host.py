@@ -196,7 +196,7 @@ def test_norm_c_abi_nulls_and_workspace():
     assert lib.tjev_gdn_norm_workspace_bytes(ctypes.byref(p), 0) == 0
     # one fp32 partial row of D per backward workgroup, at most 2048 of them
     assert lib.tjev_gdn_norm_workspace_bytes(ctypes.byref(p), 1) == 2048 * 128 * 4
-    small = _norm_params(tokens=3, heads=2, dim=16)  # 6 rows fit one workgroup of 128 rows
+    small = _norm_params(tokens=3, heads=2, dim=16)  # 6 rows fit one workgroup
     assert lib.tjev_gdn_norm_workspace_bytes(ctypes.byref(small), 1) == 16 * 4
 
 

@@ -49,17 +49,56 @@ __device__ __forceinline__ float gdiff(const Ctx<C>& cx, int i, int j) {
   return (cx.gam[i] - cx.gam[j]) + (cx.gaml[i] - cx.gaml[j]);
 }
 
+// The per-token inputs of one chunk's context held in registers (thread i < C holds token i):
+// fetch() issues the loads, commit() writes them to the LDS context (derive_ctx then fills in
+// the rest). Needs at least C threads.
+template <int C>
+struct CtxRaw {
+  int seg, before;
+  float gam, gaml, beta;
+  bool first;  // chunk 0: the token before it is "-2" (the loaded value is not used)
+  // Every thread loads (threads past C repeat token threadIdx.x % C), with no branch around the
+  // loads: a fixed count of memory operations per wave lets the compiler wait for exactly the
+  // loads it needs instead of for all outstanding ones.
+  __device__ __forceinline__ void fetch(const GdnArgs& A, int b, int h, int n) {
+    const int i = threadIdx.x % C;
+    const size_t tok = (size_t)(b * A.H + h) * A.Tp + (size_t)n * C + i;
+    seg = A.segp[(size_t)b * A.Tp + (size_t)n * C + i];
+    gam = A.gam[tok];
+    gaml = A.gaml[tok];
+    beta = A.bet[tok];
+    before = A.segp[(size_t)b * A.Tp + (n > 0 ? (size_t)n * C - 1 : 0)];
+    first = n == 0;
+  }
+  __device__ __forceinline__ void commit(Ctx<C>& cx) const {
+    const int i = threadIdx.x;
+    if (i < C) {
+      cx.seg[i] = seg;
+      cx.gam[i] = gam;
+      cx.gaml[i] = gaml;
+      cx.beta[i] = beta;
+    }
+    if (i == 0) cx.before = first ? -2 : before;
+  }
+};
+
+template <int C, int NT>
+__device__ void derive_ctx(Ctx<C>& cx);
+
 template <int C, int NT>
 __device__ void load_ctx(Ctx<C>& cx, const GdnArgs& A, int b, int h, int n) {
-  const size_t tok = (size_t)(b * A.H + h) * A.Tp + (size_t)n * C;
-  for (int i = threadIdx.x; i < C; i += NT) {
-    cx.seg[i] = A.segp[(size_t)b * A.Tp + (size_t)n * C + i];
-    cx.gam[i] = A.gam[tok + i];
-    cx.gaml[i] = A.gaml[tok + i];
-    cx.beta[i] = A.bet[tok + i];
-  }
-  if (threadIdx.x == 0) cx.before = n == 0 ? -2 : A.segp[(size_t)b * A.Tp + (size_t)n * C - 1];
+  static_assert(NT >= C, "one thread per token");
+  CtxRaw<C> raw;
+  raw.fetch(A, b, h, n);
+  raw.commit(cx);
   __syncthreads();
+  derive_ctx<C, NT>(cx);
+  __syncthreads();
+}
+
+// grow, kws, bg and carry from seg, gamma and beta (the LDS context written, then synced)
+template <int C, int NT>
+__device__ void derive_ctx(Ctx<C>& cx) {
   for (int i = threadIdx.x; i < C; i += NT) {
     const bool cont = cx.seg[i] == cx.before;
     const bool in_last = cx.seg[i] == cx.seg[C - 1];
@@ -68,7 +107,6 @@ __device__ void load_ctx(Ctx<C>& cx, const GdnArgs& A, int b, int h, int n) {
     cx.bg[i] = cx.beta[i] * cx.grow[i];                              // kbe = k . beta . grow
   }
   if (threadIdx.x == 0) cx.carry = (cx.seg[C - 1] == cx.before) ? expf(cx.gam[C - 1] + cx.gaml[C - 1]) : 0.f;
-  __syncthreads();
 }
 
 // D_ij = e^(gamma_i - gamma_j) on same-segment i >= j, else 0 (the exp taken only there)
@@ -384,6 +422,21 @@ struct RegsT {
       op.put2(c + 3, 2 * j, a[it].w * fa, b[it].w * fb);
     }
   }
+  // the same with the thread's row pair scaled by (fa, fb) (j is the same in every slot when
+  // NT is a multiple of R/2)
+  template <int P>
+  __device__ __forceinline__ void put_cols2(const Op<P>& op, float fa, float fb) const {
+    static_assert(NT % RP == 0, "one row pair per thread");
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      if (!live(it)) continue;
+      const int idx = threadIdx.x + it * NT, j = idx % RP, c = 4 * (idx / RP);
+      op.put2(c, 2 * j, a[it].x * fa, b[it].x * fb);
+      op.put2(c + 1, 2 * j, a[it].y * fa, b[it].y * fb);
+      op.put2(c + 2, 2 * j, a[it].z * fa, b[it].z * fb);
+      op.put2(c + 3, 2 * j, a[it].w * fa, b[it].w * fb);
+    }
+  }
 };
 
 template <int R, int K, int NT, int P>
@@ -409,22 +462,21 @@ struct RegsIO {
   static constexpr int V = K / 8;
   static constexpr int IT = (RP * V + NT - 1) / NT;
   float x[IT][2][8];
+  int rows;
   __device__ __forceinline__ static bool live(int it) {
     return (RP * V) % NT == 0 || (int)threadIdx.x + it * NT < RP * V;
   }
-  __device__ __forceinline__ void fetch(const T* g, int ldg, int rows) {
+  // Every thread loads (slots past the tile repeat one inside it, rows past `rows` >= 1 repeat
+  // the last valid row): no branch around the loads and no use of them until put_cols.
+  __device__ __forceinline__ void fetch(const T* g, int ldg, int rows_) {
+    rows = rows_;
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const int idx = threadIdx.x + it * NT, j = idx % RP, c = 8 * (idx / RP);
+      const int idx = (threadIdx.x + it * NT) % (RP * V), j = idx % RP, c = 8 * (idx / RP);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int r = 2 * j + h;
-        if (live(it) && r < rows) {
-          ld8(g + (size_t)r * ldg + c, x[it][h]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) x[it][h][e] = 0.f;
-        }
+        ld8(g + (size_t)(r < rows ? r : rows - 1) * ldg + c, x[it][h]);
       }
     }
   }
@@ -434,8 +486,9 @@ struct RegsIO {
     for (int it = 0; it < IT; ++it) {
       if (!live(it)) continue;
       const int idx = threadIdx.x + it * NT, j = idx % RP, c = 8 * (idx / RP);
+      const bool v0 = 2 * j < rows, v1 = 2 * j + 1 < rows;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) op.put2(c + e, 2 * j, x[it][0][e], x[it][1][e]);
+      for (int e = 0; e < 8; ++e) op.put2(c + e, 2 * j, v0 ? x[it][0][e] : 0.f, v1 ? x[it][1][e] : 0.f);
     }
   }
 };
@@ -445,6 +498,98 @@ __device__ __forceinline__ void stage_cols_io(const Op<P>& op, const T* g, int l
   t.fetch(g, ldg, rows);
   t.put_cols(op);
 }
+
+// The gates of one thread's row pair (2j, 2j+1) of a chunk, j = threadIdx.x % (C/2) -- the rows
+// the thread stages in RegsT, since NT is a multiple of C/2 -- and of the chunk's last token,
+// held in registers: fetch() only issues loads, the accessors derive (no LDS context, no
+// barrier). cont: same segment as the token before the chunk (-2 before chunk 0); in_last:
+// same segment as the chunk's last token (pallas_tpu_v2.py:226-241).
+template <int C>
+struct PairGates {
+  int s[2], sc, prev;
+  float g[2], l[2], bt[2], gc, lc;
+  bool first;
+  __device__ __forceinline__ void fetch(const GdnArgs& A, int b, int h, int n) {
+    const int j = threadIdx.x % (C / 2);
+    const size_t tb = (size_t)b * A.Tp + (size_t)n * C;
+    const size_t th = (size_t)(b * A.H + h) * A.Tp + (size_t)n * C;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      s[r] = A.segp[tb + 2 * j + r];
+      g[r] = A.gam[th + 2 * j + r];
+      l[r] = A.gaml[th + 2 * j + r];
+      bt[r] = A.bet[th + 2 * j + r];
+    }
+    sc = A.segp[tb + C - 1];
+    gc = A.gam[th + C - 1];
+    lc = A.gaml[th + C - 1];
+    prev = A.segp[n > 0 ? tb - 1 : tb];
+    first = n == 0;
+  }
+  __device__ __forceinline__ int before() const { return first ? -2 : prev; }
+  // e^gamma . cont
+  __device__ __forceinline__ float grow(int r) const { return s[r] == before() ? expf(g[r] + l[r]) : 0.f; }
+  // e^(gamma_C - gamma) . in_last
+  __device__ __forceinline__ float kws(int r) const {
+    return s[r] == sc ? expf((gc - g[r]) + (lc - l[r])) : 0.f;
+  }
+  __device__ __forceinline__ float bg(int r) const { return bt[r] * grow(r); }
+  __device__ __forceinline__ float carry() const { return sc == before() ? expf(gc + lc) : 0.f; }
+};
+
+// The A operand of one wave's 16-row strip over K, fp32 rows of a global tile held raw in
+// registers (rows i0 + lane%16, columns 32s + 8 (lane/16) .. +8): fetch() issues the loads,
+// product() converts and multiplies, as strip_mma_full does from memory.
+template <int K>
+struct StripA {
+  static constexpr int KS = (K + 31) / 32;
+  float x[KS][8];
+  __device__ __forceinline__ void fetch(const float* g, int ld, int i0) {
+    const int l = lane(), r = l & 15, kg = (l >> 4) << 3;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      if ((K % 32 == 0) || (32 * s + kg < K)) {
+        ld8(g + (size_t)(i0 + r) * ld + 32 * s + kg, x[s]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[s][e] = 0.f;
+      }
+    }
+  }
+  template <int P, int TN, class BV>
+  __device__ __forceinline__ void product(f32x4 (&acc)[TN], const BV& B, int j0) const {
+    const int l = lane(), r = l & 15, kg = (l >> 4) << 3;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const bool ok = (K % 32 == 0) || (32 * s + kg < K);
+      const Frag<P> fa = make_frag<P>(x[s]);
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        const Frag<P> fb = ok ? B.template frag<P>(j0 + 16 * t + r, 32 * s + kg) : zero_frag<P>();
+        mma<P>(acc[t], fa, fb);
+      }
+    }
+  }
+};
+
+// The fp32 values of a 16-row strip at the accumulator layout of TN 16-column tiles:
+// v[t][rr] = g[(i0 + acc_row(rr)) * ld + 16t + acc_col()].
+template <int TN>
+struct AccVals {
+  float v[TN][4];
+  __device__ __forceinline__ void fetch(const float* g, int ld, int i0) {
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) v[t][rr] = g[(size_t)(i0 + acc_row(rr)) * ld + 16 * t + acc_col()];
+  }
+  __device__ __forceinline__ void clear() {
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) v[t][rr] = 0.f;
+  }
+};
 
 template <int R, int D, int NT>
 __device__ __forceinline__ void load_tile(float* s, int LD, const float* g) {
@@ -535,18 +680,38 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
 
 // ---------------------------------------------------------------- k_scan_fwd
 // grid B*H*(D/DVT) (XCD-remapped), max(C,D)/16 waves. The state tile S [D x DVT] lives in
-// the accumulators of waves < D/16; chunks in order (pallas_tpu_v2.py:254-269). Operands of
-// each chunk step are staged once: S^T, (k kws)^T and v_new^T.
+// the accumulators of waves < D/16; chunks in order (pallas_tpu_v2.py:254-269). None of a
+// chunk step's global inputs depends on S, so each is held in registers and refilled with the
+// next chunk's values as soon as it has been used: those loads run during the rest of the
+// step (its products and barriers) instead of stalling the next one.
+template <int C, int D, int DVT, int NT>
+struct ScanFwdIn {
+  PairGates<C> gt;     // kws of the thread's k rows, and the carry
+  RegsT<C, D, NT> k;   // k rows, staged as (k kws)^T
+  StripA<D> wa;        // w rows of this wave's strip (waves < C/16)
+  AccVals<DVT / 16> u; // u at the strip's accumulator layout
+  __device__ __forceinline__ void fetch_k(const GdnArgs& A, int b, int hk, int n) {
+    k.fetch(A.kn + hoff(A, b, hk, A.Hk, n, C, D), D);
+  }
+  // waves past the C/16 strips load a strip they do not use: no branch around the loads
+  __device__ __forceinline__ void fetch_w(const GdnArgs& A, int b, int h, int n) {
+    wa.fetch(A.ww + hoff(A, b, h, A.H, n, C, D), D, 16 * (wave() % (C / 16)));
+  }
+  __device__ __forceinline__ void fetch_u(const GdnArgs& A, int b, int h, int n, int j0) {
+    u.fetch(A.uu + hoff(A, b, h, A.H, n, C, D) + j0, D, 16 * (wave() % (C / 16)));
+  }
+};
+
 template <int C, int D, int DVT, int PI, int PS>
 __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
   constexpr int NT = (C > D ? C : D) * 4;
+  constexpr int NW = NT / 64;  // wave conditions below are compile-time when every wave takes part
   using TS = OpTile<PI, DVT, D>;   // S^T: B(k=dk, j) = S[dk][j]
   using TK = OpTile<PI, D, C>;     // (k kws)^T: A(i=dk, k=c)
   using TV = OpTile<PI, DVT, C>;   // v_new^T: B(k=c, j)
   __shared__ __align__(16) char sS[TS::BYTES];
   __shared__ __align__(16) char sK[TK::BYTES];
   __shared__ __align__(16) char sV[TV::BYTES];
-  __shared__ Ctx<C> cx;
   const Op<PI> os = TS::at(sS), ok = TK::at(sK), ov = TV::at(sV);
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int tile = id % A.ntiles, bh = id / A.ntiles, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
@@ -554,9 +719,15 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
   const int w = wave();
   f32x4 accS[DVT / 16];
   zero(accS);
+  ScanFwdIn<C, D, DVT, NT> in;
+  in.gt.fetch(A, b, h, 0);
+  in.fetch_k(A, b, hk, 0);
+  in.fetch_w(A, b, h, 0);
+  in.fetch_u(A, b, h, 0, j0);
   for (int n = 0; n < A.N; ++n) {
+    const int nx = n + 1 < A.N ? n + 1 : n;  // the last step refetches its own chunk (unused)
     float* sg = A.states + ((size_t)bh * A.N + n) * D * D;
-    if (w < D / 16) {
+    if (NW == D / 16 || w < D / 16) {
 #pragma unroll
       for (int t = 0; t < DVT / 16; ++t)
 #pragma unroll
@@ -566,29 +737,32 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
           sg[i * D + j0 + j] = accS[t][rr];
         }
     }
-    load_ctx<C, NT>(cx, A, b, h, n);
-    stage_cols<C, D, NT>(ok, A.kn + hoff(A, b, hk, A.Hk, n, C, D), D, cx.kws);
+    const float carry = in.gt.carry();
+    in.k.put_cols2(ok, in.gt.kws(0), in.gt.kws(1));
+    in.fetch_k(A, b, hk, nx);
+    in.gt.fetch(A, b, h, nx);
     __syncthreads();
-    const size_t off = hoff(A, b, h, A.H, n, C, D);
-    if (w < C / 16) {  // v_new = u - w S
+    if (NW == C / 16 || w < C / 16) {  // v_new = u - w S
       f32x4 acc[DVT / 16];
       zero(acc);
-      strip_mma_full<PS, D, DVT / 16>(acc, krow(A.ww + off, D), 16 * w, os, 0);
+      in.wa.template product<PS>(acc, os, 0);
+      in.fetch_w(A, b, h, nx);
+      const size_t off = hoff(A, b, h, A.H, n, C, D);
 #pragma unroll
       for (int t = 0; t < DVT / 16; ++t)
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
-          const size_t g = off + (size_t)i * D + j0 + j;
-          const float vn = A.uu[g] - acc[t][rr];
+          const float vn = in.u.v[t][rr] - acc[t][rr];
           ov.put(j, i, vn);
-          A.vnew[g] = vn;
+          A.vnew[off + (size_t)i * D + j0 + j] = vn;
         }
+      in.fetch_u(A, b, h, nx, j0);
     }
     __syncthreads();
-    if (w < D / 16) {  // S = carry S + k_write^T v_new
+    if (NW == D / 16 || w < D / 16) {  // S = carry S + k_write^T v_new
 #pragma unroll
-      for (int t = 0; t < DVT / 16; ++t) accS[t] *= cx.carry;
+      for (int t = 0; t < DVT / 16; ++t) accS[t] *= carry;
       strip_mma<PI, C, DVT / 16>(accS, ok, 16 * w, ov, 0);
     }
     __syncthreads();
@@ -715,11 +889,40 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
 // ---------------------------------------------------------------- k_scan_bwd
 // grid B*H*(D/DVT) (XCD-remapped), max(C,D)/16 waves. G [D x DVT] in the accumulators of
 // waves < D/16, chunks reversed (pallas_tpu_v2.py:272-291). Also writes, per chunk and tile,
-// <G_after, S_after> (the last token's d gamma term: sum d_kws kws + d_carry carry).
+// <G_after, S_after> (the last token's d gamma term: sum d_kws kws + d_carry carry). As in the
+// forward scan, every global input of a step is held in registers and refilled with the
+// previous chunk's values once used.
+template <int C, int D, int DVT, int NT, class TIO>
+struct ScanBwdIn {
+  PairGates<C> gt;                // grow and beta grow of the thread's rows, and the carry
+  AccVals<DVT / 16> snext;        // S after the chunk, at G's accumulator layout (waves < D/16)
+  RegsIO<C, DVT, NT, TIO> dov;    // do columns of the tile, staged as do^T
+  RegsT<C, D, NT> qk;             // q rows, staged as (q grow)^T; then k rows, as (-k beta grow)^T
+  StripA<D> kt;                   // Kt rows of this wave's strip (waves < C/16)
+  AccVals<DVT / 16> xl;           // X_loc at the strip's accumulator layout
+  // Loads without branches (a fixed count of memory operations per wave): waves past the
+  // D/16 (C/16) strips load a strip they do not use, and the last chunk loads S before it in
+  // place of the S after it, which does not exist (its partial is 0).
+  __device__ __forceinline__ void fetch_snext(const GdnArgs& A, int bh, int n, int j0) {
+    const int nn = n + 1 < A.N ? n + 1 : n;
+    snext.fetch(A.states + ((size_t)bh * A.N + nn) * D * D + j0, D, 16 * (wave() % (D / 16)));
+  }
+  __device__ __forceinline__ void fetch_do(const GdnArgs& A, int b, int h, int n, int j0) {
+    const TIO* dout = reinterpret_cast<const TIO*>(A.d_out);
+    dov.fetch(dout + (((size_t)b * A.T + (size_t)n * C) * A.H + h) * D + j0, A.H * D, A.T - n * C);
+  }
+  __device__ __forceinline__ void fetch_kt(const GdnArgs& A, int b, int h, int n) {
+    kt.fetch(A.kt + hoff(A, b, h, A.H, n, C, D), D, 16 * (wave() % (C / 16)));
+  }
+  __device__ __forceinline__ void fetch_xl(const GdnArgs& A, int b, int h, int n, int j0) {
+    xl.fetch(A.xl + hoff(A, b, h, A.H, n, C, D) + j0, D, 16 * (wave() % (C / 16)));
+  }
+};
+
 template <int C, int D, int DVT, int PI, int PS, class TIO>
 __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
   constexpr int NT = (C > D ? C : D) * 4;
-  constexpr int NW = NT / 64;
+  constexpr int NW = NT / 64;  // wave conditions below are compile-time when every wave takes part
   using TG_ = OpTile<PI, DVT, D>;  // G^T: B(k=dk, j)
   using TQ = OpTile<PI, D, C>;     // (q grow)^T, then (-k beta grow)^T: A(i=dk, k=c)
   using TD = OpTile<PI, DVT, C>;   // do^T and X^T: B(k=c, j)
@@ -728,20 +931,29 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
   __shared__ __align__(16) char sDo[TD::BYTES];
   __shared__ __align__(16) char sX[TD::BYTES];
   __shared__ float red[NW];
-  __shared__ Ctx<C> cx;
   const Op<PI> og = TG_::at(sG), oq = TQ::at(sQ), odo = TD::at(sDo), ox = TD::at(sX);
   const int id = xcd_remap(blockIdx.x, gridDim.x);
   const int tile = id % A.ntiles, bh = id / A.ntiles, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
   const int j0 = tile * DVT;
   const int w = wave();
-  const TIO* dout = reinterpret_cast<const TIO*>(A.d_out);
   f32x4 accG[DVT / 16];
   zero(accG);
+  ScanBwdIn<C, D, DVT, NT, TIO> in;
+  {
+    const int n = A.N - 1;
+    in.gt.fetch(A, b, h, n);
+    in.fetch_snext(A, bh, n, j0);
+    in.fetch_do(A, b, h, n, j0);
+    in.qk.fetch(A.qn + hoff(A, b, hk, A.Hk, n, C, D), D);
+    in.fetch_kt(A, b, h, n);
+    in.fetch_xl(A, b, h, n, j0);
+  }
   for (int n = A.N - 1; n >= 0; --n) {
+    const int nx = n > 0 ? n - 1 : 0;  // the last step refetches chunk 0 (unused)
+    const bool has_next = n + 1 < A.N;
     float part = 0.f;
-    if (w < D / 16) {
+    if (NW == D / 16 || w < D / 16) {
       float* gdst = A.gg + ((size_t)bh * A.N + n) * D * D;
-      const float* snext = A.states + ((size_t)bh * A.N + n + 1) * D * D;
 #pragma unroll
       for (int t = 0; t < DVT / 16; ++t)
 #pragma unroll
@@ -750,46 +962,52 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
           const float g = accG[t][rr];
           og.put(j, i, g);
           gdst[i * D + j0 + j] = g;
-          if (n + 1 < A.N) part += g * snext[i * D + j0 + j];
+          part += has_next ? g * in.snext.v[t][rr] : 0.f;
         }
+      in.fetch_snext(A, bh, nx, j0);
     }
     part = sum64(part);
     if (lane() == 0) red[w] = part;
-    load_ctx<C, NT>(cx, A, b, h, n);
+    const float carry = in.gt.carry();
+    const float kb0 = -in.gt.bg(0), kb1 = -in.gt.bg(1);
+    in.dov.put_cols(odo);
+    in.fetch_do(A, b, h, nx, j0);
+    in.qk.put_cols2(oq, in.gt.grow(0), in.gt.grow(1));
+    in.qk.fetch(A.kn + hoff(A, b, hk, A.Hk, n, C, D), D);
+    in.gt.fetch(A, b, h, nx);
+    __syncthreads();
     if (threadIdx.x == 0) {
       float s = 0.f;
       for (int q = 0; q < NW; ++q) s += red[q];
       A.gsp[((size_t)bh * A.N + n) * A.ntiles + tile] = s;
     }
-    stage_cols_io<C, DVT, NT>(odo, dout + (((size_t)b * A.T + (size_t)n * C) * A.H + h) * D + j0, A.H * D,
-                              A.T - n * C);
-    stage_cols<C, D, NT>(oq, A.qn + hoff(A, b, hk, A.Hk, n, C, D), D, cx.grow);
-    __syncthreads();
-    const size_t off = hoff(A, b, h, A.H, n, C, D);
-    if (w < C / 16) {  // X = X_loc + Kt G
+    if (NW == C / 16 || w < C / 16) {  // X = X_loc + Kt G
       f32x4 acc[DVT / 16];
       zero(acc);
-      strip_mma_full<PS, D, DVT / 16>(acc, krow(A.kt + off, D), 16 * w, og, 0);
+      in.kt.template product<PS>(acc, og, 0);
+      in.fetch_kt(A, b, h, nx);
+      const size_t off = hoff(A, b, h, A.H, n, C, D);
 #pragma unroll
       for (int t = 0; t < DVT / 16; ++t)
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
-          const size_t g = off + (size_t)i * D + j0 + j;
-          const float xv = A.xl[g] + acc[t][rr];
+          const float xv = in.xl.v[t][rr] + acc[t][rr];
           ox.put(j, i, xv);
-          A.xl[g] = xv;
+          A.xl[off + (size_t)i * D + j0 + j] = xv;
         }
+      in.fetch_xl(A, b, h, nx, j0);
     }
-    if (w < D / 16) {  // G = carry G + q_read^T do
+    if (NW == D / 16 || w < D / 16) {  // G = carry G + q_read^T do
 #pragma unroll
-      for (int t = 0; t < DVT / 16; ++t) accG[t] *= cx.carry;
+      for (int t = 0; t < DVT / 16; ++t) accG[t] *= carry;
       strip_mma<PI, C, DVT / 16>(accG, oq, 16 * w, odo, 0);
     }
     __syncthreads();
-    stage_cols<C, D, NT>(oq, A.kn + hoff(A, b, hk, A.Hk, n, C, D), D, cx.bg, -1.f);
+    in.qk.put_cols2(oq, kb0, kb1);
+    in.qk.fetch(A.qn + hoff(A, b, hk, A.Hk, nx, C, D), D);
     __syncthreads();
-    if (w < D / 16)  // ... - kbe^T X
+    if (NW == D / 16 || w < D / 16)  // ... - kbe^T X
       strip_mma<PI, C, DVT / 16>(accG, oq, 16 * w, ox, 0);
     __syncthreads();
   }

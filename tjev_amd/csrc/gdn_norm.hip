@@ -36,6 +36,7 @@ struct NormArgs {
 
 constexpr int kThreads = 256;
 constexpr int kMaxBwdBlocks = 2048;
+constexpr int kFwdRows = 4;  // rows per lane group in the forward
 
 // round to the storage type and back (what astype(dtype).astype(float32) does)
 template <class T>
@@ -76,26 +77,39 @@ __device__ __forceinline__ void load_row(const void* base, long row, int D, int 
   }
 }
 
-// y = w * rnd(x * rsqrt(mean x^2 + eps)) * silu(z), 0 on padding tokens (norms.py:13-15, 36-40)
+// y = w * rnd(x * rsqrt(mean x^2 + eps)) * silu(z), 0 on padding tokens (norms.py:13-15, 36-40).
+// Each lane group takes kFwdRows rows spaced one workgroup-tile apart, every load issued first.
 template <int D, class T>
 __global__ __launch_bounds__(kThreads) void k_norm_fwd(NormArgs A) {
-  constexpr int LPR = D / 8, RPB = kThreads / LPR;
-  const long row = (long)blockIdx.x * RPB + threadIdx.x / LPR;
+  constexpr int LPR = D / 8, RPB = kThreads / LPR, R = kFwdRows;
   const int c0 = (threadIdx.x % LPR) * 8;
-  const bool live = row < A.rows;
-  float x[8], z[8];
-  load_row<T>(A.x, row, D, c0, live, x);
-  load_row<T>(A.z, row, D, c0, live, z);
-  float ss = 0.f;
+  const long row0 = (long)blockIdx.x * RPB * R + threadIdx.x / LPR;
+  float x[R][8], z[R][8];
+  int sg[R];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
-  ss = group_sum<LPR>(ss);
-  const float r = rsqrtf(ss * (1.0f / D) + A.eps);
-  const bool valid = live && (!A.seg || A.seg[row / A.heads] > 0);
-  float y[8];
+  for (int i = 0; i < R; ++i) {
+    const long row = row0 + (long)i * RPB;
+    load_row<T>(A.x, row, D, c0, row < A.rows, x[i]);
+    load_row<T>(A.z, row, D, c0, row < A.rows, z[i]);
+    sg[i] = (A.seg && row < A.rows) ? A.seg[row / A.heads] : 1;
+  }
+  float w[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = valid ? A.w[c0 + e] * rnd<T>(x[e] * r) * (z[e] * sigmoidf_(z[e])) : 0.f;
-  if (live) st8(static_cast<T*>(A.y) + row * D + c0, y);
+  for (int e = 0; e < 8; ++e) w[e] = A.w[c0 + e];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const long row = row0 + (long)i * RPB;
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += x[i][e] * x[i][e];
+    ss = group_sum<LPR>(ss);
+    const float r = rsqrtf(ss * (1.0f / D) + A.eps);
+    const bool valid = sg[i] > 0;
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = valid ? w[e] * rnd<T>(x[i][e] * r) * (z[i][e] * sigmoidf_(z[i][e])) : 0.f;
+    if (row < A.rows) st8(static_cast<T*>(A.y) + row * D + c0, y);
+  }
 }
 
 // With n = x r, r = rsqrt(mean x^2 + eps), n^ = rnd(n), s = silu(z), g = dy (0 on padding):
@@ -114,39 +128,48 @@ __global__ __launch_bounds__(kThreads) void k_norm_bwd(NormArgs A) {
     w[e] = A.w[c0 + e];
     dwacc[e] = 0.f;
   }
-  for (long base = (long)blockIdx.x * RPB; base < A.rows; base += (long)gridDim.x * RPB) {
-    const long row = base + threadIdx.x / LPR;
-    const bool live = row < A.rows;
-    float x[8], z[8], g[8];
-    load_row<T>(A.x, row, D, c0, live, x);
-    load_row<T>(A.z, row, D, c0, live, z);
-    load_row<T>(A.dy, row, D, c0, live, g);
-    const bool valid = live && (!A.seg || A.seg[row / A.heads] > 0);
-    float ss = 0.f;
+  constexpr int R = 1;  // rows per lane group per iteration (more cost occupancy)
+  for (long base = (long)blockIdx.x * RPB * R; base < A.rows; base += (long)gridDim.x * RPB * R) {
+    float x[R][8], z[R][8], g[R][8];
+    bool valid[R];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
-    ss = group_sum<LPR>(ss);
-    const float r = rsqrtf(ss * (1.0f / D) + A.eps);
-    float n[8], dn[8], dzv[8], dot = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float ge = valid ? g[e] : 0.f;
-      const float sg = sigmoidf_(z[e]);
-      const float s = z[e] * sg;
-      n[e] = x[e] * r;
-      const float nh = rnd<T>(n[e]);
-      dn[e] = rnd<T>(ge * w[e] * s);
-      dzv[e] = ge * w[e] * nh * (sg * (1.f + z[e] * (1.f - sg)));
-      dwacc[e] += ge * nh * s;
-      dot += dn[e] * n[e];
+    for (int i = 0; i < R; ++i) {
+      const long row = base + (long)i * RPB + threadIdx.x / LPR;
+      const bool live = row < A.rows;
+      load_row<T>(A.x, row, D, c0, live, x[i]);
+      load_row<T>(A.z, row, D, c0, live, z[i]);
+      load_row<T>(A.dy, row, D, c0, live, g[i]);
+      valid[i] = live && (!A.seg || A.seg[row / A.heads] > 0);
     }
-    dot = group_sum<LPR>(dot) * (1.0f / D);
-    float dxv[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) dxv[e] = r * (dn[e] - n[e] * dot);
-    if (live) {
-      st8(static_cast<T*>(A.dx) + row * D + c0, dxv);
-      st8(static_cast<T*>(A.dz) + row * D + c0, dzv);
+    for (int i = 0; i < R; ++i) {
+      const long row = base + (long)i * RPB + threadIdx.x / LPR;
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += x[i][e] * x[i][e];
+      ss = group_sum<LPR>(ss);
+      const float r = rsqrtf(ss * (1.0f / D) + A.eps);
+      float n[8], dn[8], dzv[8], dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float ge = valid[i] ? g[i][e] : 0.f;
+        const float sg = sigmoidf_(z[i][e]);
+        const float s = z[i][e] * sg;
+        n[e] = x[i][e] * r;
+        const float nh = rnd<T>(n[e]);
+        dn[e] = rnd<T>(ge * w[e] * s);
+        dzv[e] = ge * w[e] * nh * (sg * (1.f + z[i][e] * (1.f - sg)));
+        dwacc[e] += ge * nh * s;
+        dot += dn[e] * n[e];
+      }
+      dot = group_sum<LPR>(dot) * (1.0f / D);
+      float dxv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dxv[e] = r * (dn[e] - n[e] * dot);
+      if (row < A.rows) {
+        st8(static_cast<T*>(A.dx) + row * D + c0, dxv);
+        st8(static_cast<T*>(A.dz) + row * D + c0, dzv);
+      }
     }
   }
   if (!A.dwp) return;
@@ -172,7 +195,7 @@ __global__ __launch_bounds__(kThreads) void k_norm_reduce(NormArgs A, int D) {
 template <int D, class T>
 hipError_t launch(const NormArgs& A, hipStream_t st, int backward) {
   constexpr int RPB = kThreads / (D / 8);
-  const long blocks = (A.rows + RPB - 1) / RPB;
+  const long blocks = (A.rows + RPB * kFwdRows - 1) / (RPB * kFwdRows);
   const Timer* tm = active_timer();
   auto mark = [&](int k, int end) {
     if (tm) tm->mark(tm->self, k, end, st);
@@ -222,7 +245,7 @@ int validate(const tjev_gdn_norm_params* p) {
 }
 
 int bwd_blocks(const tjev_gdn_norm_params* p) {
-  const long rpb = kThreads / (p->dim / 8);
+  const long rpb = kThreads / (p->dim / 8);  // rows per workgroup iteration
   const long need = (p->tokens * p->heads + rpb - 1) / rpb;
   return (int)(need < kMaxBwdBlocks ? (need > 0 ? need : 1) : kMaxBwdBlocks);
 }

@@ -5,6 +5,8 @@
         per launch): what FETCH_SIZE / WRITE_SIZE read for it calibrates those counters.
     python -m tjev_amd.profiling stats --trace DIR --out FILE.md --command "..."
         Per-kernel launch counts and average durations from a --kernel-trace run (CSV output).
+    python -m tjev_amd.profiling counters DIR [DIR ...] [--out FILE.md]
+        Per-kernel averages of every counter of some --pmc runs.
     python -m tjev_amd.profiling traffic --fetch DIR --write DIR --copy-fetch DIR --copy-write DIR
                                          --copy-mib 1024 --out FILE.json --command "..."
         HBM bytes per launch of every kernel from two --pmc runs (FETCH_SIZE, then WRITE_SIZE),
@@ -29,7 +31,8 @@ from pathlib import Path
 
 _FIXED = [("k_scan_fwd<", "gdn_scan_fwd"), ("k_out<", "gdn_out"), ("k_bwd_local<", "gdn_bwd_local"),
           ("k_scan_bwd<", "gdn_scan_bwd"), ("k_bwd_grads<", "gdn_bwd_grads"), ("k_post<", "gdn_post"),
-          ("k_reduce<", "gdn_reduce")]
+          ("k_reduce<", "gdn_reduce"), ("k_norm_fwd<", "gdn_norm_fwd"), ("k_norm_bwd<", "gdn_norm_bwd"),
+          ("k_norm_reduce", "gdn_norm_reduce")]
 
 
 class _Namer:
@@ -139,6 +142,29 @@ def cmd_traffic(args) -> int:
     return 0
 
 
+def cmd_counters(args) -> int:
+    """Per library kernel, the average per dispatch of every counter in the --pmc runs."""
+    table: dict[str, dict[str, float]] = defaultdict(dict)
+    names: list[str] = []
+    for root in args.runs:
+        rows = _rows(root, "counter_collection.csv")
+        for counter in sorted({r["Counter_Name"] for r in rows}):
+            names.append(counter)
+            for k, v in counter_per_dispatch(root, counter).items():
+                table[k][counter] = statistics.mean(v)
+    kernels = [k for k in table if k.startswith("gdn_")]
+    lines = [f"# Counters: {args.title}", "", "Command:", "", "```", args.command, "```", "",
+             "Average per dispatch.", "", "| kernel | " + " | ".join(names) + " |",
+             "|---|" + "---:|" * len(names)]
+    for k in kernels:
+        lines.append(f"| {k} | " + " | ".join(f"{table[k].get(n, float('nan')):.4g}" for n in names) + " |")
+    text = "\n".join(lines) + "\n"
+    if args.out:
+        Path(args.out).write_text(text)
+    print(text)
+    return 0
+
+
 def cmd_copy_probe(args) -> int:
     import torch
 
@@ -169,8 +195,14 @@ def main(argv=None) -> int:
     p.add_argument("--copy-mib", type=int, default=1024)
     p.add_argument("--title", default="")
     p.add_argument("--command", default="")
+    p = sub.add_parser("counters")
+    p.add_argument("runs", nargs="+", help="rocprofv3 --pmc output directories (CSV)")
+    p.add_argument("--out", default=None)
+    p.add_argument("--title", default="")
+    p.add_argument("--command", default="")
     args = ap.parse_args(argv)
-    return {"copy-probe": cmd_copy_probe, "stats": cmd_stats, "traffic": cmd_traffic}[args.cmd](args)
+    return {"copy-probe": cmd_copy_probe, "stats": cmd_stats, "traffic": cmd_traffic,
+            "counters": cmd_counters}[args.cmd](args)
 
 
 if __name__ == "__main__":

@@ -52,15 +52,21 @@ def kernel_work(*, batch: int, length: int, key_heads: int, value_heads: int, di
         "gdn_post": {"bound": "hbm", "bytes": tokens * width * io_bytes * 2 + 3 * tok_h * D * f32
                      + 2 * tokens * value_heads * io_bytes},
         "gdn_reduce": {"bound": "hbm", "bytes": batch * n * value_heads * 16},
+        # gated RMSNorm: read x, z, write y; backward read x, z, dy, write dx, dz
+        "gdn_norm_fwd": {"bound": "hbm", "bytes": 3 * tokens * value_heads * D * io_bytes},
+        "gdn_norm_bwd": {"bound": "hbm", "bytes": 5 * tokens * value_heads * D * io_bytes},
+        "gdn_norm_reduce": {"bound": "hbm", "bytes": 2048 * D * f32},
     }
     return w
 
 
 def operator_work(*, batch: int, length: int, key_heads: int, value_heads: int, dim: int, chunk: int,
-                  io_bytes: int) -> dict:
+                  io_bytes: int, norm: bool = False) -> dict:
     """Whole fwd+bwd: algorithmic FLOPs (per token-head 18 C Dk + 14 C Dv + 2/3 C^2 + 20 Dk Dv)
     and minimal HBM bytes at the operator boundary (inputs, output, fp32 chunk states, the
-    gradients), and the roofline time max(t_mfma, t_hbm) at the bf16 / HBM peaks."""
+    gradients), and the roofline time max(t_mfma, t_hbm) at the bf16 / HBM peaks. With the
+    gated RMSNorm epilogue (``norm``) also its gate z and output y forward, and z, out and
+    d z backward (out stays the saved residual; elementwise, no FLOPs counted)."""
     C, D = chunk, dim
     tokens = batch * length
     th = tokens * value_heads
@@ -70,6 +76,9 @@ def operator_work(*, batch: int, length: int, key_heads: int, value_heads: int, 
     state = value_heads * D * D * 4 / C
     fwd = tokens * (width * s + 2 * value_heads * s + value_heads * D * s + state)
     bwd = tokens * (2 * width * s + 2 * value_heads * s + state + value_heads * D * s + 2 * value_heads * 4)
+    if norm:
+        fwd += tokens * 2 * value_heads * D * s
+        bwd += tokens * 3 * value_heads * D * s
     t_mfma = flops / (PEAK_BF16_TFLOPS * 1e12)
     t_hbm = (fwd + bwd) / (PEAK_HBM_GBS * 1e9)
     return {"flops": flops, "bytes": fwd + bwd, "t_mfma_s": t_mfma, "t_hbm_s": t_hbm,
