@@ -386,57 +386,90 @@ struct Regs {
   }
 };
 
-// The transposing load: an R x K fp32 tile (R even), each slot two consecutive source rows x 4
-// columns, so that the lanes of a wave hold consecutive row pairs and write the transposed tile
-// op(c, r) = g[r][c] * ks[r] * cst as consecutive 32-bit words. (One element per lane down a
-// column of a padded tile hits only a few LDS banks.)
-template <int R, int K, int NT>
+// z[e] = x[(e + rot) mod E] for a lane-dependent rot (a multiple of 2 below E), by one select
+// stage per bit of rot: static register indices only (a dynamic index would put x in scratch).
+template <int E>
+__device__ __forceinline__ void rotate(const float (&x)[E], int rot, float (&z)[E]) {
+#pragma unroll
+  for (int e = 0; e < E; ++e) z[e] = x[e];
+#pragma unroll
+  for (int bit = E / 2; bit >= 2; bit /= 2) {
+    float y[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) y[e] = (rot & bit) ? z[(e + bit) % E] : z[e];
+#pragma unroll
+    for (int e = 0; e < E; ++e) z[e] = y[e];
+  }
+}
+
+// The transposing load: an R x K fp32 tile (R even) staged as op(c, r) = g[r][c] * ks[r] * cst.
+// Slot mapping: G consecutive lanes read 4 consecutive columns each of one source row pair
+// (a 128-byte row segment per 8 lanes: coalesced), then the next row pair. Each lane holds rows
+// 2j and 2j+1 and writes them as 32-bit pairs of the transposed tile; lane groups q >= 4 write
+// their 4 columns in a rotated order so that the 8 groups of one write instruction fall in
+// distinct LDS banks (bf16 operand rows of (R + 8)/2 words); without ROT (fewer registers)
+// two groups share the banks of each write.
+template <int R, int K, int NT, bool ROT = true>
 struct RegsT {
   static constexpr int RP = R / 2;
   static constexpr int V = K / 4;
+  static constexpr int G = V < 8 ? V : 8;
   static constexpr int IT = (RP * V + NT - 1) / NT;
   float4 a[IT], b[IT];
   __device__ __forceinline__ static bool live(int it) {
     return (RP * V) % NT == 0 || (int)threadIdx.x + it * NT < RP * V;
   }
+  __device__ __forceinline__ static void slot(int it, int& q, int& j, int& c) {
+    const int idx = ((int)threadIdx.x + it * NT) % (RP * V), rest = idx / G;
+    q = idx % G;
+    j = rest % RP;
+    c = 4 * (q + G * (rest / RP));
+  }
+  // every thread loads (slots past the tile repeat one inside it): no branch around the loads
   __device__ __forceinline__ void fetch(const float* g, int ldg) {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const int idx = threadIdx.x + it * NT, j = idx % RP, c = 4 * (idx / RP);
-      if (live(it)) {
-        a[it] = *reinterpret_cast<const float4*>(g + (size_t)(2 * j) * ldg + c);
-        b[it] = *reinterpret_cast<const float4*>(g + (size_t)(2 * j + 1) * ldg + c);
-      }
+      int q, j, c;
+      slot(it, q, j, c);
+      a[it] = *reinterpret_cast<const float4*>(g + (size_t)(2 * j) * ldg + c);
+      b[it] = *reinterpret_cast<const float4*>(g + (size_t)(2 * j + 1) * ldg + c);
     }
+  }
+  template <int P>
+  __device__ __forceinline__ void put(const Op<P>& op, int it, float fa, float fb) const {
+    int q, j, c;
+    slot(it, q, j, c);
+    const float xa[4] = {a[it].x, a[it].y, a[it].z, a[it].w};
+    const float xb[4] = {b[it].x, b[it].y, b[it].z, b[it].w};
+    const int rot = ROT && G == 8 ? 2 * (q / 4) : 0;
+    float za[4], zb[4];
+    rotate(xa, rot, za);
+    rotate(xb, rot, zb);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) op.put2(c + ((e + rot) & 3), 2 * j, za[e] * fa, zb[e] * fb);
   }
   template <int P>
   __device__ __forceinline__ void put_cols(const Op<P>& op, const float* ks = nullptr, float cst = 1.f) const {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
       if (!live(it)) continue;
-      const int idx = threadIdx.x + it * NT, j = idx % RP, c = 4 * (idx / RP);
-      const float fa = (ks ? ks[2 * j] : 1.f) * cst, fb = (ks ? ks[2 * j + 1] : 1.f) * cst;
-      op.put2(c, 2 * j, a[it].x * fa, b[it].x * fb);
-      op.put2(c + 1, 2 * j, a[it].y * fa, b[it].y * fb);
-      op.put2(c + 2, 2 * j, a[it].z * fa, b[it].z * fb);
-      op.put2(c + 3, 2 * j, a[it].w * fa, b[it].w * fb);
+      int q, j, c;
+      slot(it, q, j, c);
+      put(op, it, (ks ? ks[2 * j] : 1.f) * cst, (ks ? ks[2 * j + 1] : 1.f) * cst);
     }
   }
-  // the same with the thread's row pair scaled by (fa, fb) (j is the same in every slot when
-  // NT is a multiple of R/2)
+  // the same with the thread's row pair scaled by (fa, fb): a thread's j is the same in every
+  // slot when NT is a multiple of G * R/2
   template <int P>
   __device__ __forceinline__ void put_cols2(const Op<P>& op, float fa, float fb) const {
-    static_assert(NT % RP == 0, "one row pair per thread");
+    static_assert(NT % (G * RP) == 0, "one row pair per thread");
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      if (!live(it)) continue;
-      const int idx = threadIdx.x + it * NT, j = idx % RP, c = 4 * (idx / RP);
-      op.put2(c, 2 * j, a[it].x * fa, b[it].x * fb);
-      op.put2(c + 1, 2 * j, a[it].y * fa, b[it].y * fb);
-      op.put2(c + 2, 2 * j, a[it].z * fa, b[it].z * fb);
-      op.put2(c + 3, 2 * j, a[it].w * fa, b[it].w * fb);
+      if (live(it)) put(op, it, fa, fb);
     }
   }
+  // the row pair (2j, 2j+1) this thread holds (put_cols2's rows)
+  __device__ __forceinline__ static int pair() { return ((int)threadIdx.x / G) % RP; }
 };
 
 template <int R, int K, int NT, int P>
@@ -456,15 +489,52 @@ __device__ __forceinline__ void stage_cols(const Op<P>& op, const float* g, int 
 // An R x K tile of a token-major activation (fp32 or bf16, rows past `rows` read as 0), 8
 // consecutive values per slot and two consecutive rows per slot, fetched at once and written
 // transposed as 32-bit row pairs: op(c, r) = g[r][c].
+// An R x K tile of a token-major activation (fp32 or bf16, rows past `rows` read as 0) staged
+// transposed: op(c, r) = g[r][c]. As RegsT with 8 consecutive values per lane (16 bytes of
+// bf16): G consecutive lanes read one row segment, lane groups rotate their write order so
+// the groups of one LDS write instruction fall in distinct banks.
+// 8 consecutive stored values held as loaded (bf16 stays packed), converted when used
+template <class T> struct Raw8;
+template <> struct Raw8<float> {
+  float4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = reinterpret_cast<const float4*>(p)[0];
+    b = reinterpret_cast<const float4*>(p)[1];
+  }
+  __device__ __forceinline__ void get(float (&o)[8]) const {
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  }
+};
+template <> struct Raw8<uint16_t> {
+  uint4 a;
+  __device__ __forceinline__ void load(const uint16_t* p) { a = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ void get(float (&o)[8]) const {
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[2 * e] = __uint_as_float(w[e] << 16);
+      o[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+    }
+  }
+};
+
 template <int R, int K, int NT, class T>
 struct RegsIO {
   static constexpr int RP = R / 2;
   static constexpr int V = K / 8;
+  static constexpr int G = V < 8 ? V : 8;
   static constexpr int IT = (RP * V + NT - 1) / NT;
-  float x[IT][2][8];
+  Raw8<T> x[IT][2];
   int rows;
   __device__ __forceinline__ static bool live(int it) {
     return (RP * V) % NT == 0 || (int)threadIdx.x + it * NT < RP * V;
+  }
+  __device__ __forceinline__ static void slot(int it, int& q, int& j, int& c) {
+    const int idx = ((int)threadIdx.x + it * NT) % (RP * V), rest = idx / G;
+    q = idx % G;
+    j = rest % RP;
+    c = 8 * (q + G * (rest / RP));
   }
   // Every thread loads (slots past the tile repeat one inside it, rows past `rows` >= 1 repeat
   // the last valid row): no branch around the loads and no use of them until put_cols.
@@ -472,11 +542,12 @@ struct RegsIO {
     rows = rows_;
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const int idx = (threadIdx.x + it * NT) % (RP * V), j = idx % RP, c = 8 * (idx / RP);
+      int q, j, c;
+      slot(it, q, j, c);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int r = 2 * j + h;
-        ld8(g + (size_t)(r < rows ? r : rows - 1) * ldg + c, x[it][h]);
+        x[it][h].load(g + (size_t)(r < rows ? r : rows - 1) * ldg + c);
       }
     }
   }
@@ -485,10 +556,17 @@ struct RegsIO {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
       if (!live(it)) continue;
-      const int idx = threadIdx.x + it * NT, j = idx % RP, c = 8 * (idx / RP);
+      int q, j, c;
+      slot(it, q, j, c);
       const bool v0 = 2 * j < rows, v1 = 2 * j + 1 < rows;
+      const int rot = G == 8 ? 2 * (q / 2) : G == 4 ? 4 * (q / 2) : 0;
+      float x0[8], x1[8], z0[8], z1[8];
+      x[it][0].get(x0);
+      x[it][1].get(x1);
+      rotate(x0, rot, z0);
+      rotate(x1, rot, z1);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) op.put2(c + e, 2 * j, v0 ? x[it][0][e] : 0.f, v1 ? x[it][1][e] : 0.f);
+      for (int e = 0; e < 8; ++e) op.put2(c + ((e + rot) & 7), 2 * j, v0 ? z0[e] : 0.f, v1 ? z1[e] : 0.f);
     }
   }
 };
@@ -499,8 +577,8 @@ __device__ __forceinline__ void stage_cols_io(const Op<P>& op, const T* g, int l
   t.put_cols(op);
 }
 
-// The gates of one thread's row pair (2j, 2j+1) of a chunk, j = threadIdx.x % (C/2) -- the rows
-// the thread stages in RegsT, since NT is a multiple of C/2 -- and of the chunk's last token,
+// The gates of one thread's row pair (2j, 2j+1) of a chunk -- the rows the thread stages in
+// RegsT (RegsT::pair()) -- and of the chunk's last token,
 // held in registers: fetch() only issues loads, the accessors derive (no LDS context, no
 // barrier). cont: same segment as the token before the chunk (-2 before chunk 0); in_last:
 // same segment as the chunk's last token (pallas_tpu_v2.py:226-241).
@@ -509,8 +587,8 @@ struct PairGates {
   int s[2], sc, prev;
   float g[2], l[2], bt[2], gc, lc;
   bool first;
-  __device__ __forceinline__ void fetch(const GdnArgs& A, int b, int h, int n) {
-    const int j = threadIdx.x % (C / 2);
+  // j: the row pair the thread stages (RegsT::pair())
+  __device__ __forceinline__ void fetch(const GdnArgs& A, int b, int h, int n, int j) {
     const size_t tb = (size_t)b * A.Tp + (size_t)n * C;
     const size_t th = (size_t)(b * A.H + h) * A.Tp + (size_t)n * C;
 #pragma unroll
@@ -720,7 +798,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
   f32x4 accS[DVT / 16];
   zero(accS);
   ScanFwdIn<C, D, DVT, NT> in;
-  in.gt.fetch(A, b, h, 0);
+  in.gt.fetch(A, b, h, 0, RegsT<C, D, NT>::pair());
   in.fetch_k(A, b, hk, 0);
   in.fetch_w(A, b, h, 0);
   in.fetch_u(A, b, h, 0, j0);
@@ -740,7 +818,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
     const float carry = in.gt.carry();
     in.k.put_cols2(ok, in.gt.kws(0), in.gt.kws(1));
     in.fetch_k(A, b, hk, nx);
-    in.gt.fetch(A, b, h, nx);
+    in.gt.fetch(A, b, h, nx, RegsT<C, D, NT>::pair());
     __syncthreads();
     if (NW == C / 16 || w < C / 16) {  // v_new = u - w S
       f32x4 acc[DVT / 16];
@@ -897,7 +975,8 @@ struct ScanBwdIn {
   PairGates<C> gt;                // grow and beta grow of the thread's rows, and the carry
   AccVals<DVT / 16> snext;        // S after the chunk, at G's accumulator layout (waves < D/16)
   RegsIO<C, DVT, NT, TIO> dov;    // do columns of the tile, staged as do^T
-  RegsT<C, D, NT> qk;             // q rows, staged as (q grow)^T; then k rows, as (-k beta grow)^T
+  RegsT<C, D, NT, false> qk;      // q rows, staged as (q grow)^T; then k rows, as (-k beta grow)^T
+                                  // (no write rotation: this kernel is at its register limit)
   StripA<D> kt;                   // Kt rows of this wave's strip (waves < C/16)
   AccVals<DVT / 16> xl;           // X_loc at the strip's accumulator layout
   // Loads without branches (a fixed count of memory operations per wave): waves past the
@@ -941,7 +1020,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
   ScanBwdIn<C, D, DVT, NT, TIO> in;
   {
     const int n = A.N - 1;
-    in.gt.fetch(A, b, h, n);
+    in.gt.fetch(A, b, h, n, RegsT<C, D, NT>::pair());
     in.fetch_snext(A, bh, n, j0);
     in.fetch_do(A, b, h, n, j0);
     in.qk.fetch(A.qn + hoff(A, b, hk, A.Hk, n, C, D), D);
@@ -974,7 +1053,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
     in.fetch_do(A, b, h, nx, j0);
     in.qk.put_cols2(oq, in.gt.grow(0), in.gt.grow(1));
     in.qk.fetch(A.kn + hoff(A, b, hk, A.Hk, n, C, D), D);
-    in.gt.fetch(A, b, h, nx);
+    in.gt.fetch(A, b, h, nx, RegsT<C, D, NT>::pair());
     __syncthreads();
     if (threadIdx.x == 0) {
       float s = 0.f;
