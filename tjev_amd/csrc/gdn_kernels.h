@@ -265,38 +265,62 @@ __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
                          : A.vv + hoff(A, b, head, A.H, n, C, D);
   float wl[5][8];
   lag_weights(A, cc, wl);
-#pragma unroll 2
-  for (int r = threadIdx.x / CG; r < C; r += RPP) {
-    const int t = n * C + r;
-    const int st = t < A.T ? sg[t] : 0;
-    float act[8];
-    if (t >= A.T) {  // the padded tail: zero qkv, segment 0
+  // Each group of CG lanes owns RG consecutive rows of the chunk and loads them with the HW rows
+  // before them (the conv halo) and their segment ids at once, at clamped addresses without
+  // branches; the conv then slides over registers (every raw row is read once).
+  constexpr int RG = C / RPP > 0 ? C / RPP : 1;
+  constexpr int HW = 4;  // taps - 1 <= 4
+  const int r0 = (threadIdx.x / CG) * RG;
+  if (RG * RPP == C || r0 < C) {
+    Raw8<TIO> raw[RG + HW];
+    int sgv[RG + HW];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) act[e] = 0.f;
-    } else if (A.taps == 0) {  // mega1: qkv is already the activation
-      ld8(x + ((size_t)b * A.T + t) * A.W + cc, act);
-    } else {  // every tap index t-L < T reads a real segment id
-      float xs[5][8], z[8];
-      bool keep[5];
-      conv_rows(A, x, sg, b, t, cc, st, xs, keep);
-      conv_z(xs, keep, wl, z);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) act[e] = st > 0 ? z[e] * sigmoidf_(z[e]) : 0.f;
+    for (int i = 0; i < RG + HW; ++i) {
+      const int tt = n * C + r0 - HW + i;
+      const int tc = tt < 0 ? 0 : (tt < A.T ? tt : A.T - 1);
+      raw[i].load(x + ((size_t)b * A.T + tc) * A.W + cc);
+      sgv[i] = sg[tc];
     }
-    if (kind < 2) {  // l2norm over the head's D channels (CG lanes)
-      float sq = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sq += act[e] * act[e];
+    for (int i = 0; i < RG; ++i) {
+      const int r = r0 + i, t = n * C + r;
+      const int st = t < A.T ? sgv[HW + i] : 0;  // the padded tail: segment 0
+      float act[8];
+      if (A.taps == 0) {  // mega1: qkv is already the activation (zero on the tail)
+        raw[HW + i].get(act);
 #pragma unroll
-      for (int m = 1; m < CG; m <<= 1) sq += __shfl_xor(sq, m);
-      float rn = sq == 0.f ? 0.f : 1.0f / sqrtf(sq + 1e-6f);
-      if (kind == 0) rn *= A.scale;
+        for (int e = 0; e < 8; ++e) act[e] = t < A.T ? act[e] : 0.f;
+      } else {  // z = sum over lags of keep * x[t-L] * w[K-1-L], lag 0 first (causal_conv1d.py:42-45)
+        float z[8];
+        raw[HW + i].get(z);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) act[e] *= rn;
+        for (int e = 0; e < 8; ++e) z[e] *= wl[0][e];
+#pragma unroll
+        for (int L = 1; L <= HW; ++L) {
+          const bool keep = L < A.taps && t - L >= 0 && sgv[HW + i - L] == st;
+          float xl[8];
+          raw[HW + i - L].get(xl);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) z[e] = keep ? z[e] + xl[e] * wl[L][e] : z[e];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) act[e] = st > 0 ? z[e] * sigmoidf_(z[e]) : 0.f;
+      }
+      if (kind < 2) {  // l2norm over the head's D channels (CG lanes)
+        float sq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sq += act[e] * act[e];
+#pragma unroll
+        for (int m = 1; m < CG; m <<= 1) sq += __shfl_xor(sq, m);
+        float rn = sq == 0.f ? 0.f : 1.0f / sqrtf(sq + 1e-6f);
+        if (kind == 0) rn *= A.scale;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) act[e] *= rn;
+      }
+      float4* o = reinterpret_cast<float4*>(dst + (size_t)r * D + cg * 8);
+      o[0] = make_float4(act[0], act[1], act[2], act[3]);
+      o[1] = make_float4(act[4], act[5], act[6], act[7]);
     }
-    float4* o = reinterpret_cast<float4*>(dst + (size_t)r * D + cg * 8);
-    o[0] = make_float4(act[0], act[1], act[2], act[3]);
-    o[1] = make_float4(act[4], act[5], act[6], act[7]);
   }
   if (slot == 0) {
     for (int i = threadIdx.x; i < C; i += 256) {
@@ -493,32 +517,6 @@ __device__ __forceinline__ void stage_cols(const Op<P>& op, const float* g, int 
 // transposed: op(c, r) = g[r][c]. As RegsT with 8 consecutive values per lane (16 bytes of
 // bf16): G consecutive lanes read one row segment, lane groups rotate their write order so
 // the groups of one LDS write instruction fall in distinct banks.
-// 8 consecutive stored values held as loaded (bf16 stays packed), converted when used
-template <class T> struct Raw8;
-template <> struct Raw8<float> {
-  float4 a, b;
-  __device__ __forceinline__ void load(const float* p) {
-    a = reinterpret_cast<const float4*>(p)[0];
-    b = reinterpret_cast<const float4*>(p)[1];
-  }
-  __device__ __forceinline__ void get(float (&o)[8]) const {
-    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
-    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
-  }
-};
-template <> struct Raw8<uint16_t> {
-  uint4 a;
-  __device__ __forceinline__ void load(const uint16_t* p) { a = *reinterpret_cast<const uint4*>(p); }
-  __device__ __forceinline__ void get(float (&o)[8]) const {
-    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      o[2 * e] = __uint_as_float(w[e] << 16);
-      o[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
-    }
-  }
-};
-
 template <int R, int K, int NT, class T>
 struct RegsIO {
   static constexpr int RP = R / 2;
