@@ -1245,76 +1245,96 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
   float wl[5][8];
   lag_weights(A, cc, wl);
   const int rows = C + (taps > 1 ? taps - 1 : 0);
-  // phase 1: dz for the chunk and the look-ahead rows, into LDS
-#pragma unroll 2
-  for (int r = threadIdx.x / CG; r < R; r += RPP) {
-    const int t = n * C + r;
-    float dz[8];
-    int st = -3;
-    if (r < rows && t < A.Tp) {  // uniform over the CG lanes of the row
-      st = sp[t];
-      float xs[5][8], z[8], act[8];
-      bool keep[5];
-      if (taps == 0) {
-        if (t < A.T) {
-          ld8(x + ((size_t)b * A.T + t) * A.W + cc, act);
-        } else {
+  // phase 1: dz for the chunk and the look-ahead rows, into LDS. Each group of CG lanes owns
+  // RG consecutive rows: their raw rows with the conv halo, segment ids and incoming gradients
+  // are all loaded first (clamped addresses, no branches), then computed from registers.
+  constexpr int HW = 4;  // taps - 1 <= 4
+  constexpr int RG = (R + RPP - 1) / RPP;
+  const int r0 = (threadIdx.x / CG) * RG;
+  Raw8<TIO> raw[RG + HW];
+  int sgv[RG + HW];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) act[e] = 0.f;
-        }
-      } else {
-        conv_rows(A, x, sp, b, t, cc, st, xs, keep);
-        conv_z(xs, keep, wl, z);
+  for (int i = 0; i < RG + HW; ++i) {
+    const int tt = n * C + r0 - HW + i;
+    const int tc = tt < 0 ? 0 : (tt < A.T ? tt : A.T - 1);
+    const int ts = tt < 0 ? 0 : (tt < A.Tp ? tt : A.Tp - 1);
+    raw[i].load(x + ((size_t)b * A.T + tc) * A.W + cc);
+    sgv[i] = sp[ts];
+  }
+  float dyv[RG][8], btv[RG];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) act[e] = st > 0 ? z[e] * sigmoidf_(z[e]) : 0.f;
+  for (int i = 0; i < RG; ++i) {
+    const int t = n * C + r0 + i, tl = t < A.Tp ? t : A.Tp - 1;
+    if (kind < 2) {  // GQA sum over the value heads of this key head
+      const float* src = (kind == 0 ? A.dqh : A.dkh) + ((size_t)(b * A.H + head * A.ratio) * A.Tp + tl) * D + cg * 8;
+      ld8(src, dyv[i]);
+      for (int v = 1; v < A.ratio; ++v) {
+        float y[8];
+        ld8(src + (size_t)v * A.Tp * D, y);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dyv[i][e] += y[e];
       }
-      float dy[8];
-      if (kind < 2) {  // GQA sum over the value heads of this key head, then l2norm backward
-        const float* src = kind == 0 ? A.dqh : A.dkh;
+    } else {  // dv = X beta
+      ld8(A.xl + ((size_t)(b * A.H + head) * A.Tp + tl) * D + cg * 8, dyv[i]);
+      btv[i] = A.bet[(size_t)(b * A.H + head) * A.Tp + tl];
+    }
+  }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dy[e] = 0.f;
-        for (int v = 0; v < A.ratio; ++v) {
-          float y[8];
-          ld8(src + ((size_t)(b * A.H + head * A.ratio + v) * A.Tp + t) * D + cg * 8, y);
+  for (int i = 0; i < RG; ++i) {
+    const int r = r0 + i, t = n * C + r;
+    if (r >= R) break;
+    const bool live = r < rows && t < A.Tp;  // uniform over the CG lanes of the row
+    const int st = live ? sgv[HW + i] : -3;
+    float z[8], act[8], dy[8];
+    if (taps == 0) {
+      raw[HW + i].get(act);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) dy[e] += y[e];
-        }
-        if (kind == 0) {
+      for (int e = 0; e < 8; ++e) act[e] = t < A.T ? act[e] : 0.f;
+    } else {  // z = sum over lags of keep * x[t-L] * w[K-1-L], lag 0 first
+      raw[HW + i].get(z);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) dy[e] *= A.scale;
-        }
-        float sq = 0.f;
+      for (int e = 0; e < 8; ++e) z[e] *= wl[0][e];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sq += act[e] * act[e];
+      for (int L = 1; L <= HW; ++L) {
+        const bool keep = L < taps && t - L >= 0 && sgv[HW + i - L] == st;
+        float xl[8];
+        raw[HW + i - L].get(xl);
 #pragma unroll
-        for (int m = 1; m < CG; m <<= 1) sq += __shfl_xor(sq, m);
-        const float rn = sq == 0.f ? 0.f : 1.0f / sqrtf(sq + 1e-6f);
-        float dot = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dot += act[e] * rn * dy[e];
-#pragma unroll
-        for (int m = 1; m < CG; m <<= 1) dot += __shfl_xor(dot, m);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dy[e] = rn * (dy[e] - act[e] * rn * dot);
-      } else {  // dv = X beta
-        const float bt = A.bet[(size_t)(b * A.H + head) * A.Tp + t];
-        ld8(A.xl + ((size_t)(b * A.H + head) * A.Tp + t) * D + cg * 8, dy);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dy[e] *= bt;
+        for (int e = 0; e < 8; ++e) z[e] = keep ? z[e] + xl[e] * wl[L][e] : z[e];
       }
-      if (taps == 0) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dz[e] = dy[e];
-      } else {  // SiLU backward on valid tokens
+      for (int e = 0; e < 8; ++e) act[e] = st > 0 ? z[e] * sigmoidf_(z[e]) : 0.f;
+    }
+    if (kind < 2) {  // l2norm backward (q's scale first)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float sgm = sigmoidf_(z[e]);
-          dz[e] = st > 0 ? dy[e] * sgm * (1.f + z[e] * (1.f - sgm)) : 0.f;
-        }
-      }
+      for (int e = 0; e < 8; ++e) dy[e] = kind == 0 ? dyv[i][e] * A.scale : dyv[i][e];
+      float sq = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sq += act[e] * act[e];
+#pragma unroll
+      for (int m = 1; m < CG; m <<= 1) sq += __shfl_xor(sq, m);
+      const float rn = sq == 0.f ? 0.f : 1.0f / sqrtf(sq + 1e-6f);
+      float dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot += act[e] * rn * dy[e];
+#pragma unroll
+      for (int m = 1; m < CG; m <<= 1) dot += __shfl_xor(dot, m);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dy[e] = rn * (dy[e] - act[e] * rn * dot);
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dz[e] = 0.f;
+      for (int e = 0; e < 8; ++e) dy[e] = dyv[i][e] * btv[i];
+    }
+    float dz[8];
+    if (taps == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dz[e] = live ? dy[e] : 0.f;
+    } else {  // SiLU backward on valid tokens
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float sgm = sigmoidf_(z[e]);
+        dz[e] = (live && st > 0) ? dy[e] * sgm * (1.f + z[e] * (1.f - sgm)) : 0.f;
+      }
     }
     float4* o = reinterpret_cast<float4*>(sdz + r * LZ + cg * 8);
     o[0] = make_float4(dz[0], dz[1], dz[2], dz[3]);
