@@ -10,6 +10,20 @@
 namespace gdn {
 namespace {
 
+// compute units of the current device (queried once per device): the persistent kernels run
+// one workgroup per CU
+int cu_count() {
+  static int cache[16] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) dev = 0;
+  if (!cache[dev]) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+    cache[dev] = c;
+  }
+  return cache[dev];
+}
+
 template <int C, int D, int PI, int PS, class TIO, class TG>
 hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) {
   constexpr int DVT = D < 32 ? D : 32;
@@ -17,6 +31,8 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
   const dim3 prep(A.B * A.N, 2 * A.Hk + A.H);
   const dim3 chunks(A.B * A.H * A.N);
   const dim3 tiles(A.B * A.H * (D / DVT));
+  const int units = A.B * A.H * A.N, cus = cu_count();
+  const dim3 persist(units < cus ? units : cus);
   auto mark = [&](int k, int end) {
     if (tm) tm->mark(tm->self, k, end, st);
   };
@@ -30,7 +46,7 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
     GDN_LAUNCH(K_PREP_FWD, (k_prep<C, D, TIO, TG>), prep, dim3(256));
     GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0>), chunks, dim3(C * 4));
     GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd<C, D, DVT, PI, PS>), tiles, dim3(NS));
-    GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO>), chunks, dim3(C * 4));
+    GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO>), persist, dim3(C * 4));
   } else {
     const int outs = A.H + (A.d_conv_w ? A.taps * A.W : 0);
     GDN_LAUNCH(K_PREP_BWD, (k_prep<C, D, TIO, TG>), prep, dim3(256));

@@ -632,17 +632,25 @@ struct StripA {
       }
     }
   }
+  // acc[t] += (rs * A)(strip) B(., j0 + 16t ..) for the tiles t < tn; rs scales this lane's
+  // A row (i0 + lane%16)
   template <int P, int TN, class BV>
-  __device__ __forceinline__ void product(f32x4 (&acc)[TN], const BV& B, int j0) const {
+  __device__ __forceinline__ void product(f32x4 (&acc)[TN], const BV& B, int j0, int tn = TN,
+                                         float rs = 1.f) const {
     const int l = lane(), r = l & 15, kg = (l >> 4) << 3;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const bool ok = (K % 32 == 0) || (32 * s + kg < K);
-      const Frag<P> fa = make_frag<P>(x[s]);
+      float xs[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xs[e] = x[s][e] * rs;
+      const Frag<P> fa = make_frag<P>(xs);
 #pragma unroll
       for (int t = 0; t < TN; ++t) {
-        const Frag<P> fb = ok ? B.template frag<P>(j0 + 16 * t + r, 32 * s + kg) : zero_frag<P>();
-        mma<P>(acc[t], fa, fb);
+        if (t < tn) {
+          const Frag<P> fb = ok ? B.template frag<P>(j0 + 16 * t + r, 32 * s + kg) : zero_frag<P>();
+          mma<P>(acc[t], fa, fb);
+        }
       }
     }
   }
@@ -846,7 +854,31 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
 }
 
 // ---------------------------------------------------------------- k_out
-// grid B*H*N, C/16 waves: o = ((q k^T) . D) v_new + q_read S_before, token-major output.
+// Persistent: one workgroup per CU (grid <= number of units) loops over the (row, head, chunk)
+// units blockIdx.x, + gridDim.x, ...; C/16 waves. Per unit: o = ((q k^T) . D) v_new + q_read
+// S_before, token-major output. Every global input of a unit is held in registers and refilled
+// with the next unit's values right after it has been used, so its loads run during the rest
+// of the unit instead of stalling the next one.
+template <int C, int D, int NT>
+struct OutIn {
+  CtxRaw<C> cx;
+  Regs<C, D, NT> k;      // k rows: B(d, j) = k[j][d]
+  StripA<D> q;           // this wave's q rows (A operand of q k^T and of q_read S)
+  RegsT<C, D, NT> v;     // v_new rows, staged as v_new^T
+  RegsT<D, D, NT> st;    // S_before rows, staged as S^T
+};
+
+struct UnitIx {
+  int n, bh, h, b, hk;
+  __device__ __forceinline__ UnitIx(const GdnArgs& A, int u) {
+    n = u % A.N;
+    bh = u / A.N;
+    h = bh % A.H;
+    b = bh / A.H;
+    hk = h / A.ratio;
+  }
+};
+
 template <int C, int D, int PI, int PS, class TIO>
 __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
   constexpr int NT = C * 4;
@@ -857,45 +889,64 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
   __shared__ __align__(16) char sB[TB::BYTES];
   __shared__ Ctx<C> cx;
   const Op<PI> ob = TB::at(sB);
-  const int id = blockIdx.x;
-  const int n = id % A.N, bh = id / A.N, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
-  load_ctx<C, NT>(cx, A, b, h, n);
-  const float* qg = A.qn + hoff(A, b, hk, A.Hk, n, C, D);
-  const float* kg = A.kn + hoff(A, b, hk, A.Hk, n, C, D);
-  const size_t off = hoff(A, b, h, A.H, n, C, D);
   const int w = wave(), i0 = 16 * w;
-  stage_rows<C, D, NT>(ob, kg, D);  // k: B(d, j) = k[j][d]
-  __syncthreads();
+  const int total = A.B * A.H * A.N;
+  OutIn<C, D, NT> in;
   {
-    f32x4 acc[C / 16];
-    zero(acc);
-    strip_mma_full<PI, D, C / 16>(acc, krow(qg, D), i0, ob, 0, w + 1);
+    const UnitIx x(A, blockIdx.x);
+    in.cx.fetch(A, x.b, x.h, x.n);
+    in.k.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D);
+    in.q.fetch(A.qn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D, i0);
+    in.v.fetch(A.vnew + hoff(A, x.b, x.h, A.H, x.n, C, D), D);
+    in.st.fetch(A.states + ((size_t)x.b * A.H + x.h) * A.N * D * D + (size_t)x.n * D * D, D);
+  }
+  for (int u = blockIdx.x; u < total; u += gridDim.x) {
+    const UnitIx x(A, u);
+    const UnitIx y(A, u + gridDim.x < total ? u + gridDim.x : u);  // the next unit (or this one again)
+    in.cx.commit(cx);
+    in.cx.fetch(A, y.b, y.h, y.n);
+    in.k.put_rows(ob);
+    __syncthreads();
+    derive_ctx<C, NT>(cx);
+    __syncthreads();
+    {
+      f32x4 acc[C / 16];
+      zero(acc);
+      in.q.template product<PI>(acc, ob, 0, w + 1);
+      // refills are issued after the product that follows each staging: the staged
+      // registers are then not live across that product
+      in.k.fetch(A.kn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D);
 #pragma unroll
-    for (int t = 0; t < C / 16; ++t)
+      for (int t = 0; t < C / 16; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
+          lds_st(sI + i * LI + j, t <= w ? acc[t][rr] * decay(cx, i, j) : 0.f);
+        }
+    }
+    __syncthreads();
+    in.v.put_cols(ob);
+    __syncthreads();
+    f32x4 o[D / 16];
+    zero(o);
+    strip_mma<PI, C, D / 16>(o, krow(sI, LI), i0, ob, 0, 0, tri_end<C>(i0));
+    in.v.fetch(A.vnew + hoff(A, y.b, y.h, A.H, y.n, C, D), D);
+    __syncthreads();
+    in.st.put_cols(ob);
+    __syncthreads();
+    in.q.template product<PS>(o, ob, 0, D / 16, cx.grow[i0 + (lane() & 15)]);
+    in.q.fetch(A.qn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D, i0);
+    in.st.fetch(A.states + ((size_t)y.b * A.H + y.h) * A.N * D * D + (size_t)y.n * D * D, D);
+    TIO* out = reinterpret_cast<TIO*>(A.out);
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t)
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-        lds_st(sI + i * LI + j, t <= w ? acc[t][rr] * decay(cx, i, j) : 0.f);
+        const int tok = x.n * C + i0 + acc_row(rr);
+        if (tok < A.T) stf(out + (((size_t)x.b * A.T + tok) * A.H + x.h) * D + 16 * t + acc_col(), o[t][rr]);
       }
+    __syncthreads();  // cx and the operand region are rewritten by the next unit
   }
-  __syncthreads();
-  stage_cols<C, D, NT>(ob, A.vnew + off, D);  // v_new^T
-  __syncthreads();
-  f32x4 o[D / 16];
-  zero(o);
-  strip_mma<PI, C, D / 16>(o, krow(sI, LI), i0, ob, 0, 0, tri_end<C>(i0));
-  __syncthreads();
-  stage_cols<D, D, NT>(ob, A.states + ((size_t)bh * A.N + n) * D * D, D);  // S^T
-  __syncthreads();
-  strip_mma_full<PS, D, D / 16>(o, scale_r(krow(qg, D), cx.grow), i0, ob, 0);
-  TIO* out = reinterpret_cast<TIO*>(A.out);
-#pragma unroll
-  for (int t = 0; t < D / 16; ++t)
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int tok = n * C + i0 + acc_row(rr);
-      if (tok < A.T) stf(out + (((size_t)b * A.T + tok) * A.H + h) * D + 16 * t + acc_col(), o[t][rr]);
-    }
 }
 
 // ---------------------------------------------------------------- k_bwd_local
