@@ -1,0 +1,141 @@
+"""GPU parity at BASELINE's full sizes (0.8B: B=4, T=4096, 16/16 heads; 9B: B=2, T=8192, 16/32
+heads; varlen: B=1, T=16384 packed segments), all D = 128, chunk 128, bf16, precision high,
+through the C ABI.
+
+The oracle cannot run these sizes in a test, so they are checked through properties that hold
+exactly for the chunked algorithm, then tied to the oracle on a small piece:
+- a segment boundary at a chunk boundary splits a row into independent problems: every output
+  and gradient of each piece (out, d_qkv, d_a, d_b) equals, bit for bit, a standalone run of
+  that piece (the state and its gradient cross the boundary multiplied by an exact 0);
+- rows are independent: the other rows equal a run without the split row;
+- one piece (T = 1024) is then held to the bf16 bar against the fp32 oracle;
+- varlen (boundaries anywhere): changing one segment's qkv leaves out, d_qkv and d_b of every
+  other token bit for bit unchanged (cross-segment terms are exact zeros), while d_a of tokens
+  sharing a chunk with it may move by rounding only (its in-chunk reverse cumsum adds the
+  other segment's d gamma, whose sum is 0 in exact arithmetic).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gdn_cases import cosine, oracle_outputs, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+C, D = 128, 128
+NAMES = ("out", "qkv", "a", "b")
+
+
+def _inputs(batch, length, hk, h, segments="one", seed=0):
+    from tjev_amd.testing import cotangent, gdn_inputs
+
+    inputs = gdn_inputs(batch=batch, length=length, key_heads=hk, value_heads=h, dim=D, dtype=torch.bfloat16,
+                        segments=segments, seed=seed)
+    return list(inputs), cotangent(batch, length, h, D).to(torch.bfloat16)
+
+
+def _run(inputs, cot, hk, h):
+    """out, d_qkv, d_a, d_b (GPU tensors in the activation dtype) from the raw launches."""
+    from tjev_amd.gdn import GdnPlan
+
+    qkv, a, b, a_log, dt_bias, w, seg = (x.cuda().contiguous() for x in inputs)
+    B, T, _ = qkv.shape
+    plan = GdnPlan(batch=B, length=T, key_heads=hk, key_dim=D, value_heads=h, value_dim=D, taps=w.shape[0],
+                   chunk=C, io_dtype=qkv.dtype, gate_dtype=a.dtype, precision="high")
+    ws = torch.empty(max(plan.fwd_bytes, plan.bwd_bytes), dtype=torch.uint8, device="cuda")
+    out = torch.empty((B, T, h, D), dtype=qkv.dtype, device="cuda")
+    states = torch.empty(plan.states_shape, dtype=torch.float32, device="cuda")
+    plan.forward(qkv, a, b, a_log, dt_bias, w, seg, out, states, ws)
+    d_qkv, d_a, d_b = torch.empty_like(qkv), torch.empty_like(a), torch.empty_like(b)
+    d_alog, d_dtb = torch.empty_like(a_log), torch.empty_like(dt_bias)
+    plan.backward(qkv, a, b, a_log, dt_bias, w, seg, states, cot.cuda().contiguous(), d_qkv, d_a, d_b, d_alog,
+                  d_dtb, None, ws)
+    torch.cuda.synchronize()
+    return dict(zip(NAMES, (out, d_qkv, d_a, d_b)))
+
+
+def _piece(inputs, cot, rows, t0, t1):
+    """inputs and cotangent of rows ``rows``, tokens [t0, t1) (segment ids renumbered from 1)."""
+    qkv, a, b, a_log, dt_bias, w, seg = inputs
+    s = seg[rows, t0:t1].clone()
+    s = torch.where(s > 0, s - s[s > 0].min() + 1, s) if (s > 0).any() else s
+    return [qkv[rows, t0:t1], a[rows, t0:t1], b[rows, t0:t1], a_log, dt_bias, w, s], cot[rows, t0:t1]
+
+
+def _same(x, y, what):
+    assert x.shape == y.shape, (what, x.shape, y.shape)
+    diff = int((x.view(torch.int16) != y.view(torch.int16)).sum()) if x.dtype == torch.bfloat16 else \
+        int((x != y).sum())
+    assert diff == 0, f"{what}: {diff} of {x.numel()} elements differ"
+
+
+def _bf16_bar(got, want):
+    o = want["out"]
+    rms = float(o.pow(2).mean().sqrt())
+    err = float((got["out"] - o).abs().max()) / rms
+    floor = float((o.to(torch.bfloat16).double() - o).abs().max()) / rms
+    assert err - floor <= 2e-2 and rel_l2(got["out"], o) <= 2e-2, (err, floor)
+    for k in ("qkv", "a", "b"):
+        assert cosine(got[k], want[k]) >= 0.9999, (k, cosine(got[k], want[k]))
+
+
+def _split_case(batch, length, hk, h, row, cut):
+    inputs, cot = _inputs(batch, length, hk, h)
+    inputs[6][row, cut:] = 2  # a second segment from a chunk boundary on
+    full = _run(inputs, cot, hk, h)
+    rows = [r for r in range(batch) if r != row]
+    print(f"full {batch}x{length} {hk}/{h}: split row {row} at {cut}", flush=True)
+    for lo, hi in ((0, cut), (cut, length)):
+        pi, pc = _piece(inputs, cot, slice(row, row + 1), lo, hi)
+        part = _run(pi, pc, hk, h)
+        for k in NAMES:
+            _same(full[k][row:row + 1, lo:hi], part[k], f"{k} of row {row} [{lo}, {hi})")
+    if rows:
+        oi, oc = _piece(inputs, cot, rows, 0, length)
+        other = _run(oi, oc, hk, h)
+        for k in NAMES:
+            _same(full[k][rows], other[k], f"{k} of rows {rows}")
+    # the first piece against the oracle (fp32, on the same bf16 values)
+    pi, pc = _piece(inputs, cot, slice(row, row + 1), 0, cut)
+    got = {k: v.double().cpu() for k, v in _run(pi, pc, hk, h).items()}
+    want = oracle_outputs([x.cpu() for x in pi], pc.float(), key_heads=hk, key_dim=D, value_heads=h, value_dim=D)
+    _bf16_bar(got, want)
+
+
+def test_fullsize_0p8b_pieces():
+    _split_case(4, 4096, 16, 16, row=0, cut=1024)
+
+
+def test_fullsize_9b_pieces():
+    _split_case(2, 8192, 16, 32, row=1, cut=1024)
+
+
+def test_fullsize_varlen_segments_are_isolated():
+    inputs, cot = _inputs(1, 16384, 16, 16, segments="geometric", seed=3)
+    seg = inputs[6][0].numpy()
+    ids, starts, counts = np.unique(seg, return_index=True, return_counts=True)
+    # a segment near the middle that starts and ends inside chunks
+    pick = next(i for i in range(len(ids) // 2, len(ids))
+                if starts[i] % C and (starts[i] + counts[i]) % C and counts[i] >= 32)
+    lo, hi = int(starts[pick]), int(starts[pick] + counts[pick])
+    print(f"varlen: {len(ids)} segments, perturbing id {ids[pick]} at [{lo}, {hi})", flush=True)
+    base = _run(inputs, cot, 16, 16)
+    changed = [x.clone() for x in inputs]
+    noise = torch.randn(changed[0][0, lo:hi].shape, generator=torch.Generator().manual_seed(5))
+    changed[0][0, lo:hi] = (changed[0][0, lo:hi].float() + noise).to(torch.bfloat16)
+    pert = _run(changed, cot, 16, 16)
+    outside = torch.ones(16384, dtype=torch.bool)
+    outside[lo:hi] = False
+    for k in ("out", "qkv", "b"):
+        _same(base[k][0, outside.cuda()], pert[k][0, outside.cuda()], f"{k} outside the changed segment")
+        assert not torch.equal(base[k][0, lo:hi], pert[k][0, lo:hi]), k
+    da, dp = base["a"][0].float(), pert["a"][0].float()
+    scale = float(da.abs().max())
+    assert float((da[outside.cuda()] - dp[outside.cuda()]).abs().max()) <= 1e-3 * scale
+    first, last = lo // C * C, (hi + C - 1) // C * C  # d_a is bitwise equal outside the shared chunks
+    far = torch.ones(16384, dtype=torch.bool)
+    far[first:last] = False
+    _same(base["a"][0, far.cuda()], pert["a"][0, far.cuda()], "d_a outside the chunks of the changed segment")
