@@ -83,10 +83,10 @@ struct CtxRaw {
 };
 
 template <int C, int NT>
-__device__ void derive_ctx(Ctx<C>& cx);
+__device__ __forceinline__ void derive_ctx(Ctx<C>& cx);
 
 template <int C, int NT>
-__device__ void load_ctx(Ctx<C>& cx, const GdnArgs& A, int b, int h, int n) {
+__device__ __forceinline__ void load_ctx(Ctx<C>& cx, const GdnArgs& A, int b, int h, int n) {
   static_assert(NT >= C, "one thread per token");
   CtxRaw<C> raw;
   raw.fetch(A, b, h, n);
@@ -98,7 +98,7 @@ __device__ void load_ctx(Ctx<C>& cx, const GdnArgs& A, int b, int h, int n) {
 
 // grow, kws, bg and carry from seg, gamma and beta (the LDS context written, then synced)
 template <int C, int NT>
-__device__ void derive_ctx(Ctx<C>& cx) {
+__device__ __forceinline__ void derive_ctx(Ctx<C>& cx) {
   for (int i = threadIdx.x; i < C; i += NT) {
     const bool cont = cx.seg[i] == cx.before;
     const bool in_last = cx.seg[i] == cx.seg[C - 1];
@@ -134,6 +134,18 @@ struct KRowLim {
     }
   }
   GDN_VIEW_FRAG
+};
+
+// indices of the (row, head, chunk) unit u of the chunk-parallel kernels
+struct UnitIx {
+  int n, bh, h, b, hk;
+  __device__ __forceinline__ UnitIx(const GdnArgs& A, int u) {
+    n = u % A.N;
+    bh = u / A.N;
+    h = bh % A.H;
+    b = bh / A.H;
+    hk = h / A.ratio;
+  }
 };
 
 // ---------------------------------------------------------------- inverse
@@ -492,6 +504,18 @@ struct RegsT {
       if (live(it)) put(op, it, fa, fb);
     }
   }
+  // op(r, c) = g[r][c]: the tile as stored (row layout)
+  template <int P>
+  __device__ __forceinline__ void put_rows(const Op<P>& op) const {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      if (!live(it)) continue;
+      int q, j, c;
+      slot(it, q, j, c);
+      op.put4(2 * j, c, a[it].x, a[it].y, a[it].z, a[it].w);
+      op.put4(2 * j + 1, c, b[it].x, b[it].y, b[it].z, b[it].w);
+    }
+  }
   // the row pair (2j, 2j+1) this thread holds (put_cols2's rows)
   __device__ __forceinline__ static int pair() { return ((int)threadIdx.x / G) % RP; }
 };
@@ -683,10 +707,12 @@ __device__ __forceinline__ void load_tile(float* s, int LD, const float* g) {
 }
 
 // ---------------------------------------------------------------- k_chunk
-// grid B*H*N, C/16 waves (one 16-row strip each). MODE 0 (forward): writes w and u.
-// MODE 1 (backward recompute): writes T and v_new = u - w S_before.
-// LDS: T in fp32 (the inverse runs in place), one operand region reused for k, kbe^T, (v beta)^T
-// and S^T (the doubling scratch borrows it too).
+// Persistent over the (row, head, chunk) units as k_out; C/16 waves (one 16-row strip each).
+// MODE 0 (forward): writes w and u. MODE 1 (backward recompute): writes T and
+// v_new = u - w S_before. LDS: T in fp32 (the inverse runs in place), one operand region reused
+// for k, kbe^T, (v beta)^T and S^T (the doubling scratch borrows it too). The next unit's
+// context and k rows are loaded at this unit's start and end; k (again), v and S of this unit
+// after the inverse, a product ahead of their use.
 template <int C, int D, int PI, int PS, int MODE>
 __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
   constexpr int NT = C * 4;
@@ -698,67 +724,89 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
   __shared__ float sT[C * LT];
   __shared__ __align__(16) char sB[RB];
   __shared__ Ctx<C> cx;
-  const int id = blockIdx.x;
-  const int n = id % A.N, bh = id / A.N, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
-  load_ctx<C, NT>(cx, A, b, h, n);
-  const float* kg = A.kn + hoff(A, b, hk, A.Hk, n, C, D);
-  const float* vg = A.vv + hoff(A, b, h, A.H, n, C, D);
-  const size_t off = hoff(A, b, h, A.H, n, C, D);
   const int w = wave(), i0 = 16 * w;
   const Op<PI> ob = TB::at(sB);
-  stage_rows<C, D, NT>(ob, kg, D);
-  __syncthreads();
-  {  // L = strict(beta_i (k k^T)_ij D_ij): tiles on and below the diagonal only
-    f32x4 acc[C / 16];
-    zero(acc);
-    strip_mma<PI, D, C / 16>(acc, ob, i0, ob, 0, 0, D, w + 1);
-#pragma unroll
-    for (int t = 0; t < C / 16; ++t)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-        lds_st(sT + i * LT + j, (i > j && t <= w) ? cx.beta[i] * acc[t][rr] * decay(cx, i, j) : 0.f);
-      }
+  const int total = A.B * A.H * A.N;
+  CtxRaw<C> rc;
+  RegsT<C, D, NT> kk;  // k: staged as rows (A and B of k k^T), then as kbe^T
+  {
+    const UnitIx x(A, blockIdx.x);
+    rc.fetch(A, x.b, x.h, x.n);
+    kk.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D);
   }
-  __syncthreads();
-  invert_unit_lower<C, PI>(sT, LT, reinterpret_cast<float*>(sB));
-  f32x4 aw[D / 16], au[D / 16];
-  zero(aw);
-  zero(au);
-  stage_cols<C, D, NT>(ob, kg, D, cx.bg);  // kbe^T
-  __syncthreads();
-  strip_mma<PI, C, D / 16>(aw, krow(sT, LT), i0, ob, 0, 0, tri_end<C>(i0));
-  __syncthreads();
-  stage_cols<C, D, NT>(ob, vg, D, cx.beta);  // (v beta)^T
-  __syncthreads();
-  strip_mma<PI, C, D / 16>(au, krow(sT, LT), i0, ob, 0, 0, tri_end<C>(i0));
-  if constexpr (MODE == 0) {
-#pragma unroll
-    for (int t = 0; t < D / 16; ++t)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const size_t g = off + (size_t)(i0 + acc_row(rr)) * D + 16 * t + acc_col();
-        A.ww[g] = aw[t][rr];
-        A.uu[g] = au[t][rr];
-      }
-  } else {
-    float* tg = A.tt + ((size_t)bh * A.N + n) * C * C;
-    for (int idx = threadIdx.x; idx < C * C; idx += NT) tg[idx] = sT[(idx / C) * LT + idx % C];
+  for (int u = blockIdx.x; u < total; u += gridDim.x) {
+    const UnitIx x(A, u);
+    const UnitIx y(A, u + gridDim.x < total ? u + gridDim.x : u);  // the next unit (or this one again)
+    const size_t off = hoff(A, x.b, x.h, A.H, x.n, C, D);
+    rc.commit(cx);
+    kk.put_rows(ob);
+    rc.fetch(A, y.b, y.h, y.n);
+    RegsT<C, D, NT> vc;  // this unit's (v beta)^T source
+    RegsT<D, D, NT> sc;  // S_before (MODE 1)
     __syncthreads();
-#pragma unroll
-    for (int t = 0; t < D / 16; ++t)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) lds_st(sT + (i0 + acc_row(rr)) * LT + 16 * t + acc_col(), aw[t][rr]);
-    stage_cols<D, D, NT>(ob, A.states + ((size_t)bh * A.N + n) * D * D, D);  // S^T
+    derive_ctx<C, NT>(cx);
     __syncthreads();
-    f32x4 ws[D / 16];
-    zero(ws);
-    strip_mma<PS, D, D / 16>(ws, krow(sT, LT), i0, ob, 0);
+    {  // L = strict(beta_i (k k^T)_ij D_ij): tiles on and below the diagonal only
+      f32x4 acc[C / 16];
+      zero(acc);
+      strip_mma<PI, D, C / 16>(acc, ob, i0, ob, 0, 0, D, w + 1);
 #pragma unroll
-    for (int t = 0; t < D / 16; ++t)
+      for (int t = 0; t < C / 16; ++t)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        A.vnew[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = au[t][rr] - ws[t][rr];
+        for (int rr = 0; rr < 4; ++rr) {
+          const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
+          lds_st(sT + i * LT + j, (i > j && t <= w) ? cx.beta[i] * acc[t][rr] * decay(cx, i, j) : 0.f);
+        }
+    }
+    __syncthreads();
+    invert_unit_lower<C, PI>(sT, LT, reinterpret_cast<float*>(sB));
+    // k again (not held across the inverse: register limit), then v
+    kk.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D);
+    vc.fetch(A.vv + off, D);
+    f32x4 aw[D / 16], au[D / 16];
+    zero(aw);
+    zero(au);
+    kk.put_cols(ob, cx.bg);  // kbe^T
+    __syncthreads();
+    strip_mma<PI, C, D / 16>(aw, krow(sT, LT), i0, ob, 0, 0, tri_end<C>(i0));
+    if constexpr (MODE == 1) sc.fetch(A.states + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * D * D, D);
+    __syncthreads();
+    vc.put_cols(ob, cx.beta);  // (v beta)^T
+    __syncthreads();
+    strip_mma<PI, C, D / 16>(au, krow(sT, LT), i0, ob, 0, 0, tri_end<C>(i0));
+    // the next unit's k before this unit's stores: waiting for it later (vmcnt counts in issue
+    // order, stores included) then does not wait for the stores
+    if constexpr (MODE == 0) kk.fetch(A.kn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D);
+    if constexpr (MODE == 0) {
+#pragma unroll
+      for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const size_t g = off + (size_t)(i0 + acc_row(rr)) * D + 16 * t + acc_col();
+          A.ww[g] = aw[t][rr];
+          A.uu[g] = au[t][rr];
+        }
+    } else {
+      kk.fetch(A.kn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D);  // before this unit's stores
+      float* tg = A.tt + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * C * C;
+      for (int idx = threadIdx.x; idx < C * C; idx += NT) tg[idx] = sT[(idx / C) * LT + idx % C];
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) lds_st(sT + (i0 + acc_row(rr)) * LT + 16 * t + acc_col(), aw[t][rr]);
+      sc.put_cols(ob);  // S^T
+      __syncthreads();
+      f32x4 ws[D / 16];
+      zero(ws);
+      strip_mma<PS, D, D / 16>(ws, krow(sT, LT), i0, ob, 0);
+#pragma unroll
+      for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          A.vnew[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = au[t][rr] - ws[t][rr];
+    }
+    __syncthreads();  // cx, sT and the operand region are rewritten by the next unit
   }
 }
 
@@ -866,17 +914,6 @@ struct OutIn {
   StripA<D> q;           // this wave's q rows (A operand of q k^T and of q_read S)
   RegsT<C, D, NT> v;     // v_new rows, staged as v_new^T
   RegsT<D, D, NT> st;    // S_before rows, staged as S^T
-};
-
-struct UnitIx {
-  int n, bh, h, b, hk;
-  __device__ __forceinline__ UnitIx(const GdnArgs& A, int u) {
-    n = u % A.N;
-    bh = u / A.N;
-    h = bh % A.H;
-    b = bh / A.H;
-    hk = h / A.ratio;
-  }
 };
 
 template <int C, int D, int PI, int PS, class TIO>
