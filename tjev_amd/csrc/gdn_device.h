@@ -96,6 +96,29 @@ template <> struct Raw8<uint16_t> {
 
 // ---------------------------------------------------------------- numerics
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+// The elementwise activations' forms on the hardware transcendentals (v_exp_f32, v_rcp_f32,
+// v_rsq_f32: about 1 ulp each, a few ulp composed), used on bf16 activations.
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+__device__ __forceinline__ float sigmoid_fast(float x) { return __builtin_amdgcn_rcpf(1.0f + exp_fast(-x)); }
+__device__ __forceinline__ float rsqrt_fast(float x) { return __builtin_amdgcn_rsqf(x); }
+// the sigmoid of an activation stored as T: the hardware form for bf16 activations (whose own
+// rounding is 2^-9), the correctly rounded one for fp32 (the fp32 parity path)
+template <class T>
+__device__ __forceinline__ float sigmoid_io(float x) {
+  if constexpr (sizeof(T) == 2) {
+    return sigmoid_fast(x);
+  } else {
+    return sigmoidf_(x);
+  }
+}
+template <class T>
+__device__ __forceinline__ float rsqrt_io(float x) {
+  if constexpr (sizeof(T) == 2) {
+    return rsqrt_fast(x);
+  } else {
+    return 1.0f / sqrtf(x);
+  }
+}
 // jax.nn.softplus = logaddexp(x, 0) = max(x, 0) + log1p(exp(-|x|))
 __device__ __forceinline__ float softplusf_(float x) {
   return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));

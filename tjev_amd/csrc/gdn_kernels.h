@@ -316,7 +316,7 @@ __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
           for (int e = 0; e < 8; ++e) z[e] = keep ? z[e] + xl[e] * wl[L][e] : z[e];
         }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) act[e] = st > 0 ? z[e] * sigmoidf_(z[e]) : 0.f;
+        for (int e = 0; e < 8; ++e) act[e] = st > 0 ? z[e] * sigmoid_io<TIO>(z[e]) : 0.f;
       }
       if (kind < 2) {  // l2norm over the head's D channels (CG lanes)
         float sq = 0.f;
@@ -1391,7 +1391,7 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
         for (int e = 0; e < 8; ++e) z[e] = keep ? z[e] + xl[e] * wl[L][e] : z[e];
       }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) act[e] = st > 0 ? z[e] * sigmoidf_(z[e]) : 0.f;
+      for (int e = 0; e < 8; ++e) act[e] = st > 0 ? z[e] * sigmoid_io<TIO>(z[e]) : 0.f;
     }
     if (kind < 2) {  // l2norm backward (q's scale first)
 #pragma unroll
@@ -1420,7 +1420,7 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
     } else {  // SiLU backward on valid tokens
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float sgm = sigmoidf_(z[e]);
+        const float sgm = sigmoid_io<TIO>(z[e]);
         dz[e] = (live && st > 0) ? dy[e] * sgm * (1.f + z[e] * (1.f - sgm)) : 0.f;
       }
     }

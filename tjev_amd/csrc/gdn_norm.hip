@@ -103,11 +103,11 @@ __global__ __launch_bounds__(kThreads) void k_norm_fwd(NormArgs A) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss += x[i][e] * x[i][e];
     ss = group_sum<LPR>(ss);
-    const float r = rsqrtf(ss * (1.0f / D) + A.eps);
+    const float r = rsqrt_io<T>(ss * (1.0f / D) + A.eps);
     const bool valid = sg[i] > 0;
     float y[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = valid ? w[e] * rnd<T>(x[i][e] * r) * (z[i][e] * sigmoidf_(z[i][e])) : 0.f;
+    for (int e = 0; e < 8; ++e) y[e] = valid ? w[e] * rnd<T>(x[i][e] * r) * (z[i][e] * sigmoid_io<T>(z[i][e])) : 0.f;
     if (row < A.rows) st8(static_cast<T*>(A.y) + row * D + c0, y);
   }
 }
@@ -148,12 +148,12 @@ __global__ __launch_bounds__(kThreads) void k_norm_bwd(NormArgs A) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss += x[i][e] * x[i][e];
       ss = group_sum<LPR>(ss);
-      const float r = rsqrtf(ss * (1.0f / D) + A.eps);
+      const float r = rsqrt_io<T>(ss * (1.0f / D) + A.eps);
       float n[8], dn[8], dzv[8], dot = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float ge = valid[i] ? g[i][e] : 0.f;
-        const float sg = sigmoidf_(z[i][e]);
+        const float sg = sigmoid_io<T>(z[i][e]);
         const float s = z[i][e] * sg;
         n[e] = x[i][e] * r;
         const float nh = rnd<T>(n[e]);
