@@ -212,3 +212,25 @@ def test_norm_operator_checks_and_no_cpu_fallback():
         gated_rmsnorm(x.reshape(2, 3, 64), x.reshape(2, 3, 64), torch.ones(16), heads=5)
     with pytest.raises(RuntimeError, match="GPU"):
         gated_rmsnorm(x, x, torch.ones(16))
+
+
+def _mir(before, after):
+    head = "# *** IR Dump {} SI Load Store Optimizer (si-load-store-opt) ***:\n# Machine code for function k: x\nname: k\n"
+    return head.format("Before") + before + head.format("After") + after
+
+
+def test_ds_check_flags_the_miscompiled_merge_only():
+    from tjev_amd.ds_check import bad_merges
+
+    before = ("DS_WRITE_B32_gfx9 %5:vgpr_32, %7:vgpr_32, 272, 0, implicit $exec :: (store (s32) into %ir.p1, addrspace 3)\n"
+              "DS_WRITE_B32_gfx9 %5:vgpr_32, %8:vgpr_32, 336, 0, implicit $exec :: (store (s32) into %ir.p2, addrspace 3)\n")
+    # the miscompile seen with ROCm 7.2: 272 and 336 bytes merged as dword offsets 17 and 84
+    wrong = ("DS_WRITE2_B32_gfx9 %5:vgpr_32, %7:vgpr_32, %8:vgpr_32, 17, 84, 0, implicit $exec :: "
+             "(store (s32) into %ir.p1, addrspace 3), (store (s32) into %ir.p2, addrspace 3)\n")
+    right = wrong.replace(" 17, 84,", " 68, 84,")
+    assert len(bad_merges(_mir(before, wrong))) == 1
+    assert bad_merges(_mir(before, right)) == []
+    # accesses off two base registers carry no offsets to compare
+    other = before.replace("DS_WRITE_B32_gfx9 %5:vgpr_32, %8", "DS_WRITE_B32_gfx9 %6:vgpr_32, %8").replace("336", "0")
+    merged = wrong.replace(" 17, 84,", " 0, 4,").replace("DS_WRITE2_B32", "DS_WRITE2ST64_B32")
+    assert bad_merges(_mir(other.replace("272", "0"), merged)) == []

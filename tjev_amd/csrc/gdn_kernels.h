@@ -1561,24 +1561,41 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
 
 // ---------------------------------------------------------------- k_reduce
 // d A_log[h] = sum over rows and chunks of the per-chunk partials, likewise d dt_bias and
-// the conv weight (pallas_tpu_mega.py:527-535, 563-568); fixed order, no atomics.
+// the conv weight (pallas_tpu_mega.py:527-535, 563-568); fixed order, no atomics. Workgroups
+// 0..H-1: one value head each, the partials summed by 256 threads in fp64 then by a fixed
+// tree; the rest: one conv weight per thread.
 template <int C>
 __global__ __launch_bounds__(256) void k_reduce(GdnArgs A) {
-  const int idx = blockIdx.x * 256 + threadIdx.x;
   const int bn = A.B * A.N;
-  if (idx < A.H) {
+  if ((int)blockIdx.x < A.H) {
+    __shared__ double ra[256], rd[256];
+    const int h = blockIdx.x;
     double sa = 0.0, sd = 0.0;
-    for (int q = 0; q < bn; ++q) {
-      sa += A.pa[(size_t)q * A.H + idx];
-      sd += A.pd[(size_t)q * A.H + idx];
+    for (int q = threadIdx.x; q < bn; q += 256) {
+      sa += A.pa[(size_t)q * A.H + h];
+      sd += A.pd[(size_t)q * A.H + h];
     }
-    A.d_a_log[idx] = (float)sa;
-    A.d_dt_bias[idx] = (float)sd;
-  } else if (A.d_conv_w && A.taps > 0 && idx - A.H < A.taps * A.W) {
-    const int j = idx - A.H;
-    float s = 0.f;
-    for (int q = 0; q < bn; ++q) s += A.dwp[(size_t)q * A.taps * A.W + j];
-    A.d_conv_w[j] = s;
+    ra[threadIdx.x] = sa;
+    rd[threadIdx.x] = sd;
+    __syncthreads();
+    for (int m = 128; m > 0; m >>= 1) {
+      if ((int)threadIdx.x < m) {
+        ra[threadIdx.x] += ra[threadIdx.x + m];
+        rd[threadIdx.x] += rd[threadIdx.x + m];
+      }
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+      A.d_a_log[h] = (float)ra[0];
+      A.d_dt_bias[h] = (float)rd[0];
+    }
+  } else {
+    const int j = ((int)blockIdx.x - A.H) * 256 + threadIdx.x;
+    if (A.d_conv_w && A.taps > 0 && j < A.taps * A.W) {
+      float s = 0.f;
+      for (int q = 0; q < bn; ++q) s += A.dwp[(size_t)q * A.taps * A.W + j];
+      A.d_conv_w[j] = s;
+    }
   }
 }
 
