@@ -9,6 +9,7 @@ namespace gdn {
 struct GdnArgs {
   int B, T, Tp, N, Hk, H, ratio, taps, W;
   int ntiles;  // Dv tiles of the scans
+  int parts;   // chunk ranges per (row, head, tile) of the scans, split where a segment resets
   float scale; // Dk^-1/2
   // inputs
   const void* qkv;

@@ -30,7 +30,14 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
   constexpr int NS = (C > D ? C : D) * 4;
   const dim3 prep(A.B * A.N, 2 * A.Hk + A.H);
   const dim3 chunks(A.B * A.H * A.N);
-  const dim3 tiles(A.B * A.H * (D / DVT));
+  // the scans: (row, head, Dv tile) chains, each split into up to `parts` chunk ranges at
+  // segment resets (rows without resets leave the extra ranges empty)
+  const int chains = A.B * A.H * (D / DVT);
+  int parts = (2 * cu_count() + chains - 1) / chains;
+  parts = parts < 1 ? 1 : (parts > A.N ? A.N : parts);
+  GdnArgs L = A;  // the launched arguments
+  L.parts = parts;
+  const dim3 tiles(chains * parts);
   const int units = A.B * A.H * A.N, cus = cu_count();
   const dim3 persist(units < cus ? units : cus);
   auto mark = [&](int k, int end) {
@@ -39,7 +46,7 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
 #define GDN_LAUNCH(id, kern, grid, block)                  \
   do {                                                     \
     mark(id, 0);                                           \
-    hipLaunchKernelGGL(kern, grid, block, 0, st, A);       \
+    hipLaunchKernelGGL(kern, grid, block, 0, st, L);       \
     mark(id, 1);                                           \
   } while (0)
   if (!backward) {

@@ -810,6 +810,56 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
   }
 }
 
+// ---------------------------------------------------------------- scan partition
+// carry of chunk c: its last token continues the segment of the token before the chunk (-2
+// before chunk 0). Where a chunk does not carry, the state after it does not depend on the state
+// before it (its last segment starts inside it and reads no earlier state), and the state
+// gradient entering it does not depend on the one after it (the rows that read the earlier
+// state, and so feed that gradient, are in another segment than the rows that write the later
+// state: their coupling terms are exact zeros). The scans split each chain there into
+// independent chunk ranges (bitwise equal to the unsplit chain).
+template <int C>
+__device__ __forceinline__ bool chunk_carries(const GdnArgs& A, int b, int c) {
+  const int32_t* sp = A.segp + (size_t)b * A.Tp;
+  const int before = c == 0 ? -2 : sp[(size_t)c * C - 1];
+  return sp[(size_t)c * C + C - 1] == before;
+}
+// The first chunk s in [q, N) where a range starts, or N; forward ranges start at chunk 0 and
+// after chunks that do not carry, backward ranges at chunks that do not carry (chunk 0 never
+// carries). One candidate per thread, then the workgroup minimum (red: NT/64 ints of LDS).
+// Called by every thread of the workgroup.
+template <int C, int NT, bool FWD>
+__device__ __forceinline__ int part_start(const GdnArgs& A, int b, int q, int* red) {
+  for (int base = q; base < A.N; base += NT) {
+    const int s = base + (int)threadIdx.x;
+    bool hit = false;
+    if (s < A.N) hit = FWD ? (s == 0 || !chunk_carries<C>(A, b, s - 1)) : !chunk_carries<C>(A, b, s);
+    int m = hit ? s : A.N;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = min(m, __shfl_xor(m, off));
+    if (lane() == 0) red[wave()] = m;
+    __syncthreads();
+    int best = A.N;
+    for (int i = 0; i < NT / 64; ++i) best = min(best, red[i]);
+    __syncthreads();
+    if (best < A.N) return best;
+  }
+  return A.N;
+}
+
+// scan workgroup id -> (part, row * heads + head, Dv tile): part-major in dispatch order (the
+// first ranges, never empty, start first), then XCD-remapped so a head's tiles share an L2
+struct ScanIx {
+  int part, bh, tile;
+  __device__ __forceinline__ ScanIx(const GdnArgs& A) {
+    const int chains = A.B * A.H * A.ntiles;
+    part = blockIdx.x / chains;
+    const int id = xcd_remap(blockIdx.x % chains, chains);
+    tile = id % A.ntiles;
+    bh = id / A.ntiles;
+  }
+};
+
 // ---------------------------------------------------------------- k_scan_fwd
 // grid B*H*(D/DVT) (XCD-remapped), max(C,D)/16 waves. The state tile S [D x DVT] lives in
 // the accumulators of waves < D/16; chunks in order (pallas_tpu_v2.py:254-269). None of a
@@ -845,19 +895,27 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
   __shared__ __align__(16) char sK[TK::BYTES];
   __shared__ __align__(16) char sV[TV::BYTES];
   const Op<PI> os = TS::at(sS), ok = TK::at(sK), ov = TV::at(sV);
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int tile = id % A.ntiles, bh = id / A.ntiles, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
+  __shared__ int red[NW];
+  const ScanIx ix(A);
+  const int tile = ix.tile, bh = ix.bh, part = ix.part;
+  const int h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
   const int j0 = tile * DVT;
   const int w = wave();
+  // this workgroup's chunks [n0, n1); from n0 - 1 (not stored) when the range starts after chunk 0
+  const int n0 = part_start<C, NT, true>(A, b, (int)((long)part * A.N / A.parts), red);
+  const int n1 = part_start<C, NT, true>(A, b, (int)((long)(part + 1) * A.N / A.parts), red);
+  if (n0 >= n1) return;
+  const int nb = n0 > 0 ? n0 - 1 : 0;
   f32x4 accS[DVT / 16];
   zero(accS);
   ScanFwdIn<C, D, DVT, NT> in;
-  in.gt.fetch(A, b, h, 0, RegsT<C, D, NT>::pair());
-  in.fetch_k(A, b, hk, 0);
-  in.fetch_w(A, b, h, 0);
-  in.fetch_u(A, b, h, 0, j0);
-  for (int n = 0; n < A.N; ++n) {
-    const int nx = n + 1 < A.N ? n + 1 : n;  // the last step refetches its own chunk (unused)
+  in.gt.fetch(A, b, h, nb, RegsT<C, D, NT>::pair());
+  in.fetch_k(A, b, hk, nb);
+  in.fetch_w(A, b, h, nb);
+  in.fetch_u(A, b, h, nb, j0);
+  for (int n = nb; n < n1; ++n) {
+    const int nx = n + 1 < n1 ? n + 1 : n;  // the last step refetches its own chunk (unused)
+    const bool emit = n >= n0;              // the replayed chunk n0 - 1 only rebuilds the state
     float* sg = A.states + ((size_t)bh * A.N + n) * D * D;
     if (NW == D / 16 || w < D / 16) {
 #pragma unroll
@@ -866,7 +924,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
         for (int rr = 0; rr < 4; ++rr) {
           const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
           os.put(j, i, accS[t][rr]);
-          sg[i * D + j0 + j] = accS[t][rr];
+          if (emit) sg[i * D + j0 + j] = accS[t][rr];
         }
     }
     const float carry = in.gt.carry();
@@ -887,7 +945,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
           const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
           const float vn = in.u.v[t][rr] - acc[t][rr];
           ov.put(j, i, vn);
-          A.vnew[off + (size_t)i * D + j0 + j] = vn;
+          if (emit) A.vnew[off + (size_t)i * D + j0 + j] = vn;
         }
       in.fetch_u(A, b, h, nx, j0);
     }
@@ -1096,16 +1154,25 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
   __shared__ __align__(16) char sDo[TD::BYTES];
   __shared__ __align__(16) char sX[TD::BYTES];
   __shared__ float red[NW];
+  __shared__ int red_i[NW];
   const Op<PI> og = TG_::at(sG), oq = TQ::at(sQ), odo = TD::at(sDo), ox = TD::at(sX);
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int tile = id % A.ntiles, bh = id / A.ntiles, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
+  const ScanIx ix(A);
+  const int tile = ix.tile, bh = ix.bh, part = ix.part;
+  const int h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
   const int j0 = tile * DVT;
   const int w = wave();
+  // this workgroup's chunks [n0, n1), reversed; from chunk n1 (not stored) when the range ends
+  // before the last chunk. That chunk's X is read while the next range may be updating it in
+  // place: both values give the same G (its rows that feed G have Kt rows of exact zeros).
+  const int n0 = part_start<C, NT, false>(A, b, (int)((long)part * A.N / A.parts), red_i);
+  const int n1 = part_start<C, NT, false>(A, b, (int)((long)(part + 1) * A.N / A.parts), red_i);
+  if (n0 >= n1) return;
+  const int ne = n1 < A.N ? n1 : n1 - 1;
   f32x4 accG[DVT / 16];
   zero(accG);
   ScanBwdIn<C, D, DVT, NT, TIO> in;
   {
-    const int n = A.N - 1;
+    const int n = ne;
     in.gt.fetch(A, b, h, n, RegsT<C, D, NT>::pair());
     in.fetch_snext(A, bh, n, j0);
     in.fetch_do(A, b, h, n, j0);
@@ -1113,8 +1180,9 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
     in.fetch_kt(A, b, h, n);
     in.fetch_xl(A, b, h, n, j0);
   }
-  for (int n = A.N - 1; n >= 0; --n) {
-    const int nx = n > 0 ? n - 1 : 0;  // the last step refetches chunk 0 (unused)
+  for (int n = ne; n >= n0; --n) {
+    const int nx = n > n0 ? n - 1 : n;  // the last step refetches its own chunk (unused)
+    const bool emit = n < n1;           // the replayed chunk n1 only rebuilds G
     const bool has_next = n + 1 < A.N;
     float part = 0.f;
     if (NW == D / 16 || w < D / 16) {
@@ -1126,7 +1194,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
           const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
           const float g = accG[t][rr];
           og.put(j, i, g);
-          gdst[i * D + j0 + j] = g;
+          if (emit) gdst[i * D + j0 + j] = g;
           part += has_next ? g * in.snext.v[t][rr] : 0.f;
         }
       in.fetch_snext(A, bh, nx, j0);
@@ -1141,7 +1209,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
     in.qk.fetch(A.kn + hoff(A, b, hk, A.Hk, n, C, D), D);
     in.gt.fetch(A, b, h, nx, RegsT<C, D, NT>::pair());
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (threadIdx.x == 0 && emit) {
       float s = 0.f;
       for (int q = 0; q < NW; ++q) s += red[q];
       A.gsp[((size_t)bh * A.N + n) * A.ntiles + tile] = s;
@@ -1159,7 +1227,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
           const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
           const float xv = in.xl.v[t][rr] + acc[t][rr];
           ox.put(j, i, xv);
-          A.xl[off + (size_t)i * D + j0 + j] = xv;
+          if (emit) A.xl[off + (size_t)i * D + j0 + j] = xv;
         }
       in.fetch_xl(A, b, h, nx, j0);
     }
