@@ -250,6 +250,11 @@ struct Op<P_F32> {
   __device__ __forceinline__ void put4(int r, int k, float v0, float v1, float v2, float v3) const {
     *reinterpret_cast<float4*>(p + r * ld + k) = make_float4(v0, v1, v2, v3);
   }
+  // eight consecutive k (k a multiple of 8)
+  __device__ __forceinline__ void put8(int r, int k, const float (&v)[8]) const {
+    *reinterpret_cast<float4*>(p + r * ld + k) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(p + r * ld + k + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  }
   template <int Q>
   __device__ __forceinline__ Frag<Q> frag(int r, int k) const {
     static_assert(Q == P_F32, "an fp32 tile feeds fp32 products");
@@ -273,6 +278,10 @@ struct Op<P_BF16> {
   }
   __device__ __forceinline__ void put4(int r, int k, float v0, float v1, float v2, float v3) const {
     *reinterpret_cast<uint2*>(hi + r * ld + k) = make_uint2(pack2(v0, v1), pack2(v2, v3));
+  }
+  __device__ __forceinline__ void put8(int r, int k, const float (&v)[8]) const {
+    *reinterpret_cast<uint4*>(hi + r * ld + k) =
+        make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
   }
   template <int Q>
   __device__ __forceinline__ Frag<Q> frag(int r, int k) const {
@@ -300,6 +309,13 @@ struct Op<P_BF16X3> {
     *reinterpret_cast<uint2*>(hi + r * ld + k) = make_uint2(pack2(v0, v1), pack2(v2, v3));
     *reinterpret_cast<uint2*>(lo + r * ld + k) =
         make_uint2(pack2(lo_part(v0), lo_part(v1)), pack2(lo_part(v2), lo_part(v3)));
+  }
+  __device__ __forceinline__ void put8(int r, int k, const float (&v)[8]) const {
+    *reinterpret_cast<uint4*>(hi + r * ld + k) =
+        make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+    *reinterpret_cast<uint4*>(lo + r * ld + k) =
+        make_uint4(pack2(lo_part(v[0]), lo_part(v[1])), pack2(lo_part(v[2]), lo_part(v[3])),
+                   pack2(lo_part(v[4]), lo_part(v[5])), pack2(lo_part(v[6]), lo_part(v[7])));
   }
   template <int Q>
   __device__ __forceinline__ Frag<Q> frag(int r, int k) const {

@@ -119,23 +119,6 @@ __device__ __forceinline__ float decay(const Ctx<C>& cx, int i, int j) {
 template <int R, int D, int NT>
 __device__ __forceinline__ void load_tile(float* s, int LD, const float* g);
 
-// row view of a token-major activation tensor with rows past the valid count read as 0
-template <class T>
-struct KRowLim {
-  const T* p;
-  int ld;
-  int rows;
-  __device__ __forceinline__ void load(int r, int k, float (&o)[8]) const {
-    if (r < rows) {
-      ld8(p + (size_t)r * ld + k, o);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = 0.f;
-    }
-  }
-  GDN_VIEW_FRAG
-};
-
 // indices of the (row, head, chunk) unit u of the chunk-parallel kernels
 struct UnitIx {
   int n, bh, h, b, hk;
@@ -668,6 +651,52 @@ struct StripA {
       float xs[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) xs[e] = x[s][e] * rs;
+      const Frag<P> fa = make_frag<P>(xs);
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        if (t < tn) {
+          const Frag<P> fb = ok ? B.template frag<P>(j0 + 16 * t + r, 32 * s + kg) : zero_frag<P>();
+          mma<P>(acc[t], fa, fb);
+        }
+      }
+    }
+  }
+  // the strip as stored into an operand tile: op(i0 + r, k) = A(i0 + r, k)
+  template <int P>
+  __device__ __forceinline__ void put_rows(const Op<P>& op, int i0) const {
+    const int l = lane(), r = l & 15, kg = (l >> 4) << 3;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      if ((K % 32 == 0) || (32 * s + kg < K)) op.put8(i0 + r, 32 * s + kg, x[s]);
+  }
+};
+
+// StripA over a token-major activation (fp32 or bf16) held as loaded: rows at or past `rows`
+// (>= 1) load the last valid row and read as 0.
+template <int K, class T>
+struct StripIO {
+  static constexpr int KS = (K + 31) / 32;
+  Raw8<T> x[KS];
+  bool valid;
+  __device__ __forceinline__ void fetch(const T* g, int ld, int i0, int rows) {
+    const int l = lane(), r = l & 15, kg = (l >> 4) << 3;
+    const int rr = i0 + r < rows ? i0 + r : rows - 1;
+    valid = i0 + r < rows;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) x[s].load(g + (size_t)rr * ld + ((32 * s + kg) % K));
+  }
+  template <int P, int TN, class BV>
+  __device__ __forceinline__ void product(f32x4 (&acc)[TN], const BV& B, int j0, int tn = TN,
+                                         float rs = 1.f) const {
+    const int l = lane(), r = l & 15, kg = (l >> 4) << 3;
+    const float f = valid ? rs : 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const bool ok = (K % 32 == 0) || (32 * s + kg < K);
+      float xs[8];
+      x[s].get(xs);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xs[e] = ok ? xs[e] * f : 0.f;
       const Frag<P> fa = make_frag<P>(xs);
 #pragma unroll
       for (int t = 0; t < TN; ++t) {
@@ -1252,14 +1281,20 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
 //   dk' = m1^T (beta k) + m2^T q + (kws . v_new) G^T
 //   dk  = dk' + beta dkb    d beta = rows(dkb, k) + rows(X, v)
 //   d gamma = rows(beta k, dkb) + rows(q, dq) - rows(k, dk')  (+ <G_after, S_after> at the
-//   chunk's last token) -- pallas_tpu_v2.py:272-318 regrouped by shared operands.
-// LDS: m1, then m2, in fp32 (read by rows and by columns); one operand region reused for v_new,
-// k^T, q^T, S and G.
+//   chunk's last token) -- pallas_tpu_v2.py:272-318 regrouped by shared operands. dkb is folded
+// into dk once complete (rows(k, dk') taken before, and from m2^T q kept apart).
+// rows(X, v) is added by k_post, which rebuilds v. Every input is read from global memory once:
+// each wave holds the X, do and v_new rows of its 16-row strip in registers (the A operands of
+// two products each; v_new's rows are also its share of the B operand of m1 and m2), and the k
+// and q rows of its strip at the accumulator layout (its share of the transposed k and q
+// operands, kept for the row sums). Stages: S, v_new, G, k^T, q^T through one LDS operand
+// region; m1, then m2, in fp32 LDS (read by rows and by columns).
 template <int C, int D, int PI, int PS, class TIO>
 __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
   constexpr int NT = C * 4;
   constexpr int LA = C + 4;
   constexpr int M = C > D ? C : D;
+  constexpr int TD = D / 16;
   using TB = OpTile<PI, M, M>;
   __shared__ float sA[C * LA];
   __shared__ __align__(16) char sB[TB::BYTES];
@@ -1267,25 +1302,32 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
   const Op<PI> ob = TB::at(sB);
   const int id = blockIdx.x;
   const int n = id % A.N, bh = id / A.N, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
-  load_ctx<C, NT>(cx, A, b, h, n);
+  const int w = wave(), i0 = 16 * w, r = lane() & 15;
   const float* qg = A.qn + hoff(A, b, hk, A.Hk, n, C, D);
   const float* kg = A.kn + hoff(A, b, hk, A.Hk, n, C, D);
   const size_t off = hoff(A, b, h, A.H, n, C, D);
-  const float* xg = A.xl + off;
-  const float* vng = A.vnew + off;
-  const float* vg = A.vv + off;
-  const float* Sg = A.states + ((size_t)bh * A.N + n) * D * D;
-  const float* Gg = A.gg + ((size_t)bh * A.N + n) * D * D;
   const TIO* dout = reinterpret_cast<const TIO*>(A.d_out);
-  const KRowLim<TIO> dov{dout + (((size_t)b * A.T + (size_t)n * C) * A.H + h) * D, A.H * D, A.T - n * C};
-  const int w = wave(), i0 = 16 * w;
-  stage_rows<C, D, NT>(ob, vng, D);  // v_new: B(dv, j) = v_new[j][dv]
+  StripA<D> xs, vn;
+  StripIO<D, TIO> dos;
+  xs.fetch(A.xl + off, D, i0);
+  dos.fetch(dout + (((size_t)b * A.T + (size_t)n * C) * A.H + h) * D, A.H * D, i0, A.T - n * C);
+  load_ctx<C, NT>(cx, A, b, h, n);
+  stage_rows<D, D, NT>(ob, A.states + ((size_t)bh * A.N + n) * D * D, D);  // S: B(dv, j=dk) = S[dk][dv]
+  vn.fetch(A.vnew + off, D, i0);
+  __syncthreads();
+  f32x4 dkb[TD], dq[TD];
+  zero(dkb);
+  zero(dq);
+  xs.template product<PS>(dkb, ob, 0, TD, -cx.grow[i0 + r]);  // -(grow X) S^T
+  dos.template product<PS>(dq, ob, 0, TD, cx.grow[i0 + r]);   // (grow do) S^T
+  __syncthreads();
+  vn.put_rows(ob, i0);  // v_new: B(dv, j) = v_new[j][dv]
   __syncthreads();
   f32x4 m2[C / 16];
   {  // m1 -> LDS, m2 -> registers
     f32x4 acc[C / 16];
     zero(acc);
-    strip_mma_full<PI, D, C / 16>(acc, krow(xg, D), i0, ob, 0, w + 1);
+    xs.template product<PI>(acc, ob, 0, w + 1);
 #pragma unroll
     for (int t = 0; t < C / 16; ++t)
 #pragma unroll
@@ -1294,7 +1336,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
         lds_st(sA + i * LA + j, (i > j && t <= w) ? -acc[t][rr] * decay(cx, i, j) : 0.f);
       }
     zero(m2);
-    strip_mma_full<PI, D, C / 16>(m2, dov, i0, ob, 0, w + 1);
+    dos.template product<PI>(m2, ob, 0, w + 1);
 #pragma unroll
     for (int t = 0; t < C / 16; ++t)
 #pragma unroll
@@ -1304,56 +1346,64 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
       }
   }
   __syncthreads();
-  stage_cols<C, D, NT>(ob, kg, D);  // k^T: B(c, j) = k[c][j]
+  stage_rows<D, D, NT>(ob, A.gg + ((size_t)bh * A.N + n) * D * D, D);  // G
   __syncthreads();
-  f32x4 dkb[D / 16], dk[D / 16], dq[D / 16];
-  zero(dkb);
+  f32x4 dk[TD];
   zero(dk);
-  zero(dq);
-  strip_mma<PI, C, D / 16>(dkb, krow(sA, LA), i0, ob, 0, 0, tri_end<C>(i0));                          // m1 k
-  strip_mma<PI, C, D / 16>(dk, scale_k(kcol(sA, LA), cx.beta), i0, ob, 0, tri_begin(i0), C);          // m1^T beta k
+  vn.template product<PS>(dk, ob, 0, TD, cx.kws[i0 + r]);  // (kws v_new) G^T
+  AccVals<TD> kk;  // (k and q are fetched late: live across the stages before, they would spill)
+  kk.fetch(kg, D, i0);
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < TD; ++t)  // k^T: B(c, j) = k[c][j]
+    ob.put4(16 * t + acc_col(), i0 + acc_row(0), kk.v[t][0], kk.v[t][1], kk.v[t][2], kk.v[t][3]);
+  __syncthreads();
+  strip_mma<PI, C, TD>(dkb, krow(sA, LA), i0, ob, 0, 0, tri_end<C>(i0));                  // m1 k
+  strip_mma<PI, C, TD>(dk, scale_k(kcol(sA, LA), cx.beta), i0, ob, 0, tri_begin(i0), C);  // m1^T beta k
+  // dkb is complete: its row sums with k, those of dk' so far, then dkb folded into dk
+  float r3[4] = {0.f, 0.f, 0.f, 0.f}, r4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < TD; ++t)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      r4[rr] += dkb[t][rr] * kk.v[t][rr];
+      r3[rr] += kk.v[t][rr] * dk[t][rr];
+      dk[t][rr] += cx.beta[i0 + acc_row(rr)] * dkb[t][rr];
+    }
   __syncthreads();
 #pragma unroll
   for (int t = 0; t < C / 16; ++t)
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) lds_st(sA + (i0 + acc_row(rr)) * LA + 16 * t + acc_col(), m2[t][rr]);
+  AccVals<TD> qq;
+  qq.fetch(qg, D, i0);
   __syncthreads();
-  strip_mma<PI, C, D / 16>(dq, krow(sA, LA), i0, ob, 0, 0, tri_end<C>(i0));                           // m2 k
+  strip_mma<PI, C, TD>(dq, krow(sA, LA), i0, ob, 0, 0, tri_end<C>(i0));  // m2 k
   __syncthreads();
-  stage_cols<C, D, NT>(ob, qg, D);  // q^T
-  __syncthreads();
-  strip_mma<PI, C, D / 16>(dk, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);                            // m2^T q
-  __syncthreads();
-  stage_rows<D, D, NT>(ob, Sg, D);  // S: B(dv, j=dk) = S[dk][dv]
-  __syncthreads();
-  strip_mma<PS, D, D / 16>(dkb, scale_r(krow(xg, D), cx.grow, -1.f), i0, ob, 0);                       // -(grow X) S^T
-  strip_mma<PS, D, D / 16>(dq, scale_r(dov, cx.grow), i0, ob, 0);                                      // (grow do) S^T
-  __syncthreads();
-  stage_rows<D, D, NT>(ob, Gg, D);  // G
-  __syncthreads();
-  strip_mma<PS, D, D / 16>(dk, scale_r(krow(vng, D), cx.kws), i0, ob, 0);                             // (kws v_new) G^T
-  // epilogue: row sums and the per-value-head dq, dk
-  float r2[4] = {0.f, 0.f, 0.f, 0.f}, r3[4] = {0.f, 0.f, 0.f, 0.f}, r4[4] = {0.f, 0.f, 0.f, 0.f};
-  float rxv[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int t = 0; t < D / 16; ++t)
+  for (int t = 0; t < TD; ++t)  // q^T
+    ob.put4(16 * t + acc_col(), i0 + acc_row(0), qq.v[t][0], qq.v[t][1], qq.v[t][2], qq.v[t][3]);
+  __syncthreads();
+  f32x4 dk2[TD];  // kept apart from dk, whose rows(k, .) would cancel the folded beta dkb
+  zero(dk2);
+  strip_mma<PI, C, TD>(dk2, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // m2^T q
+  // epilogue: row sums and the per-value-head dq, dk
+  float r2[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < TD; ++t)
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-      const float kv = kg[i * D + j], qv = qg[i * D + j];
-      r4[rr] += dkb[t][rr] * kv;
-      r2[rr] += qv * dq[t][rr];
-      r3[rr] += kv * dk[t][rr];
-      rxv[rr] += xg[i * D + j] * vg[i * D + j];
+      r2[rr] += qq.v[t][rr] * dq[t][rr];
+      r3[rr] += kk.v[t][rr] * dk2[t][rr];
       A.dqh[off + i * D + j] = dq[t][rr];
-      A.dkh[off + i * D + j] = dk[t][rr] + cx.beta[i] * dkb[t][rr];
+      A.dkh[off + i * D + j] = dk[t][rr] + dk2[t][rr];
     }
 #pragma unroll
   for (int rr = 0; rr < 4; ++rr) {
     r2[rr] = sum16(r2[rr]);
     r3[rr] = sum16(r3[rr]);
     r4[rr] = sum16(r4[rr]);
-    rxv[rr] = sum16(rxv[rr]);
   }
   if (acc_col() == 0) {
     const size_t tok = (size_t)bh * A.Tp + (size_t)n * C;
@@ -1367,7 +1417,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
         dgm += s;
       }
       A.dgam[tok + i] = dgm;
-      A.dbet[tok + i] = r4[rr] + rxv[rr];
+      A.dbet[tok + i] = r4[rr];
     }
   }
 }
@@ -1376,7 +1426,8 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
 // grid (B*N, 2*Hk + H), 256 threads: the activations' gradients back to d(qkv) -- GQA sums,
 // l2norm backward (pallas_tpu_mega.py:101-103), SiLU and the anti-causal conv backward with
 // segment masks (pallas_tpu_mega.py:161-179, 306-319) -- and, for the value heads, the gate
-// backward (pallas_tpu_mega.py:129-145): dg = reverse in-chunk cumsum of d gamma.
+// backward (pallas_tpu_mega.py:129-145): dg = reverse in-chunk cumsum of d gamma, and d beta
+// completed with rows(X, v) from the rebuilt v.
 template <int C, int D, class TIO, class TG>
 __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
   constexpr int CG = D / 8;
@@ -1386,6 +1437,7 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
   constexpr int SZ = R * LZ > 256 * 5 * 8 ? R * LZ : 256 * 5 * 8;  // also the d(conv w) scratch
   __shared__ float sdz[SZ];
   __shared__ int sseg[R];
+  __shared__ float sxv[C];  // value heads: rows(X, v) of the chunk's tokens
   const int b = blockIdx.x / A.N, n = blockIdx.x % A.N;
   const int slot = blockIdx.y;
   const int cg = threadIdx.x % CG;
@@ -1477,9 +1529,16 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
       for (int m = 1; m < CG; m <<= 1) dot += __shfl_xor(dot, m);
 #pragma unroll
       for (int e = 0; e < 8; ++e) dy[e] = rn * (dy[e] - act[e] * rn * dot);
-    } else {
+    } else {  // dv = X beta, and rows(X, v) for d beta (v is this head's activation)
+      float xv = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dy[e] = dyv[i][e] * btv[i];
+      for (int e = 0; e < 8; ++e) {
+        dy[e] = dyv[i][e] * btv[i];
+        xv += dyv[i][e] * act[e];
+      }
+#pragma unroll
+      for (int m = 1; m < CG; m <<= 1) xv += __shfl_xor(xv, m);
+      if (cg == 0 && r < C) sxv[r] = xv;
     }
     float dz[8];
     if (taps == 0) {
@@ -1609,7 +1668,7 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
         const double dad = dg * (double)(-ea * sigmoidf_(xg));
         const float dav = (float)dad;
         const float bt = sigmoidf_(bv);
-        const float dbv = A.dbet[tok + i] * bt * (1.f - bt);
+        const float dbv = (A.dbet[tok + i] + sxv[i]) * bt * (1.f - bt);
         sa += dg * (double)g;
         sd += dad;
         if (in) {
