@@ -34,6 +34,8 @@ def _args(argv=None):
     ap.add_argument("--config", default="0.8B")
     ap.add_argument("--precision", default=None, help="override the config's precision")
     ap.add_argument("--no-norm", action="store_true", help="time the GDN core alone, without the gated RMSNorm")
+    ap.add_argument("--residuals", default="all", choices=("all", "tinv", "states"),
+                    help="what the forward keeps for the backward (the operator's default: all)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=1, help="rows of the workload in the CPU baseline sample")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum timed CPU work of the baseline")
@@ -130,10 +132,10 @@ def main(argv=None) -> int:
     else:
         d_out = d_y
     plan = GdnPlan(batch=B, length=T, key_heads=Hk, key_dim=D, value_heads=H, value_dim=D, taps=w.shape[0],
-                   chunk=C, io_dtype=dtype, gate_dtype=dtype, precision=precision)
+                   chunk=C, io_dtype=dtype, gate_dtype=dtype, precision=precision, residuals=args.residuals)
     ws = torch.empty(max(plan.fwd_bytes, plan.bwd_bytes), dtype=torch.uint8, device=dev)
     out = torch.empty((B, T, H, D), dtype=dtype, device=dev)
-    states = torch.empty(plan.states_shape, dtype=torch.float32, device=dev)
+    states = plan.residuals(dev)
     d_qkv, d_a, d_b = torch.empty_like(qkv), torch.empty_like(a), torch.empty_like(b)
     d_alog, d_dtb = torch.empty_like(a_log), torch.empty_like(dt_bias)
 
@@ -199,7 +201,7 @@ def main(argv=None) -> int:
         "config": {"workload": f"{args.config} GDN layer core (mega2) fwd+bwd", "batch": B, "seq_len": T,
                    "key_heads": Hk, "value_heads": H, "head_dim": D, "chunk": C, "conv_taps": int(w.shape[0]),
                    "precision": precision, "segments": cfg["segments"],
-                   "epilogue": "gated_rmsnorm" if norm else None},
+                   "epilogue": "gated_rmsnorm" if norm else None, "residuals": args.residuals},
         "roofline": {"kernel": dominant, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
                      "unit": dk["unit"], "frac": dk["frac"], "traffic": traffic},
         "operator_roofline": {"algorithmic_gflop": op["flops"] / 1e9, "algorithmic_mb": op["bytes"] / 1e6,

@@ -16,8 +16,14 @@
  *   conv_w     [K, 2*Hk*Dk + H*Dv]     fp32       (K = taps; ignored when taps == 0)
  *   seg        [B, T] int32            segment ids, 0 = padding
  *   out        [B, T, H, Dv]           io_dtype
- *   states     [B, H, ceil(T/C), Dk, Dv] fp32     the state before each chunk: the only
- *                                                 residual the backward needs besides the inputs
+ *   residuals  fp32, tjev_gdn_residual_bytes(p) bytes, the forward's output for the backward,
+ *              each part 256-byte aligned, in this order:
+ *                states [B, H, ceil(T/C), Dk, Dv]  the state before each chunk (gdn_states)
+ *                tinv   [B, H, ceil(T/C), C, C]    (I + L)^-1 of each chunk (gdn_tinv), when
+ *                                                   residuals >= TJEV_GDN_SAVE_TINV
+ *                v_new  [B, H, ceil(T/C)*C, Dv]    u - w S of each token, when
+ *                                                   residuals == TJEV_GDN_SAVE_ALL
+ *              (C: the chunk the kernels run, max(chunk, 16))
  * T need not be a multiple of the chunk: the tail is treated as segment-0 padding with zero
  * qkv, a and b, as the reference pads (pallas_tpu_mega.py:616-621).
  */
@@ -45,6 +51,12 @@ enum tjev_gdn_precision {
 /* the reference's `inverse` (pallas_tpu_v2.py:141) */
 enum tjev_gdn_inverse { TJEV_GDN_DOUBLING = 0, TJEV_GDN_BLOCKED = 1 };
 
+/* what the forward keeps for the backward (the reference's remat residual contract names
+ * gdn_tinv and gdn_states, pallas_tpu_mega.py:543-548): the states only (the backward rebuilds
+ * T and v_new: least memory), states and T (the reference's residuals: the backward rebuilds
+ * v_new from T), or states, T and v_new (the backward rebuilds neither) */
+enum tjev_gdn_residuals { TJEV_GDN_SAVE_STATES = 0, TJEV_GDN_SAVE_TINV = 1, TJEV_GDN_SAVE_ALL = 2 };
+
 enum tjev_gdn_status {
   TJEV_GDN_OK = 0,
   TJEV_GDN_EINVAL = 1,       /* bad shape or parameter (the reference raises ValueError) */
@@ -67,20 +79,23 @@ typedef struct tjev_gdn_params {
   int32_t precision;      /* tjev_gdn_precision */
   int32_t inverse;        /* tjev_gdn_inverse */
   int32_t heads_per_step; /* accepted for the reference's signature (0 = default) */
+  int32_t residuals;      /* tjev_gdn_residuals */
 } tjev_gdn_params;
 
 /* 0 if the library has kernels for these parameters, else a status (and the message). */
 int tjev_gdn_check(const tjev_gdn_params* p);
 
-/* bytes of the states residual, and of the scratch the forward / backward need */
+/* bytes of the states part of the residuals, of all the residuals p->residuals keeps, and of
+ * the scratch the forward / backward need */
 size_t tjev_gdn_states_bytes(const tjev_gdn_params* p);
+size_t tjev_gdn_residual_bytes(const tjev_gdn_params* p);
 size_t tjev_gdn_workspace_bytes(const tjev_gdn_params* p, int backward);
 
-/* forward: replaces pallas_call "gdn_mega2_fwd" (pallas_tpu_mega.py:429-468); writes out and
- * states. `stream` is a hipStream_t. */
+/* forward: replaces pallas_call "gdn_mega2_fwd" (pallas_tpu_mega.py:429-468), whose outputs are
+ * out, tinv and states (:444-449); writes out and the residuals. `stream` is a hipStream_t. */
 int tjev_gdn_mega2_fwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a,
                        const void* b, const float* a_log, const float* dt_bias,
-                       const float* conv_w, const int32_t* seg, void* out, float* states,
+                       const float* conv_w, const int32_t* seg, void* out, float* residuals,
                        void* workspace, size_t workspace_bytes);
 
 /* backward: replaces pallas_call "gdn_mega2_bwd" (pallas_tpu_mega.py:471-524) plus the XLA sums
@@ -89,7 +104,7 @@ int tjev_gdn_mega2_fwd(const tjev_gdn_params* p, void* stream, const void* qkv, 
  * gdn_mega2_bwd_dw variant, computed only when requested). */
 int tjev_gdn_mega2_bwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a,
                        const void* b, const float* a_log, const float* dt_bias,
-                       const float* conv_w, const int32_t* seg, const float* states,
+                       const float* conv_w, const int32_t* seg, const float* residuals,
                        const void* d_out, void* d_qkv, void* d_a, void* d_b, float* d_a_log,
                        float* d_dt_bias, float* d_conv_w, void* workspace,
                        size_t workspace_bytes);

@@ -13,10 +13,13 @@ Each function follows a reference file (paths relative to the tjev repository ro
 - ``recurrent_gated_delta_rule``               xla.py:141-167
 - ``chunk_gated_delta_rule``                   xla.py:170-262 (precision "highest",
                                                inverse "solve")
+- ``chunk_tinv``                               the forward's gdn_tinv residual
+                                               (pallas_tpu_mega.py:444-449, 546): (I + L)^-1
+                                               of each chunk, L as in xla.py:205-240
 - ``masks``                                    pallas_tpu_mega.py:349-361 with
                                                pallas_tpu_v2.py:505-515 (integer logic)
 - ``heads_per_block``                          pallas_tpu_v2.py:518-525
-- ``reference_core``                           tests/kernels/test_gdn_mega.py:44-58
+- ``reference_core`` / ``core_inputs``        tests/kernels/test_gdn_mega.py:44-58
                                                (``_reference``), the recurrent variant
                                                tests/kernels/test_gdn_long.py:131-176
 - ``gated_rmsnorm``                            src/tjev/model/norms.py:13-15, 36-40
@@ -162,16 +165,11 @@ def recurrent_gated_delta_rule(q, k, v, g, beta, segment_ids=None, initial_state
     return torch.stack(outs, dim=1), s
 
 
-def chunk_gated_delta_rule(q, k, v, g, beta, segment_ids=None, initial_state=None,
-                           chunk: int = 64):
-    """Chunked WY/UT form with segment resets (xla.py:170-262) at precision "highest"
-    (the matmuls in the inputs' float dtype) with the triangular solve (``inverse="solve"``).
-
-    Pads T to a multiple of ``chunk`` with zero q/k/v/beta, g = 0 and the edge segment id
-    (xla.py:198-204). Returns (out [B,T,H,Dv], final state [B,H,Dk,Dv])."""
+def _chunk_terms(q, k, v, g, beta, segment_ids, initial_state, chunk: int) -> dict:
+    """The chunk-local terms of the chunked form (xla.py:198-240): T padded to a multiple of
+    ``chunk`` with zero q/k/v/beta, g = 0 and the edge segment id (xla.py:198-204), inputs as
+    [B,H,N,C,...], the segment masks, the in-chunk decay and L = strict((k beta) k^T . decay)."""
     batch, length, heads, dk = k.shape
-    dv = v.shape[-1]
-    dt = q.dtype
     if segment_ids is None:
         segment_ids = torch.ones((batch, length), dtype=torch.int64)
     segment_ids = segment_ids.to(torch.int64)
@@ -193,7 +191,6 @@ def chunk_gated_delta_rule(q, k, v, g, beta, segment_ids=None, initial_state=Non
     before = torch.cat([first, seg[:, :-1, -1]], dim=1)
     continues = (seg == before[..., None])[:, None]  # [B,1,N,C]
     in_last = (seg == seg[..., -1:])[:, None]
-    carry_keep = continues[..., -1]
     causal = torch.tril(torch.ones((chunk, chunk), dtype=torch.bool))
     same = ((seg[..., :, None] == seg[..., None, :]) & causal)[:, None]  # [B,1,N,C,C]
 
@@ -201,9 +198,37 @@ def chunk_gated_delta_rule(q, k, v, g, beta, segment_ids=None, initial_state=Non
     diff = cum[..., :, None] - cum[..., None, :]
     decay = torch.exp(torch.where(same, diff, torch.full_like(diff, -torch.inf)))
     k_beta = k * beta[..., None]
-    v_beta = v * beta[..., None]
     strict = torch.tril(torch.ones((chunk, chunk), dtype=torch.bool), -1)
     lower = torch.where(strict, (k_beta @ k.transpose(-1, -2)) * decay, 0.0)
+    return dict(q=q, k=k, v=v, beta=beta, n=n, length=length, continues=continues, in_last=in_last,
+                cum=cum, decay=decay, k_beta=k_beta, lower=lower)
+
+
+def chunk_tinv(k, g, beta, segment_ids=None, chunk: int = 64) -> torch.Tensor:
+    """(I + L)^-1 of every chunk [B,H,N,C,C] by triangular solve: the forward's ``gdn_tinv``
+    residual (pallas_tpu_mega.py:444-449, 546), L as in ``chunk_gated_delta_rule``."""
+    z = torch.zeros_like(k)
+    lower = _chunk_terms(z, k, z, g, beta, segment_ids, None, chunk)["lower"]
+    eye = torch.eye(chunk, dtype=k.dtype).expand(lower.shape)
+    return torch.linalg.solve_triangular(lower + eye, eye, upper=False, unitriangular=True)
+
+
+def chunk_gated_delta_rule(q, k, v, g, beta, segment_ids=None, initial_state=None,
+                           chunk: int = 64):
+    """Chunked WY/UT form with segment resets (xla.py:170-262) at precision "highest"
+    (the matmuls in the inputs' float dtype) with the triangular solve (``inverse="solve"``).
+
+    Pads T to a multiple of ``chunk`` with zero q/k/v/beta, g = 0 and the edge segment id
+    (xla.py:198-204). Returns (out [B,T,H,Dv], final state [B,H,Dk,Dv])."""
+    batch, length, heads, dk = k.shape
+    dv = v.shape[-1]
+    dt = q.dtype
+    t = _chunk_terms(q, k, v, g, beta, segment_ids, initial_state, chunk)
+    q, k, v, beta, n = t["q"], t["k"], t["v"], t["beta"], t["n"]
+    continues, in_last, cum, decay, k_beta, lower = (t[x] for x in ("continues", "in_last", "cum", "decay",
+                                                                   "k_beta", "lower"))
+    carry_keep = continues[..., -1]
+    v_beta = v * beta[..., None]
     grow = torch.exp(cum) * continues
     rhs = torch.cat([v_beta, k_beta * grow[..., None]], dim=-1)
     eye = torch.eye(chunk, dtype=dt)
@@ -278,6 +303,20 @@ def reference_core(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_h
     Every floating input is cast to ``dtype`` first (bf16 projections are judged against
     the reference on the same values in fp32, test_gdn_mega.py:281-297). Returns
     [B,T,H,Dv] in ``dtype``; differentiable by autograd."""
+    q, k, v, g, beta, seg = core_inputs(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, key_heads=key_heads,
+                                        key_dim=key_dim, value_heads=value_heads, value_dim=value_dim, conv=conv,
+                                        dtype=dtype)
+    if rule == "chunked":
+        return chunk_gated_delta_rule(q, k, v, g, beta, seg, chunk=chunk)[0]
+    if rule == "recurrent":
+        return recurrent_gated_delta_rule(q, k, v, g, beta, seg)[0]
+    raise ValueError(f"rule in (chunked, recurrent), not {rule!r}")
+
+
+def core_inputs(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_heads: int, key_dim: int,
+                value_heads: int, value_dim: int, conv: bool = True, dtype=torch.float32):
+    """q, k (repeated to the value heads), v, g, beta and the int64 segment ids that
+    ``reference_core`` feeds the delta rule (test_gdn_mega.py:44-58)."""
     qkv, a, b, a_log, dt_bias = (x.to(dtype) for x in (qkv, a, b, a_log, dt_bias))
     seg = segment_ids.to(torch.int64)
     batch, length, _ = qkv.shape
@@ -296,11 +335,7 @@ def reference_core(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_h
     g = -torch.exp(a_log) * torch.logaddexp(xg, torch.zeros_like(xg))  # jax.nn.softplus
     ratio = h // hk
     q, k = q.repeat_interleave(ratio, dim=2), k.repeat_interleave(ratio, dim=2)
-    if rule == "chunked":
-        return chunk_gated_delta_rule(q, k, v, g, beta, seg, chunk=chunk)[0]
-    if rule == "recurrent":
-        return recurrent_gated_delta_rule(q, k, v, g, beta, seg)[0]
-    raise ValueError(f"rule in (chunked, recurrent), not {rule!r}")
+    return q, k, v, g, beta, seg
 
 
 def reference_with_grads(inputs, cotangent, *, key_heads, key_dim, value_heads, value_dim,

@@ -47,7 +47,7 @@ def _run(inputs, cot, hk, h):
                    chunk=C, io_dtype=qkv.dtype, gate_dtype=a.dtype, precision="high")
     ws = torch.empty(max(plan.fwd_bytes, plan.bwd_bytes), dtype=torch.uint8, device="cuda")
     out = torch.empty((B, T, h, D), dtype=qkv.dtype, device="cuda")
-    states = torch.empty(plan.states_shape, dtype=torch.float32, device="cuda")
+    states = plan.residuals("cuda")
     plan.forward(qkv, a, b, a_log, dt_bias, w, seg, out, states, ws)
     d_qkv, d_a, d_b = torch.empty_like(qkv), torch.empty_like(a), torch.empty_like(b)
     d_alog, d_dtb = torch.empty_like(a_log), torch.empty_like(dt_bias)

@@ -50,6 +50,7 @@ def _params(**kw):
     (dict(taps=6), 1, "taps"),
     (dict(key_dim=48, value_dim=48), 2, "no kernels"),
     (dict(value_dim=32), 2, "key_dim == value_dim"),
+    (dict(residuals=3), 1, "residuals"),
 ])
 def test_c_abi_validation(bad, status, msg):
     from tjev_amd import _lib
@@ -71,6 +72,16 @@ def test_c_abi_sizes():
     assert lib.tjev_gdn_states_bytes(ctypes.byref(p)) == 4 * 16 * 32 * 128 * 128 * 4
     fwd, bwd = (lib.tjev_gdn_workspace_bytes(ctypes.byref(p), k) for k in (0, 1))
     assert 0 < fwd < bwd < (2 << 30)
+    # the residuals: states, then T (B*H*N*C*C fp32) and v_new (B*H*N*C*Dv fp32) as kept; what
+    # is kept leaves the workspaces
+    part = 4 * 16 * 32 * 128 * 128 * 4
+    assert lib.tjev_gdn_residual_bytes(ctypes.byref(p)) == part
+    for mode, total in ((1, 2 * part), (2, 3 * part)):
+        p.residuals = mode
+        assert lib.tjev_gdn_residual_bytes(ctypes.byref(p)) == total
+        assert lib.tjev_gdn_states_bytes(ctypes.byref(p)) == part
+    assert lib.tjev_gdn_workspace_bytes(ctypes.byref(p), 0) == fwd - part
+    assert lib.tjev_gdn_workspace_bytes(ctypes.byref(p), 1) == bwd - 2 * part
     # a ragged T is padded to whole chunks (segment-0 padding, as the reference pads)
     p = _params(length=100, chunk=16)
     assert lib.tjev_gdn_states_bytes(ctypes.byref(p)) == 1 * 4 * 7 * 16 * 16 * 4

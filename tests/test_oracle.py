@@ -352,3 +352,44 @@ def test_planted_mistakes_are_caught(monkeypatch):
     (gr,) = torch.autograd.grad((O.l2norm(xx) * torch.ones(1, 4, dtype=F64)).sum(), xx)
     assert not torch.all(gr == 0)
     assert orig_cat is torch.cat
+
+
+# ------------------------------------------------------------------ the gdn_tinv residual
+def test_chunk_tinv_inverts_each_chunk_brute_force():
+    """chunk_tinv against L built element by element from its definition (beta_i k_i.k_j
+    e^(gamma_i - gamma_j) for i > j in one segment, gamma the in-chunk cumsum of g) and a dense
+    fp64 inverse per chunk; a segment reset inside a chunk, padding, and T not a multiple of C."""
+    rng = np.random.default_rng(7)
+    b, t, h, d, c = 1, 40, 2, 8, 16
+    k = torch.from_numpy(rng.standard_normal((b, t, h, d)))
+    k = k / k.norm(dim=-1, keepdim=True)
+    g = torch.from_numpy(-rng.uniform(0.01, 0.5, (b, t, h)))
+    beta = torch.from_numpy(rng.uniform(0.1, 0.9, (b, t, h)))
+    seg = torch.ones((b, t), dtype=torch.int64)
+    seg[0, 21:] = 2
+    seg[0, 37:] = 0
+    got = O.chunk_tinv(k, g, beta, seg, chunk=c)
+    n = (t + c - 1) // c
+    assert got.shape == (b, h, n, c, c)
+    for hh in range(h):
+        for ch in range(n):
+            lower = np.zeros((c, c))
+            gam = np.zeros(c)
+            run = 0.0
+            for i in range(c):
+                tok = ch * c + i
+                run += float(g[0, tok, hh]) if tok < t else 0.0
+                gam[i] = run
+            for i in range(c):
+                for j in range(i):
+                    ti, tj = ch * c + i, ch * c + j
+                    if ti >= t:  # padding: zero k and beta, the edge segment id
+                        continue
+                    if int(seg[0, ti]) != int(seg[0, tj]):
+                        continue
+                    lower[i, j] = float(beta[0, ti, hh]) * float(k[0, ti, hh] @ k[0, tj, hh]) * np.exp(gam[i] - gam[j])
+            want = np.linalg.inv(np.eye(c) + lower)
+            assert np.abs(got[0, hh, ch].numpy() - want).max() < 1e-12 * max(1.0, np.abs(want).max())
+    # and the doubling restatement agrees with the solve on the same chunks
+    lower = torch.linalg.inv(got) - torch.eye(c, dtype=got.dtype)
+    assert float((O.unit_lower_inverse(lower) - got).abs().max()) < 1e-10

@@ -17,11 +17,13 @@ LIB_PATH = Path(__file__).resolve().parent / "libtjev_gdn.so"
 F32, BF16 = 0, 1
 PRECISION = {"highest": 0, "high": 1, "bf16": 2, "mixed": 3}
 INVERSE = {"doubling": 0, "blocked": 1}
+RESIDUALS = {"states": 0, "tinv": 1, "all": 2}  # tjev_gdn_residuals
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported", 3: "workspace", 4: "HIP error"}
 
 EXPORTS = (
     "tjev_gdn_check",
     "tjev_gdn_states_bytes",
+    "tjev_gdn_residual_bytes",
     "tjev_gdn_workspace_bytes",
     "tjev_gdn_mega2_fwd",
     "tjev_gdn_mega2_bwd",
@@ -42,7 +44,7 @@ class Params(ctypes.Structure):
 
     _fields_ = [(name, ctypes.c_int32) for name in (
         "batch", "length", "key_heads", "key_dim", "value_heads", "value_dim", "taps", "chunk",
-        "io_dtype", "gate_dtype", "precision", "inverse", "heads_per_step",
+        "io_dtype", "gate_dtype", "precision", "inverse", "heads_per_step", "residuals",
     )]
 
 
@@ -78,6 +80,8 @@ def load() -> ctypes.CDLL:
     lib.tjev_gdn_check.restype = i32
     lib.tjev_gdn_states_bytes.argtypes = [pp]
     lib.tjev_gdn_states_bytes.restype = sz
+    lib.tjev_gdn_residual_bytes.argtypes = [pp]
+    lib.tjev_gdn_residual_bytes.restype = sz
     lib.tjev_gdn_workspace_bytes.argtypes = [pp, i32]
     lib.tjev_gdn_workspace_bytes.restype = sz
     lib.tjev_gdn_mega2_fwd.argtypes = [pp, vp] + [vp] * 10 + [sz]

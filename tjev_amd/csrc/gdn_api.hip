@@ -66,6 +66,8 @@ int validate(const tjev_gdn_params* p) {
   if (p->io_dtype < 0 || p->io_dtype > 1 || p->gate_dtype < 0 || p->gate_dtype > 1)
     return fail(TJEV_GDN_EINVAL, "dtypes must be TJEV_GDN_F32 or TJEV_GDN_BF16");
   if (p->heads_per_step < 0) return fail(TJEV_GDN_EINVAL, "heads_per_step must be >= 0");
+  if (p->residuals < TJEV_GDN_SAVE_STATES || p->residuals > TJEV_GDN_SAVE_ALL)
+    return fail(TJEV_GDN_EINVAL, "residuals must be TJEV_GDN_SAVE_STATES, _TINV or _ALL");
   if (p->key_dim != p->value_dim)
     return fail(TJEV_GDN_EUNSUPPORTED, "this build's kernels need key_dim == value_dim");
   if (!lookup(kernel_chunk(p), p->key_dim))
@@ -106,14 +108,14 @@ Layout layout(const tjev_gdn_params* p, int backward) {
   L.gam = take(tok);
   L.gaml = take(tok);
   L.bet = take(tok);
-  L.vnew = take(hv);
+  L.vnew = p->residuals == TJEV_GDN_SAVE_ALL ? none : take(hv);  // else a residual
   if (!backward) {
     L.uu = take(hv);
     L.ww = take(hv);
     L.tt = L.xl = L.kt = L.gg = L.gsp = L.dqh = L.dkh = L.dgam = L.dbet = L.pa = L.pd = L.dwp = none;
   } else {
     L.uu = L.ww = none;
-    L.tt = take(B * H * N * C * C * 4);
+    L.tt = p->residuals == TJEV_GDN_SAVE_STATES ? take(B * H * N * C * C * 4) : none;
     L.xl = take(hv);
     L.kt = take(hv);
     L.gg = take(B * H * N * D * D * 4);
@@ -128,6 +130,32 @@ Layout layout(const tjev_gdn_params* p, int backward) {
   }
   L.total = o;
   return L;
+}
+
+// the residual buffer: states, then T and v_new as p->residuals keeps them
+struct Residuals {
+  size_t states, tinv, vnew, total;
+};
+
+Residuals residual_layout(const tjev_gdn_params* p) {
+  const size_t C = kernel_chunk(p), D = p->key_dim;
+  const size_t B = p->batch, H = p->value_heads;
+  const size_t N = (p->length + C - 1) / C;
+  const size_t none = ~size_t(0);
+  Residuals R{};
+  R.states = 0;
+  size_t o = up(B * H * N * D * D * 4);
+  R.tinv = R.vnew = none;
+  if (p->residuals >= TJEV_GDN_SAVE_TINV) {
+    R.tinv = o;
+    o += up(B * H * N * C * C * 4);
+  }
+  if (p->residuals == TJEV_GDN_SAVE_ALL) {
+    R.vnew = o;
+    o += up(B * H * N * C * D * 4);
+  }
+  R.total = o;
+  return R;
 }
 
 template <class T>
@@ -171,7 +199,16 @@ gdn::GdnArgs base_args(const tjev_gdn_params* p, void* ws, const Layout& L) {
   A.pa = at<double>(ws, L.pa);
   A.pd = at<double>(ws, L.pd);
   A.dwp = at<float>(ws, L.dwp);
+  A.res = p->residuals;
   return A;
+}
+
+// the residual parts into the arguments (T and v_new there instead of in the workspace)
+void bind_residuals(const tjev_gdn_params* p, float* res, gdn::GdnArgs& A) {
+  const Residuals R = residual_layout(p);
+  A.states = res;
+  if (R.tinv != ~size_t(0)) A.tt = at<float>(res, R.tinv);
+  if (R.vnew != ~size_t(0)) A.vnew = at<float>(res, R.vnew);
 }
 
 int aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
@@ -243,6 +280,11 @@ size_t tjev_gdn_states_bytes(const tjev_gdn_params* p) {
   return (size_t)p->batch * p->value_heads * N * p->key_dim * p->value_dim * 4;
 }
 
+size_t tjev_gdn_residual_bytes(const tjev_gdn_params* p) {
+  if (validate(p)) return 0;
+  return residual_layout(p).total;
+}
+
 size_t tjev_gdn_workspace_bytes(const tjev_gdn_params* p, int backward) {
   if (validate(p)) return 0;
   return layout(p, backward).total;
@@ -250,12 +292,12 @@ size_t tjev_gdn_workspace_bytes(const tjev_gdn_params* p, int backward) {
 
 int tjev_gdn_mega2_fwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
                        const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg, void* out,
-                       float* states, void* workspace, size_t workspace_bytes) {
+                       float* residuals, void* workspace, size_t workspace_bytes) {
   if (int s = validate(p)) return s;
-  if (!qkv || !a || !b || !a_log || !dt_bias || !seg || !out || !states || (p->taps > 0 && !conv_w))
+  if (!qkv || !a || !b || !a_log || !dt_bias || !seg || !out || !residuals || (p->taps > 0 && !conv_w))
     return fail(TJEV_GDN_EINVAL, "null tensor argument");
-  if (!aligned(qkv, 16) || !aligned(out, 16) || !aligned(states, 16) || !aligned(workspace, 256))
-    return fail(TJEV_GDN_EINVAL, "qkv, out and states must be 16-byte aligned, the workspace 256-byte aligned");
+  if (!aligned(qkv, 16) || !aligned(out, 16) || !aligned(residuals, 256) || !aligned(workspace, 256))
+    return fail(TJEV_GDN_EINVAL, "qkv and out must be 16-byte aligned, the residuals and workspace 256-byte aligned");
   const Layout L = layout(p, 0);
   if (!workspace || workspace_bytes < L.total)
     return fail(TJEV_GDN_EWORKSPACE, "forward workspace needs " + std::to_string(L.total) + " bytes");
@@ -268,22 +310,22 @@ int tjev_gdn_mega2_fwd(const tjev_gdn_params* p, void* stream, const void* qkv, 
   A.conv_w = conv_w;
   A.seg = seg;
   A.out = out;
-  A.states = states;
+  bind_residuals(p, residuals, A);
   return run(p, stream, A, 0);
 }
 
 int tjev_gdn_mega2_bwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
                        const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg,
-                       const float* states, const void* d_out, void* d_qkv, void* d_a, void* d_b, float* d_a_log,
+                       const float* residuals, const void* d_out, void* d_qkv, void* d_a, void* d_b, float* d_a_log,
                        float* d_dt_bias, float* d_conv_w, void* workspace, size_t workspace_bytes) {
   if (int s = validate(p)) return s;
-  if (!qkv || !a || !b || !a_log || !dt_bias || !seg || !states || !d_out || !d_qkv || !d_a || !d_b || !d_a_log ||
+  if (!qkv || !a || !b || !a_log || !dt_bias || !seg || !residuals || !d_out || !d_qkv || !d_a || !d_b || !d_a_log ||
       !d_dt_bias || (p->taps > 0 && !conv_w))
     return fail(TJEV_GDN_EINVAL, "null tensor argument");
   if (p->taps == 0 && d_conv_w) return fail(TJEV_GDN_EINVAL, "no conv weight gradient without a conv (taps == 0)");
-  if (!aligned(qkv, 16) || !aligned(d_out, 16) || !aligned(d_qkv, 16) || !aligned(states, 16) ||
+  if (!aligned(qkv, 16) || !aligned(d_out, 16) || !aligned(d_qkv, 16) || !aligned(residuals, 256) ||
       !aligned(workspace, 256))
-    return fail(TJEV_GDN_EINVAL, "tensors must be 16-byte aligned, the workspace 256-byte aligned");
+    return fail(TJEV_GDN_EINVAL, "tensors must be 16-byte aligned, the residuals and workspace 256-byte aligned");
   const Layout L = layout(p, 1);
   if (!workspace || workspace_bytes < L.total)
     return fail(TJEV_GDN_EWORKSPACE, "backward workspace needs " + std::to_string(L.total) + " bytes");
@@ -295,7 +337,7 @@ int tjev_gdn_mega2_bwd(const tjev_gdn_params* p, void* stream, const void* qkv, 
   A.dt_bias = dt_bias;
   A.conv_w = conv_w;
   A.seg = seg;
-  A.states = const_cast<float*>(states);
+  bind_residuals(p, const_cast<float*>(residuals), A);
   A.d_out = d_out;
   A.d_qkv = d_qkv;
   A.d_a = d_a;

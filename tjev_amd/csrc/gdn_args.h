@@ -10,6 +10,7 @@ struct GdnArgs {
   int B, T, Tp, N, Hk, H, ratio, taps, W;
   int ntiles;  // Dv tiles of the scans
   int parts;   // chunk ranges per (row, head, tile) of the scans, split where a segment resets
+  int res;     // residuals kept by the forward: 0 states, 1 and T, 2 and v_new
   float scale; // Dk^-1/2
   // inputs
   const void* qkv;

@@ -51,14 +51,22 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
   } while (0)
   if (!backward) {
     GDN_LAUNCH(K_PREP_FWD, (k_prep<C, D, TIO, TG>), prep, dim3(256));
-    GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0>), persist, dim3(C * 4));
+    if (A.res == 0) {
+      GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0>), persist, dim3(C * 4));
+    } else {  // T kept for the backward
+      GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 2>), persist, dim3(C * 4));
+    }
     GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd<C, D, DVT, PI, PS>), tiles, dim3(NS));
     GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO>), persist, dim3(C * 4));
   } else {
     const int wouts = A.d_conv_w ? A.taps * A.W : 0;  // one workgroup per head, then the conv weights
     GDN_LAUNCH(K_PREP_BWD, (k_prep<C, D, TIO, TG>), prep, dim3(256));
-    GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 1>), persist, dim3(C * 4));
-    GDN_LAUNCH(K_BWD_LOCAL, (k_bwd_local<C, D, PI, TIO>), chunks, dim3(C * 4));
+    if (A.res == 0) {  // T and v_new rebuilt
+      GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 1>), persist, dim3(C * 4));
+    } else if (A.res == 1) {  // v_new from the saved T
+      GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 3>), persist, dim3(C * 4));
+    }  // else both saved
+    GDN_LAUNCH(K_BWD_LOCAL, (k_bwd_local<C, D, PI, TIO>), persist, dim3(C * 4));
     GDN_LAUNCH(K_SCAN_BWD, (k_scan_bwd<C, D, DVT, PI, PS, TIO>), tiles, dim3(NS));
     GDN_LAUNCH(K_BWD_GRADS, (k_bwd_grads<C, D, PI, PS, TIO>), chunks, dim3(C * 4));
     GDN_LAUNCH(K_POST, (k_post<C, D, TIO, TG>), prep, dim3(256));

@@ -737,13 +737,17 @@ __device__ __forceinline__ void load_tile(float* s, int LD, const float* g) {
 
 // ---------------------------------------------------------------- k_chunk
 // Persistent over the (row, head, chunk) units as k_out; C/16 waves (one 16-row strip each).
-// MODE 0 (forward): writes w and u. MODE 1 (backward recompute): writes T and
-// v_new = u - w S_before. LDS: T in fp32 (the inverse runs in place), one operand region reused
-// for k, kbe^T, (v beta)^T and S^T (the doubling scratch borrows it too). The next unit's
-// context and k rows are loaded at this unit's start and end; k (again), v and S of this unit
-// after the inverse, a product ahead of their use.
+// MODE 0 (forward): writes w and u; MODE 2: also T (kept as a residual). MODE 1 (backward
+// recompute): writes T and v_new = u - w S_before; MODE 3: v_new from the saved T (no L, no
+// inverse). LDS: T in fp32 (the inverse runs in place), one operand region reused for k,
+// kbe^T, (v beta)^T and S^T (the doubling scratch borrows it too). The next unit's context and
+// k rows are loaded at this unit's start and end; k (again), v and S of this unit after the
+// inverse, a product ahead of their use.
 template <int C, int D, int PI, int PS, int MODE>
 __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
+  constexpr bool FWD = MODE == 0 || MODE == 2;  // writes w and u (else v_new)
+  constexpr bool LOAD_T = MODE == 3;            // T from the residuals
+  constexpr bool STORE_T = MODE == 1 || MODE == 2;
   constexpr int NT = C * 4;
   constexpr int M = C > D ? C : D;
   constexpr int LT = M + 4;
@@ -767,46 +771,56 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
     const UnitIx x(A, u);
     const UnitIx y(A, u + gridDim.x < total ? u + gridDim.x : u);  // the next unit (or this one again)
     const size_t off = hoff(A, x.b, x.h, A.H, x.n, C, D);
+    float* tg = A.tt + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * C * C;
     rc.commit(cx);
-    kk.put_rows(ob);
+    if constexpr (!LOAD_T) kk.put_rows(ob);
     rc.fetch(A, y.b, y.h, y.n);
     RegsT<C, D, NT> vc;  // this unit's (v beta)^T source
-    RegsT<D, D, NT> sc;  // S_before (MODE 1)
+    RegsT<D, D, NT> sc;  // S_before (backward)
+    if constexpr (LOAD_T) {
+      vc.fetch(A.vv + off, D);
+      load_tile<C, C, NT>(sT, LT, tg);
+    }
     __syncthreads();
     derive_ctx<C, NT>(cx);
     __syncthreads();
-    {  // L = strict(beta_i (k k^T)_ij D_ij): tiles on and below the diagonal only
-      f32x4 acc[C / 16];
-      zero(acc);
-      strip_mma<PI, D, C / 16>(acc, ob, i0, ob, 0, 0, D, w + 1);
+    if constexpr (!LOAD_T) {
+      {  // L = strict(beta_i (k k^T)_ij D_ij): tiles on and below the diagonal only
+        f32x4 acc[C / 16];
+        zero(acc);
+        strip_mma<PI, D, C / 16>(acc, ob, i0, ob, 0, 0, D, w + 1);
 #pragma unroll
-      for (int t = 0; t < C / 16; ++t)
+        for (int t = 0; t < C / 16; ++t)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-          lds_st(sT + i * LT + j, (i > j && t <= w) ? cx.beta[i] * acc[t][rr] * decay(cx, i, j) : 0.f);
-        }
+          for (int rr = 0; rr < 4; ++rr) {
+            const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
+            lds_st(sT + i * LT + j, (i > j && t <= w) ? cx.beta[i] * acc[t][rr] * decay(cx, i, j) : 0.f);
+          }
+      }
+      __syncthreads();
+      invert_unit_lower<C, PI>(sT, LT, reinterpret_cast<float*>(sB));
+      // k again (not held across the inverse: register limit), then v
+      kk.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D);
+      vc.fetch(A.vv + off, D);
     }
-    __syncthreads();
-    invert_unit_lower<C, PI>(sT, LT, reinterpret_cast<float*>(sB));
-    // k again (not held across the inverse: register limit), then v
-    kk.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D);
-    vc.fetch(A.vv + off, D);
     f32x4 aw[D / 16], au[D / 16];
     zero(aw);
     zero(au);
     kk.put_cols(ob, cx.bg);  // kbe^T
     __syncthreads();
     strip_mma<PI, C, D / 16>(aw, krow(sT, LT), i0, ob, 0, 0, tri_end<C>(i0));
-    if constexpr (MODE == 1) sc.fetch(A.states + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * D * D, D);
+    if constexpr (!FWD) sc.fetch(A.states + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * D * D, D);
     __syncthreads();
     vc.put_cols(ob, cx.beta);  // (v beta)^T
     __syncthreads();
     strip_mma<PI, C, D / 16>(au, krow(sT, LT), i0, ob, 0, 0, tri_end<C>(i0));
     // the next unit's k before this unit's stores: waiting for it later (vmcnt counts in issue
     // order, stores included) then does not wait for the stores
-    if constexpr (MODE == 0) kk.fetch(A.kn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D);
-    if constexpr (MODE == 0) {
+    kk.fetch(A.kn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D);
+    if constexpr (STORE_T) {
+      for (int idx = threadIdx.x; idx < C * C; idx += NT) tg[idx] = sT[(idx / C) * LT + idx % C];
+    }
+    if constexpr (FWD) {
 #pragma unroll
       for (int t = 0; t < D / 16; ++t)
 #pragma unroll
@@ -816,9 +830,6 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
           A.uu[g] = au[t][rr];
         }
     } else {
-      kk.fetch(A.kn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D);  // before this unit's stores
-      float* tg = A.tt + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * C * C;
-      for (int idx = threadIdx.x; idx < C * C; idx += NT) tg[idx] = sT[(idx / C) * LT + idx % C];
       __syncthreads();
 #pragma unroll
       for (int t = 0; t < D / 16; ++t)
@@ -1074,7 +1085,34 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
 }
 
 // ---------------------------------------------------------------- k_bwd_local
-// grid B*H*N, C/16 waves: X_loc = T^T (intra^T do), Kt = T^T k_write.
+// Persistent over the (row, head, chunk) units as k_out; C/16 waves. Per unit:
+// X_loc = T^T (intra^T do) with intra = (q k^T) . D, and Kt = T^T k_write (k_write = kws . k).
+// Every global input is read once per unit into registers: the context, q and k (k for both of
+// its stagings: as rows for q k^T, transposed and scaled for k_write^T) are refilled with the
+// next unit's values once used; do and T are loaded at the unit's start and after its first
+// product (holding them across units as well would spill).
+template <int C, int D, int NT, class TIO>
+struct LocalIn {
+  CtxRaw<C> cx;
+  RegsT<C, D, NT> k;          // k rows
+  StripA<D> q;                // this wave's q rows (A operand of q k^T)
+  RegsIO<C, D, NT, TIO> dov;  // do rows, staged as do^T
+  Regs<C, C, NT> tt;          // T rows
+  __device__ __forceinline__ void fetch_k(const GdnArgs& A, const UnitIx& y) {
+    k.fetch(A.kn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D);
+  }
+  __device__ __forceinline__ void fetch_q(const GdnArgs& A, const UnitIx& y, int i0) {
+    q.fetch(A.qn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D, i0);
+  }
+  __device__ __forceinline__ void fetch_do(const GdnArgs& A, const UnitIx& y) {
+    const TIO* dout = reinterpret_cast<const TIO*>(A.d_out);
+    dov.fetch(dout + (((size_t)y.b * A.T + (size_t)y.n * C) * A.H + y.h) * D, A.H * D, A.T - y.n * C);
+  }
+  __device__ __forceinline__ void fetch_t(const GdnArgs& A, const UnitIx& y) {
+    tt.fetch(A.tt + ((size_t)y.bh * A.N + y.n) * C * C, C);
+  }
+};
+
 template <int C, int D, int PI, class TIO>
 __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
   constexpr int NT = C * 4;
@@ -1085,56 +1123,70 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
   __shared__ __align__(16) char sB[TB::BYTES];
   __shared__ Ctx<C> cx;
   const Op<PI> ob = TB::at(sB);
-  const int id = blockIdx.x;
-  const int n = id % A.N, bh = id / A.N, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
-  load_ctx<C, NT>(cx, A, b, h, n);
-  const float* qg = A.qn + hoff(A, b, hk, A.Hk, n, C, D);
-  const float* kg = A.kn + hoff(A, b, hk, A.Hk, n, C, D);
-  const size_t off = hoff(A, b, h, A.H, n, C, D);
   const int w = wave(), i0 = 16 * w;
-  stage_rows<C, D, NT>(ob, kg, D);
-  __syncthreads();
+  const int total = A.B * A.H * A.N;
+  LocalIn<C, D, NT, TIO> in;
   {
-    f32x4 acc[C / 16];
-    zero(acc);
-    strip_mma_full<PI, D, C / 16>(acc, krow(qg, D), i0, ob, 0, w + 1);
-#pragma unroll
-    for (int t = 0; t < C / 16; ++t)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-        lds_st(sA + i * LA + j, t <= w ? acc[t][rr] * decay(cx, i, j) : 0.f);
-      }
+    const UnitIx x(A, blockIdx.x);
+    in.cx.fetch(A, x.b, x.h, x.n);
+    in.fetch_k(A, x);
+    in.fetch_q(A, x, i0);
   }
-  __syncthreads();
-  const TIO* dout = reinterpret_cast<const TIO*>(A.d_out);
-  stage_cols_io<C, D, NT>(ob, dout + (((size_t)b * A.T + (size_t)n * C) * A.H + h) * D, A.H * D, A.T - n * C);
-  __syncthreads();
-  f32x4 acc[D / 16];
-  zero(acc);
-  strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // intra^T do
-  __syncthreads();
-  load_tile<C, C, NT>(sA, LA, A.tt + ((size_t)bh * A.N + n) * C * C);
+  for (int u = blockIdx.x; u < total; u += gridDim.x) {
+    const UnitIx x(A, u);
+    const UnitIx y(A, u + gridDim.x < total ? u + gridDim.x : u);  // the next unit (or this one again)
+    in.cx.commit(cx);
+    in.cx.fetch(A, y.b, y.h, y.n);
+    in.fetch_do(A, x);
+    in.k.put_rows(ob);  // B(d, j) = k[j][d]
+    __syncthreads();
+    derive_ctx<C, NT>(cx);
+    __syncthreads();
+    {  // intra = (q k^T) . D
+      f32x4 acc[C / 16];
+      zero(acc);
+      in.q.template product<PI>(acc, ob, 0, w + 1);
+      in.fetch_q(A, y, i0);
+      in.fetch_t(A, x);
 #pragma unroll
-  for (int t = 0; t < D / 16; ++t)
+      for (int t = 0; t < C / 16; ++t)
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) ob.put(16 * t + acc_col(), i0 + acc_row(rr), acc[t][rr]);  // dv_loc^T
-  __syncthreads();
-  zero(acc);
-  strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // T^T dv_loc
+        for (int rr = 0; rr < 4; ++rr) {
+          const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
+          lds_st(sA + i * LA + j, t <= w ? acc[t][rr] * decay(cx, i, j) : 0.f);
+        }
+    }
+    __syncthreads();
+    in.dov.put_cols(ob);
+    __syncthreads();
+    f32x4 acc[D / 16];
+    zero(acc);
+    strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // dv_loc = intra^T do
+    __syncthreads();
+    in.tt.put_lds(sA, LA);
 #pragma unroll
-  for (int t = 0; t < D / 16; ++t)
+    for (int t = 0; t < D / 16; ++t)  // dv_loc^T: B(c, j) = dv_loc[c][j]
+      ob.put4(16 * t + acc_col(), i0 + acc_row(0), acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+    __syncthreads();
+    zero(acc);
+    strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // T^T dv_loc
+    const size_t off = hoff(A, x.b, x.h, A.H, x.n, C, D);
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) A.xl[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = acc[t][rr];
-  __syncthreads();
-  stage_cols<C, D, NT>(ob, kg, D, cx.kws);  // k_write^T
-  __syncthreads();
-  zero(acc);
-  strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // T^T k_write
+    for (int t = 0; t < D / 16; ++t)
 #pragma unroll
-  for (int t = 0; t < D / 16; ++t)
+      for (int rr = 0; rr < 4; ++rr) A.xl[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = acc[t][rr];
+    __syncthreads();
+    in.k.put_cols(ob, cx.kws);  // k_write^T
+    in.fetch_k(A, y);
+    __syncthreads();
+    zero(acc);
+    strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // T^T k_write
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) A.kt[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = acc[t][rr];
+    for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) A.kt[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = acc[t][rr];
+    __syncthreads();  // cx, T and the operand region are rewritten by the next unit
+  }
 }
 
 // ---------------------------------------------------------------- k_scan_bwd

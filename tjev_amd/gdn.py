@@ -5,8 +5,11 @@ Mirrors ``gdn_megakernel`` (src/tjev/kernels/gated_delta_rule/pallas_tpu_mega.py
 its dispatcher form ``gdn_core_mega`` (src/tjev/kernels/gated_delta_rule/__init__.py:112-149):
 same arguments, same ValueErrors before any launch, same segment-packing semantics, output
 [B, T, H, Dv] in qkv's dtype. The custom VJP of ``_core`` (pallas_tpu_mega.py:538-575) is a
-torch.autograd.Function whose only residual besides the inputs is the fp32 state before each
-chunk (the reference's ``gdn_states``); the backward recomputes everything else. The conv
+torch.autograd.Function whose residuals besides the inputs are, by ``residuals``: "tinv" the
+reference's pair (pallas_tpu_mega.py:543-548), the fp32 state before each chunk
+(``gdn_states``) and each chunk's (I + L)^-1 (``gdn_tinv``), the backward rebuilding v_new;
+"all" (the default) those and v_new, so that the backward rebuilds nothing (512 more bytes per
+token and head in fp32); "states" the states alone, the backward rebuilding T and v_new. The conv
 weight's gradient is computed only when the weight requires grad (the reference's
 ``gdn_mega2_bwd_dw`` variant, :549-551). There is no fallback: without the HIP library, or on a
 CPU tensor, the operator raises.
@@ -60,13 +63,15 @@ class GdnPlan:
     def __init__(self, *, batch: int, length: int, key_heads: int, key_dim: int, value_heads: int,
                  value_dim: int, taps: int, chunk: int, io_dtype: torch.dtype,
                  gate_dtype: torch.dtype, precision: str = "high", inverse: str = "doubling",
-                 heads_per_step: int = 0):
+                 heads_per_step: int = 0, residuals: str = "all"):
         self.lib = _lib.load()
         if io_dtype not in _DTYPES or gate_dtype not in _DTYPES:
             raise ValueError(f"the GDN megakernel takes float32 or bfloat16 tensors, not {io_dtype}/{gate_dtype}")
+        if residuals not in _lib.RESIDUALS:
+            raise ValueError(f"residuals in {tuple(_lib.RESIDUALS)}, not {residuals!r}")
         self.params = _lib.Params(batch, length, key_heads, key_dim, value_heads, value_dim, taps, chunk,
                                   _DTYPES[io_dtype], _DTYPES[gate_dtype], _lib.PRECISION[precision],
-                                  _lib.INVERSE[inverse], heads_per_step)
+                                  _lib.INVERSE[inverse], heads_per_step, _lib.RESIDUALS[residuals])
         status = self.lib.tjev_gdn_check(ctypes.byref(self.params))
         if status == 1:
             raise ValueError(self.lib.tjev_gdn_last_error().decode())
@@ -74,6 +79,7 @@ class GdnPlan:
         self.chunk_run = max(chunk, 16)
         self.n_chunks = math.ceil(length / self.chunk_run)
         self.states_shape = (batch, value_heads, self.n_chunks, key_dim, value_dim)
+        self.residual_bytes = self.lib.tjev_gdn_residual_bytes(ctypes.byref(self.params))
         self.fwd_bytes = self.lib.tjev_gdn_workspace_bytes(ctypes.byref(self.params), 0)
         self.bwd_bytes = self.lib.tjev_gdn_workspace_bytes(ctypes.byref(self.params), 1)
 
@@ -84,18 +90,27 @@ class GdnPlan:
     def workspace(self, backward: bool, device) -> torch.Tensor:
         return torch.empty(self.bwd_bytes if backward else self.fwd_bytes, dtype=torch.uint8, device=device)
 
-    def forward(self, qkv, a, b, a_log, dt_bias, conv_w, seg, out, states, workspace) -> None:
+    def residuals(self, device) -> torch.Tensor:
+        """The forward's residual buffer (fp32): the states first, then what ``residuals`` keeps."""
+        return torch.empty(self.residual_bytes // 4, dtype=torch.float32, device=device)
+
+    def states_of(self, residuals: torch.Tensor) -> torch.Tensor:
+        """The states [B, H, N, Dk, Dv] part of a residual buffer (a view)."""
+        return residuals[: math.prod(self.states_shape)].view(self.states_shape)
+
+    def forward(self, qkv, a, b, a_log, dt_bias, conv_w, seg, out, residuals, workspace) -> None:
         status = self.lib.tjev_gdn_mega2_fwd(
             ctypes.byref(self.params), self._stream(qkv.device), _ptr(qkv), _ptr(a), _ptr(b), _ptr(a_log),
-            _ptr(dt_bias), _ptr(conv_w), _ptr(seg), _ptr(out), _ptr(states), _ptr(workspace), workspace.numel())
+            _ptr(dt_bias), _ptr(conv_w), _ptr(seg), _ptr(out), _ptr(residuals), _ptr(workspace),
+            workspace.numel())
         _lib.check_status(status)
 
-    def backward(self, qkv, a, b, a_log, dt_bias, conv_w, seg, states, d_out, d_qkv, d_a, d_b, d_a_log,
+    def backward(self, qkv, a, b, a_log, dt_bias, conv_w, seg, residuals, d_out, d_qkv, d_a, d_b, d_a_log,
                  d_dt_bias, d_conv_w, workspace) -> None:
         status = self.lib.tjev_gdn_mega2_bwd(
             ctypes.byref(self.params), self._stream(qkv.device), _ptr(qkv), _ptr(a), _ptr(b), _ptr(a_log),
-            _ptr(dt_bias), _ptr(conv_w), _ptr(seg), _ptr(states), _ptr(d_out), _ptr(d_qkv), _ptr(d_a), _ptr(d_b),
-            _ptr(d_a_log), _ptr(d_dt_bias), _ptr(d_conv_w), _ptr(workspace), workspace.numel())
+            _ptr(dt_bias), _ptr(conv_w), _ptr(seg), _ptr(residuals), _ptr(d_out), _ptr(d_qkv), _ptr(d_a),
+            _ptr(d_b), _ptr(d_a_log), _ptr(d_dt_bias), _ptr(d_conv_w), _ptr(workspace), workspace.numel())
         _lib.check_status(status)
 
 
@@ -105,18 +120,18 @@ class _Core(torch.autograd.Function):
     @staticmethod
     def forward(ctx, plan: GdnPlan, qkv, a, b, a_log, dt_bias, conv_w, seg, out_shape):
         out = torch.empty(out_shape, dtype=qkv.dtype, device=qkv.device)
-        states = torch.empty(plan.states_shape, dtype=torch.float32, device=qkv.device)
+        res = plan.residuals(qkv.device)
         ws = plan.workspace(False, qkv.device)
-        plan.forward(qkv, a, b, a_log, dt_bias, conv_w, seg, out, states, ws)
+        plan.forward(qkv, a, b, a_log, dt_bias, conv_w, seg, out, res, ws)
         ctx.plan = plan
-        ctx.save_for_backward(qkv, a, b, a_log, dt_bias, conv_w, seg, states)
-        ctx.mark_non_differentiable(states)
-        return out, states
+        ctx.save_for_backward(qkv, a, b, a_log, dt_bias, conv_w, seg, res)
+        ctx.mark_non_differentiable(res)
+        return out, res
 
     @staticmethod
-    def backward(ctx, d_out, _d_states):
+    def backward(ctx, d_out, _d_res):
         plan: GdnPlan = ctx.plan
-        qkv, a, b, a_log, dt_bias, conv_w, seg, states = ctx.saved_tensors
+        qkv, a, b, a_log, dt_bias, conv_w, seg, res = ctx.saved_tensors
         if d_out is None:
             d_out = torch.zeros((qkv.shape[0], qkv.shape[1], plan.params.value_heads, plan.params.value_dim),
                                 dtype=qkv.dtype, device=qkv.device)
@@ -129,7 +144,7 @@ class _Core(torch.autograd.Function):
         want_dw = conv_w is not None and ctx.needs_input_grad[6]
         d_w = torch.empty_like(conv_w) if want_dw else None
         ws = plan.workspace(True, qkv.device)
-        plan.backward(qkv, a, b, a_log, dt_bias, conv_w, seg, states, d_out, d_qkv, d_a, d_b, d_a_log, d_dt_bias,
+        plan.backward(qkv, a, b, a_log, dt_bias, conv_w, seg, res, d_out, d_qkv, d_a, d_b, d_a_log, d_dt_bias,
                       d_w, ws)
         return None, d_qkv, d_a, d_b, d_a_log, d_dt_bias, d_w, None, None
 
@@ -161,7 +176,7 @@ def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: t
                    dt_bias: torch.Tensor, conv_weight: torch.Tensor | None, segment_ids: torch.Tensor, *,
                    key_heads: int, key_dim: int, value_heads: int, value_dim: int, chunk: int = 64,
                    precision: str = "high", inverse: str = "doubling", heads_per_step: int = 0,
-                   vmem_fraction: float = 0.0) -> torch.Tensor:
+                   vmem_fraction: float = 0.0, residuals: str = "all") -> torch.Tensor:
     """The GDN core from the projection outputs (pallas_tpu_mega.py:585-596).
 
     qkv [B, T, 2·Hk·Dk + H·Dv]: with ``conv_weight`` [K, 2·Hk·Dk + H·Dv] (mega2) the raw
@@ -169,7 +184,10 @@ def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: t
     None (mega1) the post-conv, post-SiLU, masked activations. a, b [B, T, H] raw gate
     projections, a_log, dt_bias [H]; segment_ids [B, T] (0 = padding). Returns the delta
     rule's output [B, T, H, Dv] in qkv's dtype. ``vmem_fraction`` is TPU-only and ignored;
-    ``heads_per_step`` is checked as the reference does and otherwise ignored."""
+    ``heads_per_step`` is checked as the reference does and otherwise ignored. ``residuals``
+    (this build's, not the reference's) picks what the forward keeps for the backward: "all",
+    "tinv" (the reference's gdn_states + gdn_tinv) or "states"; every choice gives the same
+    gradients up to rounding ("tinv" and "states" bit for bit)."""
     batch, length, width = qkv.shape
     taps = _check(precision, inverse, chunk, width, key_heads, key_dim, value_heads, value_dim, heads_per_step,
                   conv_weight)
@@ -178,7 +196,7 @@ def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: t
     plan = GdnPlan(batch=batch, length=length, key_heads=key_heads, key_dim=key_dim, value_heads=value_heads,
                    value_dim=value_dim, taps=0 if conv_weight is None else taps, chunk=chunk,
                    io_dtype=qkv.dtype, gate_dtype=a.dtype, precision=precision, inverse=inverse,
-                   heads_per_step=heads_per_step)
+                   heads_per_step=heads_per_step, residuals=residuals)
     b = b.to(a.dtype)
     conv_w = None if conv_weight is None else conv_weight.to(torch.float32).contiguous()
     out, _ = _Core.apply(plan, qkv.contiguous(), a.contiguous(), b.contiguous(),
@@ -189,11 +207,12 @@ def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: t
 
 def gdn_core_mega(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_heads: int, key_dim: int,
                   value_heads: int, value_dim: int, chunk: int = 64, precision: str = "high",
-                  inverse: str = "default", heads_per_step: int = 0, vmem_fraction: float = 0.0):
+                  inverse: str = "default", heads_per_step: int = 0, vmem_fraction: float = 0.0,
+                  residuals: str = "all"):
     """The dispatcher form (__init__.py:112-149): ``inverse`` "default" -> doubling. The
     reference shards rows over devices here (``batch_parallel_with``); this build runs one GPU,
     where that split is the identity."""
     return gdn_megakernel(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, key_heads=key_heads,
                           key_dim=key_dim, value_heads=value_heads, value_dim=value_dim, chunk=chunk,
                           precision=precision, inverse=kernel_inverse(inverse),
-                          heads_per_step=heads_per_step, vmem_fraction=vmem_fraction)
+                          heads_per_step=heads_per_step, vmem_fraction=vmem_fraction, residuals=residuals)
