@@ -34,8 +34,8 @@ def _args(argv=None):
     ap.add_argument("--config", default="0.8B")
     ap.add_argument("--precision", default=None, help="override the config's precision")
     ap.add_argument("--no-norm", action="store_true", help="time the GDN core alone, without the gated RMSNorm")
-    ap.add_argument("--residuals", default="all", choices=("all", "tinv", "states"),
-                    help="what the forward keeps for the backward (the operator's default: all)")
+    ap.add_argument("--residuals", default="states", choices=("states", "tinv", "all"),
+                    help="what the forward keeps for the backward (default: the chunk-boundary states only)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=1, help="rows of the workload in the CPU baseline sample")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum timed CPU work of the baseline")

@@ -5,11 +5,12 @@ Mirrors ``gdn_megakernel`` (src/tjev/kernels/gated_delta_rule/pallas_tpu_mega.py
 its dispatcher form ``gdn_core_mega`` (src/tjev/kernels/gated_delta_rule/__init__.py:112-149):
 same arguments, same ValueErrors before any launch, same segment-packing semantics, output
 [B, T, H, Dv] in qkv's dtype. The custom VJP of ``_core`` (pallas_tpu_mega.py:538-575) is a
-torch.autograd.Function whose residuals besides the inputs are, by ``residuals``: "tinv" the
-reference's pair (pallas_tpu_mega.py:543-548), the fp32 state before each chunk
-(``gdn_states``) and each chunk's (I + L)^-1 (``gdn_tinv``), the backward rebuilding v_new;
-"all" (the default) those and v_new, so that the backward rebuilds nothing (512 more bytes per
-token and head in fp32); "states" the states alone, the backward rebuilding T and v_new. The conv
+torch.autograd.Function whose residuals besides the inputs are, by ``residuals``: "states" (the
+default) the fp32 state before each chunk alone (``gdn_states``), the backward recomputing every
+intra-chunk quantity (T and v_new included); "tinv" the reference's pair
+(pallas_tpu_mega.py:543-548), the states and each chunk's (I + L)^-1 (``gdn_tinv``), the
+backward rebuilding v_new from T; "all" those and v_new, so that the backward rebuilds neither
+(each of T and v_new costs 512 bytes per token and head in fp32 at C = Dv = 128). The conv
 weight's gradient is computed only when the weight requires grad (the reference's
 ``gdn_mega2_bwd_dw`` variant, :549-551). There is no fallback: without the HIP library, or on a
 CPU tensor, the operator raises.
@@ -63,7 +64,7 @@ class GdnPlan:
     def __init__(self, *, batch: int, length: int, key_heads: int, key_dim: int, value_heads: int,
                  value_dim: int, taps: int, chunk: int, io_dtype: torch.dtype,
                  gate_dtype: torch.dtype, precision: str = "high", inverse: str = "doubling",
-                 heads_per_step: int = 0, residuals: str = "all"):
+                 heads_per_step: int = 0, residuals: str = "states"):
         self.lib = _lib.load()
         if io_dtype not in _DTYPES or gate_dtype not in _DTYPES:
             raise ValueError(f"the GDN megakernel takes float32 or bfloat16 tensors, not {io_dtype}/{gate_dtype}")
@@ -176,7 +177,7 @@ def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: t
                    dt_bias: torch.Tensor, conv_weight: torch.Tensor | None, segment_ids: torch.Tensor, *,
                    key_heads: int, key_dim: int, value_heads: int, value_dim: int, chunk: int = 64,
                    precision: str = "high", inverse: str = "doubling", heads_per_step: int = 0,
-                   vmem_fraction: float = 0.0, residuals: str = "all") -> torch.Tensor:
+                   vmem_fraction: float = 0.0, residuals: str = "states") -> torch.Tensor:
     """The GDN core from the projection outputs (pallas_tpu_mega.py:585-596).
 
     qkv [B, T, 2·Hk·Dk + H·Dv]: with ``conv_weight`` [K, 2·Hk·Dk + H·Dv] (mega2) the raw
@@ -185,9 +186,10 @@ def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: t
     projections, a_log, dt_bias [H]; segment_ids [B, T] (0 = padding). Returns the delta
     rule's output [B, T, H, Dv] in qkv's dtype. ``vmem_fraction`` is TPU-only and ignored;
     ``heads_per_step`` is checked as the reference does and otherwise ignored. ``residuals``
-    (this build's, not the reference's) picks what the forward keeps for the backward: "all",
-    "tinv" (the reference's gdn_states + gdn_tinv) or "states"; every choice gives the same
-    gradients up to rounding ("tinv" and "states" bit for bit)."""
+    (this build's, not the reference's) picks what the forward keeps for the backward: "states"
+    (chunk-boundary states only), "tinv" (the reference's gdn_states + gdn_tinv) or "all" (and
+    v_new); every choice gives the same gradients up to rounding ("tinv" and "states" bit for
+    bit)."""
     batch, length, width = qkv.shape
     taps = _check(precision, inverse, chunk, width, key_heads, key_dim, value_heads, value_dim, heads_per_step,
                   conv_weight)
@@ -208,7 +210,7 @@ def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: t
 def gdn_core_mega(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_heads: int, key_dim: int,
                   value_heads: int, value_dim: int, chunk: int = 64, precision: str = "high",
                   inverse: str = "default", heads_per_step: int = 0, vmem_fraction: float = 0.0,
-                  residuals: str = "all"):
+                  residuals: str = "states"):
     """The dispatcher form (__init__.py:112-149): ``inverse`` "default" -> doubling. The
     reference shards rows over devices here (``batch_parallel_with``); this build runs one GPU,
     where that split is the identity."""

@@ -49,8 +49,8 @@ class _Namer:
             self.preps += 1
             return "gdn_prep_fwd" if self.preps % 2 else "gdn_prep_bwd"
         m = re.search(r"k_chunk<.*,\s*(\d)>", symbol)
-        if m:
-            return "gdn_chunk_fwd" if m.group(1) == "0" else "gdn_chunk_bwd"
+        if m:  # modes 0 and 2 run in the forward, 1 and 3 in the backward
+            return "gdn_chunk_fwd" if m.group(1) in "02" else "gdn_chunk_bwd"
         return symbol
 
 
