@@ -173,23 +173,29 @@ __device__ void doubling_level(float* sT, int LT, float* tmp) {
 
 template <int C, int P>
 __device__ void invert_unit_lower(float* sT, int LT, float* tmp) {
-  const int w = wave(), l = lane(), j = l & 15, rb = (l >> 4) << 2;
-  {  // diagonal block w
-    const int base = 16 * w;
-    float x[4];
+  const int w = wave(), l = lane();
+  if (l < 16) {  // diagonal block w: lane l owns column l, X[i] = e_i - sum_{r<i} L[i][r] X[r]
+    const float* blk = sT + 16 * w * LT + 16 * w;
+    float x[16];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) x[e] = (rb + e == j) ? 1.f : 0.f;
+    for (int i = 0; i < 16; ++i) x[i] = (i == l) ? 1.f : 0.f;
 #pragma unroll
-    for (int r = 0; r < 15; ++r) {
-      const float xr = __shfl(x[r & 3], j + 16 * (r >> 2));
+    for (int i = 1; i < 16; ++i) {
+      float row[16];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = rb + e;
-        if (i > r) x[e] -= sT[(base + i) * LT + base + r] * xr;
+      for (int q = 0; q < (i + 3) / 4; ++q) {  // L[i][0 .. i-1], the same words for every lane
+        const float4 v = *reinterpret_cast<const float4*>(blk + i * LT + 4 * q);
+        row[4 * q] = v.x;
+        row[4 * q + 1] = v.y;
+        row[4 * q + 2] = v.z;
+        row[4 * q + 3] = v.w;
       }
-    }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) lds_st(sT + (base + rb + e) * LT + base + j, x[e]);
+      for (int r = 0; r < i; ++r) x[i] -= row[r] * x[r];
+    }
+    float* out = sT + 16 * w * LT + 16 * w + l;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lds_st(out + i * LT, x[i]);
   }
   __syncthreads();
   doubling_level<C, P, 16>(sT, LT, tmp);
