@@ -350,10 +350,32 @@ __device__ __forceinline__ Frag<P> zero_frag() {
 }
 
 // ---------------------------------------------------------------- strip product
+// acc[t] += fa . B(j0 + 16t + lane%16, kk) for the tiles t < tn: tiles in groups of up to four
+// whose B fragments are all read before their products, one branch per group. tn is
+// wave-uniform; the tiles of a partly used group (t >= tn) are computed too, and callers
+// passing tn < TN ignore them.
+template <int P, int TN, class BV>
+__device__ __forceinline__ void tile_row(f32x4 (&acc)[TN], const Frag<P>& fa, const BV& B, int j0, int kk, bool ok,
+                                         int tn) {
+  constexpr int G = TN < 4 ? TN : 4;
+  static_assert(TN % G == 0, "tiles in whole groups");
+  const int r = lane() & 15;
+#pragma unroll
+  for (int g = 0; g < TN / G; ++g) {
+    if (G * g < tn) {
+      Frag<P> fb[G];
+#pragma unroll
+      for (int e = 0; e < G; ++e) fb[e] = ok ? B.template frag<P>(j0 + 16 * (G * g + e) + r, kk) : zero_frag<P>();
+#pragma unroll
+      for (int e = 0; e < G; ++e) mma<P>(acc[G * g + e], fa, fb[e]);
+    }
+  }
+}
+
 // acc[t] += sum over k in [kb, ke) of A(i0 + lane%16, k) * B(k, j0 + 16t + lane%16) for the
-// tiles t < tn (wave-uniform; the rest are skipped). kb is a multiple of 32; ke <= K. K is a
-// multiple of 16; when K is 16 the lanes of the upper contraction half feed zeros. A and B are
-// views (converted on use) or Op tiles (pre-converted).
+// tiles t < tn (see tile_row). kb is a multiple of 32; ke <= K. K is a multiple of 16; when K
+// is 16 the lanes of the upper contraction half feed zeros. A and B are views (converted on
+// use) or Op tiles (pre-converted).
 template <int P, int K, int TN, class AV, class BV>
 __device__ __forceinline__ void strip_mma(f32x4 (&acc)[TN], const AV& A, int i0, const BV& B, int j0,
                                           int kb = 0, int ke = K, int tn = TN) {
@@ -363,41 +385,7 @@ __device__ __forceinline__ void strip_mma(f32x4 (&acc)[TN], const AV& A, int i0,
   for (int k = kb; k < ke; k += 32) {
     const bool ok = (K % 32 == 0) || (k + kg < K);
     const Frag<P> fa = ok ? A.template frag<P>(i0 + r, k + kg) : zero_frag<P>();
-#pragma unroll
-    for (int t = 0; t < TN; ++t) {
-      if (t < tn) {
-        const Frag<P> fb = ok ? B.template frag<P>(j0 + 16 * t + r, k + kg) : zero_frag<P>();
-        mma<P>(acc[t], fa, fb);
-      }
-    }
-  }
-}
-
-// The same over the full contraction [0, K), every A fragment of the strip fetched first: for A
-// operands read from global memory, whose loads then overlap instead of each k-step waiting.
-template <int P, int K, int TN, class AV, class BV>
-__device__ __forceinline__ void strip_mma_full(f32x4 (&acc)[TN], const AV& A, int i0, const BV& B, int j0,
-                                               int tn = TN) {
-  constexpr int KS = (K + 31) / 32;
-  const int l = lane();
-  const int r = l & 15;
-  const int kg = (l >> 4) << 3;
-  Frag<P> fa[KS];
-#pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    const bool ok = (K % 32 == 0) || (32 * s + kg < K);
-    fa[s] = ok ? A.template frag<P>(i0 + r, 32 * s + kg) : zero_frag<P>();
-  }
-#pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    const bool ok = (K % 32 == 0) || (32 * s + kg < K);
-#pragma unroll
-    for (int t = 0; t < TN; ++t) {
-      if (t < tn) {
-        const Frag<P> fb = ok ? B.template frag<P>(j0 + 16 * t + r, 32 * s + kg) : zero_frag<P>();
-        mma<P>(acc[t], fa[s], fb);
-      }
-    }
+    tile_row<P, TN>(acc, fa, B, j0, k + kg, ok, tn);
   }
 }
 

@@ -628,7 +628,8 @@ struct PairGates {
 
 // The A operand of one wave's 16-row strip over K, fp32 rows of a global tile held raw in
 // registers (rows i0 + lane%16, columns 32s + 8 (lane/16) .. +8): fetch() issues the loads,
-// product() converts and multiplies, as strip_mma_full does from memory.
+// product() converts and multiplies (as strip_mma does from memory, with every A fragment
+// already in registers).
 template <int K>
 struct StripA {
   static constexpr int KS = (K + 31) / 32;
@@ -658,13 +659,7 @@ struct StripA {
 #pragma unroll
       for (int e = 0; e < 8; ++e) xs[e] = x[s][e] * rs;
       const Frag<P> fa = make_frag<P>(xs);
-#pragma unroll
-      for (int t = 0; t < TN; ++t) {
-        if (t < tn) {
-          const Frag<P> fb = ok ? B.template frag<P>(j0 + 16 * t + r, 32 * s + kg) : zero_frag<P>();
-          mma<P>(acc[t], fa, fb);
-        }
-      }
+      tile_row<P, TN>(acc, fa, B, j0, 32 * s + kg, ok, tn);
     }
   }
   // the strip as stored into an operand tile: op(i0 + r, k) = A(i0 + r, k)
@@ -704,13 +699,7 @@ struct StripIO {
 #pragma unroll
       for (int e = 0; e < 8; ++e) xs[e] = ok ? xs[e] * f : 0.f;
       const Frag<P> fa = make_frag<P>(xs);
-#pragma unroll
-      for (int t = 0; t < TN; ++t) {
-        if (t < tn) {
-          const Frag<P> fb = ok ? B.template frag<P>(j0 + 16 * t + r, 32 * s + kg) : zero_frag<P>();
-          mma<P>(acc[t], fa, fb);
-        }
-      }
+      tile_row<P, TN>(acc, fa, B, j0, 32 * s + kg, ok, tn);
     }
   }
 };
@@ -1095,8 +1084,8 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
 // X_loc = T^T (intra^T do) with intra = (q k^T) . D, and Kt = T^T k_write (k_write = kws . k).
 // Every global input is read once per unit into registers: the context, q and k (k for both of
 // its stagings: as rows for q k^T, transposed and scaled for k_write^T) are refilled with the
-// next unit's values once used; do and T are loaded at the unit's start and after its first
-// product (holding them across units as well would spill).
+// next unit's values once used; do and T are loaded at the unit's start and after the product
+// before their use (holding them longer would spill).
 template <int C, int D, int NT, class TIO>
 struct LocalIn {
   CtxRaw<C> cx;
@@ -1153,7 +1142,6 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
       zero(acc);
       in.q.template product<PI>(acc, ob, 0, w + 1);
       in.fetch_q(A, y, i0);
-      in.fetch_t(A, x);
 #pragma unroll
       for (int t = 0; t < C / 16; ++t)
 #pragma unroll
@@ -1168,6 +1156,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
     f32x4 acc[D / 16];
     zero(acc);
     strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // dv_loc = intra^T do
+    in.fetch_t(A, x);
     __syncthreads();
     in.tt.put_lds(sA, LA);
 #pragma unroll
