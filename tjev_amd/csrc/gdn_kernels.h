@@ -115,6 +115,44 @@ __device__ __forceinline__ float decay(const Ctx<C>& cx, int i, int j) {
   return (i >= j && cx.seg[i] == cx.seg[j]) ? expf(gdiff(cx, i, j)) : 0.f;
 }
 
+// D over one wave's 16-row strip (rows i0 + acc_row(rr)), tile by tile. Below the diagonal the
+// exponential factors through the strip's first row p = i0: for j < p <= i,
+// e^(gamma_i - gamma_j) = e^(gamma_i - gamma_p) e^(gamma_p - gamma_j) with both factors <= 1
+// (gamma never increases along a chunk: g <= 0), so a lane takes 4 exponentials for its rows
+// and 1 per tile instead of 4 per tile; the diagonal tile takes each one directly.
+template <int C>
+struct StripDecay {
+  float a[4];  // e^(gamma_i - gamma_p) of the lane's rows
+  int s[4];    // their segment ids
+  __device__ __forceinline__ StripDecay(const Ctx<C>& cx, int i0) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int i = i0 + acc_row(rr);
+      a[rr] = expf(gdiff(cx, i, i0));
+      s[rr] = cx.seg[i];
+    }
+  }
+  // d[rr] = D(i0 + acc_row(rr), 16t + acc_col()) for the strip of wave w (i0 = 16w)
+  __device__ __forceinline__ void tile(const Ctx<C>& cx, int i0, int t, int w, float (&d)[4]) const {
+    const int j = 16 * t + acc_col();
+    const int sj = cx.seg[j];
+    if (t < w) {
+      const float b = expf(gdiff(cx, i0, j));
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) d[rr] = s[rr] == sj ? a[rr] * b : 0.f;
+    } else if (t == w) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int i = i0 + acc_row(rr);
+        d[rr] = (i >= j && s[rr] == sj) ? expf(gdiff(cx, i, j)) : 0.f;
+      }
+    } else {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) d[rr] = 0.f;
+    }
+  }
+};
+
 // R x D fp32 tile from global (row stride D) into LDS (row stride LD), every load issued first
 template <int R, int D, int NT>
 __device__ __forceinline__ void load_tile(float* s, int LD, const float* g);
@@ -784,13 +822,17 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
         f32x4 acc[C / 16];
         zero(acc);
         strip_mma<PI, D, C / 16>(acc, ob, i0, ob, 0, 0, D, w + 1);
+        const StripDecay<C> sd(cx, i0);
 #pragma unroll
-        for (int t = 0; t < C / 16; ++t)
+        for (int t = 0; t < C / 16; ++t) {
+          float d[4];
+          sd.tile(cx, i0, t, w, d);
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr) {
             const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-            lds_st(sT + i * LT + j, (i > j && t <= w) ? cx.beta[i] * acc[t][rr] * decay(cx, i, j) : 0.f);
+            lds_st(sT + i * LT + j, i > j ? cx.beta[i] * acc[t][rr] * d[rr] : 0.f);
           }
+        }
       }
       __syncthreads();
       invert_unit_lower<C, PI>(sT, LT, reinterpret_cast<float*>(sB));
@@ -1046,13 +1088,14 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
       // refills are issued after the product that follows each staging: the staged
       // registers are then not live across that product
       in.k.fetch(A.kn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D);
+      const StripDecay<C> sd(cx, i0);
 #pragma unroll
-      for (int t = 0; t < C / 16; ++t)
+      for (int t = 0; t < C / 16; ++t) {
+        float d[4];
+        sd.tile(cx, i0, t, w, d);
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-          lds_st(sI + i * LI + j, t <= w ? acc[t][rr] * decay(cx, i, j) : 0.f);
-        }
+        for (int rr = 0; rr < 4; ++rr) lds_st(sI + (i0 + acc_row(rr)) * LI + 16 * t + acc_col(), acc[t][rr] * d[rr]);
+      }
     }
     __syncthreads();
     in.v.put_cols(ob);
@@ -1142,13 +1185,14 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
       zero(acc);
       in.q.template product<PI>(acc, ob, 0, w + 1);
       in.fetch_q(A, y, i0);
+      const StripDecay<C> sd(cx, i0);
 #pragma unroll
-      for (int t = 0; t < C / 16; ++t)
+      for (int t = 0; t < C / 16; ++t) {
+        float d[4];
+        sd.tile(cx, i0, t, w, d);
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-          lds_st(sA + i * LA + j, t <= w ? acc[t][rr] * decay(cx, i, j) : 0.f);
-        }
+        for (int rr = 0; rr < 4; ++rr) lds_st(sA + (i0 + acc_row(rr)) * LA + 16 * t + acc_col(), acc[t][rr] * d[rr]);
+      }
     }
     __syncthreads();
     in.dov.put_cols(ob);
@@ -1374,23 +1418,27 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
   {  // m1 -> LDS, m2 -> registers
     f32x4 acc[C / 16];
     zero(acc);
+    const StripDecay<C> sd(cx, i0);
     xs.template product<PI>(acc, ob, 0, w + 1);
 #pragma unroll
-    for (int t = 0; t < C / 16; ++t)
+    for (int t = 0; t < C / 16; ++t) {
+      float d[4];
+      sd.tile(cx, i0, t, w, d);
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-        lds_st(sA + i * LA + j, (i > j && t <= w) ? -acc[t][rr] * decay(cx, i, j) : 0.f);
+        lds_st(sA + i * LA + j, i > j ? -acc[t][rr] * d[rr] : 0.f);
       }
+    }
     zero(m2);
     dos.template product<PI>(m2, ob, 0, w + 1);
 #pragma unroll
-    for (int t = 0; t < C / 16; ++t)
+    for (int t = 0; t < C / 16; ++t) {
+      float d[4];
+      sd.tile(cx, i0, t, w, d);
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-        m2[t][rr] = t <= w ? m2[t][rr] * decay(cx, i, j) : 0.f;
-      }
+      for (int rr = 0; rr < 4; ++rr) m2[t][rr] *= d[rr];
+    }
   }
   __syncthreads();
   stage_rows<D, D, NT>(ob, A.gg + ((size_t)bh * A.N + n) * D * D, D);  // G
