@@ -11,7 +11,11 @@ kernel's average duration (HIP events on the launch stream) for the dominant ker
 roofline. The CPU baseline is the oracle (a CPU restatement of tjev's XLA chunked path, fp32,
 torch autograd) on a bounded sample of the same workload.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 0.8B|9B|varlen|tiny]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 0.8B|9B|varlen|tiny|4B-block]
+
+``--config 4B-block`` times BASELINE's block config instead: the 4B-shaped GDN block with merged
+LoRA r64 (projections on hipBLASLt, core and norm in the HIP library), with peak activation
+bytes.
 """
 
 from __future__ import annotations
@@ -97,6 +101,121 @@ def _traffic(config: str, precision: str, kernel: str):
         return None
 
 
+BLOCK = dict(batch=2, length=8192, hidden=2560, key_heads=16, key_dim=128, value_heads=32, value_dim=128, rank=64,
+             chunk=128, precision="high")
+
+
+def _block_bench(args) -> dict:
+    """BASELINE's block config: the 4B-shaped GDN block (src/tjev/model/gdn.py:126-164) fwd+bwd
+    with merged LoRA r64 on every projection (tjev_amd/block.py), bf16, one segment per row.
+    A step is the block's forward and the backward of sum(out * dy) to x and every adapter.
+    Peak activation bytes: the step's allocator peak above what is resident before it
+    (weights, adapters, inputs)."""
+    import torch
+
+    from oracle.gdn_oracle import gdn_block
+    from tjev_amd import _lib
+    from tjev_amd.block import GatedDeltaNetBlock
+
+    c = BLOCK
+    B, T, hid = c["batch"], c["length"], c["hidden"]
+    blk = GatedDeltaNetBlock(hidden=hid, key_heads=c["key_heads"], key_dim=c["key_dim"],
+                             value_heads=c["value_heads"], value_dim=c["value_dim"], rank=c["rank"],
+                             dtype=torch.bfloat16, chunk=c["chunk"], precision=c["precision"],
+                             residuals=args.residuals)
+    gen = torch.Generator().manual_seed(21)
+    x = torch.randn((B, T, hid), generator=gen).to(torch.bfloat16).cuda().requires_grad_(True)
+    seg = torch.ones((B, T), dtype=torch.int32, device="cuda")
+    dy = torch.randn((B, T, hid), generator=gen).to(torch.bfloat16).cuda()
+    leaves = [x, *blk.parameters()]
+    outs = {}
+
+    def step():
+        out = blk(x, seg)
+        outs["grads"] = torch.autograd.grad(out, leaves, dy)
+        outs["out"] = out
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    resident = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    step()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated() - resident
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    with _lib.KernelTimer() as kt:
+        for _ in range(args.steps):
+            step()
+    hip_ms = sum(kt.ms.values()) / args.steps
+    finite = bool(torch.isfinite(outs["out"].float()).all()) and all(bool(torch.isfinite(g).all()) for g in outs["grads"])
+    # projection GEMMs: forward x W' (4 in-projections + out_proj), backward dx and the adapter
+    # products; the merge W + s A B per projection and call
+    Hk, Dk, H, Dv, r = c["key_heads"], c["key_dim"], c["value_heads"], c["value_dim"], c["rank"]
+    outs_in = [2 * Hk * Dk + H * Dv, H * Dv, H, H]
+    n = B * T
+    fwd = sum(2 * n * hid * o for o in outs_in) + 2 * n * H * Dv * hid
+    bwd = fwd + sum(2 * n * hid * r + 2 * n * o * r * 2 + 2 * n * hid * r for o in outs_in) \
+        + 2 * n * H * Dv * r + 2 * n * hid * r * 2 + 2 * n * H * Dv * r
+    merge = sum(2 * hid * r * o for o in outs_in) + 2 * H * Dv * r * hid
+    gemm_flops = fwd + bwd + merge
+    gemm_ms = ms - hip_ms
+    ach = gemm_flops / (gemm_ms * 1e-3) / 1e12
+    report = {
+        "metric": METRIC, "value": n / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "4B-shaped GDN block fwd+bwd (merged LoRA r64, flat gated RMSNorm)", "batch": B,
+                   "seq_len": T, "hidden": hid, "key_heads": Hk, "value_heads": H, "head_dim": Dk, "lora_rank": r,
+                   "chunk": c["chunk"], "precision": c["precision"], "segments": "one",
+                   "residuals": args.residuals},
+        "peak_activation_bytes": peak,
+        "roofline": {"kernel": "projections (hipBLASLt GEMMs, merge and glue: the step less the HIP library's kernels)",
+                     "bound": "mfma", "achieved": ach, "peak": 2500.0, "unit": "TFLOP/s", "frac": ach / 2500.0,
+                     "traffic": None},
+        "split_ms": {"hip_kernels": hip_ms, "projections_and_glue": gemm_ms},
+        "gemm_gflop": gemm_flops / 1e9,
+        "finite": finite,
+    }
+    if not args.no_cpu_baseline:  # the oracle block on one row of 1024 tokens, fp32
+        sample_t = 1024
+        blk_cpu = {nm: (getattr(blk, nm).weight.float().cpu(), getattr(blk, nm).lora_a.detach().cpu(),
+                        getattr(blk, nm).lora_b.detach().cpu(), getattr(blk, nm).scale)
+                   for nm in ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a", "out_proj")}
+        blk_cpu.update(conv=blk.conv.cpu(), a_log=blk.a_log.cpu(), dt_bias=blk.dt_bias.cpu(), norm=blk.norm_weight.cpu())
+        xc = x.detach()[:1, :sample_t].float().cpu()
+        sc = seg[:1, :sample_t].cpu()
+        dyc = dy[:1, :sample_t].float().cpu()
+
+        def one_pass():
+            xl = xc.clone().requires_grad_(True)
+            ps = {k: ((v[0], v[1].clone().requires_grad_(True), v[2].clone().requires_grad_(True), v[3])
+                      if isinstance(v, tuple) else v) for k, v in blk_cpu.items()}
+            out = gdn_block(xl, sc, ps, key_heads=Hk, key_dim=Dk, value_heads=H, value_dim=Dv, chunk=c["chunk"])
+            torch.autograd.grad((out * dyc).sum(), [xl] + [t for v in ps.values() if isinstance(v, tuple) for t in v[1:3]])
+
+        one_pass()
+        passes, total = 0, 0.0
+        while total < args.cpu_seconds or passes < 1:
+            t0 = time.perf_counter()
+            one_pass()
+            total += time.perf_counter() - t0
+            passes += 1
+        threads = torch.get_num_threads()
+        report["cpu_baseline"] = {
+            "value": passes * sample_t / total, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle gdn_block (CPU restatement of tjev's GatedDeltaNet with merged LoRA, fp32, torch "
+                       f"autograd) fwd+bwd on B=1 T={sample_t} of the same block, {passes} passes after 1 "
+                       f"warm-up, {total:.1f} s timed, {threads} threads")}
+    return report
+
+
 def main(argv=None) -> int:
     args = _args(argv)
     if args.gpus != 1:
@@ -113,6 +232,13 @@ def main(argv=None) -> int:
     from tjev_amd.roofline import PEAK_BF16_TFLOPS, PEAK_FP32_TFLOPS, PEAK_HBM_GBS, kernel_work, operator_work
     from tjev_amd.testing import CONFIGS, cotangent, gdn_inputs
 
+    if args.config == "4B-block":
+        report = _block_bench(args)
+        if args.details:
+            with open(args.details, "w") as f:
+                json.dump(report, f, indent=1)
+        print(json.dumps(report), flush=True)
+        return 0
     cfg = dict(CONFIGS[args.config])
     precision = args.precision or cfg["precision"]
     dtype = cfg["dtype"]

@@ -23,6 +23,9 @@ Each function follows a reference file (paths relative to the tjev repository ro
                                                (``_reference``), the recurrent variant
                                                tests/kernels/test_gdn_long.py:131-176
 - ``gated_rmsnorm``                            src/tjev/model/norms.py:13-15, 36-40
+- ``merged_projection`` / ``unmerged_projection``  src/tjev/model/lora.py:284-301 / 132-150
+- ``gdn_block``                                src/tjev/model/gdn.py:126-164 (flat norm,
+                                               every projection adapted)
 
 Gradients come from torch autograd through these functions, as the reference takes
 ``jax.grad`` of the same XLA program (test_gdn_mega.py:75-86). Arithmetic runs in the dtype
@@ -364,3 +367,49 @@ def fp64_truth(inputs, cotangent, **kw):
     kw = dict(kw)
     kw.update(rule="recurrent", dtype=torch.float64)
     return reference_with_grads(inputs, cotangent, **kw)
+
+
+# --------------------------------------------------------------------------- the GDN block
+def merged_projection(x: torch.Tensor, weight: torch.Tensor, lora_a: torch.Tensor, lora_b: torch.Tensor,
+                      scale: float, dtype) -> torch.Tensor:
+    """x W' with W' = W + s A B (lora.py:284-301, ``_merge`` and ``_base_matmul``): A and B
+    cast to ``dtype`` first, their product and the sum in the accumulation dtype, W' rounded
+    once to ``dtype``. x [..., in], W [in, out], A [in, r], B [r, out]."""
+    acc = torch.float64 if dtype == torch.float64 else torch.float32
+    delta = lora_a.to(dtype).to(acc) @ lora_b.to(dtype).to(acc)
+    merged = (weight.to(acc) + scale * delta).to(dtype)
+    return (x.to(dtype).to(acc) @ merged.to(acc)).to(dtype)
+
+
+def unmerged_projection(x, weight, lora_a, lora_b, scale: float, dtype):
+    """x W + s (x A) B, the unmerged form of the same projection (lora.py:132-150, 236-250)."""
+    acc = torch.float64 if dtype == torch.float64 else torch.float32
+    xa = x.to(dtype).to(acc) @ lora_a.to(dtype).to(acc)
+    base = x.to(dtype).to(acc) @ weight.to(dtype).to(acc)
+    return (base + scale * (xa @ lora_b.to(dtype).to(acc))).to(dtype)
+
+
+def gdn_block(x, segment_ids, params: dict, *, key_heads: int, key_dim: int, value_heads: int, value_dim: int,
+              dtype=torch.float32, eps: float = 1e-6, chunk: int = 64, merged: bool = True, io_dtype=None):
+    """``GatedDeltaNet.__call__`` (gdn.py:126-164) with ``gdn_norm=flat`` and every projection
+    adapted: x with padding rows zeroed -> in_proj_qkv, in_proj_z, in_proj_b, in_proj_a ->
+    ``reference_core`` (conv, gates, l2norm, chunked delta rule) -> the gated RMSNorm of each
+    head (norms.py:42-62: the flat form is the same arithmetic) -> padding select -> out_proj.
+    ``params``: {name: (W, A, B, scale)} for the five projections, and "conv", "a_log",
+    "dt_bias", "norm" tensors. Differentiable by autograd (the adapters' gradients are the
+    low-rank formulas of lora.py:320-366). ``io_dtype`` (bf16): the activations between the
+    stages are stored in it, as the reference's bf16 layer stores them (projection outputs,
+    the core's output, the norm's output), the core computing in ``dtype``."""
+    io = io_dtype or dtype
+    proj = merged_projection if merged else unmerged_projection
+    batch, length, _ = x.shape
+    valid = (segment_ids > 0)[..., None]
+    x = torch.where(valid, x, torch.zeros((), dtype=x.dtype)).to(io)
+    qkv, z, b, a = (proj(x, *params[n], io) for n in ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a"))
+    out = reference_core(qkv, a, b, params["a_log"], params["dt_bias"], params["conv"], segment_ids,
+                         key_heads=key_heads, key_dim=key_dim, value_heads=value_heads, value_dim=value_dim,
+                         chunk=chunk, dtype=dtype)
+    zh = z.reshape(batch, length, value_heads, value_dim)
+    out = gated_rmsnorm(out.to(io), zh, params["norm"], eps).reshape(batch, length, -1)
+    out = torch.where(valid, out, torch.zeros((), dtype=out.dtype))
+    return proj(out, *params["out_proj"], io)

@@ -393,3 +393,62 @@ def test_chunk_tinv_inverts_each_chunk_brute_force():
     # and the doubling restatement agrees with the solve on the same chunks
     lower = torch.linalg.inv(got) - torch.eye(c, dtype=got.dtype)
     assert float((O.unit_lower_inverse(lower) - got).abs().max()) < 1e-10
+
+
+# ------------------------------------------------------------------ the GDN block
+def test_merged_projection_equals_unmerged_fp64():
+    """lora.py's two forms of one adapted projection, x (W + s A B) and x W + s (x A) B, agree
+    in fp64, values and the gradients of x, A and B (the merged form's autograd gives the
+    low-rank formulas dA = s x^T (dy B^T), dB = s (x A)^T dy)."""
+    rng = np.random.default_rng(11)
+    f = lambda *s: torch.from_numpy(rng.standard_normal(s))  # noqa: E731
+    x, w, a, b, dy = f(7, 12), f(12, 9), f(12, 3), f(3, 9), f(7, 9)
+    leaves = [t.clone().requires_grad_(True) for t in (x, a, b)]
+    ym = O.merged_projection(leaves[0], w, leaves[1], leaves[2], 1.7, F64)
+    gm = torch.autograd.grad((ym * dy).sum(), leaves)
+    leaves2 = [t.clone().requires_grad_(True) for t in (x, a, b)]
+    yu = O.unmerged_projection(leaves2[0], w, leaves2[1], leaves2[2], 1.7, F64)
+    gu = torch.autograd.grad((yu * dy).sum(), leaves2)
+    assert float((ym - yu).detach().abs().max()) < 1e-12
+    for p, q in zip(gm, gu):
+        assert float((p - q).abs().max()) < 1e-12
+    assert torch.allclose(gm[1], 1.7 * x.T @ (dy @ b.T)) and torch.allclose(gm[2], 1.7 * (x @ a).T @ dy)
+
+
+def test_merged_projection_rounds_the_merged_kernel_once():
+    """W' = W + s bf16(A) bf16(B) summed in the accumulation dtype and rounded once to the
+    compute dtype (lora.py:284-295); x = [1] reads W' row 0."""
+    w = torch.tensor([[1.0, 0.5]])
+    a = torch.tensor([[2.0 ** -5]])
+    b = torch.tensor([[2.0 ** -5, 3 * 2.0 ** -5]])
+    x = torch.tensor([[1.0]])
+    y = O.merged_projection(x, w, a, b, 0.5, torch.bfloat16)
+    # W' = [1 + 2^-11, 0.5 + 3 * 2^-11]: both deltas are below half a bf16 ulp (2^-8 at 1,
+    # 2^-9 at 0.5), so the merged kernel is W itself; in fp32 it is not
+    assert y.dtype == torch.bfloat16 and y.tolist() == [[1.0, 0.5]]
+    y32 = O.merged_projection(x, w, a, b, 0.5, torch.float32)
+    assert y32.tolist() == [[1.0 + 2.0 ** -11, 0.5 + 3 * 2.0 ** -11]]
+
+
+def test_gdn_block_zero_adapters_reduce_to_the_base_layer():
+    """With B = 0 the block is the unadapted layer: base projections, the reference core, the
+    gated norm, the padding select and out_proj, composed by hand here in fp64."""
+    rng = np.random.default_rng(12)
+    f = lambda *s: torch.from_numpy(rng.standard_normal(s))  # noqa: E731
+    hidden, hk, h, d = 8, 1, 2, 4
+    width = 2 * hk * d + h * d
+    names = {"in_proj_qkv": width, "in_proj_z": h * d, "in_proj_b": h, "in_proj_a": h}
+    p = {n: (f(hidden, o) * 0.3, f(hidden, 2), torch.zeros(2, o, dtype=F64), 2.0) for n, o in names.items()}
+    p["out_proj"] = (f(h * d, hidden) * 0.3, f(h * d, 2), torch.zeros(2, hidden, dtype=F64), 2.0)
+    p.update(conv=f(4, width) * 0.5, a_log=torch.rand(h, dtype=F64), dt_bias=f(h), norm=1 + 0.1 * f(d))
+    x = f(2, 11, hidden)
+    seg = torch.tensor([[1] * 6 + [2] * 3 + [0] * 2, [1] * 11], dtype=torch.int32)
+    got = O.gdn_block(x, seg, p, key_heads=hk, key_dim=d, value_heads=h, value_dim=d, dtype=F64, chunk=4)
+    xm = torch.where((seg > 0)[..., None], x, 0.0)
+    qkv, z, b, a = (xm @ p[n][0] for n in ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a"))
+    core = O.reference_core(qkv, a, b, p["a_log"], p["dt_bias"], p["conv"], seg, key_heads=hk, key_dim=d,
+                            value_heads=h, value_dim=d, chunk=4, dtype=F64)
+    normed = O.gated_rmsnorm(core, z.reshape(2, 11, h, d), p["norm"]).reshape(2, 11, -1)
+    want = torch.where((seg > 0)[..., None], normed, 0.0) @ p["out_proj"][0]
+    assert float((got - want).abs().max()) < 1e-12
+    assert torch.all(got[0, 9:] == 0)

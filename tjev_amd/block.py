@@ -1,0 +1,157 @@
+"""tjev's Gated DeltaNet block on MI355X: ``GatedDeltaNet.__call__`` (src/tjev/model/gdn.py:126-164)
+with merged-LoRA projections (src/tjev/model/lora.py:191-223 ``grouped``, :262-369
+``_merged_matmuls``) and the flat gated RMSNorm (src/tjev/model/norms.py:42-62).
+
+    x (padding rows zeroed) -> in_proj_qkv, in_proj_z, in_proj_b, in_proj_a (one input; each
+    adapter merged per call, W' = W + s*A*B rounded once to the compute dtype) -> the GDN
+    megakernel core (HIP) -> the gated RMSNorm on the heads side by side with the padding
+    select (HIP) -> out_proj (merged LoRA)
+
+The projections are plain GEMMs on hipBLASLt (torch.mm). Their backward is the reference's
+custom VJP (lora.py:320-366): dx = sum_i dy_i W'_i^T, dA_i = s_i x^T (dy_i B_i^T),
+dB_i = s_i (x A_i)^T dy_i, with fp32 accumulation and results, never the full dW. The frozen
+kernels, the conv weight, A_log, dt_bias and the norm weight take no gradient; the adapters
+(fp32, cast to the compute dtype for the products) train. LoRA scale: rsLoRA, alpha/sqrt(rank)
+(src/tjev/config/schema.py:44-45, 79-81).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .gdn import gdn_megakernel
+from .norm import gated_rmsnorm
+
+
+def _mm32(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a @ b accumulated and returned in fp32 (the reference's preferred_element_type=f32)."""
+    if a.dtype == torch.float32:
+        return a @ b.to(torch.float32)
+    return torch.mm(a, b, out_dtype=torch.float32)
+
+
+class _MergedLoRA(torch.autograd.Function):
+    """``_merged_matmuls`` (lora.py:303-369) for projections sharing the input x [N, in]:
+    y_i = x W'_i, W'_i = (W_i + s_i A_i B_i) in the compute dtype, A_i and B_i rounded to it
+    first and their product accumulated in fp32 (``_merge``, :284-295)."""
+
+    @staticmethod
+    def forward(ctx, x, scales, *params):
+        n = len(scales)
+        ws, a_s, b_s = params[:n], params[n:2 * n], params[2 * n:]
+        dtype = x.dtype
+        merged = [(w.to(torch.float32) + s * _mm32(a.to(dtype), b.to(dtype))).to(dtype)
+                  for w, a, b, s in zip(ws, a_s, b_s, scales)]
+        ys = tuple(x @ m for m in merged)
+        ctx.scales = scales
+        ctx.save_for_backward(x, *merged, *a_s, *b_s)
+        return ys
+
+    @staticmethod
+    def backward(ctx, *dys):
+        scales = ctx.scales
+        n = len(scales)
+        x, *rest = ctx.saved_tensors
+        merged, a_s, b_s = rest[:n], rest[n:2 * n], rest[2 * n:]
+        dtype = x.dtype
+        dys = [torch.zeros((x.shape[0], m.shape[1]), dtype=dtype, device=x.device) if dy is None
+               else dy.to(dtype).contiguous() for dy, m in zip(dys, merged)]
+        # dx = sum_i dy_i W'_i^T: one product over the concatenated outputs (fp32 accumulation)
+        dx = torch.cat(dys, dim=1) @ torch.cat(merged, dim=1).t().contiguous()
+        # the adapters: one pass over x for every A, x^T [s_1 t_1 | s_2 t_2 | ...]
+        ranks = [a.shape[1] for a in a_s]
+        xa = x @ torch.cat([a.to(dtype) for a in a_s], dim=1)
+        t = torch.cat([(s * _mm32(dy, b.to(dtype).t().contiguous())).to(dtype)
+                       for dy, b, s in zip(dys, b_s, scales)], dim=1)
+        xt = x.t().contiguous()
+        da = torch.split(_mm32(xt, t), ranks, dim=1)
+        xas = torch.split(xa, ranks, dim=1)
+        db = [s * _mm32(xai.t().contiguous(), dy) for xai, dy, s in zip(xas, dys, scales)]
+        return (dx, None, *([None] * n), *[d.to(a.dtype) for d, a in zip(da, a_s)],
+                *[d.to(b.dtype) for d, b in zip(db, b_s)])
+
+
+class LoRALinear:
+    """A frozen projection W [in, out] (compute dtype) with a trainable adapter A [in, r],
+    B [r, out] (fp32) and scale s (``Linear``, lora.py:69-188, merged form)."""
+
+    def __init__(self, weight: torch.Tensor, lora_a: torch.Tensor, lora_b: torch.Tensor, scale: float):
+        self.weight = weight
+        self.lora_a = lora_a
+        self.lora_b = lora_b
+        self.scale = float(scale)
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        (y,) = grouped(x, self)
+        return y
+
+
+def grouped(x: torch.Tensor, *linears: LoRALinear) -> list[torch.Tensor]:
+    """``[l(x) for l in linears]`` for projections sharing x (lora.py:191-223), merged."""
+    dtype = linears[0].weight.dtype
+    lead = x.shape[:-1]
+    x2 = x.to(dtype).reshape(-1, x.shape[-1]).contiguous()
+    ys = _MergedLoRA.apply(x2, tuple(l.scale for l in linears), *(l.weight for l in linears),
+                           *(l.lora_a for l in linears), *(l.lora_b for l in linears))
+    return [y.reshape(*lead, y.shape[-1]) for y in ys]
+
+
+class GatedDeltaNetBlock:
+    """The block with every projection adapted (rank ``rank``, merged) and the flat norm
+    (``compute.gdn_norm=flat``, ``compute.lora_impl=merged``), random weights of the given
+    shape (no checkpoint is loaded). ``init``: the adapters as BASELINE's block config draws
+    them (A ~ N(0, 1/r), B ~ N(0, 0.01)), base kernels ~ N(0, 1/fan_in), conv ~ N(0, 0.5),
+    A_log ~ U(0, ln 16), dt_bias ~ N(0, 1), norm weight 1."""
+
+    def __init__(self, *, hidden: int, key_heads: int, key_dim: int, value_heads: int, value_dim: int,
+                 taps: int = 4, rank: int = 64, alpha: float = 32.0, dtype=torch.bfloat16, device="cuda",
+                 seed: int = 0, chunk: int = 64, precision: str = "high", inverse: str = "doubling",
+                 residuals: str = "states", eps: float = 1e-6, b_std: float = 0.1):
+        self.hidden, self.hk, self.dk, self.h, self.dv = hidden, key_heads, key_dim, value_heads, value_dim
+        self.dtype, self.chunk, self.precision, self.inverse = dtype, chunk, precision, inverse
+        self.residuals, self.eps = residuals, eps
+        gen = torch.Generator().manual_seed(seed)
+
+        def normal(*shape, std=1.0):
+            return (torch.randn(shape, generator=gen) * std).to(device)
+
+        scale = alpha / math.sqrt(rank)
+        width = 2 * key_heads * key_dim + value_heads * value_dim
+
+        def proj(fan_in, fan_out):
+            w = normal(fan_in, fan_out, std=fan_in ** -0.5).to(dtype)
+            a = normal(fan_in, rank, std=rank ** -0.5).requires_grad_(True)
+            b = normal(rank, fan_out, std=b_std).requires_grad_(True)
+            return LoRALinear(w, a, b, scale)
+
+        self.in_proj_qkv = proj(hidden, width)
+        self.in_proj_z = proj(hidden, value_heads * value_dim)
+        self.in_proj_b = proj(hidden, value_heads)
+        self.in_proj_a = proj(hidden, value_heads)
+        self.out_proj = proj(value_heads * value_dim, hidden)
+        self.conv = normal(taps, width, std=0.5)
+        self.a_log = (torch.rand(value_heads, generator=gen) * math.log(16.0)).to(device)
+        self.dt_bias = normal(value_heads)
+        self.norm_weight = torch.ones(value_dim, device=device)
+
+    def projections(self) -> list[LoRALinear]:
+        return [self.in_proj_qkv, self.in_proj_z, self.in_proj_b, self.in_proj_a, self.out_proj]
+
+    def parameters(self) -> list[torch.Tensor]:
+        """The trainable adapters: (A, B) of every projection."""
+        return [t for p in self.projections() for t in (p.lora_a, p.lora_b)]
+
+    def __call__(self, x: torch.Tensor, segment_ids: torch.Tensor) -> torch.Tensor:
+        """x [B, T, hidden] -> [B, T, hidden] (gdn.py:126-164, gdn_input_mask on)."""
+        batch, length, _ = x.shape
+        valid = (segment_ids > 0)[..., None]
+        x = torch.where(valid, x, torch.zeros((), dtype=x.dtype, device=x.device)).to(self.dtype)
+        qkv, z, b, a = grouped(x, self.in_proj_qkv, self.in_proj_z, self.in_proj_b, self.in_proj_a)
+        out = gdn_megakernel(qkv, a, b, self.a_log, self.dt_bias, self.conv, segment_ids, key_heads=self.hk,
+                             key_dim=self.dk, value_heads=self.h, value_dim=self.dv, chunk=self.chunk,
+                             precision=self.precision, inverse=self.inverse, residuals=self.residuals)
+        out = out.reshape(batch, length, self.h * self.dv)
+        out = gated_rmsnorm(out, z, self.norm_weight, self.eps, heads=self.h, segment_ids=segment_ids)
+        return self.out_proj(out)
