@@ -98,6 +98,30 @@ int tjev_gdn_mega2_fwd(const tjev_gdn_params* p, void* stream, const void* qkv, 
                        const float* conv_w, const int32_t* seg, void* out, float* residuals,
                        void* workspace, size_t workspace_bytes);
 
+/* the forward plus the state a decode step continues from (the serving prefill; no
+ * counterpart in the megakernel, whose XLA sibling returns the final state,
+ * xla.py:170-262): final_state [B, H, Dk, Dv] fp32, the recurrent state after token T-1
+ * (xla.py:141-167 run to the last token: restarted where the segment id changes), and
+ * conv_state [B, K-1, W] io_dtype, the raw rows T-K+1 .. T-1 (oldest first), zero before the
+ * row or outside token T-1's segment. Either may be null. */
+int tjev_gdn_mega2_fwd_state(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a,
+                             const void* b, const float* a_log, const float* dt_bias,
+                             const float* conv_w, const int32_t* seg, void* out, float* residuals,
+                             float* final_state, void* conv_state, void* workspace,
+                             size_t workspace_bytes);
+
+/* One decode step, T = 1 token per row (p->length == 1; chunk and residuals are ignored):
+ * the reference's token recurrence (xla.py:141-167, its "T=1 decode step") on the
+ * megakernel's inputs, with the conv over the kept rows (HF causal_conv1d_update). qkv [B, W]
+ * (raw; post-conv when taps == 0), a, b [B, H]; conv_state [B, K-1, W] io_dtype read, and
+ * conv_state_out the same history shifted by the new row (must not alias conv_state); state
+ * [B, H, Dk, Dv] fp32 read and state_out written (may alias state); out [B, H, Dv] io_dtype.
+ * The step continues the segment the state belongs to (no reset). */
+int tjev_gdn_decode_step(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a,
+                         const void* b, const float* a_log, const float* dt_bias,
+                         const float* conv_w, const void* conv_state, const float* state,
+                         void* out, void* conv_state_out, float* state_out);
+
 /* backward: replaces pallas_call "gdn_mega2_bwd" (pallas_tpu_mega.py:471-524) plus the XLA sums
  * of _core_bwd (:563-571): d_qkv (io_dtype), d_a, d_b (gate_dtype), d_a_log and d_dt_bias ([H] fp32), and,
  * when d_conv_w is not null, the conv weight's gradient [K, W] fp32 (the reference's
@@ -145,7 +169,7 @@ int tjev_gdn_gated_rmsnorm_bwd(const tjev_gdn_norm_params* p, void* stream, cons
  * and writes, for kernel ids 0..n-1, the summed milliseconds and the launch count.
  * TJEV_GDN_KERNELS is the number of ids; tjev_gdn_kernel_name(id) names them. Not thread-safe:
  * profile from one host thread. */
-#define TJEV_GDN_KERNELS 14
+#define TJEV_GDN_KERNELS 16
 int tjev_gdn_profile_begin(void);
 int tjev_gdn_profile_end(float* ms, int* launches, int n);
 const char* tjev_gdn_kernel_name(int kernel);

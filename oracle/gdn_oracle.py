@@ -26,6 +26,8 @@ Each function follows a reference file (paths relative to the tjev repository ro
 - ``merged_projection`` / ``unmerged_projection``  src/tjev/model/lora.py:284-301 / 132-150
 - ``gdn_block``                                src/tjev/model/gdn.py:126-164 (flat norm,
                                                every projection adapted)
+- ``decode_step``                              xla.py:141-167 at T = 1 with an initial state,
+                                               the conv as HF causal_conv1d_update
 
 Gradients come from torch autograd through these functions, as the reference takes
 ``jax.grad`` of the same XLA program (test_gdn_mega.py:75-86). Arithmetic runs in the dtype
@@ -413,3 +415,26 @@ def gdn_block(x, segment_ids, params: dict, *, key_heads: int, key_dim: int, val
     out = gated_rmsnorm(out.to(io), zh, params["norm"], eps).reshape(batch, length, -1)
     out = torch.where(valid, out, torch.zeros((), dtype=out.dtype))
     return proj(out, *params["out_proj"], io)
+
+
+# --------------------------------------------------------------------------- decode
+def decode_step(qkv, a, b, a_log, dt_bias, conv_weight, conv_state, state, *, key_heads: int, key_dim: int,
+                value_heads: int, value_dim: int, dtype=torch.float32):
+    """One token per row after a prefill (xla.py:141-167 with T = 1 and ``initial_state``; the
+    conv over the kept rows as HF ``causal_conv1d_update``): qkv [B, W], a, b [B, H],
+    conv_state [B, K-1, W] (oldest first), state [B, H, Dk, Dv]. Returns (out [B, H, Dv],
+    conv_state', state'). The window [conv_state; qkv] is one segment, so the last row's conv
+    reads exactly the kept rows."""
+    conv = conv_weight is not None
+    rows = qkv[:, None] if not conv or conv_state is None else torch.cat([conv_state.to(qkv.dtype), qkv[:, None]], 1)
+    batch, window, _ = rows.shape
+    pad = lambda x: torch.cat([torch.zeros((batch, window - 1, x.shape[-1]), dtype=x.dtype), x[:, None]], 1)  # noqa: E731
+    seg = torch.ones((batch, window), dtype=torch.int64)
+    q, k, v, g, beta, _ = core_inputs(rows, pad(a), pad(b), a_log, dt_bias, conv_weight, seg, key_heads=key_heads,
+                                      key_dim=key_dim, value_heads=value_heads, value_dim=value_dim, conv=conv,
+                                      dtype=dtype)
+    last = slice(window - 1, window)
+    out, new_state = recurrent_gated_delta_rule(q[:, last], k[:, last], v[:, last], g[:, last], beta[:, last],
+                                                initial_state=state.to(dtype))
+    new_conv = None if not conv or conv_state is None else rows[:, 1:]
+    return out[:, 0], new_conv, new_state

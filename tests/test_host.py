@@ -245,3 +245,42 @@ def test_ds_check_flags_the_miscompiled_merge_only():
     other = before.replace("DS_WRITE_B32_gfx9 %5:vgpr_32, %8", "DS_WRITE_B32_gfx9 %6:vgpr_32, %8").replace("336", "0")
     merged = wrong.replace(" 17, 84,", " 0, 4,").replace("DS_WRITE2_B32", "DS_WRITE2ST64_B32")
     assert bad_merges(_mir(other.replace("272", "0"), merged)) == []
+
+
+def test_decode_step_validation():
+    """The decode step's checks, before any launch: one token per row, grouped heads, a
+    history buffer distinct from the one it reads, and non-null tensors."""
+    from tjev_amd import _lib
+
+    lib = _lib.load()
+    p = _params(length=1)
+    bufs = [ctypes.c_void_p(256 * (i + 1)) for i in range(11)]
+    assert lib.tjev_gdn_decode_step(ctypes.byref(_params(length=2)), None, *bufs) == 1
+    assert "one token per row" in lib.tjev_gdn_last_error().decode()
+    assert lib.tjev_gdn_decode_step(ctypes.byref(_params(length=1, value_heads=5)), None, *bufs) == 1
+    assert "groups of" in lib.tjev_gdn_last_error().decode()
+    alias = list(bufs)
+    alias[9] = alias[6]  # conv_state_out == conv_state
+    assert lib.tjev_gdn_decode_step(ctypes.byref(p), None, *alias) == 1
+    assert "alias" in lib.tjev_gdn_last_error().decode()
+    nulls = list(bufs)
+    nulls[7] = None  # state
+    assert lib.tjev_gdn_decode_step(ctypes.byref(p), None, *nulls) == 1
+    assert "null" in lib.tjev_gdn_last_error().decode()
+    assert lib.tjev_gdn_decode_step(ctypes.byref(_params(length=1, key_dim=48, value_dim=48)), None, *bufs) == 2
+
+
+def test_serving_rejects_cpu_tensors():
+    import torch
+
+    from tjev_amd.serve import gdn_decode_step, gdn_prefill
+
+    x = torch.zeros(1, 16, 2 * 16 + 2 * 16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        gdn_prefill(x, torch.zeros(1, 16, 2), torch.zeros(1, 16, 2), torch.zeros(2), torch.zeros(2),
+                    torch.zeros(4, 64), torch.ones(1, 16, dtype=torch.int32), key_heads=1, key_dim=16,
+                    value_heads=2, value_dim=16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        gdn_decode_step(x[:, 0], torch.zeros(1, 2), torch.zeros(1, 2), torch.zeros(2), torch.zeros(2),
+                        torch.zeros(4, 64), torch.zeros(1, 3, 64), torch.zeros(1, 2, 16, 16), key_heads=1,
+                        key_dim=16, value_heads=2, value_dim=16)

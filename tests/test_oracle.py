@@ -452,3 +452,30 @@ def test_gdn_block_zero_adapters_reduce_to_the_base_layer():
     want = torch.where((seg > 0)[..., None], normed, 0.0) @ p["out_proj"][0]
     assert float((got - want).abs().max()) < 1e-12
     assert torch.all(got[0, 9:] == 0)
+
+
+# ------------------------------------------------------------------ decode
+def test_decode_step_continues_the_recurrence():
+    """test_gated_delta_rule.py:61-73's continuation on the megakernel's inputs: the token
+    recurrence over T+3 tokens equals a prefill of T (its final state and last K-1 raw rows)
+    followed by three decode steps, output and state, in fp64 (mega2 and mega1)."""
+    from tjev_amd.testing import gdn_inputs
+
+    for conv in (True, False):
+        qkv, a, b, a_log, dt_bias, w, _ = gdn_inputs(batch=2, length=23, key_heads=1, value_heads=2, dim=8,
+                                                     dtype=F64, seed=13)
+        w = w.to(F64) if conv else None
+        kw = dict(key_heads=1, key_dim=8, value_heads=2, value_dim=8)
+        seg = torch.ones((2, 23), dtype=torch.int64)
+        full = O.reference_core(qkv, a, b, a_log, dt_bias, w, seg, conv=conv, rule="recurrent", dtype=F64, **kw)
+        q, k, v, g, beta, _ = O.core_inputs(qkv[:, :20], a[:, :20], b[:, :20], a_log, dt_bias, w, seg[:, :20],
+                                            conv=conv, dtype=F64, **kw)
+        _, state = O.recurrent_gated_delta_rule(q, k, v, g, beta, seg[:, :20])
+        hist = qkv[:, 17:20] if conv else None
+        for t in range(20, 23):
+            out, hist, state = O.decode_step(qkv[:, t], a[:, t], b[:, t], a_log, dt_bias, w, hist, state,
+                                             dtype=F64, **kw)
+            assert float((out - full[:, t]).abs().max()) < 1e-12
+        _, end = O.recurrent_gated_delta_rule(*O.core_inputs(qkv, a, b, a_log, dt_bias, w, seg, conv=conv,
+                                                               dtype=F64, **kw)[:5], seg)
+        assert float((state - end).abs().max()) < 1e-12

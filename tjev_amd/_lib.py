@@ -26,6 +26,8 @@ EXPORTS = (
     "tjev_gdn_residual_bytes",
     "tjev_gdn_workspace_bytes",
     "tjev_gdn_mega2_fwd",
+    "tjev_gdn_mega2_fwd_state",
+    "tjev_gdn_decode_step",
     "tjev_gdn_mega2_bwd",
     "tjev_gdn_norm_workspace_bytes",
     "tjev_gdn_gated_rmsnorm_fwd",
@@ -36,7 +38,7 @@ EXPORTS = (
     "tjev_gdn_last_error",
     "tjev_gdn_version",
 )
-N_KERNELS = 14  # TJEV_GDN_KERNELS
+N_KERNELS = 16  # TJEV_GDN_KERNELS
 
 
 class Params(ctypes.Structure):
@@ -86,6 +88,10 @@ def load() -> ctypes.CDLL:
     lib.tjev_gdn_workspace_bytes.restype = sz
     lib.tjev_gdn_mega2_fwd.argtypes = [pp, vp] + [vp] * 10 + [sz]
     lib.tjev_gdn_mega2_fwd.restype = i32
+    lib.tjev_gdn_mega2_fwd_state.argtypes = [pp, vp] + [vp] * 12 + [sz]
+    lib.tjev_gdn_mega2_fwd_state.restype = i32
+    lib.tjev_gdn_decode_step.argtypes = [pp, vp] + [vp] * 11
+    lib.tjev_gdn_decode_step.restype = i32
     lib.tjev_gdn_mega2_bwd.argtypes = [pp, vp] + [vp] * 16 + [sz]
     lib.tjev_gdn_mega2_bwd.restype = i32
     npp = ctypes.POINTER(NormParams)

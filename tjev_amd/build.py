@@ -28,8 +28,8 @@ FLAGS = [
 ]
 
 
-# units built once: the C ABI and the gated RMSNorm
-EXTRA_UNITS = ("gdn_api", "gdn_norm")
+# units built once: the C ABI, the gated RMSNorm and the decode step
+EXTRA_UNITS = ("gdn_api", "gdn_norm", "gdn_decode")
 
 
 def shapes() -> list[tuple[int, int]]:

@@ -217,7 +217,7 @@ int aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % 
 const char* const kKernelNames[gdn::K_COUNT] = {
     "gdn_prep_fwd", "gdn_chunk_fwd", "gdn_scan_fwd", "gdn_out",       "gdn_prep_bwd",   "gdn_chunk_bwd",
     "gdn_bwd_local", "gdn_scan_bwd", "gdn_bwd_grads", "gdn_post",     "gdn_reduce",     "gdn_norm_fwd",
-    "gdn_norm_bwd",  "gdn_norm_reduce"};
+    "gdn_norm_bwd",  "gdn_norm_reduce", "gdn_final_state", "gdn_decode"};
 
 struct Profiler {
   bool on = false;
@@ -311,6 +311,33 @@ int tjev_gdn_mega2_fwd(const tjev_gdn_params* p, void* stream, const void* qkv, 
   A.seg = seg;
   A.out = out;
   bind_residuals(p, residuals, A);
+  return run(p, stream, A, 0);
+}
+
+int tjev_gdn_mega2_fwd_state(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
+                             const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg,
+                             void* out, float* residuals, float* final_state, void* conv_state, void* workspace,
+                             size_t workspace_bytes) {
+  if (int s = validate(p)) return s;
+  if (!qkv || !a || !b || !a_log || !dt_bias || !seg || !out || !residuals || (p->taps > 0 && !conv_w))
+    return fail(TJEV_GDN_EINVAL, "null tensor argument");
+  if (!aligned(qkv, 16) || !aligned(out, 16) || !aligned(residuals, 256) || !aligned(workspace, 256))
+    return fail(TJEV_GDN_EINVAL, "qkv and out must be 16-byte aligned, the residuals and workspace 256-byte aligned");
+  const Layout L = layout(p, 0);
+  if (!workspace || workspace_bytes < L.total)
+    return fail(TJEV_GDN_EWORKSPACE, "forward workspace needs " + std::to_string(L.total) + " bytes");
+  gdn::GdnArgs A = base_args(p, workspace, L);
+  A.qkv = qkv;
+  A.ga = a;
+  A.gb = b;
+  A.a_log = a_log;
+  A.dt_bias = dt_bias;
+  A.conv_w = conv_w;
+  A.seg = seg;
+  A.out = out;
+  bind_residuals(p, residuals, A);
+  A.final_state = final_state;
+  A.conv_state = conv_state;
   return run(p, stream, A, 0);
 }
 

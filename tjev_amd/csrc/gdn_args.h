@@ -22,7 +22,9 @@ struct GdnArgs {
   const int32_t* seg;
   // forward outputs
   void* out;
-  float* states;  // [B, H, N, Dk, Dv]
+  float* states;       // [B, H, N, Dk, Dv]
+  float* final_state;  // [B, H, Dk, Dv] the state after token T-1 (or null)
+  void* conv_state;    // [B, K-1, W] the raw rows before token T (or null)
   // backward
   const void* d_out;
   void* d_qkv;

@@ -1,0 +1,222 @@
+// One decode step of the GDN layer core for gfx950: T = 1 new token per row, continuing the
+// conv history and the recurrent state left by the prefill (or by the previous step). It is
+// the token recurrence of xla.py:141-167 (the reference's "T=1 decode step") on the
+// megakernel's inputs, with the conv over the K-1 kept raw rows and the new one (HF
+// causal_conv1d_update), SiLU, the q/k l2norm and the gates as k_prep computes them.
+//
+// One workgroup per (row, value head, Dv tile of 32): it rebuilds its q and k head and its
+// v tile from the raw rows, then updates its D x 32 slice of the state: s = s e^g,
+// delta = (v - s^T k) beta, s += k delta^T, o = s^T q. Each thread holds D/8 rows of one
+// column; the two column sums go through LDS. The state is read and written once (in place
+// allowed: each slice belongs to one workgroup); the new conv history goes to a separate
+// buffer, written by the head-0 workgroups of each row.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "../../include/tjev_gdn.h"
+#include "gdn_device.h"
+#include "gdn_launch.h"
+
+namespace gdn {
+namespace {
+
+struct DecodeArgs {
+  int B, Hk, H, ratio, taps, W;
+  float scale;
+  const void* qkv;       // [B, W] the new raw row
+  const void* ga;        // [B, H]
+  const void* gb;        // [B, H]
+  const float* a_log;    // [H]
+  const float* dt_bias;  // [H]
+  const float* conv_w;   // [K, W]
+  const void* conv_in;   // [B, K-1, W] the raw rows before it, oldest first
+  const float* state;    // [B, H, Dk, Dv]
+  void* out;             // [B, H, Dv]
+  void* conv_out;        // [B, K-1, W]
+  float* state_out;      // [B, H, Dk, Dv]
+};
+
+constexpr int kThreads = 256;
+
+// the activation of channel c: the causal conv over the K-1 kept rows and the new one, lag 0
+// first (causal_conv1d.py:42-45), then SiLU; the new row itself without a conv (taps == 0)
+template <class TIO>
+__device__ __forceinline__ float activation(const DecodeArgs& A, int b, int c) {
+  const TIO* x = reinterpret_cast<const TIO*>(A.qkv);
+  const float xt = ldf(x + (size_t)b * A.W + c);
+  if (A.taps == 0) return xt;
+  const TIO* hist = reinterpret_cast<const TIO*>(A.conv_in) + (size_t)b * (A.taps - 1) * A.W;
+  float z = xt * A.conv_w[(size_t)(A.taps - 1) * A.W + c];
+  for (int L = 1; L < A.taps; ++L) z += ldf(hist + (size_t)(A.taps - 1 - L) * A.W + c) * A.conv_w[(size_t)(A.taps - 1 - L) * A.W + c];
+  return z * sigmoid_io<TIO>(z);
+}
+
+// sum over the block of one value per thread (wave sums, then the waves in order)
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = sum64(v);
+  __syncthreads();
+  if (lane() == 0) red[wave()] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int q = 0; q < kThreads / 64; ++q) s += red[q];
+  return s;
+}
+
+template <int D, class TIO, class TG>
+__global__ __launch_bounds__(kThreads) void k_decode(DecodeArgs A) {
+  constexpr int DT = D < 32 ? D : 32;
+  constexpr int NTL = D / DT;
+  constexpr int RG = kThreads / DT;
+  constexpr int RPT = (D + RG - 1) / RG;
+  __shared__ float sq[D], sk[D], sv[DT];
+  __shared__ float red[kThreads / 64];
+  __shared__ float part[RG][DT];
+  __shared__ float gate[2];
+  const int tile = blockIdx.x % NTL, bh = blockIdx.x / NTL, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
+  const int tid = threadIdx.x;
+  // q and k of key head hk, v of value head h (this tile's columns)
+  float aq = 0.f, ak = 0.f;
+  if (tid < D) aq = activation<TIO>(A, b, hk * D + tid);
+  if (tid < D) ak = activation<TIO>(A, b, A.Hk * D + hk * D + tid);
+  if (tid < DT) sv[tid] = activation<TIO>(A, b, 2 * A.Hk * D + h * D + tile * DT + tid);
+  // l2norm (xla.py:42-53; r = 0 on an all-zero row), q scaled by Dk^-1/2
+  const float sqq = block_sum(aq * aq, red);
+  const float skk = block_sum(ak * ak, red);
+  const float rq = (sqq == 0.f ? 0.f : 1.0f / sqrtf(sqq + 1e-6f)) * A.scale;
+  const float rk = skk == 0.f ? 0.f : 1.0f / sqrtf(skk + 1e-6f);
+  if (tid < D) {
+    sq[tid] = aq * rq;
+    sk[tid] = ak * rk;
+  }
+  if (tid == 0) {  // beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias)
+    const float av = ldf(reinterpret_cast<const TG*>(A.ga) + (size_t)b * A.H + h);
+    const float bv = ldf(reinterpret_cast<const TG*>(A.gb) + (size_t)b * A.H + h);
+    gate[0] = sigmoidf_(bv);
+    gate[1] = expf(-expf(A.a_log[h]) * softplusf_(av + A.dt_bias[h]));
+  }
+  __syncthreads();
+  const int j = tid % DT, rg = tid / DT;
+  const float* src = A.state + (size_t)bh * D * D + tile * DT + j;
+  float s[RPT];
+  float mem = 0.f;
+  const float decay = gate[1];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg * RPT + r;
+    s[r] = i < D ? src[(size_t)i * D] * decay : 0.f;
+    mem += i < D ? s[r] * sk[i] : 0.f;
+  }
+  part[rg][j] = mem;
+  __syncthreads();
+  float m = 0.f;
+#pragma unroll
+  for (int q = 0; q < RG; ++q) m += part[q][j];
+  const float delta = (sv[j] - m) * gate[0];
+  float o = 0.f;
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg * RPT + r;
+    if (i < D) {
+      s[r] += sk[i] * delta;
+      o += s[r] * sq[i];
+    }
+  }
+  float* dst = A.state_out + (size_t)bh * D * D + tile * DT + j;
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg * RPT + r;
+    if (i < D) dst[(size_t)i * D] = s[r];
+  }
+  __syncthreads();
+  part[rg][j] = o;
+  __syncthreads();
+  if (tid < DT) {
+    float acc = 0.f;
+#pragma unroll
+    for (int q = 0; q < RG; ++q) acc += part[q][tid];
+    stf(reinterpret_cast<TIO*>(A.out) + (size_t)bh * D + tile * DT + tid, acc);
+  }
+  if (h == 0 && tile == 0 && A.taps > 1) {  // the history shifted by the new row
+    const int k1 = A.taps - 1;
+    const TIO* hist = reinterpret_cast<const TIO*>(A.conv_in) + (size_t)b * k1 * A.W;
+    const TIO* x = reinterpret_cast<const TIO*>(A.qkv) + (size_t)b * A.W;
+    TIO* out = reinterpret_cast<TIO*>(A.conv_out) + (size_t)b * k1 * A.W;
+    for (int idx = tid; idx < k1 * A.W; idx += kThreads) {
+      const int r = idx / A.W, c = idx % A.W;
+      out[idx] = r + 1 < k1 ? hist[(size_t)(r + 1) * A.W + c] : x[c];
+    }
+  }
+}
+
+template <int D>
+hipError_t launch(const DecodeArgs& A, int io, int gate, hipStream_t st) {
+  const dim3 grid(A.B * A.H * (D / (D < 32 ? D : 32)));
+  if (io == TJEV_GDN_BF16 && gate == TJEV_GDN_BF16) hipLaunchKernelGGL((k_decode<D, uint16_t, uint16_t>), grid, dim3(kThreads), 0, st, A);
+  if (io == TJEV_GDN_BF16 && gate == TJEV_GDN_F32) hipLaunchKernelGGL((k_decode<D, uint16_t, float>), grid, dim3(kThreads), 0, st, A);
+  if (io == TJEV_GDN_F32 && gate == TJEV_GDN_BF16) hipLaunchKernelGGL((k_decode<D, float, uint16_t>), grid, dim3(kThreads), 0, st, A);
+  if (io == TJEV_GDN_F32 && gate == TJEV_GDN_F32) hipLaunchKernelGGL((k_decode<D, float, float>), grid, dim3(kThreads), 0, st, A);
+  return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace gdn
+
+extern "C" int tjev_gdn_decode_step(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a,
+                                    const void* b, const float* a_log, const float* dt_bias, const float* conv_w,
+                                    const void* conv_state, const float* state, void* out, void* conv_state_out,
+                                    float* state_out) {
+  auto fail = [](int status, const std::string& msg) { return gdn::fail(status, msg.c_str()); };
+  if (!p) return fail(TJEV_GDN_EINVAL, "null params");
+  if (p->batch <= 0 || p->key_heads <= 0 || p->value_heads <= 0)
+    return fail(TJEV_GDN_EINVAL, "batch and head counts must be positive");
+  if (p->length != 1) return fail(TJEV_GDN_EINVAL, "a decode step takes one token per row (length 1)");
+  if (p->value_heads % p->key_heads)
+    return fail(TJEV_GDN_EINVAL, std::to_string(p->value_heads) + " value heads are not groups of " +
+                                     std::to_string(p->key_heads) + " key heads");
+  if (p->key_dim != p->value_dim) return fail(TJEV_GDN_EUNSUPPORTED, "this build's kernels need key_dim == value_dim");
+  const int D = p->key_dim;
+  if (D != 16 && D != 32 && D != 64 && D != 128)
+    return fail(TJEV_GDN_EUNSUPPORTED, "decode kernels exist for head dims 16, 32, 64 and 128");
+  if (p->taps < 0 || p->taps > 5) return fail(TJEV_GDN_EINVAL, "conv kernel of " + std::to_string(p->taps) + " taps: 1..5");
+  if (p->io_dtype < 0 || p->io_dtype > 1 || p->gate_dtype < 0 || p->gate_dtype > 1)
+    return fail(TJEV_GDN_EINVAL, "dtypes must be TJEV_GDN_F32 or TJEV_GDN_BF16");
+  if (!qkv || !a || !b || !a_log || !dt_bias || !state || !out || !state_out ||
+      (p->taps > 0 && !conv_w) || (p->taps > 1 && (!conv_state || !conv_state_out)))
+    return fail(TJEV_GDN_EINVAL, "null tensor argument");
+  if (p->taps > 1 && conv_state == conv_state_out)
+    return fail(TJEV_GDN_EINVAL, "conv_state_out must not alias conv_state (every head reads the history)");
+  gdn::DecodeArgs A{};
+  A.B = p->batch;
+  A.Hk = p->key_heads;
+  A.H = p->value_heads;
+  A.ratio = p->value_heads / p->key_heads;
+  A.taps = p->taps;
+  A.W = 2 * p->key_heads * D + p->value_heads * D;
+  A.scale = 1.0f / sqrtf((float)D);
+  A.qkv = qkv;
+  A.ga = a;
+  A.gb = b;
+  A.a_log = a_log;
+  A.dt_bias = dt_bias;
+  A.conv_w = conv_w;
+  A.conv_in = conv_state;
+  A.state = state;
+  A.out = out;
+  A.conv_out = conv_state_out;
+  A.state_out = state_out;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const gdn::Timer* tm = gdn::active_timer();
+  if (tm) tm->mark(tm->self, gdn::K_DECODE, 0, st);
+  hipError_t e = hipSuccess;
+  switch (D) {
+    case 16: e = gdn::launch<16>(A, p->io_dtype, p->gate_dtype, st); break;
+    case 32: e = gdn::launch<32>(A, p->io_dtype, p->gate_dtype, st); break;
+    case 64: e = gdn::launch<64>(A, p->io_dtype, p->gate_dtype, st); break;
+    default: e = gdn::launch<128>(A, p->io_dtype, p->gate_dtype, st); break;
+  }
+  if (tm) tm->mark(tm->self, gdn::K_DECODE, 1, st);
+  if (e != hipSuccess) return fail(TJEV_GDN_EHIP, std::string("HIP launch failed: ") + hipGetErrorString(e));
+  return 0;
+}

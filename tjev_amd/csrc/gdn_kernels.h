@@ -1122,6 +1122,77 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
   }
 }
 
+// ---------------------------------------------------------------- k_final_state
+// grid B*H*(D/DT), 256 threads: the recurrent state after token T-1 of each row, for a decode
+// step that continues it (xla.py:141-167 run to the last token). It is the scan's update of
+// the last chunk with T-1 as that chunk's last token (the chunk step, pallas_tpu_v2.py:254-269,
+// truncated there): S = carry' S_before + sum over the chunk's tokens t <= T-1 of token T-1's
+// segment of e^(gamma_{T-1} - gamma_t) k_t v_new_t^T, carry' = e^(gamma_{T-1}) when that
+// segment began before the chunk. The rows of v_new up to T-1 do not depend on later rows.
+template <int C, int D>
+__global__ __launch_bounds__(256) void k_final_state(GdnArgs A) {
+  constexpr int DT = D < 32 ? D : 32;
+  constexpr int NTL = D / DT;
+  constexpr int RG = 256 / DT;              // row groups of a tile
+  constexpr int RPT = (D + RG - 1) / RG;    // rows per thread
+  __shared__ float sk[C * D];
+  __shared__ float sv[C * DT];
+  __shared__ float sw[C];
+  const int tile = blockIdx.x % NTL, bh = blockIdx.x / NTL, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
+  const int last = A.T - 1, nl = last / C, t0 = nl * C, cnt = last - t0 + 1;
+  const size_t tb = (size_t)b * A.Tp, th = (size_t)bh * A.Tp;
+  const float* kg = A.kn + ((size_t)(b * A.Hk + hk) * A.Tp + t0) * D;
+  const float* vg = A.vnew + (th + t0) * D + tile * DT;
+  for (int idx = threadIdx.x; idx < cnt * D; idx += 256) sk[idx] = kg[idx];
+  for (int idx = threadIdx.x; idx < cnt * DT; idx += 256) sv[idx] = vg[(size_t)(idx / DT) * D + idx % DT];
+  const int sl = A.segp[tb + last];
+  const float gl = A.gam[th + last], ll = A.gaml[th + last];
+  for (int t = threadIdx.x; t < cnt; t += 256)
+    sw[t] = A.segp[tb + t0 + t] == sl ? expf((gl - A.gam[th + t0 + t]) + (ll - A.gaml[th + t0 + t])) : 0.f;
+  const int before = nl > 0 ? A.segp[tb + t0 - 1] : -2;
+  const float carry = sl == before ? expf(gl + ll) : 0.f;
+  __syncthreads();
+  const int j = threadIdx.x % DT, rg = threadIdx.x / DT;
+  const float* S = A.states + ((size_t)bh * A.N + nl) * D * D + tile * DT + j;
+  float acc[RPT];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg * RPT + r;
+    acc[r] = i < D ? carry * S[(size_t)i * D] : 0.f;
+  }
+  for (int t = 0; t < cnt; ++t) {
+    const float wv = sw[t] * sv[t * DT + j];
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+      const int i = rg * RPT + r;
+      if (i < D) acc[r] += sk[t * D + i] * wv;
+    }
+  }
+  float* dst = A.final_state + (size_t)bh * D * D + tile * DT + j;
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg * RPT + r;
+    if (i < D) dst[(size_t)i * D] = acc[r];
+  }
+}
+
+// ---------------------------------------------------------------- k_conv_state
+// grid B, 256 threads: the raw rows T-K+1 .. T-1 of each row (oldest first, [B, K-1, W]), zero
+// before the row's start or outside token T-1's segment: the conv history a decode step
+// continuing that segment reads (the tap masks of causal_conv1d.py:10-17).
+template <class TIO>
+__global__ __launch_bounds__(256) void k_conv_state(GdnArgs A) {
+  const int b = blockIdx.x, k1 = A.taps - 1, last = A.T - 1;
+  const TIO* x = reinterpret_cast<const TIO*>(A.qkv);
+  TIO* dst = reinterpret_cast<TIO*>(A.conv_state) + (size_t)b * k1 * A.W;
+  const int sl = A.seg[(size_t)b * A.T + last];
+  for (int idx = threadIdx.x; idx < k1 * A.W; idx += 256) {
+    const int r = idx / A.W, c = idx % A.W, t = last - k1 + 1 + r;
+    const bool keep = t >= 0 && A.seg[(size_t)b * A.T + (t >= 0 ? t : 0)] == sl;
+    dst[idx] = keep ? x[((size_t)b * A.T + t) * A.W + c] : TIO(0);
+  }
+}
+
 // ---------------------------------------------------------------- k_bwd_local
 // Persistent over the (row, head, chunk) units as k_out; C/16 waves. Per unit:
 // X_loc = T^T (intra^T do) with intra = (q k^T) . D, and Kt = T^T k_write (k_write = kws . k).

@@ -12,6 +12,7 @@ enum KernelId : int {
   K_PREP_FWD = 0, K_CHUNK_FWD, K_SCAN_FWD, K_OUT,
   K_PREP_BWD, K_CHUNK_BWD, K_BWD_LOCAL, K_SCAN_BWD, K_BWD_GRADS, K_POST, K_REDUCE,
   K_NORM_FWD, K_NORM_BWD, K_NORM_REDUCE,
+  K_FINAL_STATE, K_DECODE,
   K_COUNT
 };
 
