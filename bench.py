@@ -11,11 +11,11 @@ kernel's average duration (HIP events on the launch stream) for the dominant ker
 roofline. The CPU baseline is the oracle (a CPU restatement of tjev's XLA chunked path, fp32,
 torch autograd) on a bounded sample of the same workload.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 0.8B|9B|varlen|tiny|4B-block]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 0.8B|9B|varlen|tiny|4B-block|decode]
 
 ``--config 4B-block`` times BASELINE's block config instead: the 4B-shaped GDN block with merged
 LoRA r64 (projections on hipBLASLt, core and norm in the HIP library), with peak activation
-bytes.
+bytes; ``--config decode`` the serving path's one-token decode step (64 rows, 0.8B head shape).
 """
 
 from __future__ import annotations
@@ -216,6 +216,54 @@ def _block_bench(args) -> dict:
     return report
 
 
+def _decode_bench(args) -> dict:
+    """One-token decode steps at the 0.8B layer shape (Hk = H = 16, D = 128, conv 4) for a
+    batch of 64 rows, bf16 activations, fp32 state updated in place: the serving path's step
+    (tjev_amd/serve.py). HBM-bound on the state: 2 x 64 KB per (row, head) per step."""
+    import torch
+
+    from tjev_amd import _lib
+    from tjev_amd.serve import gdn_decode_step
+    from tjev_amd.testing import gdn_inputs
+
+    B, Hk, H, D = 64, 16, 16, 128
+    qkv, a, b, a_log, dt_bias, w, _ = (x.cuda() for x in gdn_inputs(batch=B, length=4, key_heads=Hk, value_heads=H,
+                                                                       dim=D, dtype=torch.bfloat16))
+    state = (torch.randn((B, H, D, D), generator=torch.Generator().manual_seed(5)) * 0.05).cuda()
+    hist = qkv[:, :3].contiguous()
+    kw = dict(key_heads=Hk, key_dim=D, value_heads=H, value_dim=D)
+
+    def step():
+        gdn_decode_step(qkv[:, 3], a[:, 3], b[:, 3], a_log, dt_bias, w, hist, state, inplace=True, **kw)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    with _lib.KernelTimer() as kt:
+        for _ in range(args.steps):
+            step()
+    k_ms = kt.ms["gdn_decode"] / kt.launches["gdn_decode"]
+    state_bytes = 2 * B * H * D * D * 4
+    ach = state_bytes / (k_ms * 1e-3) / 1e9
+    return {
+        "metric": METRIC, "value": B / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "0.8B GDN layer core decode step (one token per row, state in place)", "batch": B,
+                   "key_heads": Hk, "value_heads": H, "head_dim": D, "conv_taps": 4},
+        "roofline": {"kernel": "gdn_decode", "bound": "hbm", "achieved": ach, "peak": 8000.0, "unit": "GB/s",
+                     "frac": ach / 8000.0, "traffic": None},
+        "kernel_ms": k_ms,
+    }
+
+
 def main(argv=None) -> int:
     args = _args(argv)
     if args.gpus != 1:
@@ -232,8 +280,8 @@ def main(argv=None) -> int:
     from tjev_amd.roofline import PEAK_BF16_TFLOPS, PEAK_FP32_TFLOPS, PEAK_HBM_GBS, kernel_work, operator_work
     from tjev_amd.testing import CONFIGS, cotangent, gdn_inputs
 
-    if args.config == "4B-block":
-        report = _block_bench(args)
+    if args.config in ("4B-block", "decode"):
+        report = _block_bench(args) if args.config == "4B-block" else _decode_bench(args)
         if args.details:
             with open(args.details, "w") as f:
                 json.dump(report, f, indent=1)

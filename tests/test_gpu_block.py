@@ -93,7 +93,7 @@ def test_merged_lora_backward_matches_autograd():
     ys_ref = [xr @ (w + 2.5 * (a @ b)) for w, a, b in ref_leaves]
     want = torch.autograd.grad(sum((y * d).sum() for y, d in zip(ys_ref, dys)), [xr] + [t for _, a, b in ref_leaves for t in (a, b)])
     for y, yr in zip(ys, ys_ref):
-        assert rel(y.double().cpu(), yr.double().cpu()) <= 1e-5
+        assert rel(y.detach().double().cpu(), yr.detach().double().cpu()) <= 1e-5
     for g, h in zip(got, want):
         assert rel(g.double().cpu(), h.double().cpu()) <= 1e-5
 

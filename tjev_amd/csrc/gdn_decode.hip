@@ -6,8 +6,8 @@
 //
 // One workgroup per (row, value head, Dv tile of 32): it rebuilds its q and k head and its
 // v tile from the raw rows, then updates its D x 32 slice of the state: s = s e^g,
-// delta = (v - s^T k) beta, s += k delta^T, o = s^T q. Each thread holds D/8 rows of one
-// column; the two column sums go through LDS. The state is read and written once (in place
+// delta = (v - s^T k) beta, s += k delta^T, o = s^T q. Each thread holds 4 adjacent columns
+// of D/32 rows (16-byte accesses); the two column sums go through lane shuffles and LDS. The state is read and written once (in place
 // allowed: each slice belongs to one workgroup); the new conv history goes to a separate
 // buffer, written by the head-0 workgroups of each row.
 #include <hip/hip_runtime.h>
@@ -68,14 +68,25 @@ template <int D, class TIO, class TG>
 __global__ __launch_bounds__(kThreads) void k_decode(DecodeArgs A) {
   constexpr int DT = D < 32 ? D : 32;
   constexpr int NTL = D / DT;
-  constexpr int RG = kThreads / DT;
-  constexpr int RPT = (D + RG - 1) / RG;
+  constexpr int QPR = DT / 4;                 // column quads of a tile (one per thread)
+  constexpr int RG = kThreads / QPR;          // row groups
+  constexpr int RPT = (D + RG - 1) / RG;      // rows per thread
+  constexpr int GPW = 64 / QPR;               // row groups per wave
   __shared__ float sq[D], sk[D], sv[DT];
   __shared__ float red[kThreads / 64];
-  __shared__ float part[RG][DT];
+  __shared__ float part[kThreads / 64][DT];
   __shared__ float gate[2];
   const int tile = blockIdx.x % NTL, bh = blockIdx.x / NTL, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
   const int tid = threadIdx.x;
+  const int cq = tid % QPR, rg = tid / QPR, c0 = 4 * cq;
+  // the state slice first (16-byte loads): its loads run while q, k and v are built
+  const float* src = A.state + (size_t)bh * D * D + tile * DT + c0;
+  float4 s[RPT];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg * RPT + r;
+    s[r] = *reinterpret_cast<const float4*>(src + (size_t)(i < D ? i : D - 1) * D);
+  }
   // q and k of key head hk, v of value head h (this tile's columns)
   float aq = 0.f, ak = 0.f;
   if (tid < D) aq = activation<TIO>(A, b, hk * D + tid);
@@ -97,46 +108,59 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeArgs A) {
     gate[1] = expf(-expf(A.a_log[h]) * softplusf_(av + A.dt_bias[h]));
   }
   __syncthreads();
-  const int j = tid % DT, rg = tid / DT;
-  const float* src = A.state + (size_t)bh * D * D + tile * DT + j;
-  float s[RPT];
-  float mem = 0.f;
+  // column sums over the rows: within the thread, across the wave's row groups (xor
+  // shuffles over the lanes of one column quad), then across the waves through LDS
+  auto column_sums = [&](float4 v, float (&out)[4]) {
+    float x[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int m = QPR; m < 64; m <<= 1)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] += __shfl_xor(x[e], m);
+    __syncthreads();
+    if (lane() < QPR) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) part[wave()][c0 + e] = x[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float t = 0.f;
+#pragma unroll
+      for (int q = 0; q < kThreads / 64; ++q) t += part[q][c0 + e];
+      out[e] = t;
+    }
+  };
   const float decay = gate[1];
+  float4 mem = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
     const int i = rg * RPT + r;
-    s[r] = i < D ? src[(size_t)i * D] * decay : 0.f;
-    mem += i < D ? s[r] * sk[i] : 0.f;
+    const float kv = i < D ? sk[i] : 0.f;
+    s[r].x *= decay; s[r].y *= decay; s[r].z *= decay; s[r].w *= decay;
+    mem.x += s[r].x * kv; mem.y += s[r].y * kv; mem.z += s[r].z * kv; mem.w += s[r].w * kv;
   }
-  part[rg][j] = mem;
-  __syncthreads();
-  float m = 0.f;
-#pragma unroll
-  for (int q = 0; q < RG; ++q) m += part[q][j];
-  const float delta = (sv[j] - m) * gate[0];
-  float o = 0.f;
+  float m[4];
+  column_sums(mem, m);
+  const float bt = gate[0];
+  const float dl[4] = {(sv[c0] - m[0]) * bt, (sv[c0 + 1] - m[1]) * bt, (sv[c0 + 2] - m[2]) * bt,
+                       (sv[c0 + 3] - m[3]) * bt};
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+  float* dst = A.state_out + (size_t)bh * D * D + tile * DT + c0;
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
     const int i = rg * RPT + r;
     if (i < D) {
-      s[r] += sk[i] * delta;
-      o += s[r] * sq[i];
+      const float kv = sk[i], qv = sq[i];
+      s[r].x += kv * dl[0]; s[r].y += kv * dl[1]; s[r].z += kv * dl[2]; s[r].w += kv * dl[3];
+      o.x += s[r].x * qv; o.y += s[r].y * qv; o.z += s[r].z * qv; o.w += s[r].w * qv;
+      *reinterpret_cast<float4*>(dst + (size_t)i * D) = s[r];
     }
   }
-  float* dst = A.state_out + (size_t)bh * D * D + tile * DT + j;
+  float ov[4];
+  column_sums(o, ov);
+  if (rg == 0) {
 #pragma unroll
-  for (int r = 0; r < RPT; ++r) {
-    const int i = rg * RPT + r;
-    if (i < D) dst[(size_t)i * D] = s[r];
-  }
-  __syncthreads();
-  part[rg][j] = o;
-  __syncthreads();
-  if (tid < DT) {
-    float acc = 0.f;
-#pragma unroll
-    for (int q = 0; q < RG; ++q) acc += part[q][tid];
-    stf(reinterpret_cast<TIO*>(A.out) + (size_t)bh * D + tile * DT + tid, acc);
+    for (int e = 0; e < 4; ++e) stf(reinterpret_cast<TIO*>(A.out) + (size_t)bh * D + tile * DT + c0 + e, ov[e]);
   }
   if (h == 0 && tile == 0 && A.taps > 1) {  // the history shifted by the new row
     const int k1 = A.taps - 1;
