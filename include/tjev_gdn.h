@@ -80,6 +80,7 @@ typedef struct tjev_gdn_params {
   int32_t inverse;        /* tjev_gdn_inverse */
   int32_t heads_per_step; /* accepted for the reference's signature (0 = default) */
   int32_t residuals;      /* tjev_gdn_residuals */
+  int32_t qk_dtype;       /* tjev_gdn_dtype of q, k, d_q, d_k (the v2 entry points only) */
 } tjev_gdn_params;
 
 /* 0 if the library has kernels for these parameters, else a status (and the message). */
@@ -121,6 +122,20 @@ int tjev_gdn_decode_step(const tjev_gdn_params* p, void* stream, const void* qkv
                          const void* b, const float* a_log, const float* dt_bias,
                          const float* conv_w, const void* conv_state, const float* state,
                          void* out, void* conv_state_out, float* state_out);
+
+/* The v2 operator (tjev's chunk_gated_delta_rule_v2, pallas_tpu_v2.py:541-582, behind
+ * gdn_impl=pallas_tpu_v2): the same chunked delta rule on given q, k [B, T, Hk, Dk] (qk_dtype;
+ * used as given: the model passes l2norm(q) * Dk^-1/2 and l2norm(k)), v [B, T, H, Dv]
+ * (io_dtype), g (log decay) and beta [B, T, H] (gate_dtype); out [B, T, H, Dv] in io_dtype.
+ * taps must be 0. The residuals and workspace are as for the megakernel. The backward writes
+ * d_q, d_k (qk_dtype), d_v (io_dtype), d_g and d_beta (gate_dtype). */
+int tjev_gdn_v2_fwd(const tjev_gdn_params* p, void* stream, const void* q, const void* k, const void* v,
+                    const void* g, const void* beta, const int32_t* seg, void* out, float* residuals,
+                    void* workspace, size_t workspace_bytes);
+int tjev_gdn_v2_bwd(const tjev_gdn_params* p, void* stream, const void* q, const void* k, const void* v,
+                    const void* g, const void* beta, const int32_t* seg, const float* residuals,
+                    const void* d_out, void* d_q, void* d_k, void* d_v, void* d_g, void* d_beta,
+                    void* workspace, size_t workspace_bytes);
 
 /* backward: replaces pallas_call "gdn_mega2_bwd" (pallas_tpu_mega.py:471-524) plus the XLA sums
  * of _core_bwd (:563-571): d_qkv (io_dtype), d_a, d_b (gate_dtype), d_a_log and d_dt_bias ([H] fp32), and,

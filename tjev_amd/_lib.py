@@ -28,6 +28,8 @@ EXPORTS = (
     "tjev_gdn_mega2_fwd",
     "tjev_gdn_mega2_fwd_state",
     "tjev_gdn_decode_step",
+    "tjev_gdn_v2_fwd",
+    "tjev_gdn_v2_bwd",
     "tjev_gdn_mega2_bwd",
     "tjev_gdn_norm_workspace_bytes",
     "tjev_gdn_gated_rmsnorm_fwd",
@@ -46,7 +48,7 @@ class Params(ctypes.Structure):
 
     _fields_ = [(name, ctypes.c_int32) for name in (
         "batch", "length", "key_heads", "key_dim", "value_heads", "value_dim", "taps", "chunk",
-        "io_dtype", "gate_dtype", "precision", "inverse", "heads_per_step", "residuals",
+        "io_dtype", "gate_dtype", "precision", "inverse", "heads_per_step", "residuals", "qk_dtype",
     )]
 
 
@@ -92,6 +94,10 @@ def load() -> ctypes.CDLL:
     lib.tjev_gdn_mega2_fwd_state.restype = i32
     lib.tjev_gdn_decode_step.argtypes = [pp, vp] + [vp] * 11
     lib.tjev_gdn_decode_step.restype = i32
+    lib.tjev_gdn_v2_fwd.argtypes = [pp, vp] + [vp] * 9 + [sz]
+    lib.tjev_gdn_v2_fwd.restype = i32
+    lib.tjev_gdn_v2_bwd.argtypes = [pp, vp] + [vp] * 14 + [sz]
+    lib.tjev_gdn_v2_bwd.restype = i32
     lib.tjev_gdn_mega2_bwd.argtypes = [pp, vp] + [vp] * 16 + [sz]
     lib.tjev_gdn_mega2_bwd.restype = i32
     npp = ctypes.POINTER(NormParams)

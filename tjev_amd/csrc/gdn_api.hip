@@ -66,6 +66,7 @@ int validate(const tjev_gdn_params* p) {
   if (p->io_dtype < 0 || p->io_dtype > 1 || p->gate_dtype < 0 || p->gate_dtype > 1)
     return fail(TJEV_GDN_EINVAL, "dtypes must be TJEV_GDN_F32 or TJEV_GDN_BF16");
   if (p->heads_per_step < 0) return fail(TJEV_GDN_EINVAL, "heads_per_step must be >= 0");
+  if (p->qk_dtype < 0 || p->qk_dtype > 1) return fail(TJEV_GDN_EINVAL, "qk_dtype must be TJEV_GDN_F32 or TJEV_GDN_BF16");
   if (p->residuals < TJEV_GDN_SAVE_STATES || p->residuals > TJEV_GDN_SAVE_ALL)
     return fail(TJEV_GDN_EINVAL, "residuals must be TJEV_GDN_SAVE_STATES, _TINV or _ALL");
   if (p->key_dim != p->value_dim)
@@ -262,6 +263,14 @@ int run(const tjev_gdn_params* p, void* stream, gdn::GdnArgs& A, int backward) {
   return 0;
 }
 
+int run_v2(const tjev_gdn_params* p, void* stream, gdn::GdnArgs& A, int backward) {
+  const gdn::ShapeTable* t = lookup(kernel_chunk(p), p->key_dim);
+  const gdn::GdnFn fn = t->fnv2[p->precision][p->io_dtype][p->qk_dtype][p->gate_dtype];
+  const hipError_t e = fn(A, static_cast<hipStream_t>(stream), backward, gdn::active_timer());
+  if (e != hipSuccess) return fail(TJEV_GDN_EHIP, std::string("HIP launch failed: ") + hipGetErrorString(e));
+  return 0;
+}
+
 }  // namespace
 
 namespace gdn {
@@ -339,6 +348,61 @@ int tjev_gdn_mega2_fwd_state(const tjev_gdn_params* p, void* stream, const void*
   A.final_state = final_state;
   A.conv_state = conv_state;
   return run(p, stream, A, 0);
+}
+
+int tjev_gdn_v2_fwd(const tjev_gdn_params* p, void* stream, const void* q, const void* k, const void* v,
+                    const void* g, const void* beta, const int32_t* seg, void* out, float* residuals, void* workspace,
+                    size_t workspace_bytes) {
+  if (int s = validate(p)) return s;
+  if (p->taps != 0) return fail(TJEV_GDN_EINVAL, "the v2 operator has no conv: taps must be 0");
+  if (!q || !k || !v || !g || !beta || !seg || !out || !residuals) return fail(TJEV_GDN_EINVAL, "null tensor argument");
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16) || !aligned(residuals, 256) ||
+      !aligned(workspace, 256))
+    return fail(TJEV_GDN_EINVAL, "q, k, v and out must be 16-byte aligned, the residuals and workspace 256-byte aligned");
+  const Layout L = layout(p, 0);
+  if (!workspace || workspace_bytes < L.total)
+    return fail(TJEV_GDN_EWORKSPACE, "forward workspace needs " + std::to_string(L.total) + " bytes");
+  gdn::GdnArgs A = base_args(p, workspace, L);
+  A.q2 = q;
+  A.k2 = k;
+  A.v2 = v;
+  A.g2 = g;
+  A.b2 = beta;
+  A.seg = seg;
+  A.out = out;
+  bind_residuals(p, residuals, A);
+  return run_v2(p, stream, A, 0);
+}
+
+int tjev_gdn_v2_bwd(const tjev_gdn_params* p, void* stream, const void* q, const void* k, const void* v,
+                    const void* g, const void* beta, const int32_t* seg, const float* residuals, const void* d_out,
+                    void* d_q, void* d_k, void* d_v, void* d_g, void* d_beta, void* workspace,
+                    size_t workspace_bytes) {
+  if (int s = validate(p)) return s;
+  if (p->taps != 0) return fail(TJEV_GDN_EINVAL, "the v2 operator has no conv: taps must be 0");
+  if (!q || !k || !v || !g || !beta || !seg || !residuals || !d_out || !d_q || !d_k || !d_v || !d_g || !d_beta)
+    return fail(TJEV_GDN_EINVAL, "null tensor argument");
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(d_out, 16) || !aligned(d_q, 16) ||
+      !aligned(d_k, 16) || !aligned(d_v, 16) || !aligned(residuals, 256) || !aligned(workspace, 256))
+    return fail(TJEV_GDN_EINVAL, "tensors must be 16-byte aligned, the residuals and workspace 256-byte aligned");
+  const Layout L = layout(p, 1);
+  if (!workspace || workspace_bytes < L.total)
+    return fail(TJEV_GDN_EWORKSPACE, "backward workspace needs " + std::to_string(L.total) + " bytes");
+  gdn::GdnArgs A = base_args(p, workspace, L);
+  A.q2 = q;
+  A.k2 = k;
+  A.v2 = v;
+  A.g2 = g;
+  A.b2 = beta;
+  A.seg = seg;
+  bind_residuals(p, const_cast<float*>(residuals), A);
+  A.d_out = d_out;
+  A.d_q2 = d_q;
+  A.d_k2 = d_k;
+  A.d_v2 = d_v;
+  A.d_g2 = d_g;
+  A.d_b2 = d_beta;
+  return run_v2(p, stream, A, 1);
 }
 
 int tjev_gdn_mega2_bwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,

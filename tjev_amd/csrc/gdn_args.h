@@ -25,6 +25,17 @@ struct GdnArgs {
   float* states;       // [B, H, N, Dk, Dv]
   float* final_state;  // [B, H, Dk, Dv] the state after token T-1 (or null)
   void* conv_state;    // [B, K-1, W] the raw rows before token T (or null)
+  // the v2 operator's inputs q, k [B,T,Hk,D], v [B,T,H,D], g, beta [B,T,H] and their gradients
+  const void* q2;
+  const void* k2;
+  const void* v2;
+  const void* g2;
+  const void* b2;
+  void* d_q2;
+  void* d_k2;
+  void* d_v2;
+  void* d_g2;
+  void* d_b2;
   // backward
   const void* d_out;
   void* d_qkv;

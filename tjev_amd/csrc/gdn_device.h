@@ -68,6 +68,18 @@ __device__ __forceinline__ void ld8(const uint16_t* p, float (&o)[8]) {
   }
 }
 
+// 8 consecutive values stored as T (bf16 rounds to nearest even)
+__device__ __forceinline__ void st8_io(float* p, const float (&v)[8]) {
+  reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+  reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+__device__ __forceinline__ void st8_io(uint16_t* p, const float (&v)[8]) {
+  uint32_t w[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) w[e] = (uint32_t)f2bf(v[2 * e]) | ((uint32_t)f2bf(v[2 * e + 1]) << 16);
+  *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // 8 consecutive stored values held as loaded (bf16 stays packed), converted when used
 template <class T> struct Raw8;
 template <> struct Raw8<float> {

@@ -2,6 +2,7 @@
 // gdn_shapes.def with -DGDN_C=<chunk> -DGDN_D=<head dim>.
 #include "gdn_kernels.h"
 #include "gdn_launch.h"
+#include "gdn_v2.h"
 
 #ifndef GDN_C
 #error "build with -DGDN_C=<chunk> -DGDN_D=<head dim>"
@@ -12,6 +13,8 @@ namespace {
 
 // compute units of the current device (queried once per device): the persistent kernels run
 // one workgroup per CU
+dim3 chunks_grid(const GdnArgs& A) { return dim3(A.B * A.H * A.N); }
+
 int cu_count() {
   static int cache[16] = {0};
   int dev = 0;
@@ -78,6 +81,66 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
   return hipGetLastError();
 }
 
+// the v2 operator: its own ends (k_prep_v2, k_post_v2) around the same middle kernels
+template <int C, int D, int PI, int PS, class TIO, class TQK, class TG>
+hipError_t run_v2(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) {
+  constexpr int DVT = D < 32 ? D : 32;
+  constexpr int NS = (C > D ? C : D) * 4;
+  const dim3 ends(A.B * A.N, 2 * A.Hk + A.H);
+  const int chains = A.B * A.H * (D / DVT);
+  int parts = (2 * cu_count() + chains - 1) / chains;
+  parts = parts < 1 ? 1 : (parts > A.N ? A.N : parts);
+  GdnArgs L = A;
+  L.parts = parts;
+  const dim3 tiles(chains * parts);
+  const int units = A.B * A.H * A.N, cus = cu_count();
+  const dim3 persist(units < cus ? units : cus);
+  auto mark = [&](int k, int end) {
+    if (tm) tm->mark(tm->self, k, end, st);
+  };
+#define GDN_LAUNCH(id, kern, grid, block)                  \
+  do {                                                     \
+    mark(id, 0);                                           \
+    hipLaunchKernelGGL(kern, grid, block, 0, st, L);       \
+    mark(id, 1);                                           \
+  } while (0)
+  if (!backward) {
+    GDN_LAUNCH(K_PREP_FWD, (k_prep_v2<C, D, TIO, TQK, TG>), ends, dim3(256));
+    if (A.res == 0) {
+      GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0>), persist, dim3(C * 4));
+    } else {
+      GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 2>), persist, dim3(C * 4));
+    }
+    GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd<C, D, DVT, PI, PS>), tiles, dim3(NS));
+    GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO>), persist, dim3(C * 4));
+  } else {
+    GDN_LAUNCH(K_PREP_BWD, (k_prep_v2<C, D, TIO, TQK, TG>), ends, dim3(256));
+    if (A.res == 0) {
+      GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 1>), persist, dim3(C * 4));
+    } else if (A.res == 1) {
+      GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 3>), persist, dim3(C * 4));
+    }
+    GDN_LAUNCH(K_BWD_LOCAL, (k_bwd_local<C, D, PI, TIO>), persist, dim3(C * 4));
+    GDN_LAUNCH(K_SCAN_BWD, (k_scan_bwd<C, D, DVT, PI, PS, TIO>), tiles, dim3(NS));
+    GDN_LAUNCH(K_BWD_GRADS, (k_bwd_grads<C, D, PI, PS, TIO>), chunks_grid(A), dim3(C * 4));
+    GDN_LAUNCH(K_POST, (k_post_v2<C, D, TIO, TQK, TG>), ends, dim3(256));
+  }
+#undef GDN_LAUNCH
+  return hipGetLastError();
+}
+
+template <int PI, int PS>
+void fill_v2(GdnFn (&f)[2][2][2]) {
+  f[0][0][0] = run_v2<GDN_C, GDN_D, PI, PS, float, float, float>;
+  f[0][0][1] = run_v2<GDN_C, GDN_D, PI, PS, float, float, uint16_t>;
+  f[0][1][0] = run_v2<GDN_C, GDN_D, PI, PS, float, uint16_t, float>;
+  f[0][1][1] = run_v2<GDN_C, GDN_D, PI, PS, float, uint16_t, uint16_t>;
+  f[1][0][0] = run_v2<GDN_C, GDN_D, PI, PS, uint16_t, float, float>;
+  f[1][0][1] = run_v2<GDN_C, GDN_D, PI, PS, uint16_t, float, uint16_t>;
+  f[1][1][0] = run_v2<GDN_C, GDN_D, PI, PS, uint16_t, uint16_t, float>;
+  f[1][1][1] = run_v2<GDN_C, GDN_D, PI, PS, uint16_t, uint16_t, uint16_t>;
+}
+
 template <int PI, int PS>
 void fill(GdnFn (&f)[2][2]) {
   f[0][0] = run<GDN_C, GDN_D, PI, PS, float, float>;
@@ -94,6 +157,10 @@ ShapeTable make() {
   fill<P_BF16X3, P_BF16X3>(t.fn[1]); // high
   fill<P_BF16, P_BF16>(t.fn[2]);     // bf16
   fill<P_BF16X3, P_BF16>(t.fn[3]);   // mixed
+  fill_v2<P_F32, P_F32>(t.fnv2[0]);
+  fill_v2<P_BF16X3, P_BF16X3>(t.fnv2[1]);
+  fill_v2<P_BF16, P_BF16>(t.fnv2[2]);
+  fill_v2<P_BF16X3, P_BF16>(t.fnv2[3]);
   return t;
 }
 

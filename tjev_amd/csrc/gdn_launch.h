@@ -27,7 +27,8 @@ typedef hipError_t (*GdnFn)(const GdnArgs&, hipStream_t, int backward, const Tim
 
 struct ShapeTable {
   int C, D;
-  GdnFn fn[4][2][2];  // [precision][io dtype][gate dtype]
+  GdnFn fn[4][2][2];       // [precision][io dtype][gate dtype]
+  GdnFn fnv2[4][2][2][2];  // the v2 operator: [precision][io dtype][q/k dtype][gate dtype]
 };
 
 // Shared by the C ABI's units (defined in gdn_api.hip): record the message of a nonzero status

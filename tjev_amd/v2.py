@@ -1,0 +1,85 @@
+"""tjev's v2 operator on MI355X: ``chunk_gated_delta_rule_v2`` (src/tjev/kernels/gated_delta_rule/
+pallas_tpu_v2.py:541-582), the chunked gated delta rule on given q, k, v, g, beta -- what the
+model calls with ``gdn_impl=pallas_tpu_v2`` after its own conv, l2norm and gates (gdn.py:47-97)
+-- computed by the HIP library's chunk, scan and output kernels through its C ABI.
+
+Same arguments, defaults and ValueErrors as the reference; out [B, T, H, Dv] in v's dtype; q
+and k keep their dtype (fp32 or bf16), g and beta theirs. GQA: value head h reads key head
+h // (H / Hk). The custom VJP gives d q, d k, d v, d g and d beta. ``vmem_fraction`` is
+TPU-only and ignored; ``heads_per_step`` is checked as the reference does. ``residuals`` as
+for ``gdn_megakernel`` (this build's choice of what the forward keeps). No fallback: without
+the HIP library, or on a CPU tensor, the operator raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .gdn import INVERSE_BLOCKS, LANES, PRECISIONS, GdnPlan, _ptr, heads_per_block
+
+_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+
+
+class _V2(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, plan: GdnPlan, q, k, v, g, beta, seg):
+        out = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+        res = plan.residuals(v.device)
+        ws = plan.workspace(False, v.device)
+        _lib.check_status(plan.lib.tjev_gdn_v2_fwd(
+            ctypes.byref(plan.params), plan._stream(v.device), _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta),
+            _ptr(seg), _ptr(out), _ptr(res), _ptr(ws), ws.numel()))
+        ctx.plan = plan
+        ctx.save_for_backward(q, k, v, g, beta, seg, res)
+        return out
+
+    @staticmethod
+    def backward(ctx, d_out):
+        plan: GdnPlan = ctx.plan
+        q, k, v, g, beta, seg, res = ctx.saved_tensors
+        d_out = d_out.to(v.dtype).contiguous()
+        d_q, d_k, d_v = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        d_g, d_beta = torch.empty_like(g), torch.empty_like(beta)
+        ws = plan.workspace(True, v.device)
+        _lib.check_status(plan.lib.tjev_gdn_v2_bwd(
+            ctypes.byref(plan.params), plan._stream(v.device), _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta),
+            _ptr(seg), _ptr(res), _ptr(d_out), _ptr(d_q), _ptr(d_k), _ptr(d_v), _ptr(d_g), _ptr(d_beta), _ptr(ws),
+            ws.numel()))
+        return None, d_q, d_k, d_v, d_g, d_beta, None
+
+
+def chunk_gated_delta_rule_v2(q, k, v, g, beta, segment_ids=None, *, chunk: int = 64, precision: str = "high",
+                              inverse: str = "doubling", heads_per_step: int = 0, vmem_fraction: float = 0.0,
+                              residuals: str = "states") -> torch.Tensor:
+    """q, k [B,T,Hk,Dk] (Hk divides H), v [B,T,H,Dv], g, beta [B,T,H] -> out [B,T,H,Dv] in v's
+    dtype (pallas_tpu_v2.py:541-582). T is padded to whole chunks with segment-0 tokens."""
+    if precision not in PRECISIONS:
+        raise ValueError(f"precision in {PRECISIONS}")
+    if inverse not in INVERSE_BLOCKS:
+        raise ValueError(f"gdn_impl=pallas_tpu_v2 inverse in {tuple(INVERSE_BLOCKS)}")
+    batch, length, kheads, dk = k.shape
+    heads, dv = v.shape[2], v.shape[-1]
+    if heads % kheads:
+        raise ValueError(f"{heads} value heads are not groups of {kheads} key heads")
+    if chunk & (chunk - 1):
+        raise ValueError("gdn_impl=pallas_tpu_v2 needs a power-of-two chunk")
+    if 3 * heads_per_block(heads, heads // kheads, heads_per_step or 8) > LANES:
+        raise ValueError("at most 42 heads per step")
+    if q.shape != k.shape or v.shape[:2] != q.shape[:2] or g.shape != (batch, length, heads) or g.shape != beta.shape:
+        raise ValueError(f"shapes q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}, g {tuple(g.shape)}, "
+                         f"beta {tuple(beta.shape)} do not agree")
+    if not v.is_cuda:
+        raise RuntimeError("chunk_gated_delta_rule_v2 runs on the GPU (HIP); got a CPU tensor")
+    if segment_ids is None:
+        segment_ids = torch.ones((batch, length), dtype=torch.int32, device=v.device)
+    qk_dtype = q.dtype if q.dtype in _DTYPES else torch.float32
+    plan = GdnPlan(batch=batch, length=length, key_heads=kheads, key_dim=dk, value_heads=heads, value_dim=dv, taps=0,
+                   chunk=chunk, io_dtype=v.dtype, gate_dtype=g.dtype if g.dtype in _DTYPES else torch.float32,
+                   precision=precision, inverse=inverse, heads_per_step=heads_per_step, residuals=residuals)
+    plan.params.qk_dtype = _DTYPES[qk_dtype]
+    gd = torch.bfloat16 if plan.params.gate_dtype == _lib.BF16 else torch.float32
+    return _V2.apply(plan, q.to(qk_dtype).contiguous(), k.to(qk_dtype).contiguous(), v.contiguous(),
+                     g.to(gd).contiguous(), beta.to(gd).contiguous(), segment_ids.to(torch.int32).contiguous())
