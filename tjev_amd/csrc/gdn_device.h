@@ -416,23 +416,28 @@ template <int K> __device__ __forceinline__ int tri_end(int i0) { return min(K, 
 // ... and of an upper-triangular one (a transposed lower-triangular): k >= i0
 __device__ __forceinline__ int tri_begin(int i0) { return (i0 / 32) * 32; }
 
+// v of another lane of the same 16-lane row by a DPP control (quad permutes, mirrors)
+template <int CTRL>
+__device__ __forceinline__ float dpp_read(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// sum over each aligned group of N consecutive lanes (N a power of two <= 64), in every lane
+// of the group: within a 16-lane row by DPP (lane ^ 1, lane ^ 2 as quad permutes, then the
+// row's half mirror and mirror, which pair the quads and the halves), across rows by xor
+// shuffles
+template <int N>
+__device__ __forceinline__ float sum_lanes(float v) {
+  if constexpr (N >= 2) v += dpp_read<0xB1>(v);   // quad_perm [1,0,3,2]
+  if constexpr (N >= 4) v += dpp_read<0x4E>(v);   // quad_perm [2,3,0,1]
+  if constexpr (N >= 8) v += dpp_read<0x141>(v);  // row_half_mirror
+  if constexpr (N >= 16) v += dpp_read<0x140>(v); // row_mirror
+  if constexpr (N >= 32) v += __shfl_xor(v, 16);
+  if constexpr (N >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
 // sum over the 16 lanes that share lane/16 (one accumulator row across a tile's columns)
-__device__ __forceinline__ float sum16(float v) {
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 4);
-  v += __shfl_xor(v, 8);
-  return v;
-}
-__device__ __forceinline__ float sum64(float v) {
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 4);
-  v += __shfl_xor(v, 8);
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
-}
+__device__ __forceinline__ float sum16(float v) { return sum_lanes<16>(v); }
+__device__ __forceinline__ float sum64(float v) { return sum_lanes<64>(v); }
 
 __device__ __forceinline__ double sum64d(double v) {
 #pragma unroll

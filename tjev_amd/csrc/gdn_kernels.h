@@ -349,8 +349,7 @@ __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
         float sq = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) sq += act[e] * act[e];
-#pragma unroll
-        for (int m = 1; m < CG; m <<= 1) sq += __shfl_xor(sq, m);
+        sq = sum_lanes<CG>(sq);
         float rn = sq == 0.f ? 0.f : 1.0f / sqrtf(sq + 1e-6f);
         if (kind == 0) rn *= A.scale;
 #pragma unroll
@@ -1685,14 +1684,12 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
       float sq = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) sq += act[e] * act[e];
-#pragma unroll
-      for (int m = 1; m < CG; m <<= 1) sq += __shfl_xor(sq, m);
+      sq = sum_lanes<CG>(sq);
       const float rn = sq == 0.f ? 0.f : 1.0f / sqrtf(sq + 1e-6f);
       float dot = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) dot += act[e] * rn * dy[e];
-#pragma unroll
-      for (int m = 1; m < CG; m <<= 1) dot += __shfl_xor(dot, m);
+      dot = sum_lanes<CG>(dot);
 #pragma unroll
       for (int e = 0; e < 8; ++e) dy[e] = rn * (dy[e] - act[e] * rn * dot);
     } else {  // dv = X beta, and rows(X, v) for d beta (v is this head's activation)
@@ -1702,8 +1699,7 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
         dy[e] = dyv[i][e] * btv[i];
         xv += dyv[i][e] * act[e];
       }
-#pragma unroll
-      for (int m = 1; m < CG; m <<= 1) xv += __shfl_xor(xv, m);
+      xv = sum_lanes<CG>(xv);
       if (cg == 0 && r < C) sxv[r] = xv;
     }
     float dz[8];

@@ -62,9 +62,7 @@ __device__ __forceinline__ void st8(uint16_t* p, const float (&v)[8]) {
 // sum over the LPR lanes of one row (groups of LPR consecutive lanes, LPR a power of two)
 template <int LPR>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int m = LPR / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
+  return sum_lanes<LPR>(v);
 }
 
 template <class T>

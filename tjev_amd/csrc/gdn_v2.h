@@ -125,8 +125,7 @@ __global__ __launch_bounds__(256) void k_post_v2(GdnArgs A) {
         d[e] = x[e] * bt;
         xv += x[e] * v[e];
       }
-#pragma unroll
-      for (int m = 1; m < CG; m <<= 1) xv += __shfl_xor(xv, m);
+      xv = sum_lanes<CG>(xv);
       if (cg == 0) sxv[r] = xv;
       if (t < A.T) st8_io(reinterpret_cast<TIO*>(A.d_v2) + (((size_t)b * A.T + t) * A.H + head) * D + cg * 8, d);
     }
