@@ -109,14 +109,9 @@ __device__ __forceinline__ void derive_ctx(Ctx<C>& cx) {
   if (threadIdx.x == 0) cx.carry = (cx.seg[C - 1] == cx.before) ? expf(cx.gam[C - 1] + cx.gaml[C - 1]) : 0.f;
 }
 
-// D_ij = e^(gamma_i - gamma_j) on same-segment i >= j, else 0 (the exp taken only there)
-template <int C>
-__device__ __forceinline__ float decay(const Ctx<C>& cx, int i, int j) {
-  return (i >= j && cx.seg[i] == cx.seg[j]) ? expf(gdiff(cx, i, j)) : 0.f;
-}
-
-// D over one wave's 16-row strip (rows i0 + acc_row(rr)), tile by tile. Below the diagonal the
-// exponential factors through the strip's first row p = i0: for j < p <= i,
+// D_ij = e^(gamma_i - gamma_j) on same-segment i >= j, else 0, over one wave's 16-row strip
+// (rows i0 + acc_row(rr)), tile by tile. Below the diagonal the exponential factors through
+// the strip's first row p = i0: for j < p <= i,
 // e^(gamma_i - gamma_j) = e^(gamma_i - gamma_p) e^(gamma_p - gamma_j) with both factors <= 1
 // (gamma never increases along a chunk: g <= 0), so a lane takes 4 exponentials for its rows
 // and 1 per tile instead of 4 per tile; the diagonal tile takes each one directly.
