@@ -277,7 +277,7 @@ def main(argv=None) -> int:
     from tjev_amd.gdn import GdnPlan
     from tjev_amd.norm import _params as _norm_params
     from tjev_amd.norm import norm_backward, norm_forward
-    from tjev_amd.roofline import PEAK_BF16_TFLOPS, PEAK_FP32_TFLOPS, PEAK_HBM_GBS, kernel_work, operator_work
+    from tjev_amd.roofline import PEAK_BF16_TFLOPS, PEAK_FP32_TFLOPS, kernel_roofline, kernel_work, operator_work
     from tjev_amd.testing import CONFIGS, cotangent, gdn_inputs
 
     if args.config in ("4B-block", "decode"):
@@ -340,20 +340,11 @@ def main(argv=None) -> int:
     per_kernel = {k: kt.ms[k] / kt.launches[k] for k in kt.ms if kt.launches[k]}
     io_bytes = 2 if dtype == torch.bfloat16 else 4
     shape = dict(batch=B, length=T, key_heads=Hk, value_heads=H, dim=D, chunk=C, io_bytes=io_bytes)
-    work = kernel_work(**shape)
+    work = kernel_work(**shape, residuals=args.residuals)
     shape["norm"] = norm
     peak_mfma = PEAK_FP32_TFLOPS if precision == "highest" else PEAK_BF16_TFLOPS
-    kernels = {}
-    for name, avg_ms in per_kernel.items():
-        wk = work[name]
-        if wk["bound"] == "mfma":
-            ach = wk["flops"] / (avg_ms * 1e-3) / 1e12
-            kernels[name] = {"ms": avg_ms, "bound": "mfma", "achieved": ach, "unit": "TFLOP/s", "peak": peak_mfma,
-                             "frac": ach / peak_mfma, "algorithmic": wk["flops"]}
-        else:
-            ach = wk["bytes"] / (avg_ms * 1e-3) / 1e9
-            kernels[name] = {"ms": avg_ms, "bound": "hbm", "achieved": ach, "unit": "GB/s", "peak": PEAK_HBM_GBS,
-                             "frac": ach / PEAK_HBM_GBS, "algorithmic": wk["bytes"]}
+    kernels = {name: {"ms": avg_ms, **kernel_roofline(work[name], avg_ms * 1e-3, peak_mfma)}
+               for name, avg_ms in per_kernel.items()}
     dominant = max(kernels, key=lambda k: kernels[k]["ms"])
     dk = kernels[dominant]
     traffic = _traffic(args.config, precision, dominant)
@@ -377,7 +368,8 @@ def main(argv=None) -> int:
                    "precision": precision, "segments": cfg["segments"],
                    "epilogue": "gated_rmsnorm" if norm else None, "residuals": args.residuals},
         "roofline": {"kernel": dominant, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
-                     "unit": dk["unit"], "frac": dk["frac"], "traffic": traffic},
+                     "unit": dk["unit"], "frac": dk["frac"], "traffic": traffic,
+                     "hbm_frac": dk["hbm_frac"], "mfma_frac": dk["mfma_frac"]},
         "operator_roofline": {"algorithmic_gflop": op["flops"] / 1e9, "algorithmic_mb": op["bytes"] / 1e6,
                               "ceiling_tokens_per_s": op["ceiling_tokens_per_s"],
                               "frac": value / op["ceiling_tokens_per_s"],

@@ -20,9 +20,12 @@ PEAK_HBM_GBS = 8000.0
 
 
 def kernel_work(*, batch: int, length: int, key_heads: int, value_heads: int, dim: int, chunk: int,
-                io_bytes: int) -> dict[str, dict]:
-    """Per-launch algorithmic work of each kernel: {"flops": F} for the MFMA kernels,
-    {"bytes": B} for the HBM-bound ones, with the bound they are judged on."""
+                io_bytes: int, residuals: str = "states") -> dict[str, dict]:
+    """Per-launch algorithmic work of each kernel: {"bytes": B, "flops": F}. Bytes are the
+    minimal HBM traffic of the kernel's own inputs and outputs (each tensor read or written
+    once); FLOPs count the dense chunk contractions once (zero for the elementwise kernels).
+    ``residuals`` (states | tinv | all) sets what the forward's chunk kernel writes and what
+    the backward's reads, as the library's residual policy does."""
     C, D = chunk, dim
     n = -(-length // C)
     tp = n * C
@@ -35,29 +38,61 @@ def kernel_work(*, batch: int, length: int, key_heads: int, value_heads: int, di
     sd = 2 * C * D * D                         # one C x D x D product
     inv = C ** 3 / 3
     f32 = 4
+    act_k = tok_k * D * f32                    # q or k (key heads), fp32
+    act_v = tok_h * D * f32                    # v, w, u, v_new, X, Kt, dq / dk per value head, fp32
+    mats = units * D * D * f32                 # chunk-boundary states S or their gradients G
+    tinv = units * C * C * f32                 # T per chunk
+    io = tok_h * D * io_bytes                  # out or d out
+    ctx = batch * tp * 4 + 3 * tok_h * f32     # segment ids, gamma (hi, lo), beta
+    prep = tokens * (width + 2 * value_heads) * io_bytes + (2 * tok_k + tok_h) * D * f32 + 3 * tok_h * f32
     w = {
         # conv + gates + l2norm: read qkv, a, b; write q, k (key heads), v, gamma (hi, lo), beta
-        "gdn_prep_fwd": {"bound": "hbm", "bytes": tokens * (width + 2 * value_heads) * io_bytes
-                         + (2 * tok_k + tok_h) * D * f32 + 3 * tok_h * f32},
-        "gdn_chunk_fwd": {"bound": "mfma", "flops": units * (3 * sq + inv)},
-        "gdn_scan_fwd": {"bound": "hbm", "bytes": tok_h * D * f32 * 4 + units * D * D * f32},
-        "gdn_out": {"bound": "mfma", "flops": units * (2 * sq + sd)},
-        "gdn_prep_bwd": {"bound": "hbm", "bytes": tokens * (width + 2 * value_heads) * io_bytes
-                         + (2 * tok_k + tok_h) * D * f32 + 3 * tok_h * f32},
-        "gdn_chunk_bwd": {"bound": "mfma", "flops": units * (3 * sq + inv + sd)},
-        "gdn_bwd_local": {"bound": "mfma", "flops": units * 4 * sq},
-        "gdn_scan_bwd": {"bound": "hbm", "bytes": tok_h * D * f32 * 5 + units * D * D * f32 * 2},
-        "gdn_bwd_grads": {"bound": "mfma", "flops": units * (6 * sq + 3 * sd)},
+        "gdn_prep_fwd": {"bytes": prep, "flops": 0},
+        # k, v -> w, u (and T kept for the backward unless only the states are)
+        "gdn_chunk_fwd": {"bytes": act_k + act_v + ctx + 2 * act_v + (tinv if residuals != "states" else 0),
+                          "flops": units * (3 * sq + inv)},
+        # w, u, k -> v_new, S before each chunk
+        "gdn_scan_fwd": {"bytes": tok_h * D * f32 * 4 + units * D * D * f32, "flops": 0},
+        # q, k, v_new, S -> out
+        "gdn_out": {"bytes": 2 * act_k + act_v + mats + ctx + io, "flops": units * (2 * sq + sd)},
+        "gdn_prep_bwd": {"bytes": prep, "flops": 0},
+        # k, v, S (and T under tinv) -> v_new (and T under states)
+        "gdn_chunk_bwd": {"bytes": act_k + 2 * act_v + mats + tinv + ctx,
+                          "flops": units * ((3 * sq + inv + sd) if residuals == "states" else (2 * sq + sd))},
+        # q, k, d out, T -> X_loc, Kt
+        "gdn_bwd_local": {"bytes": 2 * act_k + io + tinv + ctx + 2 * act_v, "flops": units * 4 * sq},
+        "gdn_scan_bwd": {"bytes": tok_h * D * f32 * 5 + units * D * D * f32 * 2, "flops": 0},
+        # q, k, X, v_new, S, G, d out -> dq, dk per value head, d gamma, d beta
+        "gdn_bwd_grads": {"bytes": 2 * act_k + 4 * act_v + 2 * mats + io + ctx + 2 * tok_h * f32,
+                          "flops": units * (6 * sq + 3 * sd)},
         # GQA sums, l2norm / SiLU / conv backward: read qkv, dq, dk, X, beta; write d_qkv, da, db
-        "gdn_post": {"bound": "hbm", "bytes": tokens * width * io_bytes * 2 + 3 * tok_h * D * f32
-                     + 2 * tokens * value_heads * io_bytes},
-        "gdn_reduce": {"bound": "hbm", "bytes": batch * n * value_heads * 16},
+        "gdn_post": {"bytes": tokens * width * io_bytes * 2 + 3 * tok_h * D * f32
+                     + 2 * tokens * value_heads * io_bytes, "flops": 0},
+        "gdn_reduce": {"bytes": batch * n * value_heads * 16, "flops": 0},
         # gated RMSNorm: read x, z, write y; backward read x, z, dy, write dx, dz
-        "gdn_norm_fwd": {"bound": "hbm", "bytes": 3 * tokens * value_heads * D * io_bytes},
-        "gdn_norm_bwd": {"bound": "hbm", "bytes": 5 * tokens * value_heads * D * io_bytes},
-        "gdn_norm_reduce": {"bound": "hbm", "bytes": 2048 * D * f32},
+        "gdn_norm_fwd": {"bytes": 3 * tokens * value_heads * D * io_bytes, "flops": 0},
+        "gdn_norm_bwd": {"bytes": 5 * tokens * value_heads * D * io_bytes, "flops": 0},
+        "gdn_norm_reduce": {"bytes": 2048 * D * f32, "flops": 0},
     }
     return w
+
+
+def kernel_roofline(work: dict, seconds: float, peak_tflops: float) -> dict:
+    """One launch of ``seconds`` against its roofline: the bound is the resource whose ideal
+    time (algorithmic bytes at the HBM peak, algorithmic FLOPs at ``peak_tflops``) is longer,
+    and ``achieved`` / ``frac`` are taken on that bound; ``mfma_frac`` / ``hbm_frac`` give
+    both."""
+    t_hbm = work["bytes"] / (PEAK_HBM_GBS * 1e9)
+    t_mfma = work["flops"] / (peak_tflops * 1e12)
+    gbs = work["bytes"] / seconds / 1e9
+    tfs = work["flops"] / seconds / 1e12
+    r = {"hbm_frac": gbs / PEAK_HBM_GBS, "mfma_frac": tfs / peak_tflops,
+         "algorithmic_bytes": work["bytes"], "algorithmic_flops": work["flops"]}
+    if t_mfma > t_hbm:
+        r.update(bound="mfma", achieved=tfs, unit="TFLOP/s", peak=peak_tflops, frac=tfs / peak_tflops)
+    else:
+        r.update(bound="hbm", achieved=gbs, unit="GB/s", peak=PEAK_HBM_GBS, frac=gbs / PEAK_HBM_GBS)
+    return r
 
 
 def operator_work(*, batch: int, length: int, key_heads: int, value_heads: int, dim: int, chunk: int,
