@@ -7,6 +7,10 @@
         Per-kernel launch counts and average durations from a --kernel-trace run (CSV output).
     python -m tjev_amd.profiling counters DIR [DIR ...] [--out FILE.md]
         Per-kernel averages of every counter of some --pmc runs.
+    python -m tjev_amd.profiling mfma --pmc DIR --trace DIR --out FILE.md [--cus 256] [--xcds 8]
+        MFMA work and busy fraction per kernel from one --pmc run of SQ_INSTS_VALU_MFMA_MOPS_BF16,
+        SQ_INSTS_VALU_MFMA_MOPS_F32, SQ_VALU_MFMA_BUSY_CYCLES, SQ_BUSY_CYCLES and GRBM_GUI_ACTIVE,
+        with the durations of a --kernel-trace run of the same command.
     python -m tjev_amd.profiling traffic --fetch DIR --write DIR --copy-fetch DIR --copy-write DIR
                                          --copy-mib 1024 --out FILE.json --command "..."
         HBM bytes per launch of every kernel from two --pmc runs (FETCH_SIZE, then WRITE_SIZE),
@@ -165,6 +169,41 @@ def cmd_counters(args) -> int:
     return 0
 
 
+MFMA_COUNTERS = ("SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU_MFMA_MOPS_F32", "SQ_VALU_MFMA_BUSY_CYCLES",
+                 "SQ_BUSY_CYCLES", "GRBM_GUI_ACTIVE")
+
+
+def cmd_mfma(args) -> int:
+    """Executed MFMA work (MOPS counters, 512 FLOPs per unit) over the traced duration against
+    the dense peaks, and SQ_VALU_MFMA_BUSY_CYCLES over the SIMDs' cycles (GRBM_GUI_ACTIVE reads
+    the sum over the XCDs: per-XCD cycles x CUs x 4 SIMDs). The clock is the per-XCD cycles
+    over the traced duration."""
+    dur = trace_durations(args.trace)
+    cnt = {c: counter_per_dispatch(args.pmc, c) for c in MFMA_COUNTERS}
+    lines = [f"# MFMA counters: {args.title}", "", "Commands:", "", "```", args.command, "```", "",
+             "Per dispatch, averaged over a kernel's launches. `executed` = 512 x (MOPS_BF16 + MOPS_F32)",
+             "FLOPs (bf16x3 counts its three passes); `exec frac` = executed FLOP/s against the dense peak",
+             "(2.5 PFLOP/s bf16, 157.3 TFLOP/s fp32); `busy` = SQ_VALU_MFMA_BUSY_CYCLES /",
+             f"(GRBM_GUI_ACTIVE / {args.xcds} XCDs x {args.cus} CUs x 4 SIMDs), the MFMA pipes' busy fraction at",
+             "the clock the kernel ran at (`clock` = GRBM_GUI_ACTIVE / XCDs over the duration).", "",
+             "| kernel | avg us | clock GHz | executed bf16 GFLOP | executed fp32 GFLOP | exec frac | busy | "
+             + " | ".join(MFMA_COUNTERS) + " |", "|---|" + "---:|" * (6 + len(MFMA_COUNTERS))]
+    for k in sorted((k for k in cnt["GRBM_GUI_ACTIVE"] if k.startswith("gdn_")), key=lambda k: k):
+        avg = {c: statistics.mean(cnt[c][k]) if cnt[c].get(k) else float("nan") for c in MFMA_COUNTERS}
+        us = statistics.mean(dur[k]) if dur.get(k) else float("nan")
+        bf, f32 = 512 * avg["SQ_INSTS_VALU_MFMA_MOPS_BF16"], 512 * avg["SQ_INSTS_VALU_MFMA_MOPS_F32"]
+        frac = (bf / 2.5e15 + f32 / 157.3e12) / (us * 1e-6)
+        cycles = avg["GRBM_GUI_ACTIVE"] / args.xcds
+        busy = avg["SQ_VALU_MFMA_BUSY_CYCLES"] / (cycles * args.cus * 4)
+        lines.append(f"| {k} | {us:.1f} | {cycles / (us * 1e3):.2f} | {bf / 1e9:.2f} | {f32 / 1e9:.2f} | {frac:.3f} | "
+                     f"{busy:.3f} | "
+                     + " | ".join(f"{avg[c]:.4g}" for c in MFMA_COUNTERS) + " |")
+    text = "\n".join(lines) + "\n"
+    Path(args.out).write_text(text)
+    print(text)
+    return 0
+
+
 def cmd_copy_probe(args) -> int:
     import torch
 
@@ -200,9 +239,17 @@ def main(argv=None) -> int:
     p.add_argument("--out", default=None)
     p.add_argument("--title", default="")
     p.add_argument("--command", default="")
+    p = sub.add_parser("mfma")
+    p.add_argument("--pmc", required=True)
+    p.add_argument("--trace", required=True)
+    p.add_argument("--out", required=True)
+    p.add_argument("--cus", type=int, default=256)
+    p.add_argument("--xcds", type=int, default=8)
+    p.add_argument("--title", default="")
+    p.add_argument("--command", default="")
     args = ap.parse_args(argv)
     return {"copy-probe": cmd_copy_probe, "stats": cmd_stats, "traffic": cmd_traffic,
-            "counters": cmd_counters}[args.cmd](args)
+            "counters": cmd_counters, "mfma": cmd_mfma}[args.cmd](args)
 
 
 if __name__ == "__main__":
