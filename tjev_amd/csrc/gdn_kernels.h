@@ -936,7 +936,7 @@ struct ScanIx {
 // the accumulators of waves < D/16; chunks in order (pallas_tpu_v2.py:254-269). None of a
 // chunk step's global inputs depends on S, so each is held in registers and refilled with the
 // next chunk's values as soon as it has been used: those loads run during the rest of the
-// step (its products and barriers) instead of stalling the next one.
+// step (its products and barriers) instead of stalling the next one. Two barriers per step.
 template <int C, int D, int DVT, int NT>
 struct ScanFwdIn {
   PairGates<C> gt;     // kws of the thread's k rows, and the carry
@@ -999,9 +999,6 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
         }
     }
     const float carry = in.gt.carry();
-    in.k.put_cols2(ok, in.gt.kws(0), in.gt.kws(1));
-    in.fetch_k(A, b, hk, nx);
-    in.gt.fetch(A, b, h, nx, RegsT<C, D, NT>::pair());
     __syncthreads();
     if (NW == C / 16 || w < C / 16) {  // v_new = u - w S
       f32x4 acc[DVT / 16];
@@ -1020,13 +1017,18 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
         }
       in.fetch_u(A, b, h, nx, j0);
     }
+    // (k kws)^T after the product, so one wave's staging overlaps the other's MFMA work
+    in.k.put_cols2(ok, in.gt.kws(0), in.gt.kws(1));
+    in.fetch_k(A, b, hk, nx);
+    in.gt.fetch(A, b, h, nx, RegsT<C, D, NT>::pair());
     __syncthreads();
     if (NW == D / 16 || w < D / 16) {  // S = carry S + k_write^T v_new
 #pragma unroll
       for (int t = 0; t < DVT / 16; ++t) accS[t] *= carry;
       strip_mma<PI, C, DVT / 16>(accS, ok, 16 * w, ov, 0);
     }
-    __syncthreads();
+    // no barrier here: the next step's first writes go to the S tile, which this product
+    // does not read, and the k and v_new tiles are rewritten only after its first barrier
   }
 }
 
