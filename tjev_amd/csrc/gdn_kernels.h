@@ -167,45 +167,66 @@ struct UnitIx {
 // ---------------------------------------------------------------- inverse
 // (I + L)^-1 in place for the strictly lower-triangular L in sT (C x C, row stride LT):
 // exact 16x16 diagonal blocks by forward substitution (one wave per block, on the VALU),
-// then doubling levels s = 16 .. C/2: T_LL = -T_BR (L_LL T_TL) on MFMA
-// (pallas_tpu_v2.py:144-193; xla.py:82-100). tmp holds C*(C/2+4)/2 floats.
+// then doubling levels s = 16 .. C/2 on MFMA, T_LL = -T_BR (L_LL T_TL) (pallas_tpu_v2.py:144-193;
+// xla.py:82-100). sTT (C x LT floats) keeps T transposed as it is built, so the right
+// operand T_TL is read by rows. A level's product L_LL T_TL is kept transposed in the pair's
+// upper-right block of sT (unused by a lower-triangular T) and read by rows in turn. Products
+// with a triangular operand run over whole 32-wide contraction steps, so they read the upper
+// 16 x 16 corners of the 32 x 32 diagonal blocks of sT (and the lower corners of sTT): those
+// hold zeros when read (the level-16 products kept there are cleared at level 32, or at the
+// end when C = 32). On return sT holds T with the upper triangle zero wherever a product with
+// 32-wide steps reads it, and the level products elsewhere above the diagonal; the caller
+// synchronises before reading sT.
 template <int C, int P, int S>
-__device__ void doubling_level(float* sT, int LT, float* tmp) {
+__device__ __forceinline__ void doubling_level(float* sT, float* sTT, int LT) {
   if constexpr (S < C) {
-    constexpr int NW = C / 16;
-    constexpr int TPS = S / 16;
-    constexpr int NB = C / (2 * S);
-    constexpr int LP = S + 4;
-    const int w = wave();
-    for (int q = w; q < NB * TPS * TPS; q += NW) {
-      const int p = q / (TPS * TPS), ti = (q / TPS) % TPS, tj = q % TPS;
-      const int r0 = 2 * S * p;
-      f32x4 acc[1];
+    constexpr int TPS = S / 16;                 // 16-wide tiles per side of a pair's block
+    constexpr int TW = S >= 32 ? S / 32 : 1;    // tiles per wave, all in one row strip
+    const int w = wave(), l = lane();
+    const int strip = w >> 1, half = w & 1;     // C/32 row strips of 16 rows, two waves each
+    const int p = strip / TPS, ti = strip % TPS;
+    const int r0 = 2 * S * p;
+    const int tj0 = half * TW;
+    const bool on = S >= 32 || half == 0;
+    const int c = acc_col(), g4 = (l >> 4) << 2;
+    if (on) {  // tmp = L_LL T_TL for rows 16 ti, kept transposed at sT[r0 + j][r0 + S + i]
+      f32x4 acc[TW];
       zero(acc);
-      strip_mma<P, S, 1>(acc, krow(sT + (r0 + S) * LT + r0, LT), 16 * ti, kcol(sT + r0 * LT + r0, LT), 16 * tj);
+      strip_mma<P, S, TW>(acc, krow(sT + (r0 + S) * LT + r0, LT), 16 * ti, krow(sTT + r0 * LT + r0, LT), 16 * tj0,
+                          tri_begin(16 * tj0));
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        lds_st(tmp + p * S * LP + (16 * ti + acc_row(rr)) * LP + 16 * tj + acc_col(), acc[0][rr]);
+      for (int t = 0; t < TW; ++t)
+        *reinterpret_cast<float4*>(sT + (r0 + 16 * (tj0 + t) + c) * LT + r0 + S + 16 * ti + g4) =
+            make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+    }
+    if constexpr (S == 32) {  // clear the level-16 products: read as zeros from the next phase on
+      for (int idx = threadIdx.x; idx < (C / 32) * 256; idx += C * 4) {
+        const int q = idx >> 8, r = (idx >> 4) & 15, k = idx & 15;
+        sT[(32 * q + r) * LT + 32 * q + 16 + k] = 0.f;
+      }
     }
     __syncthreads();
-    for (int q = w; q < NB * TPS * TPS; q += NW) {
-      const int p = q / (TPS * TPS), ti = (q / TPS) % TPS, tj = q % TPS;
-      const int r0 = 2 * S * p;
-      f32x4 acc[1];
+    if (on) {  // T_LL = -T_BR tmp
+      f32x4 acc[TW];
       zero(acc);
-      strip_mma<P, S, 1>(acc, krow(sT + (r0 + S) * LT + r0 + S, LT), 16 * ti, kcol(tmp + p * S * LP, LP), 16 * tj, 0,
-                         tri_end<S>(16 * ti));
+      strip_mma<P, S, TW>(acc, krow(sT + (r0 + S) * LT + r0 + S, LT), 16 * ti, krow(sT + r0 * LT + r0 + S, LT),
+                          16 * tj0, 0, tri_end<S>(16 * ti));
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        lds_st(sT + (r0 + S + 16 * ti + acc_row(rr)) * LT + r0 + 16 * tj + acc_col(), -acc[0][rr]);
+      for (int t = 0; t < TW; ++t) {
+        const int j = r0 + 16 * (tj0 + t) + c, i = r0 + S + 16 * ti + g4;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) lds_st(sT + (i + rr) * LT + j, -acc[t][rr]);
+        if constexpr (2 * S < C)  // the last level's T_TL is never read again
+          *reinterpret_cast<float4*>(sTT + j * LT + i) = make_float4(-acc[t][0], -acc[t][1], -acc[t][2], -acc[t][3]);
+      }
     }
     __syncthreads();
-    doubling_level<C, P, 2 * S>(sT, LT, tmp);
+    doubling_level<C, P, 2 * S>(sT, sTT, LT);
   }
 }
 
 template <int C, int P>
-__device__ void invert_unit_lower(float* sT, int LT, float* tmp) {
+__device__ __forceinline__ void invert_unit_lower(float* sT, int LT, float* sTT) {
   const int w = wave(), l = lane();
   if (l < 16) {  // diagonal block w: lane l owns column l, X[i] = e_i - sum_{r<i} L[i][r] X[r]
     const float* blk = sT + 16 * w * LT + 16 * w;
@@ -229,9 +250,26 @@ __device__ void invert_unit_lower(float* sT, int LT, float* tmp) {
     float* out = sT + 16 * w * LT + 16 * w + l;
 #pragma unroll
     for (int i = 0; i < 16; ++i) lds_st(out + i * LT, x[i]);
+    float4* outT = reinterpret_cast<float4*>(sTT + (16 * w + l) * LT + 16 * w);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) outT[q] = make_float4(x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]);
+  } else if (w % 2 == 1) {  // zeros in sTT's lower 16 x 16 corner of the 32 x 32 diagonal block
+    for (int idx = l - 16; idx < 256; idx += 48) {
+      const int r = idx >> 4, k = idx & 15;
+      sTT[(16 * w + r) * LT + 16 * (w - 1) + k] = 0.f;
+    }
   }
   __syncthreads();
-  doubling_level<C, P, 16>(sT, LT, tmp);
+  doubling_level<C, P, 16>(sT, sTT, LT);
+  if constexpr (C == 32) {  // no level 32 to clear the level-16 product
+    for (int idx = threadIdx.x; idx < 256; idx += C * 4) sT[(idx >> 4) * LT + 16 + (idx & 15)] = 0.f;
+  }
+}
+// The same as a call: its addresses are then not kept live across a caller's loop (the
+// backward recompute, at its register limit, would spill)
+template <int C, int P>
+__device__ __noinline__ void invert_unit_lower_call(float* sT, int LT, float* sTT) {
+  invert_unit_lower<C, P>(sT, LT, sTT);
 }
 
 // ---------------------------------------------------------------- conv helpers
@@ -767,7 +805,7 @@ __device__ __forceinline__ void load_tile(float* s, int LD, const float* g) {
 // MODE 0 (forward): writes w and u; MODE 2: also T (kept as a residual). MODE 1 (backward
 // recompute): writes T and v_new = u - w S_before; MODE 3: v_new from the saved T (no L, no
 // inverse). LDS: T in fp32 (the inverse runs in place), one operand region reused for k,
-// kbe^T, (v beta)^T and S^T (the doubling scratch borrows it too). The next unit's context and
+// kbe^T, (v beta)^T and S^T (and T^T during the inverse). The next unit's context and
 // k rows are loaded at this unit's start and end; k (again), v and S of this unit after the
 // inverse, a product ahead of their use.
 template <int C, int D, int PI, int PS, int MODE>
@@ -779,9 +817,8 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
   constexpr int M = C > D ? C : D;
   constexpr int LT = M + 4;
   using TB = OpTile<PI, M, M>;
-  constexpr int TMP = C * (C / 2 + 4) / 2;
-  constexpr int RB = TB::BYTES > TMP * 4 ? TB::BYTES : TMP * 4;
-  __shared__ float sT[C * LT];
+  constexpr int RB = TB::BYTES > C * LT * 4 ? TB::BYTES : C * LT * 4;  // also T^T during the inverse
+  __shared__ __align__(16) float sT[C * LT];
   __shared__ __align__(16) char sB[RB];
   __shared__ Ctx<C> cx;
   const int w = wave(), i0 = 16 * w;
@@ -829,7 +866,11 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
         }
       }
       __syncthreads();
-      invert_unit_lower<C, PI>(sT, LT, reinterpret_cast<float*>(sB));
+      if constexpr (MODE == 1) {
+        invert_unit_lower_call<C, PI>(sT, LT, reinterpret_cast<float*>(sB));
+      } else {
+        invert_unit_lower<C, PI>(sT, LT, reinterpret_cast<float*>(sB));
+      }
       // k again (not held across the inverse: register limit), then v
       kk.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D);
       vc.fetch(A.vv + off, D);
@@ -849,7 +890,8 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
     // order, stores included) then does not wait for the stores
     kk.fetch(A.kn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D);
     if constexpr (STORE_T) {
-      for (int idx = threadIdx.x; idx < C * C; idx += NT) tg[idx] = sT[(idx / C) * LT + idx % C];
+      for (int idx = threadIdx.x; idx < C * C; idx += NT)  // lower triangle (the rest is scratch)
+        tg[idx] = idx % C <= idx / C ? sT[(idx / C) * LT + idx % C] : 0.f;
     }
     if constexpr (FWD) {
 #pragma unroll
