@@ -51,6 +51,15 @@ __device__ __forceinline__ float ldf(const uint16_t* p) { return bf2f(*p); }
 __device__ __forceinline__ void stf(float* p, float v) { *p = v; }
 __device__ __forceinline__ void stf(uint16_t* p, float v) { *p = f2bf(v); }
 
+// 4 consecutive elements (8-byte aligned for bf16, 16-byte for fp32)
+__device__ __forceinline__ void st4_io(float* p, const float (&v)[4]) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void st4_io(uint16_t* p, const float (&v)[4]) {
+  *reinterpret_cast<uint2*>(p) = make_uint2((uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16),
+                                            (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16));
+}
+
 // 8 consecutive elements (16-byte aligned for bf16, 32-byte for fp32) as floats
 __device__ __forceinline__ void ld8(const float* p, float (&o)[8]) {
   const float4 a = reinterpret_cast<const float4*>(p)[0];
@@ -421,6 +430,21 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_read(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
+// 4 x 4 transpose within each quad of lanes: lane q of the quad holds v[r] = M[r][q] before
+// and v[c] = M[q][c] after, by two exchanges of 2 x 2 blocks (quad permutes). Applied to an
+// accumulator tile, lane (g, 4m + q) then holds row 4g + q, columns 4m .. 4m + 3.
+__device__ __forceinline__ void quad_transpose(float (&v)[4]) {
+  const int q = lane() & 3;
+  const bool odd = q & 1, hi = q & 2;
+  const float r0 = dpp_read<0xB1>(odd ? v[0] : v[1]), r2 = dpp_read<0xB1>(odd ? v[2] : v[3]);  // lane q ^ 1
+  const float n0 = odd ? r0 : v[0], n1 = odd ? v[1] : r0, n2 = odd ? r2 : v[2], n3 = odd ? v[3] : r2;
+  const float u0 = dpp_read<0x4E>(hi ? n0 : n2), u1 = dpp_read<0x4E>(hi ? n1 : n3);  // lane q ^ 2
+  v[0] = hi ? u0 : n0;
+  v[1] = hi ? u1 : n1;
+  v[2] = hi ? n2 : u0;
+  v[3] = hi ? n3 : u1;
+}
+
 // sum over each aligned group of N consecutive lanes (N a power of two <= 64), in every lane
 // of the group: within a 16-lane row by DPP (lane ^ 1, lane ^ 2 as quad permutes, then the
 // row's half mirror and mirror, which pair the quads and the halves), across rows by xor

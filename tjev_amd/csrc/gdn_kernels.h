@@ -881,6 +881,12 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
     kk.put_cols(ob, cx.bg);  // kbe^T
     __syncthreads();
     strip_mma<PI, C, D / 16>(aw, krow(sT, LT), i0, ob, 0, 0, tri_end<C>(i0));
+    if constexpr (FWD) {  // w now: its stores drain during the u product
+#pragma unroll
+      for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) A.ww[off + (size_t)(i0 + acc_row(rr)) * D + 16 * t + acc_col()] = aw[t][rr];
+    }
     if constexpr (!FWD) sc.fetch(A.states + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * D * D, D);
     __syncthreads();
     vc.put_cols(ob, cx.beta);  // (v beta)^T
@@ -897,11 +903,7 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
 #pragma unroll
       for (int t = 0; t < D / 16; ++t)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const size_t g = off + (size_t)(i0 + acc_row(rr)) * D + 16 * t + acc_col();
-          A.ww[g] = aw[t][rr];
-          A.uu[g] = au[t][rr];
-        }
+        for (int rr = 0; rr < 4; ++rr) A.uu[off + (size_t)(i0 + acc_row(rr)) * D + 16 * t + acc_col()] = au[t][rr];
     } else {
       __syncthreads();
 #pragma unroll
@@ -1149,13 +1151,16 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
     in.q.fetch(A.qn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D, i0);
     in.st.fetch(A.states + ((size_t)y.b * A.H + y.h) * A.N * D * D + (size_t)y.n * D * D, D);
     TIO* out = reinterpret_cast<TIO*>(A.out);
+    {  // quad transposes: each lane stores 4 consecutive columns of one row
+      const int tok = x.n * C + i0 + ((lane() >> 4) << 2) + (lane() & 3);
+      TIO* orow = out + (((size_t)x.b * A.T + (tok < A.T ? tok : 0)) * A.H + x.h) * D + (lane() & 12);
 #pragma unroll
-    for (int t = 0; t < D / 16; ++t)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int tok = x.n * C + i0 + acc_row(rr);
-        if (tok < A.T) stf(out + (((size_t)x.b * A.T + tok) * A.H + x.h) * D + 16 * t + acc_col(), o[t][rr]);
+      for (int t = 0; t < D / 16; ++t) {
+        float v[4] = {o[t][0], o[t][1], o[t][2], o[t][3]};
+        quad_transpose(v);
+        if (tok < A.T) st4_io(orow + 16 * t, v);
       }
+    }
     __syncthreads();  // cx and the operand region are rewritten by the next unit
   }
 }
