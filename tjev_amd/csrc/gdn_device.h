@@ -445,6 +445,16 @@ __device__ __forceinline__ void quad_transpose(float (&v)[4]) {
   v[3] = hi ? n3 : u1;
 }
 
+// A 16 x 16 accumulator tile stored row-major at p (its element (0, 0); row stride ld, fp32
+// or bf16): a quad transpose, then 4 consecutive columns of one row per lane.
+template <class T>
+__device__ __forceinline__ void st_tile(T* p, size_t ld, const f32x4& a) {
+  float v[4] = {a[0], a[1], a[2], a[3]};
+  quad_transpose(v);
+  const int l = lane();
+  st4_io(p + (size_t)(((l >> 4) << 2) + (l & 3)) * ld + (l & 12), v);
+}
+
 // sum over each aligned group of N consecutive lanes (N a power of two <= 64), in every lane
 // of the group: within a 16-lane row by DPP (lane ^ 1, lane ^ 2 as quad permutes, then the
 // row's half mirror and mirror, which pair the quads and the halves), across rows by xor

@@ -1325,9 +1325,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
     strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // T^T dv_loc
     const size_t off = hoff(A, x.b, x.h, A.H, x.n, C, D);
 #pragma unroll
-    for (int t = 0; t < D / 16; ++t)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) A.xl[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = acc[t][rr];
+    for (int t = 0; t < D / 16; ++t) st_tile(A.xl + off + (size_t)i0 * D + 16 * t, D, acc[t]);
     __syncthreads();
     in.k.put_cols(ob, cx.kws);  // k_write^T
     in.fetch_k(A, y);
@@ -1335,9 +1333,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
     zero(acc);
     strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // T^T k_write
 #pragma unroll
-    for (int t = 0; t < D / 16; ++t)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) A.kt[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = acc[t][rr];
+    for (int t = 0; t < D / 16; ++t) st_tile(A.kt + off + (size_t)i0 * D + 16 * t, D, acc[t]);
     __syncthreads();  // cx, T and the operand region are rewritten by the next unit
   }
 }
@@ -1422,15 +1418,15 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
     if (NW == D / 16 || w < D / 16) {
       float* gdst = A.gg + ((size_t)bh * A.N + n) * D * D;
 #pragma unroll
-      for (int t = 0; t < DVT / 16; ++t)
+      for (int t = 0; t < DVT / 16; ++t) {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-          const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
           const float g = accG[t][rr];
-          og.put(j, i, g);
-          if (emit) gdst[i * D + j0 + j] = g;
+          og.put(16 * t + acc_col(), 16 * w + acc_row(rr), g);
           part += has_next ? g * in.snext.v[t][rr] : 0.f;
         }
+        if (emit) st_tile(gdst + 16 * w * D + j0 + 16 * t, D, accG[t]);
+      }
       in.fetch_snext(A, bh, nx, j0);
     }
     part = sum64(part);
@@ -1455,14 +1451,15 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
       in.fetch_kt(A, b, h, nx);
       const size_t off = hoff(A, b, h, A.H, n, C, D);
 #pragma unroll
-      for (int t = 0; t < DVT / 16; ++t)
+      for (int t = 0; t < DVT / 16; ++t) {
+        f32x4 xv;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-          const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
-          const float xv = in.xl.v[t][rr] + acc[t][rr];
-          ox.put(j, i, xv);
-          if (emit) A.xl[off + (size_t)i * D + j0 + j] = xv;
+          xv[rr] = in.xl.v[t][rr] + acc[t][rr];
+          ox.put(16 * t + acc_col(), 16 * w + acc_row(rr), xv[rr]);
         }
+        if (emit) st_tile(A.xl + off + (size_t)16 * w * D + j0 + 16 * t, D, xv);
+      }
       in.fetch_xl(A, b, h, nx, j0);
     }
     if (NW == D / 16 || w < D / 16) {  // G = carry G + q_read^T do
