@@ -29,12 +29,8 @@ __device__ __forceinline__ int wave() { return threadIdx.x >> 6; }
 // ---------------------------------------------------------------- bf16 storage
 // bf16 tensors are held as uint16_t; conversion rounds to nearest even (as torch does).
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
-__device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// (gfx950's v_cvt_pk_bf16_f32: round to nearest even, NaN stays NaN)
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 // A single fp32 store into LDS that the backend may not pair with its neighbours. ROCm 7.2's
 // SI load/store optimizer can merge two such stores into one ds_write2_b32 with a wrongly

@@ -1699,7 +1699,7 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
     if (r >= R) break;
     const bool live = r < rows && t < A.Tp;  // uniform over the CG lanes of the row
     const int st = live ? sgv[HW + i] : -3;
-    float z[8], act[8], dy[8];
+    float z[8], sg[8], act[8], dy[8];
     if (taps == 0) {
       raw[HW + i].get(act);
 #pragma unroll
@@ -1717,7 +1717,10 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
         for (int e = 0; e < 8; ++e) z[e] = keep ? z[e] + xl[e] * wl[L][e] : z[e];
       }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) act[e] = st > 0 ? z[e] * sigmoid_io<TIO>(z[e]) : 0.f;
+      for (int e = 0; e < 8; ++e) {
+        sg[e] = sigmoid_io<TIO>(z[e]);  // once: SiLU and its backward
+        act[e] = st > 0 ? z[e] * sg[e] : 0.f;
+      }
     }
     if (kind < 2) {  // l2norm backward (q's scale first)
 #pragma unroll
@@ -1749,10 +1752,7 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
       for (int e = 0; e < 8; ++e) dz[e] = live ? dy[e] : 0.f;
     } else {  // SiLU backward on valid tokens
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float sgm = sigmoid_io<TIO>(z[e]);
-        dz[e] = (live && st > 0) ? dy[e] * sgm * (1.f + z[e] * (1.f - sgm)) : 0.f;
-      }
+      for (int e = 0; e < 8; ++e) dz[e] = (live && st > 0) ? dy[e] * sg[e] * (1.f + z[e] * (1.f - sg[e])) : 0.f;
     }
     float4* o = reinterpret_cast<float4*>(sdz + r * LZ + cg * 8);
     o[0] = make_float4(dz[0], dz[1], dz[2], dz[3]);
