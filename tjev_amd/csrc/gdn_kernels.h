@@ -265,12 +265,6 @@ __device__ __forceinline__ void invert_unit_lower(float* sT, int LT, float* sTT)
     for (int idx = threadIdx.x; idx < 256; idx += C * 4) sT[(idx >> 4) * LT + 16 + (idx & 15)] = 0.f;
   }
 }
-// The same as a call: its addresses are then not kept live across a caller's loop (the
-// backward recompute, at its register limit, would spill)
-template <int C, int P>
-__device__ __noinline__ void invert_unit_lower_call(float* sT, int LT, float* sTT) {
-  invert_unit_lower<C, P>(sT, LT, sTT);
-}
 
 // ---------------------------------------------------------------- conv helpers
 // Per-lag conv weights of 8 channels: wl[L] multiplies token t-L (w[K-1-L]), zero past the taps.
@@ -803,11 +797,12 @@ __device__ __forceinline__ void load_tile(float* s, int LD, const float* g) {
 // ---------------------------------------------------------------- k_chunk
 // Persistent over the (row, head, chunk) units as k_out; C/16 waves (one 16-row strip each).
 // MODE 0 (forward): writes w and u; MODE 2: also T (kept as a residual). MODE 1 (backward
-// recompute): writes T and v_new = u - w S_before; MODE 3: v_new from the saved T (no L, no
-// inverse). LDS: T in fp32 (the inverse runs in place), one operand region reused for k,
-// kbe^T, (v beta)^T and S^T (and T^T during the inverse). The next unit's context and
-// k rows are loaded at this unit's start and end; k (again), v and S of this unit after the
-// inverse, a product ahead of their use.
+// recompute): writes T and v_new = u - w S_before, computed as T (v beta - kbe S_before) (one
+// state-path product and one with T instead of w, u and w S); MODE 3: v_new from the saved T
+// (no L, no inverse). LDS: T in fp32 (the inverse runs in place), one operand region reused
+// for k, kbe^T, (v beta)^T, S^T and Y^T (and T^T during the inverse). The next unit's context
+// and k rows are loaded at this unit's start and end; the forward's k (again) and v after the
+// inverse, a product ahead of their use; the backward's S, k strip and v during the inverse.
 template <int C, int D, int PI, int PS, int MODE>
 __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
   constexpr bool FWD = MODE == 0 || MODE == 2;  // writes w and u (else v_new)
@@ -839,11 +834,15 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
     rc.commit(cx);
     if constexpr (!LOAD_T) kk.put_rows(ob);
     rc.fetch(A, y.b, y.h, y.n);
-    RegsT<C, D, NT> vc;  // this unit's (v beta)^T source
-    RegsT<D, D, NT> sc;  // S_before (backward)
+    RegsT<C, D, NT> vc;  // this unit's (v beta)^T source (forward)
+    RegsT<D, D, NT> sc;  // S_before, its strip of k and its v at the accumulator layout (backward)
+    StripA<D> ks;
+    AccVals<D / 16> va;
     if constexpr (LOAD_T) {
-      vc.fetch(A.vv + off, D);
       load_tile<C, C, NT>(sT, LT, tg);
+      sc.fetch(A.states + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * D * D, D);
+      ks.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D, i0);
+      va.fetch(A.vv + off, D, i0);
     }
     __syncthreads();
     derive_ctx<C, NT>(cx);
@@ -865,15 +864,48 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
           }
         }
       }
-      __syncthreads();
-      if constexpr (MODE == 1) {
-        invert_unit_lower_call<C, PI>(sT, LT, reinterpret_cast<float*>(sB));
-      } else {
-        invert_unit_lower<C, PI>(sT, LT, reinterpret_cast<float*>(sB));
+      if constexpr (!FWD) {  // in flight during the inverse
+        sc.fetch(A.states + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * D * D, D);
+        ks.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D, i0);
       }
-      // k again (not held across the inverse: register limit), then v
-      kk.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D);
-      vc.fetch(A.vv + off, D);
+      __syncthreads();
+      invert_unit_lower<C, PI>(sT, LT, reinterpret_cast<float*>(sB));
+      if constexpr (FWD) {  // k again (not held across the inverse: register limit), then v
+        kk.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D);
+        vc.fetch(A.vv + off, D);
+      } else {
+        va.fetch(A.vv + off, D, i0);
+      }
+    }
+    if constexpr (!FWD) {  // v_new = T (v beta - kbe S_before): one state-path product, one with T
+      f32x4 yv[D / 16];
+      zero(yv);
+      sc.put_cols(ob);  // S^T
+      __syncthreads();
+      ks.template product<PS>(yv, ob, 0, D / 16, -cx.bg[i0 + (lane() & 15)]);  // - kbe S
+#pragma unroll
+      for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) yv[t][rr] += va.v[t][rr] * cx.beta[i0 + acc_row(rr)];
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < D / 16; ++t)  // Y^T: B(c, j) = Y[c][j]
+        ob.put4(16 * t + acc_col(), i0 + acc_row(0), yv[t][0], yv[t][1], yv[t][2], yv[t][3]);
+      kk.fetch(A.kn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D);  // the next unit's k
+      __syncthreads();
+      f32x4 vn[D / 16];
+      zero(vn);
+      strip_mma<PI, C, D / 16>(vn, krow(sT, LT), i0, ob, 0, 0, tri_end<C>(i0));
+      if constexpr (STORE_T) {
+        for (int idx = threadIdx.x; idx < C * C; idx += NT)  // lower triangle (the rest is scratch)
+          tg[idx] = idx % C <= idx / C ? sT[(idx / C) * LT + idx % C] : 0.f;
+      }
+#pragma unroll
+      for (int t = 0; t < D / 16; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) A.vnew[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = vn[t][rr];
+      __syncthreads();  // cx, sT and the operand region are rewritten by the next unit
+      continue;
     }
     f32x4 aw[D / 16], au[D / 16];
     zero(aw);
@@ -881,13 +913,10 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
     kk.put_cols(ob, cx.bg);  // kbe^T
     __syncthreads();
     strip_mma<PI, C, D / 16>(aw, krow(sT, LT), i0, ob, 0, 0, tri_end<C>(i0));
-    if constexpr (FWD) {  // w now: its stores drain during the u product
 #pragma unroll
-      for (int t = 0; t < D / 16; ++t)
+    for (int t = 0; t < D / 16; ++t)  // w now: its stores drain during the u product
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) A.ww[off + (size_t)(i0 + acc_row(rr)) * D + 16 * t + acc_col()] = aw[t][rr];
-    }
-    if constexpr (!FWD) sc.fetch(A.states + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * D * D, D);
+      for (int rr = 0; rr < 4; ++rr) A.ww[off + (size_t)(i0 + acc_row(rr)) * D + 16 * t + acc_col()] = aw[t][rr];
     __syncthreads();
     vc.put_cols(ob, cx.beta);  // (v beta)^T
     __syncthreads();
@@ -899,28 +928,10 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
       for (int idx = threadIdx.x; idx < C * C; idx += NT)  // lower triangle (the rest is scratch)
         tg[idx] = idx % C <= idx / C ? sT[(idx / C) * LT + idx % C] : 0.f;
     }
-    if constexpr (FWD) {
 #pragma unroll
-      for (int t = 0; t < D / 16; ++t)
+    for (int t = 0; t < D / 16; ++t)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) A.uu[off + (size_t)(i0 + acc_row(rr)) * D + 16 * t + acc_col()] = au[t][rr];
-    } else {
-      __syncthreads();
-#pragma unroll
-      for (int t = 0; t < D / 16; ++t)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) lds_st(sT + (i0 + acc_row(rr)) * LT + 16 * t + acc_col(), aw[t][rr]);
-      sc.put_cols(ob);  // S^T
-      __syncthreads();
-      f32x4 ws[D / 16];
-      zero(ws);
-      strip_mma<PS, D, D / 16>(ws, krow(sT, LT), i0, ob, 0);
-#pragma unroll
-      for (int t = 0; t < D / 16; ++t)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          A.vnew[off + (i0 + acc_row(rr)) * D + 16 * t + acc_col()] = au[t][rr] - ws[t][rr];
-    }
+      for (int rr = 0; rr < 4; ++rr) A.uu[off + (size_t)(i0 + acc_row(rr)) * D + 16 * t + acc_col()] = au[t][rr];
     __syncthreads();  // cx, sT and the operand region are rewritten by the next unit
   }
 }

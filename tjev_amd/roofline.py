@@ -2,12 +2,12 @@
 HBM bytes, per kernel launch and for the whole operator, against MI355X's published peaks.
 
 Per value head and chunk (C tokens, Dk = Dv = D), counting 2*m*n*k per product as in the
-reference's cost model (pallas_tpu_v2.py:126-138) and the operator count of the build notes:
+reference's cost model (pallas_tpu_v2.py:126-138):
   forward:  6 C^2 D + C^3/3 + 6 C D^2       (k k^T, the inverse, T [v beta | kbe], q k^T,
                                              intra v_new, [w; q_read] S, k_write^T v_new)
-  backward: recompute k k^T, the inverse, T [v beta | kbe], w S_before, then the products of
-            the reverse chunk step (intra^T do, T^T(.), T^T k_write, Kt G, q_read^T do, kbe^T X,
-            the m1 / m2 products and the state-gradient products).
+  backward: recompute k k^T, the inverse, kbe S_before and T (v beta - kbe S_before), then the
+            products of the reverse chunk step (intra^T do, T^T(.), T^T k_write, Kt G, q_read^T do,
+            kbe^T X, the m1 / m2 products and the state-gradient products).
 Elementwise work (conv, gates, l2norm, exps) is not counted in FLOPs.
 """
 
@@ -56,9 +56,9 @@ def kernel_work(*, batch: int, length: int, key_heads: int, value_heads: int, di
         # q, k, v_new, S -> out
         "gdn_out": {"bytes": 2 * act_k + act_v + mats + ctx + io, "flops": units * (2 * sq + sd)},
         "gdn_prep_bwd": {"bytes": prep, "flops": 0},
-        # k, v, S (and T under tinv) -> v_new (and T under states)
+        # k, v, S (and T under tinv) -> v_new = T (v beta - kbe S) (and T under states)
         "gdn_chunk_bwd": {"bytes": act_k + 2 * act_v + mats + tinv + ctx,
-                          "flops": units * ((3 * sq + inv + sd) if residuals == "states" else (2 * sq + sd))},
+                          "flops": units * ((2 * sq + inv + sd) if residuals == "states" else (sq + sd))},
         # q, k, d out, T -> X_loc, Kt
         "gdn_bwd_local": {"bytes": 2 * act_k + io + tinv + ctx + 2 * act_v, "flops": units * 4 * sq},
         "gdn_scan_bwd": {"bytes": tok_h * D * f32 * 5 + units * D * D * f32 * 2, "flops": 0},
