@@ -21,7 +21,15 @@ namespace gdn {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-enum : int { P_F32 = 0, P_BF16X3 = 1, P_BF16 = 2 };
+enum : int { P_F32 = 0, P_BF16X3 = 1, P_BF16 = 2, P_X3_BEXACT = 3, P_X3_AEXACT = 4 };
+// P_X3_BEXACT / P_X3_AEXACT: a bf16x3 product whose B (A) operand holds bf16 values exactly (its
+// low plane is zero, e.g. a bf16 activation): the pass that multiplies by that low plane only
+// adds exact zeros and is skipped, so the result is the bf16x3 one. The other operand is split.
+template <int P> constexpr int a_prec() { return P == P_X3_BEXACT ? P_BF16X3 : P == P_X3_AEXACT ? P_BF16 : P; }
+template <int P> constexpr int b_prec() { return P == P_X3_BEXACT ? P_BF16 : P == P_X3_AEXACT ? P_BF16X3 : P; }
+// the bf16x3 product when the operands are stored as x (its tiles' precision when bf16-exact)
+template <int P, bool EXACT_B> constexpr int exact_b() { return P == P_BF16X3 && EXACT_B ? P_X3_BEXACT : P; }
+template <int P, bool EXACT_A> constexpr int exact_a() { return P == P_BF16X3 && EXACT_A ? P_X3_AEXACT : P; }
 
 __device__ __forceinline__ int lane() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave() { return threadIdx.x >> 6; }
@@ -165,11 +173,17 @@ __device__ __forceinline__ Frag<P> make_frag(const float (&x)[8]) {
 }
 
 template <int P>
-__device__ __forceinline__ void mma(f32x4& acc, const Frag<P>& a, const Frag<P>& b) {
+__device__ __forceinline__ void mma(f32x4& acc, const Frag<a_prec<P>()>& a, const Frag<b_prec<P>()>& b) {
   if constexpr (P == P_F32) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[e], b.v[e], acc, 0, 0, 0);
   } else if constexpr (P == P_BF16) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.hi, acc, 0, 0, 0);
+  } else if constexpr (P == P_X3_BEXACT) {  // as bf16x3 without the a.hi * b.lo = 0 pass
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, b.hi, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.hi, acc, 0, 0, 0);
+  } else if constexpr (P == P_X3_AEXACT) {  // as bf16x3 without the a.lo * b.hi = 0 pass
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.lo, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.hi, acc, 0, 0, 0);
   } else {  // the small cross terms first, then hi*hi
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, b.hi, acc, 0, 0, 0);
@@ -322,6 +336,10 @@ struct Op<P_BF16X3> {
     *reinterpret_cast<uint32_t*>(hi + r * ld + k) = pack2(v0, v1);
     *reinterpret_cast<uint32_t*>(lo + r * ld + k) = pack2(lo_part(v0), lo_part(v1));
   }
+  // bf16-exact values: the high plane only (the tile then feeds P_X3_BEXACT products)
+  __device__ __forceinline__ void put2_hi(int r, int k, float v0, float v1) const {
+    *reinterpret_cast<uint32_t*>(hi + r * ld + k) = pack2(v0, v1);
+  }
   __device__ __forceinline__ void put4(int r, int k, float v0, float v1, float v2, float v3) const {
     *reinterpret_cast<uint2*>(hi + r * ld + k) = make_uint2(pack2(v0, v1), pack2(v2, v3));
     *reinterpret_cast<uint2*>(lo + r * ld + k) =
@@ -372,17 +390,18 @@ __device__ __forceinline__ Frag<P> zero_frag() {
 // wave-uniform; the tiles of a partly used group (t >= tn) are computed too, and callers
 // passing tn < TN ignore them.
 template <int P, int TN, class BV>
-__device__ __forceinline__ void tile_row(f32x4 (&acc)[TN], const Frag<P>& fa, const BV& B, int j0, int kk, bool ok,
-                                         int tn) {
+__device__ __forceinline__ void tile_row(f32x4 (&acc)[TN], const Frag<a_prec<P>()>& fa, const BV& B, int j0, int kk,
+                                         bool ok, int tn) {
   constexpr int G = TN < 4 ? TN : 4;
+  constexpr int PB = b_prec<P>();
   static_assert(TN % G == 0, "tiles in whole groups");
   const int r = lane() & 15;
 #pragma unroll
   for (int g = 0; g < TN / G; ++g) {
     if (G * g < tn) {
-      Frag<P> fb[G];
+      Frag<PB> fb[G];
 #pragma unroll
-      for (int e = 0; e < G; ++e) fb[e] = ok ? B.template frag<P>(j0 + 16 * (G * g + e) + r, kk) : zero_frag<P>();
+      for (int e = 0; e < G; ++e) fb[e] = ok ? B.template frag<PB>(j0 + 16 * (G * g + e) + r, kk) : zero_frag<PB>();
 #pragma unroll
       for (int e = 0; e < G; ++e) mma<P>(acc[G * g + e], fa, fb[e]);
     }
@@ -401,7 +420,8 @@ __device__ __forceinline__ void strip_mma(f32x4 (&acc)[TN], const AV& A, int i0,
   const int kg = (l >> 4) << 3;
   for (int k = kb; k < ke; k += 32) {
     const bool ok = (K % 32 == 0) || (k + kg < K);
-    const Frag<P> fa = ok ? A.template frag<P>(i0 + r, k + kg) : zero_frag<P>();
+    constexpr int PA = a_prec<P>();
+    const Frag<PA> fa = ok ? A.template frag<PA>(i0 + r, k + kg) : zero_frag<PA>();
     tile_row<P, TN>(acc, fa, B, j0, k + kg, ok, tn);
   }
 }

@@ -626,7 +626,8 @@ struct RegsIO {
       }
     }
   }
-  template <int P>
+  // HI_ONLY (bf16 values into a bf16x3 tile): the high plane only, for P_X3_BEXACT products
+  template <int P, bool HI_ONLY = false>
   __device__ __forceinline__ void put_cols(const Op<P>& op) const {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
@@ -641,16 +642,16 @@ struct RegsIO {
       rotate(x0, rot, z0);
       rotate(x1, rot, z1);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) op.put2(c + ((e + rot) & 7), 2 * j, v0 ? z0[e] : 0.f, v1 ? z1[e] : 0.f);
+      for (int e = 0; e < 8; ++e) {
+        if constexpr (HI_ONLY) {
+          op.put2_hi(c + ((e + rot) & 7), 2 * j, v0 ? z0[e] : 0.f, v1 ? z1[e] : 0.f);
+        } else {
+          op.put2(c + ((e + rot) & 7), 2 * j, v0 ? z0[e] : 0.f, v1 ? z1[e] : 0.f);
+        }
+      }
     }
   }
 };
-template <int R, int K, int NT, int P, class T>
-__device__ __forceinline__ void stage_cols_io(const Op<P>& op, const T* g, int ldg, int rows) {
-  RegsIO<R, K, NT, T> t;
-  t.fetch(g, ldg, rows);
-  t.put_cols(op);
-}
 
 // The gates of one thread's row pair (2j, 2j+1) of a chunk -- the rows the thread stages in
 // RegsT (RegsT::pair()) -- and of the chunk's last token,
@@ -722,7 +723,7 @@ struct StripA {
       float xs[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) xs[e] = x[s][e] * rs;
-      const Frag<P> fa = make_frag<P>(xs);
+      const Frag<a_prec<P>()> fa = make_frag<a_prec<P>()>(xs);
       tile_row<P, TN>(acc, fa, B, j0, 32 * s + kg, ok, tn);
     }
   }
@@ -762,7 +763,7 @@ struct StripIO {
       x[s].get(xs);
 #pragma unroll
       for (int e = 0; e < 8; ++e) xs[e] = ok ? xs[e] * f : 0.f;
-      const Frag<P> fa = make_frag<P>(xs);
+      const Frag<a_prec<P>()> fa = make_frag<a_prec<P>()>(xs);
       tile_row<P, TN>(acc, fa, B, j0, 32 * s + kg, ok, tn);
     }
   }
@@ -1320,11 +1321,12 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
       }
     }
     __syncthreads();
-    in.dov.put_cols(ob);
+    constexpr int PDO = exact_b<PI, sizeof(TIO) == 2>();  // do is bf16-exact for bf16 I/O
+    in.dov.template put_cols<PI, PDO == P_X3_BEXACT>(ob);
     __syncthreads();
     f32x4 acc[D / 16];
     zero(acc);
-    strip_mma<PI, C, D / 16>(acc, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // dv_loc = intra^T do
+    strip_mma<PDO, C, D / 16>(acc, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // dv_loc = intra^T do
     in.fetch_t(A, x);
     __syncthreads();
     in.tt.put_lds(sA, LA);
@@ -1444,7 +1446,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
     if (lane() == 0) red[w] = part;
     const float carry = in.gt.carry();
     const float kb0 = -in.gt.bg(0), kb1 = -in.gt.bg(1);
-    in.dov.put_cols(odo);
+    in.dov.template put_cols<PI, exact_b<PI, sizeof(TIO) == 2>() == P_X3_BEXACT>(odo);  // do^T
     in.fetch_do(A, b, h, nx, j0);
     in.qk.put_cols2(oq, in.gt.grow(0), in.gt.grow(1));
     in.qk.fetch(A.kn + hoff(A, b, hk, A.Hk, n, C, D), D);
@@ -1476,7 +1478,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
     if (NW == D / 16 || w < D / 16) {  // G = carry G + q_read^T do
 #pragma unroll
       for (int t = 0; t < DVT / 16; ++t) accG[t] *= carry;
-      strip_mma<PI, C, DVT / 16>(accG, oq, 16 * w, odo, 0);
+      strip_mma<exact_b<PI, sizeof(TIO) == 2>(), C, DVT / 16>(accG, oq, 16 * w, odo, 0);  // do: bf16 exact
     }
     __syncthreads();
     in.qk.put_cols2(oq, kb0, kb1);
@@ -1553,7 +1555,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
       }
     }
     zero(m2);
-    dos.template product<PI>(m2, ob, 0, w + 1);
+    dos.template product<exact_a<PI, sizeof(TIO) == 2>()>(m2, ob, 0, w + 1);  // do: bf16 exact
 #pragma unroll
     for (int t = 0; t < C / 16; ++t) {
       float d[4];
