@@ -22,6 +22,7 @@ CASES = [
     ((1, 120, 2, 4), 16, [16, 33, 50, 67, 95], {}),
     ((1, 120, 2, 2), 16, [16, 33, 50, 67, 95], {}),
     ((1, 1100, 2, 4), 64, [510, 513, 1024, 1027], {}),
+    ((1, 150, 2, 4), 32, [31, 64, 65, 98], {}),  # one doubling level (the level-16 product cleared at the end)
     ((2, 200, 2, 4), 64, None, {"inverse": "blocked"}),
     ((1, 256, 2, 4), 128, None, {"inverse": "blocked"}),
     ((1, 200, 4, 8), 64, None, {"heads_per_step": 4}),
