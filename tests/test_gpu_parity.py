@@ -52,6 +52,22 @@ def test_hip_matches_oracle_fp32(case, conv):
         assert err < TOL[name], (name, errors)
 
 
+@pytest.mark.parametrize("taps", [1, 2, 5])
+def test_hip_conv_widths_fp32(taps):
+    """Conv kernels of 1, 2 and 5 taps (the model's is 4): the halo and look-ahead rows are sized
+    to taps - 1, with segment cuts right after a chunk start and before a chunk end."""
+    d, hk, h = 16, 2, 4
+    inputs, cot = case_inputs(1, 150, hk, h, d, cuts=[31, 64, 65, 98], taps=taps)
+    shape = dict(key_heads=hk, key_dim=d, value_heads=h, value_dim=d, conv=True)
+    print(f"taps {taps}", flush=True)
+    got = hip_outputs(inputs, cot, chunk=32, precision="highest", **shape)
+    want = oracle_outputs(inputs, cot, **shape)
+    errors = {k: rel(got[k], want[k]) for k in got}
+    assert all(bool(torch.isfinite(v).all()) for v in got.values())
+    for name, err in errors.items():
+        assert err < TOL[name], (name, errors)
+
+
 def test_hip_tiny_config_fp32():
     """BASELINE config 1 (B=1, T=512, Hk=H=4, D=64, chunk 64, fp32 "highest", one segment).
     Output and per-token gradients: max relative error <= 1e-5 against the fp32 reference path;

@@ -335,7 +335,7 @@ __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
   // before them (the conv halo) and their segment ids at once, at clamped addresses without
   // branches; the conv then slides over registers (every raw row is read once).
   constexpr int RG = C / RPP > 0 ? C / RPP : 1;
-  constexpr int HW = 4;  // taps - 1 <= 4
+  constexpr int HW = 4;  // taps - 1 <= 4 (a halo of 3 for taps <= 4 measured slower here)
   const int r0 = (threadIdx.x / CG) * RG;
   if (RG * RPP == C || r0 < C) {
     Raw8<TIO> raw[RG + HW];
@@ -1647,8 +1647,9 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
 // segment masks (pallas_tpu_mega.py:161-179, 306-319) -- and, for the value heads, the gate
 // backward (pallas_tpu_mega.py:129-145): dg = reverse in-chunk cumsum of d gamma, and d beta
 // completed with rows(X, v) from the rebuilt v.
-template <int C, int D, class TIO, class TG>
+template <int C, int D, class TIO, class TG, int HW>
 __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
+  static_assert(HW == 3 || HW == 4, "the conv halo: taps - 1 rows (launched with HW >= taps - 1)");
   constexpr int CG = D / 8;
   constexpr int RPP = 256 / CG;
   constexpr int R = C + 4;  // the chunk's rows and 4 look-ahead rows (taps <= 5)
@@ -1675,7 +1676,6 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
   // phase 1: dz for the chunk and the look-ahead rows, into LDS. Each group of CG lanes owns
   // RG consecutive rows: their raw rows with the conv halo, segment ids and incoming gradients
   // are all loaded first (clamped addresses, no branches), then computed from registers.
-  constexpr int HW = 4;  // taps - 1 <= 4
   constexpr int RG = (R + RPP - 1) / RPP;
   const int r0 = (threadIdx.x / CG) * RG;
   Raw8<TIO> raw[RG + HW];
@@ -1774,9 +1774,10 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
   }
   __syncthreads();
   // phase 2: the anti-causal conv, dx[t] = sum over lags of w[K-1-L] keep_L[t+L] dz[t+L]
-  float dwa[5][8];
+  constexpr int NL = HW + 1;  // lags 0 .. taps - 1
+  float dwa[NL][8];
 #pragma unroll
-  for (int L = 0; L < 5; ++L)
+  for (int L = 0; L < NL; ++L)
 #pragma unroll
     for (int e = 0; e < 8; ++e) dwa[L][e] = 0.f;
   const bool want_dw = A.d_conv_w && taps > 0;
@@ -1796,7 +1797,7 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = dz[e] * wl[0][e];
 #pragma unroll
-      for (int L = 1; L < 5; ++L) {
+      for (int L = 1; L < NL; ++L) {
         if (L < taps && sseg[r + L] == st) {
           const float* dl = sdz + (r + L) * LZ + cg * 8;
 #pragma unroll
@@ -1808,7 +1809,7 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
         bool keep[5];
         conv_rows(A, x, sp, b, t, cc, st, xs, keep);
 #pragma unroll
-        for (int L = 0; L < 5; ++L)
+        for (int L = 0; L < NL; ++L)
           if (keep[L]) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) dwa[L][e] += dz[e] * xs[L][e];
@@ -1835,14 +1836,14 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
     __syncthreads();
     float* sdw = sdz;  // [thread][lag][8]
 #pragma unroll
-    for (int L = 0; L < 5; ++L)
+    for (int L = 0; L < NL; ++L)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sdw[(threadIdx.x * 5 + L) * 8 + e] = dwa[L][e];
+      for (int e = 0; e < 8; ++e) sdw[(threadIdx.x * NL + L) * 8 + e] = dwa[L][e];
     __syncthreads();
     for (int idx = threadIdx.x; idx < taps * D; idx += 256) {
       const int L = idx / D, c = idx % D, g = c / 8, e = c % 8;
       float s = 0.f;
-      for (int q = 0; q < RPP; ++q) s += sdw[((q * CG + g) * 5 + L) * 8 + e];
+      for (int q = 0; q < RPP; ++q) s += sdw[((q * CG + g) * NL + L) * 8 + e];
       A.dwp[(((size_t)b * A.N + n) * taps + (taps - 1 - L)) * A.W + c0 + c] = s;
     }
   }
