@@ -68,6 +68,23 @@ def test_hip_conv_widths_fp32(taps):
         assert err < TOL[name], (name, errors)
 
 
+@pytest.mark.parametrize("d,chunk", [(16, 32), (16, 128), (64, 64)])
+def test_hip_frozen_conv_weight_fp32(d, chunk):
+    """The conv weight not differentiated (pallas_tpu_mega.py:548-571 emits no dz then), as in
+    the benchmark's step: the backward's own conv path without the d(conv w) partials."""
+    hk, h = 2, 4
+    inputs, cot = case_inputs(1, 300, hk, h, d, cuts=[chunk - 1, chunk + 1, 2 * chunk + 2])
+    shape = dict(key_heads=hk, key_dim=d, value_heads=h, value_dim=d, conv=True)
+    print(f"frozen conv d={d} chunk={chunk}", flush=True)
+    got = hip_outputs(inputs, cot, chunk=chunk, precision="highest", want_w=False, **shape)
+    want = oracle_outputs(inputs, cot, **shape)
+    assert "w" not in got
+    errors = {k: rel(got[k], want[k]) for k in got}
+    assert all(bool(torch.isfinite(v).all()) for v in got.values())
+    for name, err in errors.items():
+        assert err < TOL[name], (name, errors)
+
+
 def test_hip_tiny_config_fp32():
     """BASELINE config 1 (B=1, T=512, Hk=H=4, D=64, chunk 64, fp32 "highest", one segment).
     Output and per-token gradients: max relative error <= 1e-5 against the fp32 reference path;

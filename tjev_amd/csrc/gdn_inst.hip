@@ -74,9 +74,16 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
     GDN_LAUNCH(K_BWD_LOCAL, (k_bwd_local<C, D, PI, TIO>), persist, dim3(C * 4));
     GDN_LAUNCH(K_SCAN_BWD, (k_scan_bwd<C, D, DVT, PI, PS, TIO>), tiles, dim3(NS));
     GDN_LAUNCH(K_BWD_GRADS, (k_bwd_grads<C, D, PI, PS, TIO>), chunks, dim3(C * 4));
-    // the conv halo sized to the taps (taps - 1 <= 3 for the model's conv of 4)
-    if (A.taps <= 4) GDN_LAUNCH(K_POST, (k_post<C, D, TIO, TG, 3>), prep, dim3(256));
-    else GDN_LAUNCH(K_POST, (k_post<C, D, TIO, TG, 4>), prep, dim3(256));
+    // the conv halo sized to the taps (taps - 1 <= 3 for the model's conv of 4); d(conv w)
+    // accumulated only when it is wanted
+    const bool dw = A.d_conv_w && A.taps > 0;
+    if (A.taps <= 4) {
+      if (dw) GDN_LAUNCH(K_POST, (k_post<C, D, TIO, TG, 3, true>), prep, dim3(256));
+      else GDN_LAUNCH(K_POST, (k_post<C, D, TIO, TG, 3, false>), prep, dim3(256));
+    } else {
+      if (dw) GDN_LAUNCH(K_POST, (k_post<C, D, TIO, TG, 4, true>), prep, dim3(256));
+      else GDN_LAUNCH(K_POST, (k_post<C, D, TIO, TG, 4, false>), prep, dim3(256));
+    }
     GDN_LAUNCH(K_REDUCE, (k_reduce<C>), dim3(A.H + (wouts + 255) / 256), dim3(256));
   }
 #undef GDN_LAUNCH

@@ -1646,21 +1646,24 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
 // l2norm backward (pallas_tpu_mega.py:101-103), SiLU and the anti-causal conv backward with
 // segment masks (pallas_tpu_mega.py:161-179, 306-319) -- and, for the value heads, the gate
 // backward (pallas_tpu_mega.py:129-145): dg = reverse in-chunk cumsum of d gamma, and d beta
-// completed with rows(X, v) from the rebuilt v.
-template <int C, int D, class TIO, class TG, int HW>
-__global__ __launch_bounds__(256) void k_post(GdnArgs A) {
+// completed with rows(X, v) from the rebuilt v. DW: also this chunk's partial of d(conv w)
+// (pallas_tpu_mega.py:527-535), launched only when it is wanted.
+template <int C, int D, class TIO, class TG, int HW, bool DW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_post(GdnArgs A) {
   static_assert(HW == 3 || HW == 4, "the conv halo: taps - 1 rows (launched with HW >= taps - 1)");
   constexpr int CG = D / 8;
-  constexpr int RPP = 256 / CG;
-  constexpr int R = C + 4;  // the chunk's rows and 4 look-ahead rows (taps <= 5)
+  constexpr int NG = 256 / CG;                  // row groups of CG lanes
+  constexpr int RG = (C + HW + NG - 1) / NG;    // consecutive rows per group: the chunk's, then HW look-ahead rows
+  constexpr int HS = RG < HW ? RG : HW;         // a group's first rows, read by the groups before it
   constexpr int LZ = D + 4;
-  constexpr int SZ = R * LZ > 256 * 5 * 8 ? R * LZ : 256 * 5 * 8;  // also the d(conv w) scratch
-  __shared__ float sdz[SZ];
-  __shared__ int sseg[R];
-  __shared__ float sxv[C];  // value heads: rows(X, v) of the chunk's tokens
+  constexpr int NL = HW + 1;                    // lags 0 .. taps - 1
+  __shared__ float shd[NG * HS * LZ];           // dz of each group's first HS rows
+  __shared__ int shs[NG * HS];                  // and their segment ids
+  __shared__ float sxv[C];                      // value heads: rows(X, v) of the chunk's tokens
+  __shared__ float sdw[DW ? 4 * NL * D : 1];    // per-wave sums of d(conv w)
   const int b = blockIdx.x / A.N, n = blockIdx.x % A.N;
   const int slot = blockIdx.y;
-  const int cg = threadIdx.x % CG;
+  const int cg = threadIdx.x % CG, grp = threadIdx.x / CG;
   int kind, head, c0;
   if (slot < A.Hk) { kind = 0; head = slot; c0 = slot * D; }
   else if (slot < 2 * A.Hk) { kind = 1; head = slot - A.Hk; c0 = A.Hk * D + head * D; }
@@ -1670,14 +1673,33 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
   const TIO* x = reinterpret_cast<const TIO*>(A.qkv);
   TIO* dx = reinterpret_cast<TIO*>(A.d_qkv);
   const int32_t* sp = A.segp + (size_t)b * A.Tp;
+  // the gate backward's inputs (value heads, wave 0), fetched first so that they arrive
+  // during the chunk's rows
+  constexpr int E = (C + 63) / 64;
+  const bool gate_wave = kind == 2 && threadIdx.x < 64;
+  const size_t tok = (size_t)(b * A.H + head) * A.Tp + (size_t)n * C;
+  float gdg[E], gdb[E], gav[E], gbv[E];
+  if (gate_wave) {
+    const TG* ga = reinterpret_cast<const TG*>(A.ga);
+    const TG* gb = reinterpret_cast<const TG*>(A.gb);
+#pragma unroll
+    for (int q = 0; q < E; ++q) {
+      const int i = threadIdx.x * E + q, t = n * C + i;
+      const int ic = i < C ? i : C - 1, tc = t < A.T ? t : A.T - 1;
+      gdg[q] = A.dgam[tok + ic];
+      gdb[q] = A.dbet[tok + ic];
+      gav[q] = ldf(ga + ((size_t)b * A.T + tc) * A.H + head);
+      gbv[q] = ldf(gb + ((size_t)b * A.T + tc) * A.H + head);
+    }
+  }
   float wl[5][8];
   lag_weights(A, cc, wl);
   const int rows = C + (taps > 1 ? taps - 1 : 0);
-  // phase 1: dz for the chunk and the look-ahead rows, into LDS. Each group of CG lanes owns
-  // RG consecutive rows: their raw rows with the conv halo, segment ids and incoming gradients
-  // are all loaded first (clamped addresses, no branches), then computed from registers.
-  constexpr int RG = (R + RPP - 1) / RPP;
-  const int r0 = (threadIdx.x / CG) * RG;
+  // Each group owns RG consecutive rows: their raw rows with the conv halo, segment ids and
+  // incoming gradients are all loaded first (clamped addresses, no branches), then dz row by
+  // row from registers; dx of a row follows as soon as dz of its HW look-ahead rows is there,
+  // and the last HW rows take the next groups' first rows from LDS after one barrier.
+  const int r0 = grp * RG;
   Raw8<TIO> raw[RG + HW];
   int sgv[RG + HW];
 #pragma unroll
@@ -1706,10 +1728,43 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
       btv[i] = A.bet[(size_t)(b * A.H + head) * A.Tp + tl];
     }
   }
+  float dzr[RG][8];
+  int str[RG];
+  // dx of own row j (rows < C of real tokens): the anti-causal conv,
+  // dx[t] = sum over lags of w[K-1-L] keep_L[t+L] dz[t+L]; `ext` rows come from LDS
+  auto emit = [&](int j, bool ext) {
+    const int r = r0 + j, t = n * C + r;
+    if (r >= C || t >= A.T) return;
+    float o[8];
+    if (taps == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = dzr[j][e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = dzr[j][e] * wl[0][e];
+#pragma unroll
+      for (int L = 1; L <= HW; ++L) {
+        if (j + L < RG) {
+          if (L < taps && str[j + L] == str[j]) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] += wl[L][e] * dzr[j + L][e];
+          }
+        } else if (ext) {  // row r + L: the first rows of group grp + (j + L) / RG (r + L < C + HW)
+          const int k = (grp + (j + L) / RG) * HS + (j + L) % RG;
+          if (L < taps && shs[k] == str[j]) {
+            const float4* q = reinterpret_cast<const float4*>(shd + k * LZ + cg * 8);
+            const float4 p0 = q[0], p1 = q[1];
+            o[0] += wl[L][0] * p0.x; o[1] += wl[L][1] * p0.y; o[2] += wl[L][2] * p0.z; o[3] += wl[L][3] * p0.w;
+            o[4] += wl[L][4] * p1.x; o[5] += wl[L][5] * p1.y; o[6] += wl[L][6] * p1.z; o[7] += wl[L][7] * p1.w;
+          }
+        }
+      }
+    }
+    st8_io(dx + ((size_t)b * A.T + t) * A.W + cc, o);
+  };
 #pragma unroll
   for (int i = 0; i < RG; ++i) {
     const int r = r0 + i, t = n * C + r;
-    if (r >= R) break;
     const bool live = r < rows && t < A.Tp;  // uniform over the CG lanes of the row
     const int st = live ? sgv[HW + i] : -3;
     float z[8], sg[8], act[8], dy[8];
@@ -1759,109 +1814,80 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
       xv = sum_lanes<CG>(xv);
       if (cg == 0 && r < C) sxv[r] = xv;
     }
-    float dz[8];
     if (taps == 0) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dz[e] = live ? dy[e] : 0.f;
+      for (int e = 0; e < 8; ++e) dzr[i][e] = live ? dy[e] : 0.f;
     } else {  // SiLU backward on valid tokens
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dz[e] = (live && st > 0) ? dy[e] * sg[e] * (1.f + z[e] * (1.f - sg[e])) : 0.f;
+      for (int e = 0; e < 8; ++e) dzr[i][e] = (live && st > 0) ? dy[e] * sg[e] * (1.f + z[e] * (1.f - sg[e])) : 0.f;
     }
-    float4* o = reinterpret_cast<float4*>(sdz + r * LZ + cg * 8);
-    o[0] = make_float4(dz[0], dz[1], dz[2], dz[3]);
-    o[1] = make_float4(dz[4], dz[5], dz[6], dz[7]);
-    if (cg == 0) sseg[r] = st;
+    str[i] = st;
+    if (i < HS) {
+      float4* o = reinterpret_cast<float4*>(shd + (grp * HS + i) * LZ + cg * 8);
+      o[0] = make_float4(dzr[i][0], dzr[i][1], dzr[i][2], dzr[i][3]);
+      o[1] = make_float4(dzr[i][4], dzr[i][5], dzr[i][6], dzr[i][7]);
+      if (cg == 0) shs[grp * HS + i] = st;
+    }
+    if (i >= HW) emit(i - HW, false);
   }
   __syncthreads();
-  // phase 2: the anti-causal conv, dx[t] = sum over lags of w[K-1-L] keep_L[t+L] dz[t+L]
-  constexpr int NL = HW + 1;  // lags 0 .. taps - 1
-  float dwa[NL][8];
 #pragma unroll
-  for (int L = 0; L < NL; ++L)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) dwa[L][e] = 0.f;
-  const bool want_dw = A.d_conv_w && taps > 0;
-#pragma unroll 2
-  for (int r = threadIdx.x / CG; r < C; r += RPP) {
-    const int t = n * C + r;
-    const int st = sseg[r];
-    float o[8], dz[8];
-    const float4* d0 = reinterpret_cast<const float4*>(sdz + r * LZ + cg * 8);
-    const float4 p0 = d0[0], p1 = d0[1];
-    dz[0] = p0.x; dz[1] = p0.y; dz[2] = p0.z; dz[3] = p0.w;
-    dz[4] = p1.x; dz[5] = p1.y; dz[6] = p1.z; dz[7] = p1.w;
-    if (taps == 0) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = dz[e];
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = dz[e] * wl[0][e];
-#pragma unroll
-      for (int L = 1; L < NL; ++L) {
-        if (L < taps && sseg[r + L] == st) {
-          const float* dl = sdz + (r + L) * LZ + cg * 8;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[e] += wl[L][e] * dl[e];
-        }
-      }
-      if (want_dw) {  // d w[K-1-L] += keep_L[t] dz[t] x[t-L]
-        float xs[5][8];
-        bool keep[5];
-        conv_rows(A, x, sp, b, t, cc, st, xs, keep);
-#pragma unroll
-        for (int L = 0; L < NL; ++L)
-          if (keep[L]) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) dwa[L][e] += dz[e] * xs[L][e];
-          }
-      }
-    }
-    if (t < A.T) {
-      TIO* dst = dx + ((size_t)b * A.T + t) * A.W + cc;
-      if constexpr (sizeof(TIO) == 2) {
-        uint4 pk;
-        pk.x = (uint32_t)f2bf(o[0]) | ((uint32_t)f2bf(o[1]) << 16);
-        pk.y = (uint32_t)f2bf(o[2]) | ((uint32_t)f2bf(o[3]) << 16);
-        pk.z = (uint32_t)f2bf(o[4]) | ((uint32_t)f2bf(o[5]) << 16);
-        pk.w = (uint32_t)f2bf(o[6]) | ((uint32_t)f2bf(o[7]) << 16);
-        *reinterpret_cast<uint4*>(dst) = pk;
-      } else {
-        float4* q = reinterpret_cast<float4*>(dst);
-        q[0] = make_float4(o[0], o[1], o[2], o[3]);
-        q[1] = make_float4(o[4], o[5], o[6], o[7]);
-      }
-    }
-  }
-  if (want_dw) {  // per-workgroup partial of d(conv weight), fixed sum order
-    __syncthreads();
-    float* sdw = sdz;  // [thread][lag][8]
+  for (int j = (RG > HW ? RG - HW : 0); j < RG; ++j) emit(j, true);
+  if constexpr (DW) {
+    // d w[K-1-L] += keep_L[t] dz[t] x[t-L] over the group's rows of the chunk, from its raw rows
+    // loaded again (cache hits) once the prefetched gradients are spent
+    float dwa[NL][8];
 #pragma unroll
     for (int L = 0; L < NL; ++L)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sdw[(threadIdx.x * NL + L) * 8 + e] = dwa[L][e];
+      for (int e = 0; e < 8; ++e) dwa[L][e] = 0.f;
+#pragma unroll
+    for (int i = 0; i < RG + HW; ++i) {
+      const int tt = n * C + r0 - HW + i;
+      raw[i].load(x + ((size_t)b * A.T + (tt < 0 ? 0 : (tt < A.T ? tt : A.T - 1))) * A.W + cc);
+    }
+#pragma unroll
+    for (int i = 0; i < RG; ++i) {
+      const int r = r0 + i, t = n * C + r;
+#pragma unroll
+      for (int L = 0; L < NL; ++L) {
+        const bool keep = r < C && L < taps && t - L >= 0 && (L == 0 || sgv[HW + i - L] == str[i]);
+        float xl[8];
+        raw[HW + i - L].get(xl);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dwa[L][e] = keep ? dwa[L][e] + dzr[i][e] * xl[e] : dwa[L][e];
+      }
+    }
+    // this chunk's partial: the wave's groups summed by shuffles, then the waves, fixed order
+#pragma unroll
+    for (int L = 0; L < NL; ++L)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float v = dwa[L][e];
+#pragma unroll
+        for (int m = CG; m < 64; m <<= 1) v += __shfl_xor(v, m);
+        if (lane() < CG) sdw[(wave() * NL + L) * D + cg * 8 + e] = v;
+      }
     __syncthreads();
     for (int idx = threadIdx.x; idx < taps * D; idx += 256) {
-      const int L = idx / D, c = idx % D, g = c / 8, e = c % 8;
+      const int L = idx / D, c = idx % D;
       float s = 0.f;
-      for (int q = 0; q < RPP; ++q) s += sdw[((q * CG + g) * NL + L) * 8 + e];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) s += sdw[(w * NL + L) * D + c];
       A.dwp[(((size_t)b * A.N + n) * taps + (taps - 1 - L)) * A.W + c0 + c] = s;
     }
   }
-  if (kind == 2 && threadIdx.x < 64) {  // gate backward of value head `head`
-    constexpr int E = (C + 63) / 64;
+  if (gate_wave) {  // gate backward of value head `head`
     const int l = threadIdx.x;
-    const TG* ga = reinterpret_cast<const TG*>(A.ga);
-    const TG* gb = reinterpret_cast<const TG*>(A.gb);
     TG* da = reinterpret_cast<TG*>(A.d_a);
     TG* db = reinterpret_cast<TG*>(A.d_b);
     const float ea = expf(A.a_log[head]), dtb = A.dt_bias[head];
-    const size_t tok = (size_t)(b * A.H + head) * A.Tp + (size_t)n * C;
     // dg = reverse in-chunk cumsum of d gamma, and the A_log / dt_bias partial sums, in fp64
     double dgv[E], run = 0.0;
 #pragma unroll
     for (int q = E - 1; q >= 0; --q) {
       const int i = l * E + q;
-      run += i < C ? (double)A.dgam[tok + i] : 0.0;
+      run += i < C ? (double)gdg[q] : 0.0;
       dgv[q] = run;  // inclusive suffix within the lane
     }
     double inc = run;  // inclusive suffix scan of lane totals
@@ -1877,15 +1903,15 @@ __global__ __launch_bounds__(256) void k_post(GdnArgs A) {
       const int i = l * E + q, t = n * C + i;
       if (i < C) {
         const bool in = t < A.T;
-        const float av = in ? ldf(ga + ((size_t)b * A.T + t) * A.H + head) : 0.f;
-        const float bv = in ? ldf(gb + ((size_t)b * A.T + t) * A.H + head) : 0.f;
+        const float av = in ? gav[q] : 0.f;
+        const float bv = in ? gbv[q] : 0.f;
         const double dg = excl + dgv[q];
         const float xg = av + dtb;
         const float g = -ea * softplusf_(xg);
         const double dad = dg * (double)(-ea * sigmoidf_(xg));
         const float dav = (float)dad;
         const float bt = sigmoidf_(bv);
-        const float dbv = (A.dbet[tok + i] + sxv[i]) * bt * (1.f - bt);
+        const float dbv = (gdb[q] + sxv[i]) * bt * (1.f - bt);
         sa += dg * (double)g;
         sd += dad;
         if (in) {
