@@ -769,6 +769,45 @@ struct StripIO {
   }
 };
 
+// One wave's 16 columns [c0, c0 + 16) of a C x D fp32 row tile, staged transposed into the
+// wave's own rows c0 .. c0 + 15 of an A(i = column, k = row) operand: lane l holds the row
+// pairs (2j, 2j + 1), j = l/4 + 16 it, at columns c0 + 4 (l % 4) .. + 3 (a load covers 16 rows
+// of 64 bytes; a write's 64 lanes fall in distinct banks of the bf16 planes). No other wave
+// reads those operand rows, so staging and use need no workgroup barrier.
+template <int C>
+struct StripT {
+  static constexpr int RP = C / 2;
+  static constexpr int U = (RP * 4 + 63) / 64;
+  float4 a[U], b[U];
+  __device__ __forceinline__ static int pair(int it) { return ((lane() >> 2) + 16 * it) % RP; }
+  __device__ __forceinline__ static bool live(int it) { return RP * 4 >= 64 * (it + 1) || (lane() >> 2) + 16 * it < RP; }
+  // every lane loads (lanes past the tile repeat a pair inside it): no branch around the loads
+  __device__ __forceinline__ void fetch(const float* g, int ld, int c0) {
+    const int col = c0 + 4 * (lane() & 3);
+#pragma unroll
+    for (int it = 0; it < U; ++it) {
+      const int j = pair(it);
+      a[it] = *reinterpret_cast<const float4*>(g + (size_t)(2 * j) * ld + col);
+      b[it] = *reinterpret_cast<const float4*>(g + (size_t)(2 * j + 1) * ld + col);
+    }
+  }
+  // op(c0 + e, r) = g[r][c0 + e] * sc[r] for the held rows r
+  template <int P>
+  __device__ __forceinline__ void put(const Op<P>& op, int c0, const float* sc) const {
+    const int col = c0 + 4 * (lane() & 3);
+#pragma unroll
+    for (int it = 0; it < U; ++it) {
+      if (!live(it)) continue;
+      const int j = pair(it);
+      const float fa = sc[2 * j], fb = sc[2 * j + 1];
+      const float xa[4] = {a[it].x, a[it].y, a[it].z, a[it].w};
+      const float xb[4] = {b[it].x, b[it].y, b[it].z, b[it].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) op.put2(col + e, 2 * j, xa[e] * fa, xb[e] * fb);
+    }
+  }
+};
+
 // The fp32 values of a 16-row strip at the accumulator layout of TN 16-column tiles:
 // v[t][rr] = g[(i0 + acc_row(rr)) * ld + 16t + acc_col()].
 template <int TN>
@@ -1359,11 +1398,11 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
 // previous chunk's values once used.
 template <int C, int D, int DVT, int NT, class TIO>
 struct ScanBwdIn {
-  PairGates<C> gt;                // grow and beta grow of the thread's rows, and the carry
+  PairGates<C> gt;                // wave 0: grow and beta grow of the lane's row pair, and the carry
   AccVals<DVT / 16> snext;        // S after the chunk, at G's accumulator layout (waves < D/16)
   RegsIO<C, DVT, NT, TIO> dov;    // do columns of the tile, staged as do^T
-  RegsT<C, D, NT, false> qk;      // q rows, staged as (q grow)^T; then k rows, as (-k beta grow)^T
-                                  // (no write rotation: this kernel is at its register limit)
+  StripT<C> qk;                   // the wave's 16 columns of q, staged as (q grow)^T; then of k,
+                                  // as (-k beta grow)^T (waves < D/16)
   StripA<D> kt;                   // Kt rows of this wave's strip (waves < C/16)
   AccVals<DVT / 16> xl;           // X_loc at the strip's accumulator layout
   // Loads without branches (a fixed count of memory operations per wave): waves past the
@@ -1383,6 +1422,19 @@ struct ScanBwdIn {
   __device__ __forceinline__ void fetch_xl(const GdnArgs& A, int b, int h, int n, int j0) {
     xl.fetch(A.xl + hoff(A, b, h, A.H, n, C, D) + j0, D, 16 * (wave() % (C / 16)));
   }
+  __device__ __forceinline__ void fetch_qk(const float* g) { qk.fetch(g, D, 16 * (wave() % (D / 16))); }
+  // wave 0: the row scales of the chunk whose gates it holds, into sc[0] (grow), sc[1]
+  // (-beta grow) and the carry into sc[2][0]
+  __device__ __forceinline__ void put_gates(float (*sc)[C]) const {
+    const int j = lane();
+    if (j < C / 2) {
+      sc[0][2 * j] = gt.grow(0);
+      sc[0][2 * j + 1] = gt.grow(1);
+      sc[1][2 * j] = -gt.bg(0);
+      sc[1][2 * j + 1] = -gt.bg(1);
+    }
+    if (j == 0) sc[2][0] = gt.carry();
+  }
 };
 
 template <int C, int D, int DVT, int PI, int PS, class TIO>
@@ -1398,6 +1450,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
   __shared__ __align__(16) char sX[TD::BYTES];
   __shared__ float red[NW];
   __shared__ int red_i[NW];
+  __shared__ float sgate[2][3][C];  // per chunk parity: grow, -beta grow, the carry (written by wave 0)
   const Op<PI> og = TG_::at(sG), oq = TQ::at(sQ), odo = TD::at(sDo), ox = TD::at(sX);
   const ScanIx ix(A);
   const int tile = ix.tile, bh = ix.bh, part = ix.part;
@@ -1416,13 +1469,20 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
   ScanBwdIn<C, D, DVT, NT, TIO> in;
   {
     const int n = ne;
-    in.gt.fetch(A, b, h, n, RegsT<C, D, NT>::pair());
+    if (w == 0) {
+      in.gt.fetch(A, b, h, n, lane() % (C / 2));
+      in.put_gates(sgate[n & 1]);
+      in.gt.fetch(A, b, h, n > n0 ? n - 1 : n, lane() % (C / 2));
+    }
     in.fetch_snext(A, bh, n, j0);
     in.fetch_do(A, b, h, n, j0);
-    in.qk.fetch(A.qn + hoff(A, b, hk, A.Hk, n, C, D), D);
+    in.fetch_qk(A.qn + hoff(A, b, hk, A.Hk, n, C, D));
     in.fetch_kt(A, b, h, n);
     in.fetch_xl(A, b, h, n, j0);
+    __syncthreads();
   }
+  // Two barriers per step: the q and k operands are staged by each wave into its own rows, and
+  // the gates of the next chunk are published by wave 0 between the barriers (two buffers)
   for (int n = ne; n >= n0; --n) {
     const int nx = n > n0 ? n - 1 : n;  // the last step refetches its own chunk (unused)
     const bool emit = n < n1;           // the replayed chunk n1 only rebuilds G
@@ -1444,13 +1504,13 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
     }
     part = sum64(part);
     if (lane() == 0) red[w] = part;
-    const float carry = in.gt.carry();
-    const float kb0 = -in.gt.bg(0), kb1 = -in.gt.bg(1);
+    const float(*sc)[C] = sgate[n & 1];
     in.dov.template put_cols<PI, exact_b<PI, sizeof(TIO) == 2>() == P_X3_BEXACT>(odo);  // do^T
     in.fetch_do(A, b, h, nx, j0);
-    in.qk.put_cols2(oq, in.gt.grow(0), in.gt.grow(1));
-    in.qk.fetch(A.kn + hoff(A, b, hk, A.Hk, n, C, D), D);
-    in.gt.fetch(A, b, h, nx, RegsT<C, D, NT>::pair());
+    if (NW == D / 16 || w < D / 16) {  // (q grow)^T, the wave's own rows
+      in.qk.put(oq, 16 * w, sc[0]);
+      in.fetch_qk(A.kn + hoff(A, b, hk, A.Hk, n, C, D));
+    }
     __syncthreads();
     if (threadIdx.x == 0 && emit) {
       float s = 0.f;
@@ -1475,18 +1535,23 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
       }
       in.fetch_xl(A, b, h, nx, j0);
     }
-    if (NW == D / 16 || w < D / 16) {  // G = carry G + q_read^T do
+    if (NW == D / 16 || w < D / 16) {  // G = carry G + q_read^T do, then (-k beta grow)^T in the same rows
+      const float carry = sc[2][0];
 #pragma unroll
       for (int t = 0; t < DVT / 16; ++t) accG[t] *= carry;
       strip_mma<exact_b<PI, sizeof(TIO) == 2>(), C, DVT / 16>(accG, oq, 16 * w, odo, 0);  // do: bf16 exact
+      in.qk.put(oq, 16 * w, sc[1]);
+      in.fetch_qk(A.qn + hoff(A, b, hk, A.Hk, nx, C, D));
     }
-    __syncthreads();
-    in.qk.put_cols2(oq, kb0, kb1);
-    in.qk.fetch(A.qn + hoff(A, b, hk, A.Hk, nx, C, D), D);
+    if (w == 0 && nx != n) {  // the next chunk's gates (other buffer: this chunk's are read until the barrier)
+      in.put_gates(sgate[nx & 1]);
+      in.gt.fetch(A, b, h, nx > n0 ? nx - 1 : nx, lane() % (C / 2));
+    }
     __syncthreads();
     if (NW == D / 16 || w < D / 16)  // ... - kbe^T X
       strip_mma<PI, C, DVT / 16>(accG, oq, 16 * w, ox, 0);
-    __syncthreads();
+    // no barrier here: the next step's writes before its first barrier go to G^T, do^T, the
+    // wave's own q rows and red, none of which this product reads
   }
 }
 
