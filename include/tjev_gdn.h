@@ -117,7 +117,8 @@ int tjev_gdn_mega2_fwd_state(const tjev_gdn_params* p, void* stream, const void*
  * (raw; post-conv when taps == 0), a, b [B, H]; conv_state [B, K-1, W] io_dtype read, and
  * conv_state_out the same history shifted by the new row (must not alias conv_state); state
  * [B, H, Dk, Dv] fp32 read and state_out written (may alias state); out [B, H, Dv] io_dtype.
- * The step continues the segment the state belongs to (no reset). */
+ * qkv, conv_state, conv_state_out, state and state_out are 16-byte aligned. The step
+ * continues the segment the state belongs to (no reset). */
 int tjev_gdn_decode_step(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a,
                          const void* b, const float* a_log, const float* dt_bias,
                          const float* conv_w, const void* conv_state, const float* state,

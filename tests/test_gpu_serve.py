@@ -61,23 +61,31 @@ def test_prefill_final_state_and_history(length, cuts, pad):
             assert torch.equal(hist[r, i].cpu(), expect), (r, i)
 
 
+@pytest.mark.parametrize("dim,taps", [(64, 4), (128, 4), (128, 2), (16, 5)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_decode_step_matches_oracle(dtype):
+def test_decode_step_matches_oracle(dtype, dim, taps):
+    """One decode step against the oracle's, at head dims of 1 to 4 state tiles and conv
+    kernels of 2 to 5 taps (histories of 1 to 4 rows)."""
     from oracle.gdn_oracle import decode_step
     from tjev_amd.serve import gdn_decode_step
+    from tjev_amd.testing import gdn_inputs
 
+    shape = dict(key_heads=2, key_dim=dim, value_heads=4, value_dim=dim)
     gen = torch.Generator().manual_seed(3)
-    qkv, a, b, a_log, dt_bias, w, _ = _inputs(3, 4, dtype, 9)
-    state = torch.randn((3, 4, 64, 64), generator=gen) * 0.1
-    out, hist2, state2 = gdn_decode_step(qkv[:, 3].cuda(), a[:, 3].cuda(), b[:, 3].cuda(), a_log.cuda(),
-                                         dt_bias.cuda(), w.cuda(), qkv[:, :3].cuda(), state.cuda(), **SHAPE)
+    t = 5
+    qkv, a, b, a_log, dt_bias, w, _ = gdn_inputs(batch=3, length=t + 1, key_heads=2, value_heads=4, dim=dim,
+                                                 dtype=dtype, seed=9, taps=taps)
+    hist = qkv[:, t - (taps - 1):t]
+    state = torch.randn((3, 4, dim, dim), generator=gen) * 0.1
+    out, hist2, state2 = gdn_decode_step(qkv[:, t].cuda(), a[:, t].cuda(), b[:, t].cuda(), a_log.cuda(),
+                                         dt_bias.cuda(), w.cuda(), hist.cuda(), state.cuda(), **shape)
     torch.cuda.synchronize()
     f = lambda x: x.double()  # noqa: E731
-    want_out, want_hist, want_state = decode_step(f(qkv[:, 3]), f(a[:, 3]), f(b[:, 3]), f(a_log), f(dt_bias), f(w),
-                                                  f(qkv[:, :3]), state.double(), dtype=torch.float64, **SHAPE)
-    assert torch.equal(hist2.cpu(), torch.cat([qkv[:, 1:3], qkv[:, 3:4]], 1))
+    want_out, want_hist, want_state = decode_step(f(qkv[:, t]), f(a[:, t]), f(b[:, t]), f(a_log), f(dt_bias), f(w),
+                                                  f(hist), state.double(), dtype=torch.float64, **shape)
+    assert torch.equal(hist2.cpu(), torch.cat([hist[:, 1:], qkv[:, t:t + 1]], 1))
     e_out, e_state = rel(out.double().cpu(), want_out), rel(state2.double().cpu(), want_state)
-    print(f"{dtype}: decode out rel {e_out:.2e}, state rel {e_state:.2e}", flush=True)
+    print(f"{dtype} D={dim} taps={taps}: decode out rel {e_out:.2e}, state rel {e_state:.2e}", flush=True)
     if dtype == torch.float32:
         assert e_out <= 1e-5 and e_state <= 1e-5
     else:  # bf16 activations: the output's own rounding (2^-8 relative) dominates

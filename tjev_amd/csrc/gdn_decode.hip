@@ -9,7 +9,7 @@
 // delta = (v - s^T k) beta, s += k delta^T, o = s^T q. Each thread holds 4 adjacent columns
 // of D/32 rows (16-byte accesses); the two column sums go through lane shuffles and LDS. The state is read and written once (in place
 // allowed: each slice belongs to one workgroup); the new conv history goes to a separate
-// buffer, written by the head-0 workgroups of each row.
+// buffer, copied in 16-byte pieces by all the workgroups of each row.
 #include <hip/hip_runtime.h>
 
 #include <string>
@@ -39,28 +39,51 @@ struct DecodeArgs {
 
 constexpr int kThreads = 256;
 
-// the activation of channel c: the causal conv over the K-1 kept rows and the new one, lag 0
-// first (causal_conv1d.py:42-45), then SiLU; the new row itself without a conv (taps == 0)
+// channel c's raw values for its activation: the new row and the K-1 kept rows with their conv
+// weights, loaded as soon as the workgroup starts
 template <class TIO>
-__device__ __forceinline__ float activation(const DecodeArgs& A, int b, int c) {
-  const TIO* x = reinterpret_cast<const TIO*>(A.qkv);
-  const float xt = ldf(x + (size_t)b * A.W + c);
-  if (A.taps == 0) return xt;
-  const TIO* hist = reinterpret_cast<const TIO*>(A.conv_in) + (size_t)b * (A.taps - 1) * A.W;
-  float z = xt * A.conv_w[(size_t)(A.taps - 1) * A.W + c];
-  for (int L = 1; L < A.taps; ++L) z += ldf(hist + (size_t)(A.taps - 1 - L) * A.W + c) * A.conv_w[(size_t)(A.taps - 1 - L) * A.W + c];
-  return z * sigmoid_io<TIO>(z);
-}
-
-// sum over the block of one value per thread (wave sums, then the waves in order)
-__device__ __forceinline__ float block_sum(float v, float* red) {
-  v = sum64(v);
-  __syncthreads();
-  if (lane() == 0) red[wave()] = v;
-  __syncthreads();
-  float s = 0.f;
+struct TapRow {
+  float x[5], w[5];  // x[L] = x[t - L], w[L] = w[K-1-L]
+  __device__ __forceinline__ void fetch(const DecodeArgs& A, int b, int c) {
+    x[0] = ldf(reinterpret_cast<const TIO*>(A.qkv) + (size_t)b * A.W + c);
+    if (A.taps == 0) return;
+    const TIO* hist = reinterpret_cast<const TIO*>(A.conv_in) + (size_t)b * (A.taps - 1) * A.W;
+    w[0] = A.conv_w[(size_t)(A.taps - 1) * A.W + c];
 #pragma unroll
-  for (int q = 0; q < kThreads / 64; ++q) s += red[q];
+    for (int L = 1; L < 5; ++L) {
+      if (L < A.taps) {
+        x[L] = ldf(hist + (size_t)(A.taps - 1 - L) * A.W + c);
+        w[L] = A.conv_w[(size_t)(A.taps - 1 - L) * A.W + c];
+      }
+    }
+  }
+  // the causal conv, lag 0 first (causal_conv1d.py:42-45), then SiLU; the new row itself
+  // without a conv (taps == 0)
+  __device__ __forceinline__ float act(const DecodeArgs& A) const {
+    if (A.taps == 0) return x[0];
+    float z = x[0] * w[0];
+#pragma unroll
+    for (int L = 1; L < 5; ++L)
+      if (L < A.taps) z += x[L] * w[L];
+    return z * sigmoid_io<TIO>(z);
+  }
+};
+
+// the block sums of two values per thread (wave sums, then the waves in order)
+__device__ __forceinline__ float2 block_sum2(float a, float b, float (*red)[kThreads / 64]) {
+  a = sum64(a);
+  b = sum64(b);
+  if (lane() == 0) {
+    red[0][wave()] = a;
+    red[1][wave()] = b;
+  }
+  __syncthreads();
+  float2 s = make_float2(0.f, 0.f);
+#pragma unroll
+  for (int q = 0; q < kThreads / 64; ++q) {
+    s.x += red[0][q];
+    s.y += red[1][q];
+  }
   return s;
 }
 
@@ -71,15 +94,29 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeArgs A) {
   constexpr int QPR = DT / 4;                 // column quads of a tile (one per thread)
   constexpr int RG = kThreads / QPR;          // row groups
   constexpr int RPT = (D + RG - 1) / RG;      // rows per thread
-  constexpr int GPW = 64 / QPR;               // row groups per wave
   __shared__ float sq[D], sk[D], sv[DT];
-  __shared__ float red[kThreads / 64];
+  __shared__ float red[2][kThreads / 64];
   __shared__ float part[kThreads / 64][DT];
   __shared__ float gate[2];
   const int tile = blockIdx.x % NTL, bh = blockIdx.x / NTL, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
   const int tid = threadIdx.x;
   const int cq = tid % QPR, rg = tid / QPR, c0 = 4 * cq;
-  // the state slice first (16-byte loads): its loads run while q, k and v are built
+  // the activations' raw inputs and the gates first, then the state slice (16-byte loads):
+  // memory operations complete in issue order, so building q, k and v waits only for the
+  // former while the state's loads are still in flight
+  TapRow<TIO> tq, tk, tv;
+  if (tid < D) {
+    tq.fetch(A, b, hk * D + tid);
+    tk.fetch(A, b, A.Hk * D + hk * D + tid);
+  }
+  if (tid < DT) tv.fetch(A, b, 2 * A.Hk * D + h * D + tile * DT + tid);
+  float av = 0.f, bv = 0.f, alog = 0.f, dtb = 0.f;
+  if (tid == 0) {
+    av = ldf(reinterpret_cast<const TG*>(A.ga) + (size_t)b * A.H + h);
+    bv = ldf(reinterpret_cast<const TG*>(A.gb) + (size_t)b * A.H + h);
+    alog = A.a_log[h];
+    dtb = A.dt_bias[h];
+  }
   const float* src = A.state + (size_t)bh * D * D + tile * DT + c0;
   float4 s[RPT];
 #pragma unroll
@@ -88,24 +125,20 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeArgs A) {
     s[r] = *reinterpret_cast<const float4*>(src + (size_t)(i < D ? i : D - 1) * D);
   }
   // q and k of key head hk, v of value head h (this tile's columns)
-  float aq = 0.f, ak = 0.f;
-  if (tid < D) aq = activation<TIO>(A, b, hk * D + tid);
-  if (tid < D) ak = activation<TIO>(A, b, A.Hk * D + hk * D + tid);
-  if (tid < DT) sv[tid] = activation<TIO>(A, b, 2 * A.Hk * D + h * D + tile * DT + tid);
+  const float aq = tid < D ? tq.act(A) : 0.f;
+  const float ak = tid < D ? tk.act(A) : 0.f;
+  if (tid < DT) sv[tid] = tv.act(A);
+  if (tid == 0) {  // beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias)
+    gate[0] = sigmoidf_(bv);
+    gate[1] = expf(-expf(alog) * softplusf_(av + dtb));
+  }
   // l2norm (xla.py:42-53; r = 0 on an all-zero row), q scaled by Dk^-1/2
-  const float sqq = block_sum(aq * aq, red);
-  const float skk = block_sum(ak * ak, red);
-  const float rq = (sqq == 0.f ? 0.f : 1.0f / sqrtf(sqq + 1e-6f)) * A.scale;
-  const float rk = skk == 0.f ? 0.f : 1.0f / sqrtf(skk + 1e-6f);
+  const float2 ss = block_sum2(aq * aq, ak * ak, red);
+  const float rq = (ss.x == 0.f ? 0.f : 1.0f / sqrtf(ss.x + 1e-6f)) * A.scale;
+  const float rk = ss.y == 0.f ? 0.f : 1.0f / sqrtf(ss.y + 1e-6f);
   if (tid < D) {
     sq[tid] = aq * rq;
     sk[tid] = ak * rk;
-  }
-  if (tid == 0) {  // beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias)
-    const float av = ldf(reinterpret_cast<const TG*>(A.ga) + (size_t)b * A.H + h);
-    const float bv = ldf(reinterpret_cast<const TG*>(A.gb) + (size_t)b * A.H + h);
-    gate[0] = sigmoidf_(bv);
-    gate[1] = expf(-expf(A.a_log[h]) * softplusf_(av + A.dt_bias[h]));
   }
   __syncthreads();
   // column sums over the rows: within the thread, across the wave's row groups (xor
@@ -162,14 +195,15 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeArgs A) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) stf(reinterpret_cast<TIO*>(A.out) + (size_t)bh * D + tile * DT + c0 + e, ov[e]);
   }
-  if (h == 0 && tile == 0 && A.taps > 1) {  // the history shifted by the new row
-    const int k1 = A.taps - 1;
-    const TIO* hist = reinterpret_cast<const TIO*>(A.conv_in) + (size_t)b * k1 * A.W;
-    const TIO* x = reinterpret_cast<const TIO*>(A.qkv) + (size_t)b * A.W;
-    TIO* out = reinterpret_cast<TIO*>(A.conv_out) + (size_t)b * k1 * A.W;
-    for (int idx = tid; idx < k1 * A.W; idx += kThreads) {
-      const int r = idx / A.W, c = idx % A.W;
-      out[idx] = r + 1 < k1 ? hist[(size_t)(r + 1) * A.W + c] : x[c];
+  if (A.taps > 1) {  // the history shifted by the new row, in 16-byte pieces spread over the row's workgroups
+    constexpr int E = 16 / sizeof(TIO);
+    const int k1 = A.taps - 1, wu = A.W / E, units = k1 * wu;
+    const uint4* hist = reinterpret_cast<const uint4*>(reinterpret_cast<const TIO*>(A.conv_in) + (size_t)b * k1 * A.W);
+    const uint4* x = reinterpret_cast<const uint4*>(reinterpret_cast<const TIO*>(A.qkv) + (size_t)b * A.W);
+    uint4* out = reinterpret_cast<uint4*>(reinterpret_cast<TIO*>(A.conv_out) + (size_t)b * k1 * A.W);
+    for (int u = (h * NTL + tile) * kThreads + tid; u < units; u += A.H * NTL * kThreads) {
+      const int r = u / wu, c = u % wu;
+      out[u] = r + 1 < k1 ? hist[(size_t)(r + 1) * wu + c] : x[c];
     }
   }
 }
@@ -211,6 +245,9 @@ extern "C" int tjev_gdn_decode_step(const tjev_gdn_params* p, void* stream, cons
     return fail(TJEV_GDN_EINVAL, "null tensor argument");
   if (p->taps > 1 && conv_state == conv_state_out)
     return fail(TJEV_GDN_EINVAL, "conv_state_out must not alias conv_state (every head reads the history)");
+  auto al16 = [](const void* q) { return q == nullptr || (reinterpret_cast<uintptr_t>(q) % 16) == 0; };
+  if (!al16(qkv) || !al16(state) || !al16(state_out) || (p->taps > 1 && (!al16(conv_state) || !al16(conv_state_out))))
+    return fail(TJEV_GDN_EINVAL, "qkv, the conv states and the states must be 16-byte aligned");
   gdn::DecodeArgs A{};
   A.B = p->batch;
   A.Hk = p->key_heads;
