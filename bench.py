@@ -231,10 +231,13 @@ def _decode_bench(args) -> dict:
                                                                        dim=D, dtype=torch.bfloat16))
     state = (torch.randn((B, H, D, D), generator=torch.Generator().manual_seed(5)) * 0.05).cuda()
     hist = qkv[:, :3].contiguous()
+    # the new token's rows as a serving loop receives them from the projections: contiguous
+    # [B, W] and [B, H] tensors (strided slices would add a copy kernel each per step)
+    x_t, a_t, b_t = qkv[:, 3].contiguous(), a[:, 3].contiguous(), b[:, 3].contiguous()
     kw = dict(key_heads=Hk, key_dim=D, value_heads=H, value_dim=D)
 
     def step():
-        gdn_decode_step(qkv[:, 3], a[:, 3], b[:, 3], a_log, dt_bias, w, hist, state, inplace=True, **kw)
+        gdn_decode_step(x_t, a_t, b_t, a_log, dt_bias, w, hist, state, inplace=True, **kw)
 
     for _ in range(args.warmup):
         step()
