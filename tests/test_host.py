@@ -249,7 +249,7 @@ def test_ds_check_flags_the_miscompiled_merge_only():
 
 def test_decode_step_validation():
     """The decode step's checks, before any launch: one token per row, grouped heads, a
-    history buffer distinct from the one it reads, and non-null tensors."""
+    history buffer distinct from the one it reads, non-null and 16-byte aligned tensors."""
     from tjev_amd import _lib
 
     lib = _lib.load()
@@ -268,6 +268,11 @@ def test_decode_step_validation():
     assert lib.tjev_gdn_decode_step(ctypes.byref(p), None, *nulls) == 1
     assert "null" in lib.tjev_gdn_last_error().decode()
     assert lib.tjev_gdn_decode_step(ctypes.byref(_params(length=1, key_dim=48, value_dim=48)), None, *bufs) == 2
+    for i in (0, 6, 7, 9, 10):  # qkv, conv_state, state, conv_state_out, state_out: 16-byte pieces
+        odd = list(bufs)
+        odd[i] = ctypes.c_void_p(256 * 20 + 8)
+        assert lib.tjev_gdn_decode_step(ctypes.byref(p), None, *odd) == 1
+        assert "16-byte aligned" in lib.tjev_gdn_last_error().decode()
 
 
 def test_serving_rejects_cpu_tensors():
