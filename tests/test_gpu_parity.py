@@ -68,14 +68,15 @@ def test_hip_conv_widths_fp32(taps):
         assert err < TOL[name], (name, errors)
 
 
-@pytest.mark.parametrize("d,chunk", [(16, 32), (16, 128), (64, 64)])
-def test_hip_frozen_conv_weight_fp32(d, chunk):
+@pytest.mark.parametrize("d,chunk,taps", [(16, 32, 4), (16, 128, 4), (64, 64, 4), (16, 32, 5)])
+def test_hip_frozen_conv_weight_fp32(d, chunk, taps):
     """The conv weight not differentiated (pallas_tpu_mega.py:548-571 emits no dz then), as in
-    the benchmark's step: the backward's own conv path without the d(conv w) partials."""
+    the benchmark's step: the backward's own conv path without the d(conv w) partials (with
+    the 3-row halo of the model's conv of 4 taps, and the 4-row one of 5 taps)."""
     hk, h = 2, 4
-    inputs, cot = case_inputs(1, 300, hk, h, d, cuts=[chunk - 1, chunk + 1, 2 * chunk + 2])
+    inputs, cot = case_inputs(1, 300, hk, h, d, cuts=[chunk - 1, chunk + 1, 2 * chunk + 2], taps=taps)
     shape = dict(key_heads=hk, key_dim=d, value_heads=h, value_dim=d, conv=True)
-    print(f"frozen conv d={d} chunk={chunk}", flush=True)
+    print(f"frozen conv d={d} chunk={chunk} taps={taps}", flush=True)
     got = hip_outputs(inputs, cot, chunk=chunk, precision="highest", want_w=False, **shape)
     want = oracle_outputs(inputs, cot, **shape)
     assert "w" not in got
