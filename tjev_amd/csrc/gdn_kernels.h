@@ -276,38 +276,6 @@ __device__ __forceinline__ void lag_weights(const GdnArgs& A, int cc, float (&wl
     for (int e = 0; e < 8; ++e) wl[L][e] = (L < A.taps) ? A.conv_w[(size_t)(A.taps - 1 - L) * A.W + cc + e] : 0.f;
 }
 
-// Raw rows t, t-1, .. t-4 of 8 channels (zeros outside [0, T) and past the taps) and whether
-// each tap stays in token t's segment (causal_conv1d.py:10-17).
-template <class TIO>
-__device__ __forceinline__ void conv_rows(const GdnArgs& A, const TIO* x, const int32_t* sp, int b, int t, int cc,
-                                          int st, float (&xs)[5][8], bool (&keep)[5]) {
-  const int taps = A.taps > 0 ? A.taps : 1;
-#pragma unroll
-  for (int L = 0; L < 5; ++L) {
-    const int tt = t - L;
-    keep[L] = L < taps && tt >= 0 && (L == 0 || sp[tt] == st);
-    if (L < taps && tt >= 0 && tt < A.T) {
-      ld8(x + ((size_t)b * A.T + tt) * A.W + cc, xs[L]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xs[L][e] = 0.f;
-    }
-  }
-}
-
-// z = sum over lags of keep * x[t-L] * w[K-1-L], lag 0 first (causal_conv1d.py:42-45)
-__device__ __forceinline__ void conv_z(const float (&xs)[5][8], const bool (&keep)[5], const float (&wl)[5][8],
-                                       float (&z)[8]) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float v = xs[0][e] * wl[0][e];
-#pragma unroll
-    for (int L = 1; L < 5; ++L)
-      if (keep[L]) v += xs[L][e] * wl[L][e];
-    z[e] = v;
-  }
-}
-
 // ---------------------------------------------------------------- k_prep
 // grid (B*N, 2*Hk + H), 256 threads. Slot y: q head y (< Hk), k head y - Hk, v head y - 2Hk.
 // Every (token, 8 channels) is independent: D/8 lanes per token row. l2norm of xla.py:42-53.
