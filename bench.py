@@ -11,11 +11,12 @@ kernel's average duration (HIP events on the launch stream) for the dominant ker
 roofline. The CPU baseline is the oracle (a CPU restatement of tjev's XLA chunked path, fp32,
 torch autograd) on a bounded sample of the same workload.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 0.8B|9B|varlen|tiny|4B-block|decode]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 0.8B|9B|varlen|tiny|4B-block|decode|v2]
 
 ``--config 4B-block`` times BASELINE's block config instead: the 4B-shaped GDN block with merged
 LoRA r64 (projections on hipBLASLt, core and norm in the HIP library), with peak activation
-bytes; ``--config decode`` the serving path's one-token decode step (64 rows, 0.8B head shape).
+bytes; ``--config decode`` the serving path's one-token decode step (64 rows, 0.8B head shape);
+``--config v2`` the v2 operator (pre-gated q, k, v, g, beta) fwd+bwd at the 0.8B layer shape.
 """
 
 from __future__ import annotations
@@ -267,6 +268,80 @@ def _decode_bench(args) -> dict:
     }
 
 
+def _v2_bench(args) -> dict:
+    """The v2 operator (``chunk_gated_delta_rule_v2``, pallas_tpu_v2.py:541-582, the kernels behind
+    ``gdn_impl=pallas_tpu_v2``) fwd+bwd at the 0.8B layer shape (B=4, T=4096, Hk=H=16, D=128,
+    chunk 128, precision high, one segment per row): q and k l2-normalised with q scaled by
+    Dk^-1/2 (as gdn.py:90-92 passes them), v ~ N(0, 1) in bf16; g = -exp(A_log) softplus(a +
+    dt_bias) and beta = sigmoid(b) in fp32 from BASELINE's distributions. A step is the forward
+    and the backward of sum(out * dy) to q, k, v, g and beta. The chunk, scan and gradient kernels
+    are the megakernel's (the roofline object is the dominant one's); the ends are v2's own."""
+    import math
+
+    import torch
+
+    from tjev_amd import _lib
+    from tjev_amd.roofline import PEAK_BF16_TFLOPS, kernel_roofline, kernel_work
+    from tjev_amd.v2 import chunk_gated_delta_rule_v2
+
+    B, T, Hk, H, D, C = 4, 4096, 16, 16, 128, 128
+    gen = torch.Generator().manual_seed(13)
+
+    def rn(*shape):
+        return torch.randn(shape, generator=gen)
+
+    q = torch.nn.functional.normalize(rn(B, T, Hk, D), dim=-1) * D ** -0.5
+    k = torch.nn.functional.normalize(rn(B, T, Hk, D), dim=-1)
+    a_log = torch.rand(H, generator=gen) * math.log(16.0)
+    g = -torch.exp(a_log) * torch.nn.functional.softplus(rn(B, T, H) + rn(H))
+    beta = torch.sigmoid(rn(B, T, H))
+    leaves = [x.to(torch.bfloat16).cuda().requires_grad_(True) for x in (q, k, rn(B, T, H, D))]
+    leaves += [x.cuda().requires_grad_(True) for x in (g, beta)]
+    seg = torch.ones((B, T), dtype=torch.int32, device="cuda")
+    dy = rn(B, T, H, D).to(torch.bfloat16).cuda()
+
+    def step():
+        out = chunk_gated_delta_rule_v2(*leaves, seg, chunk=C, precision="high", residuals=args.residuals)
+        return torch.autograd.grad(out, leaves, dy)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        grads = step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    finite = all(bool(torch.isfinite(x.float()).all()) for x in grads)
+    with _lib.KernelTimer() as kt:
+        for _ in range(args.steps):
+            step()
+    per_kernel = {n: kt.ms[n] / kt.launches[n] for n in kt.ms if kt.launches[n]}
+    work = kernel_work(batch=B, length=T, key_heads=Hk, value_heads=H, dim=D, chunk=C, io_bytes=2,
+                       residuals=args.residuals)
+    ends = ("gdn_prep_fwd", "gdn_prep_bwd", "gdn_post")  # v2's own ends: their work differs from mega2's
+    kernels = {n: ({"ms": t} if n in ends else {"ms": t, **kernel_roofline(work[n], t * 1e-3, PEAK_BF16_TFLOPS)})
+               for n, t in per_kernel.items()}
+    dominant = max((n for n in kernels if n not in ends), key=lambda n: kernels[n]["ms"])
+    dk = kernels[dominant]
+    return {
+        "metric": METRIC, "value": B * T / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "0.8B GDN layer core, v2 operator (pre-gated q, k, v, g, beta) fwd+bwd", "batch": B,
+                   "seq_len": T, "key_heads": Hk, "value_heads": H, "head_dim": D, "chunk": C, "precision": "high",
+                   "segments": "one", "residuals": args.residuals},
+        "roofline": {"kernel": dominant, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
+                     "unit": dk["unit"], "frac": dk["frac"], "traffic": None, "hbm_frac": dk["hbm_frac"],
+                     "mfma_frac": dk["mfma_frac"]},
+        "kernels": {n: {kk: (round(vv, 6) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for n, v in kernels.items()},
+        "finite": finite,
+    }
+
+
 def main(argv=None) -> int:
     args = _args(argv)
     if args.gpus != 1:
@@ -283,8 +358,8 @@ def main(argv=None) -> int:
     from tjev_amd.roofline import PEAK_BF16_TFLOPS, PEAK_FP32_TFLOPS, kernel_roofline, kernel_work, operator_work
     from tjev_amd.testing import CONFIGS, cotangent, gdn_inputs
 
-    if args.config in ("4B-block", "decode"):
-        report = _block_bench(args) if args.config == "4B-block" else _decode_bench(args)
+    if args.config in ("4B-block", "decode", "v2"):
+        report = {"4B-block": _block_bench, "decode": _decode_bench, "v2": _v2_bench}[args.config](args)
         if args.details:
             with open(args.details, "w") as f:
                 json.dump(report, f, indent=1)
