@@ -96,7 +96,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeArgs A) {
   constexpr int RPT = (D + RG - 1) / RG;      // rows per thread
   __shared__ float sq[D], sk[D], sv[DT];
   __shared__ float red[2][kThreads / 64];
-  __shared__ float part[kThreads / 64][DT];
+  __shared__ float part[2][kThreads / 64][DT];  // one buffer per column sum: no barrier before a write
   __shared__ float gate[2];
   const int tile = blockIdx.x % NTL, bh = blockIdx.x / NTL, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
   const int tid = threadIdx.x;
@@ -143,23 +143,22 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeArgs A) {
   __syncthreads();
   // column sums over the rows: within the thread, across the wave's row groups (xor
   // shuffles over the lanes of one column quad), then across the waves through LDS
-  auto column_sums = [&](float4 v, float (&out)[4]) {
+  auto column_sums = [&](int k, float4 v, float (&out)[4]) {
     float x[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int m = QPR; m < 64; m <<= 1)
 #pragma unroll
       for (int e = 0; e < 4; ++e) x[e] += __shfl_xor(x[e], m);
-    __syncthreads();
     if (lane() < QPR) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) part[wave()][c0 + e] = x[e];
+      for (int e = 0; e < 4; ++e) part[k][wave()][c0 + e] = x[e];
     }
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float t = 0.f;
 #pragma unroll
-      for (int q = 0; q < kThreads / 64; ++q) t += part[q][c0 + e];
+      for (int q = 0; q < kThreads / 64; ++q) t += part[k][q][c0 + e];
       out[e] = t;
     }
   };
@@ -173,7 +172,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeArgs A) {
     mem.x += s[r].x * kv; mem.y += s[r].y * kv; mem.z += s[r].z * kv; mem.w += s[r].w * kv;
   }
   float m[4];
-  column_sums(mem, m);
+  column_sums(0, mem, m);
   const float bt = gate[0];
   const float dl[4] = {(sv[c0] - m[0]) * bt, (sv[c0 + 1] - m[1]) * bt, (sv[c0 + 2] - m[2]) * bt,
                        (sv[c0 + 3] - m[3]) * bt};
@@ -190,7 +189,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeArgs A) {
     }
   }
   float ov[4];
-  column_sums(o, ov);
+  column_sums(1, o, ov);
   if (rg == 0) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) stf(reinterpret_cast<TIO*>(A.out) + (size_t)bh * D + tile * DT + c0 + e, ov[e]);
