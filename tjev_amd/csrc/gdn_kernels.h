@@ -809,8 +809,9 @@ __device__ __forceinline__ void load_tile(float* s, int LD, const float* g) {
 // state-path product and one with T instead of w, u and w S); MODE 3: v_new from the saved T
 // (no L, no inverse). LDS: T in fp32 (the inverse runs in place), one operand region reused
 // for k, kbe^T, (v beta)^T, S^T and Y^T (and T^T during the inverse). The next unit's context
-// and k rows are loaded at this unit's start and end; the forward's k (again) and v after the
-// inverse, a product ahead of their use; the backward's S, k strip and v during the inverse.
+// and k rows are loaded at this unit's start and end; the forward's k (again) and v, and the
+// backward's S and k strip, during the inverse; the backward's v after it (held across the
+// inverse, it would spill).
 template <int C, int D, int PI, int PS, int MODE>
 __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
   constexpr bool FWD = MODE == 0 || MODE == 2;  // writes w and u (else v_new)
@@ -876,12 +877,13 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
         sc.fetch(A.states + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * D * D, D);
         ks.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D, i0);
       }
-      __syncthreads();
-      invert_unit_lower<C, PI>(sT, LT, reinterpret_cast<float*>(sB));
-      if constexpr (FWD) {  // k again (not held across the inverse: register limit), then v
+      if constexpr (FWD) {  // k again and v, in flight during the inverse
         kk.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D);
         vc.fetch(A.vv + off, D);
-      } else {
+      }
+      __syncthreads();
+      invert_unit_lower<C, PI>(sT, LT, reinterpret_cast<float*>(sB));
+      if constexpr (!FWD) {
         va.fetch(A.vv + off, D, i0);
       }
     }
