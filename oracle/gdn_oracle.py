@@ -19,6 +19,7 @@ Each function follows a reference file (paths relative to the tjev repository ro
 - ``masks``                                    pallas_tpu_mega.py:349-361 with
                                                pallas_tpu_v2.py:505-515 (integer logic)
 - ``heads_per_block``                          pallas_tpu_v2.py:518-525
+- ``gates``                                  pallas_tpu_mega.py:106-145, test_gdn_mega.py:52-53
 - ``reference_core`` / ``core_inputs``        tests/kernels/test_gdn_mega.py:44-58
                                                (``_reference``), the recurrent variant
                                                tests/kernels/test_gdn_long.py:131-176
@@ -335,12 +336,19 @@ def core_inputs(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_head
     q = l2norm(q.reshape(batch, length, hk, dk)) * dk ** -0.5
     k = l2norm(k.reshape(batch, length, hk, dk))
     v = v.reshape(batch, length, h, dv)
-    beta = torch.sigmoid(b)
-    xg = a + dt_bias
-    g = -torch.exp(a_log) * torch.logaddexp(xg, torch.zeros_like(xg))  # jax.nn.softplus
+    g, beta = gates(a, b, a_log, dt_bias)
     ratio = h // hk
     q, k = q.repeat_interleave(ratio, dim=2), k.repeat_interleave(ratio, dim=2)
     return q, k, v, g, beta, seg
+
+
+def gates(a, b, a_log, dt_bias):
+    """(g, beta) from the raw gate projections a, b [..., H] (pallas_tpu_mega.py:106-145,
+    test_gdn_mega.py:52-53): g = -e^{A_log} softplus(a + dt_bias) with jax.nn.softplus =
+    logaddexp(x, 0), beta = sigmoid(b)."""
+    xg = a + dt_bias
+    g = -torch.exp(a_log) * torch.logaddexp(xg, torch.zeros_like(xg))
+    return g, torch.sigmoid(b)
 
 
 def reference_with_grads(inputs, cotangent, *, key_heads, key_dim, value_heads, value_dim,
@@ -357,7 +365,8 @@ def reference_with_grads(inputs, cotangent, *, key_heads, key_dim, value_heads, 
                          chunk=chunk, dtype=dtype)
     loss = torch.sum(out * cotangent.to(dtype))
     targets = leaves + ([wl] if (wl is not None and wl.requires_grad) else [])
-    grads = torch.autograd.grad(loss, targets)
+    grads = torch.autograd.grad(loss, targets, allow_unused=True)  # (an input the loss ignores: zeros)
+    grads = [torch.zeros_like(t) if g is None else g for g, t in zip(grads, targets)]
     names = ["qkv", "a", "b", "A_log", "dt_bias", "w"]
     result = {"out": out.detach()}
     result.update({n: g.detach() for n, g in zip(names, grads)})

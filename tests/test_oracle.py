@@ -219,27 +219,203 @@ def test_gated_rmsnorm_backward_matches_hf(dtype):
         assert float((g.double() - h.double()).abs().max()) <= tol * scale
 
 
-# ------------------------------------------------------------------ gates
-def test_gates_closed_forms():
-    """beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias) with jax.nn.softplus =
-    logaddexp(x, 0): against the formulas evaluated in Python's math at a few points,
-    including large |x| where a naive log(1 + exp(x)) overflows."""
+# ------------------------------------------------------------------ gates and the core's inputs
+# (a, dt_bias, A_log, b) points: ordinary values, the BASELINE A_log range end (ln 16), large
+# |a + dt_bias| where a naive log(1 + e^x) overflows or loses everything, and saturated b
+GATE_POINTS = [(0.3, -0.5, 0.4, 0.1), (-2.0, 1.5, 2.772588722239781, -3.0), (25.0, 0.0, 0.0, 40.0),
+               (-30.0, -5.0, 1.0, -40.0), (0.0, 0.0, -1.5, 0.0), (700.0, 10.0, 0.5, 5.0)]
+
+
+def _gates_by_hand(a, dt_bias, a_log, b):
+    """g = -e^{A_log} softplus(a + dt_bias), beta = 1 / (1 + e^{-b}) in Python's math, softplus
+    as max(x, 0) + log1p(e^{-|x|}) (test_gdn_mega.py:52-53 with jax.nn.softplus)."""
     import math
 
-    xs = [-50.0, -3.0, -1e-3, 0.0, 0.7, 20.0, 80.0]
-    for x in xs:
-        sp = float(torch.logaddexp(torch.tensor(x, dtype=F64), torch.tensor(0.0, dtype=F64)))
-        want = x + math.log1p(math.exp(-x)) if x > 0 else math.log1p(math.exp(x))
-        assert abs(sp - want) <= 1e-15 * max(1.0, abs(want))
-    seg = torch.ones((1, 3), dtype=torch.int64)
-    qkv = torch.zeros((1, 3, 2 * 1 * 2 + 1 * 2), dtype=F64)
-    a = torch.tensor([[[0.3], [-2.0], [5.0]]], dtype=F64)
-    b = torch.tensor([[[0.1], [0.2], [-0.3]]], dtype=F64)
-    a_log, dt = torch.tensor([0.4], dtype=F64), torch.tensor([-0.5], dtype=F64)
-    a.requires_grad_(True)
-    out = O.reference_core(qkv, a, b, a_log, dt, None, seg, key_heads=1, key_dim=2, value_heads=1, value_dim=2,
-                           conv=False, dtype=F64)
-    assert torch.all(out == 0)  # zero q, k, v: nothing to read or write
+    x = a + dt_bias
+    softplus = max(x, 0.0) + math.log1p(math.exp(-abs(x)))
+    beta = 1.0 / (1.0 + math.exp(-b)) if b >= 0 else math.exp(b) / (1.0 + math.exp(b))
+    return -math.exp(a_log) * softplus, beta
+
+
+def test_gates_closed_forms():
+    """The oracle's gates at hand-picked points against the formulas evaluated in Python's math
+    (pallas_tpu_mega.py:106-145; test_gdn_mega.py:52-53), both as ``gates`` and through
+    ``core_inputs`` (per value head, zero qkv: the gates do not depend on it)."""
+    a = torch.tensor([[[p[0] for p in GATE_POINTS]]], dtype=F64)
+    dt = torch.tensor([p[1] for p in GATE_POINTS], dtype=F64)
+    a_log = torch.tensor([p[2] for p in GATE_POINTS], dtype=F64)
+    b = torch.tensor([[[p[3] for p in GATE_POINTS]]], dtype=F64)
+    want = [_gates_by_hand(*p) for p in GATE_POINTS]
+    g, beta = O.gates(a, b, a_log, dt)
+    h = len(GATE_POINTS)
+    _, _, _, g2, beta2, _ = O.core_inputs(torch.zeros((1, 1, 2 * 1 * 2 + h * 2), dtype=F64), a, b, a_log, dt,
+                                          torch.ones((4, 2 * 1 * 2 + h * 2), dtype=F64),
+                                          torch.ones((1, 1), dtype=torch.int64), key_heads=1, key_dim=2,
+                                          value_heads=h, value_dim=2, dtype=F64)
+    for got_g, got_b in ((g, beta), (g2, beta2)):
+        for i, (wg, wb) in enumerate(want):
+            assert abs(float(got_g[0, 0, i]) - wg) <= 1e-14 * max(1.0, abs(wg)), (i, float(got_g[0, 0, i]), wg)
+            assert abs(float(got_b[0, 0, i]) - wb) <= 1e-15, (i, float(got_b[0, 0, i]), wb)
+
+
+def _hf_core(inputs, cot, *, key_heads, key_dim, value_heads, value_dim, monkeypatch):
+    """HF transformers' Qwen3_5GatedDeltaNet.forward (modeling_qwen3_5.py:432-530, an
+    implementation independent of this repository) in float64 on given projections: the
+    in_proj modules return qkv, a, b as given, conv1d / A_log / dt_bias hold the oracle's
+    parameters, the delta rule is replaced by the float64 token recurrence (HF's own rule
+    casts to float32) after HF's in-kernel l2norm and q scale, and the core output is read at
+    the norm's input. Returns the rule's inputs as HF composed them (q, k after its l2norm and
+    scale, v, g, beta), the core output [B,T,H,Dv] and the gradients of sum(out * cot) w.r.t.
+    qkv, a, b, A_log, dt_bias and the conv weight (as [K, W])."""
+    hf = pytest.importorskip("transformers.models.qwen3_5.modeling_qwen3_5")
+    from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5TextConfig
+
+    qkv, a, b, a_log, dt_bias, w, _ = inputs
+    batch, length, _ = qkv.shape
+    cfg = Qwen3_5TextConfig(hidden_size=8, linear_num_key_heads=key_heads, linear_num_value_heads=value_heads,
+                            linear_key_head_dim=key_dim, linear_value_head_dim=value_dim,
+                            linear_conv_kernel_dim=w.shape[0], num_hidden_layers=1,
+                            layer_types=["linear_attention"], hidden_act="silu", rms_norm_eps=1e-6)
+    torch.manual_seed(0)
+    m = hf.Qwen3_5GatedDeltaNet(cfg, 0).double()
+    leaves = {n: x.detach().to(F64).clone().requires_grad_(True) for n, x in (("qkv", qkv), ("a", a), ("b", b))}
+
+    class Given(torch.nn.Module):
+        def __init__(self, t):
+            super().__init__()
+            self.t = t
+
+        def forward(self, _x):
+            return self.t
+
+    m.in_proj_qkv, m.in_proj_a, m.in_proj_b = Given(leaves["qkv"]), Given(leaves["a"]), Given(leaves["b"])
+    m.in_proj_z = Given(torch.zeros((batch, length, value_heads * value_dim), dtype=F64))
+    with torch.no_grad():
+        m.conv1d.weight.copy_(w.to(F64).T[:, None, :])
+        m.A_log.copy_(a_log.to(F64))
+        m.dt_bias.copy_(dt_bias.to(F64))
+    seen = {}
+
+    def rule64(query, key, value, g, beta, chunk_size=64, initial_state=None, output_final_state=False,
+               use_qk_l2norm_in_kernel=False, **kw):
+        if use_qk_l2norm_in_kernel:  # modeling_qwen3_5.py torch_chunk_gated_delta_rule's preamble
+            query, key = hf.l2norm(query, dim=-1, eps=1e-6), hf.l2norm(key, dim=-1, eps=1e-6)
+        query = query * query.shape[-1] ** -0.5
+        seen.update(q=query, k=key, v=value, g=g, beta=beta)
+        out, state = O.recurrent_gated_delta_rule(query, key, value, g, beta)
+        return out, (state if output_final_state else None)
+
+    monkeypatch.setattr(hf, "torch_chunk_gated_delta_rule", rule64)
+    core = {}
+
+    def grab(_mod, args):  # returns None: the norm's arguments stay as they are
+        core["out"] = args[0]
+
+    m.norm.register_forward_pre_hook(grab)
+    m(torch.zeros((batch, length, 8), dtype=F64))
+    out = core["out"].reshape(batch, length, value_heads, value_dim)
+    params = [m.A_log, m.dt_bias, m.conv1d.weight]
+    grads = torch.autograd.grad((out * cot.to(F64)).sum(), [leaves["qkv"], leaves["a"], leaves["b"], *params])
+    names = ["qkv", "a", "b", "A_log", "dt_bias", "w"]
+    result = {"out": out.detach()}
+    result.update({n: g.detach() for n, g in zip(names, grads)})
+    result["w"] = result["w"][:, 0, :].T
+    return {k: v.detach() for k, v in seen.items()}, result
+
+
+def _hf_vs_oracle(monkeypatch, seed=21):
+    """Relative max errors of the oracle's composed core against HF's Qwen3_5GatedDeltaNet on
+    one segment (T = 45, not a multiple of the chunk 16; GQA 2 -> 4 heads; BASELINE's gate
+    spreads, A_log ~ U(0, ln 16)): the rule's inputs, the output and every gradient."""
+    from tjev_amd.testing import cotangent, gdn_inputs
+
+    shape = dict(key_heads=2, key_dim=8, value_heads=4, value_dim=8)
+    qkv, a, b, a_log, dt_bias, w, seg = gdn_inputs(batch=2, length=45, key_heads=2, value_heads=4, dim=8,
+                                                   seed=seed, style="baseline")
+    cot = cotangent(2, 45, 4, 8, seed=seed + 1)
+    # HF evaluates e^{A_log} in float32 (A_log.float().exp()); the oracle is given the A_log
+    # whose float64 exponential is that float32 value, so both decay by the same rates
+    a_log_hf = torch.log(a_log.to(F64).float().exp().to(F64))
+    inputs = (qkv.to(F64), a.to(F64), b.to(F64), a_log.to(F64), dt_bias.to(F64), w.to(F64), seg)
+    seen, hf = _hf_core(inputs, cot, monkeypatch=monkeypatch, **shape)
+    ours_in = O.core_inputs(*inputs[:3], a_log_hf, *inputs[4:], dtype=F64, **shape)
+    ours = O.reference_with_grads((*inputs[:3], a_log_hf, *inputs[4:]), cot, dtype=F64, chunk=16, **shape)
+    err = {}
+    for name, x in zip(("q", "k", "v", "g", "beta"), ours_in[:5]):
+        err["in:" + name] = float((x - seen[name]).abs().max() / seen[name].abs().max())
+    for name in hf:
+        err[name] = float((ours[name] - hf[name]).abs().max() / hf[name].abs().max())
+    return err
+
+
+def test_core_inputs_match_hf_gated_deltanet(monkeypatch):
+    """The oracle's composition conv -> SiLU -> split -> l2norm(q, k) -> q Dk^-1/2 -> gates ->
+    GQA repeat (``core_inputs``, test_gdn_mega.py:44-58) against HF's GatedDeltaNet layer in
+    float64: the delta rule's inputs and the core output agree to float64 rounding, and so
+    does every gradient but those of a and A_log, which HF takes through float32 casts
+    (``a.float()``, ``A_log.float().exp()``): those agree to float32 rounding."""
+    err = _hf_vs_oracle(monkeypatch)
+    for name, e in err.items():
+        assert e <= (2e-7 if name in ("a", "A_log") else 1e-10), (name, err)
+
+
+def test_padding_tokens_read_nothing_and_write_zeros():
+    """valid = seg > 0 (pallas_tpu_mega.py:195-201, test_gdn_mega.py:47-48): padding tokens have
+    zero q, k and v after the conv, their outputs are exactly 0, and the other tokens equal a
+    run without them."""
+    from tjev_amd.testing import gdn_inputs
+
+    shape = dict(key_heads=2, key_dim=8, value_heads=4, value_dim=8)
+    qkv, a, b, a_log, dt_bias, w, _ = gdn_inputs(batch=1, length=40, key_heads=2, value_heads=4, dim=8, seed=3,
+                                                 dtype=F64)
+    seg = torch.ones((1, 40), dtype=torch.int64)
+    seg[0, 33:] = 0
+    q, k, v, _, _, _ = O.core_inputs(qkv, a, b, a_log, dt_bias, w, seg, dtype=F64, **shape)
+    assert torch.all(q[0, 33:] == 0) and torch.all(k[0, 33:] == 0) and torch.all(v[0, 33:] == 0)
+    out = O.reference_core(qkv, a, b, a_log, dt_bias, w, seg, chunk=16, dtype=F64, **shape)
+    assert torch.all(out[0, 33:] == 0)
+    alone = O.reference_core(qkv[:, :33], a[:, :33], b[:, :33], a_log, dt_bias, w, seg[:, :33], chunk=16, dtype=F64,
+                             **shape)
+    assert float((out[:, :33] - alone).abs().max()) < 1e-12
+
+
+def _slipped_gates(kind):
+    def gates(a, b, a_log, dt_bias):
+        sp = lambda x: torch.logaddexp(x, torch.zeros_like(x))  # noqa: E731
+        if kind == "softplus(a) + dt_bias":
+            return -torch.exp(a_log) * (sp(a) + dt_bias), torch.sigmoid(b)
+        if kind == "A_log without exp":
+            return -a_log * sp(a + dt_bias), torch.sigmoid(b)
+        if kind == "beta = sigmoid(a)":
+            return -torch.exp(a_log) * sp(a + dt_bias), torch.sigmoid(a)
+        raise AssertionError(kind)
+    return gates
+
+
+@pytest.mark.parametrize("kind", ["softplus(a) + dt_bias", "A_log without exp", "beta = sigmoid(a)",
+                                  "key heads tiled, not interleaved", "scale on k"])
+def test_planted_composition_slips_are_caught(monkeypatch, kind):
+    """A slip planted in the oracle's gates or composition fails the HF layer comparison and
+    (for the gates) the closed forms."""
+    if kind in ("softplus(a) + dt_bias", "A_log without exp", "beta = sigmoid(a)"):
+        monkeypatch.setattr(O, "gates", _slipped_gates(kind))
+        with pytest.raises(AssertionError):
+            test_gates_closed_forms()
+    else:
+        orig = O.core_inputs
+
+        def slipped(*args, **kw):
+            q, k, v, g, beta, seg = orig(*args, **kw)
+            ratio = kw["value_heads"] // kw["key_heads"]
+            if kind == "key heads tiled, not interleaved":
+                q, k = (x[:, :, ::ratio].repeat(1, 1, ratio, 1) for x in (q, k))
+            else:
+                q, k = q * kw["key_dim"] ** 0.5, k * kw["key_dim"] ** -0.5
+            return q, k, v, g, beta, seg
+
+        monkeypatch.setattr(O, "core_inputs", slipped)
+    err = _hf_vs_oracle(monkeypatch)
+    assert max(err.values()) > 1e-3, (kind, err)
 
 
 # ------------------------------------------------------------------ masks
