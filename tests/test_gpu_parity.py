@@ -88,10 +88,12 @@ def test_hip_frozen_conv_weight_fp32(d, chunk, taps):
 
 def test_hip_tiny_config_fp32():
     """BASELINE config 1 (B=1, T=512, Hk=H=4, D=64, chunk 64, fp32 "highest", one segment).
-    Output and per-token gradients: max relative error <= 1e-5 against the fp32 reference path;
-    every gradient: cosine >= 0.999999. The A_log / dt_bias gradients are sums over every token
-    (the reference allows them 5x the per-token tolerance, test_gdn_mega.py:89-91): judged
-    against the fp64 truth, within 1e-4 and within 3x the fp32 reference path's own error."""
+    Output and every gradient: max relative error <= 1e-5 against the fp32 reference path, and
+    <= 5e-5 on the sums over every token (A_log, dt_bias: test_gdn_mega.py:89-91); gradient
+    cosine >= 0.999999. The sums are also held to the fp32 reference path's own error against
+    the fp64 truth: the kernels form dg without the terms that cancel in the reference's
+    reverse cumsum of d gamma, whose fp32 noise the sums amplify (3.1e-5 on d A_log in the fp32
+    path at this config)."""
     from tjev_amd.testing import cotangent, gdn_inputs
 
     inputs = gdn_inputs(batch=1, length=512, key_heads=4, value_heads=4, dim=64)
@@ -105,12 +107,33 @@ def test_hip_tiny_config_fp32():
     print("tiny fp32 (vs fp32 ref / vs fp64 / fp32 ref vs fp64 / cos):",
           {k: "/".join(f"{x:.1e}" for x in v[:3]) + f"/{v[3]:.8f}" for k, v in report.items()})
     for name, (r32, r64, own, c) in report.items():
+        assert r32 <= TOL[name], (name, report)
         if name in ("A_log", "dt_bias"):
-            assert r64 <= 1e-4 and r64 <= 3 * own, (name, report)
-        else:
-            assert r32 <= 1e-5, (name, report)
+            assert r64 <= own, (name, report)
         if name != "out":
             assert c >= 0.999999, (name, report)
+
+
+def test_hip_reference_high_case():
+    """The reference's precision="high" case ((2, 200, 2, 4), chunk 64, test_gdn_mega.py:111).
+    On its CPU run the reference's dots are fp32 whatever the precision (test_gdn_long.py's
+    emulated_high: "CPU dots are fp32 whatever the precision"), so that case checks fp32
+    arithmetic at the fp32 tolerance: here at "highest" against TOL. Its bf16x3 arithmetic
+    ("high" here, as on the TPU) is held to the reference's emulated-bf16x3 bar
+    (test_gdn_long.py:183-187, relative L2)."""
+    inputs, cot = case_inputs(2, 200, 2, 4, 16)
+    shape = dict(key_heads=2, key_dim=16, value_heads=4, value_dim=16)
+    want = oracle_outputs(inputs, cot, **shape)
+    got = hip_outputs(inputs, cot, chunk=64, precision="highest", **shape)
+    errors = {k: rel(got[k], want[k]) for k in got}
+    high = hip_outputs(inputs, cot, chunk=64, precision="high", **shape)
+    l2 = {k: rel_l2(high[k], want[k]) for k in high}
+    print("reference high case: highest max-rel", {k: f"{v:.1e}" for k, v in errors.items()},
+          "high rel-L2", {k: f"{v:.1e}" for k, v in l2.items()})
+    for name, err in errors.items():
+        assert err < TOL[name], (name, errors)
+    for name, err in l2.items():
+        assert err < HIGH_TOL[name], (name, l2)
 
 
 HIGH_TOL = {"out": 5e-5, "qkv": 5e-5, "a": 1.5e-4, "b": 5e-5, "A_log": 2e-3, "dt_bias": 2e-3, "w": 5e-5}

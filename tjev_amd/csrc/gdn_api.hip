@@ -81,7 +81,8 @@ int validate(const tjev_gdn_params* p) {
 }
 
 struct Layout {
-  size_t segp, qn, kn, vv, gam, gaml, bet, uu, ww, vnew, tt, xl, kt, gg, gsp, dqh, dkh, dgam, dbet, pa, pd, dwp;
+  size_t segp, qn, kn, vv, gam, gaml, bet, uu, ww, vnew, tt, qk, xl, kt, gg, gsp, dqh, dkh, dgam, dkws, dcross, dbet, pa, pd,
+      dwp;
   size_t total;
 };
 
@@ -113,10 +114,12 @@ Layout layout(const tjev_gdn_params* p, int backward) {
   if (!backward) {
     L.uu = take(hv);
     L.ww = take(hv);
-    L.tt = L.xl = L.kt = L.gg = L.gsp = L.dqh = L.dkh = L.dgam = L.dbet = L.pa = L.pd = L.dwp = none;
+    L.tt = L.qk = L.xl = L.kt = L.gg = L.gsp = L.dqh = L.dkh = L.dgam = L.dkws = L.dcross = L.dbet = L.pa = L.pd = L.dwp =
+        none;
   } else {
     L.uu = L.ww = none;
     L.tt = p->residuals == TJEV_GDN_SAVE_STATES ? take(B * H * N * C * C * 4) : none;
+    L.qk = take(B * H * N * C * C * 4);
     L.xl = take(hv);
     L.kt = take(hv);
     L.gg = take(B * H * N * D * D * 4);
@@ -124,6 +127,8 @@ Layout layout(const tjev_gdn_params* p, int backward) {
     L.dqh = take(hv);
     L.dkh = take(hv);
     L.dgam = take(tok);
+    L.dkws = take(tok);
+    L.dcross = take(tok);
     L.dbet = take(tok);
     L.pa = take(B * N * H * 8);
     L.pd = take(B * N * H * 8);
@@ -189,6 +194,7 @@ gdn::GdnArgs base_args(const tjev_gdn_params* p, void* ws, const Layout& L) {
   A.ww = at<float>(ws, L.ww);
   A.vnew = at<float>(ws, L.vnew);
   A.tt = at<float>(ws, L.tt);
+  A.qk = at<float>(ws, L.qk);
   A.xl = at<float>(ws, L.xl);
   A.kt = at<float>(ws, L.kt);
   A.gg = at<float>(ws, L.gg);
@@ -196,6 +202,8 @@ gdn::GdnArgs base_args(const tjev_gdn_params* p, void* ws, const Layout& L) {
   A.dqh = at<float>(ws, L.dqh);
   A.dkh = at<float>(ws, L.dkh);
   A.dgam = at<float>(ws, L.dgam);
+  A.dkws = at<float>(ws, L.dkws);
+  A.dcross = at<float>(ws, L.dcross);
   A.dbet = at<float>(ws, L.dbet);
   A.pa = at<double>(ws, L.pa);
   A.pd = at<double>(ws, L.pd);

@@ -56,13 +56,16 @@ struct GdnArgs {
   float* ww;      // [B, H, Tp, D]   w = T kbe               (forward)
   float* vnew;    // [B, H, Tp, D]   v_new
   float* tt;      // [B, H, N, C, C] T = (I+L)^-1           (backward)
+  float* qk;      // [B, H, N, C, C] q k^T on and below the diagonal tiles (backward)
   float* xl;      // [B, H, Tp, D]   X_loc, then X
   float* kt;      // [B, H, Tp, D]   T^T k_write
   float* gg;      // [B, H, N, D, D] G after each chunk
-  float* gsp;     // [B, H, N, ntiles] <G_after, S_after> per Dv tile
+  float* gsp;     // [B, H, N, ntiles] <G_after, S_before> per Dv tile (d carry)
   float* dqh;     // [B, H, Tp, D]   dq per value head
   float* dkh;     // [B, H, Tp, D]   dk per value head
-  float* dgam;    // [B, H, Tp]
+  float* dgam;    // [B, H, Tp]      d g terms summed over the chunk's later tokens (e^gamma factors)
+  float* dkws;    // [B, H, Tp]      d g terms summed over the chunk's earlier tokens (e^(gamma_C - gamma))
+  float* dcross;  // [B, H, Tp]      d g terms of the token itself (decay pairs across it, the carry)
   float* dbet;    // [B, H, Tp]
   double* pa;     // [B, N, H] partial d A_log (fp64)
   double* pd;     // [B, N, H] partial d dt_bias (fp64)

@@ -49,6 +49,62 @@ __device__ __forceinline__ float gdiff(const Ctx<C>& cx, int i, int j) {
   return (cx.gam[i] - cx.gam[j]) + (cx.gaml[i] - cx.gaml[j]);
 }
 
+// dg_t = sum_{s >= t} a_s + sum_{s < t} f_s + x_t over one chunk's tokens, in fp64 (the
+// gradient of the log decays from k_bwd_grads' three per-token terms). One wave; lane l holds
+// tokens l E .. l E + E - 1 (values of tokens past the chunk are ignored).
+template <int C, int E>
+__device__ __forceinline__ void chunk_dg(const float (&a)[E], const float (&f)[E], const float (&x)[E],
+                                         double (&dg)[E]) {
+  const int l = lane();
+  double sa[E], pf[E], run = 0.0, runf = 0.0;
+#pragma unroll
+  for (int q = E - 1; q >= 0; --q) {  // inclusive suffix of a within the lane
+    run += l * E + q < C ? (double)a[q] : 0.0;
+    sa[q] = run;
+  }
+#pragma unroll
+  for (int q = 0; q < E; ++q) {  // exclusive prefix of f within the lane
+    pf[q] = runf;
+    runf += l * E + q < C ? (double)f[q] : 0.0;
+  }
+  double inc = run, incf = runf;  // across the lanes: a suffix scan of a, a prefix scan of f
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const double dn = __shfl_down(inc, d);
+    const double up = __shfl_up(incf, d);
+    if (l + d < 64) inc += dn;
+    if (l >= d) incf += up;
+  }
+  const double ea = inc - run, ef = incf - runf;
+#pragma unroll
+  for (int q = 0; q < E; ++q) dg[q] = ea + sa[q] + ef + pf[q] + (double)x[q];
+}
+
+// One 16 x 16 tile of E (rows i of the wave's strip at acc_row(rr), columns j = 16 t +
+// acc_col()) into the sums over token pairs across t, x_t = sum_{i >= t > j} E_ij: rp[rr] holds
+// row i's sum over the columns before the tile and is advanced past it; cp gets, for the lane's
+// column t, the sum over the strip's rows i >= t of row i's sum over j < t (diag: the tile on
+// the strip's diagonal, where only rows i >= t count; E is zero for j >= i). The prefixes along
+// a row are DPP shifts within the lane's 16-lane row.
+__device__ __forceinline__ void cross_tile(const f32x4& e, bool diag, float (&rp)[4], float& cp) {
+  const int c = acc_col();
+  float col = 0.f;
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    float inc = e[rr];  // inclusive prefix over the tile's 16 columns (row_shr 1, 2, 4, 8)
+    inc += dpp_read<0x111>(inc);
+    inc += dpp_read<0x112>(inc);
+    inc += dpp_read<0x114>(inc);
+    inc += dpp_read<0x118>(inc);
+    const float pre = rp[rr] + dpp_read<0x111>(inc);  // exclusive: 0 in the row's first lane
+    col += (!diag || acc_row(rr) >= c) ? pre : 0.f;
+    rp[rr] += sum16(e[rr]);
+  }
+  col += __shfl_xor(col, 16);
+  col += __shfl_xor(col, 32);
+  cp += col;
+}
+
 // The per-token inputs of one chunk's context held in registers (thread i < C holds token i):
 // fetch() issues the loads, commit() writes them to the LDS context (derive_ctx then fills in
 // the rest). Needs at least C threads.
@@ -1260,6 +1316,7 @@ __global__ __launch_bounds__(256) void k_conv_state(GdnArgs A) {
 // ---------------------------------------------------------------- k_bwd_local
 // Persistent over the (row, head, chunk) units as k_out; C/16 waves. Per unit:
 // X_loc = T^T (intra^T do) with intra = (q k^T) . D, and Kt = T^T k_write (k_write = kws . k).
+// Also stores q k^T's tiles on and below the diagonal (k_bwd_grads' decay pairs read them).
 // Every global input is read once per unit into registers: the context, q and k (k for both of
 // its stagings: as rows for q k^T, transposed and scaled for k_write^T) are refilled with the
 // next unit's values once used; do and T are loaded at the unit's start and after the product
@@ -1320,6 +1377,10 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
       zero(acc);
       in.q.template product<PI>(acc, ob, 0, w + 1);
       in.fetch_q(A, y, i0);
+      float* qkg = A.qk + ((size_t)x.bh * A.N + x.n) * C * C + (size_t)i0 * C;
+#pragma unroll
+      for (int t = 0; t < C / 16; ++t)  // q k^T below the diagonal, for the decay gradient's pair sums
+        if (t <= w) st_tile(qkg + 16 * t, C, acc[t]);
       const StripDecay<C> sd(cx, i0);
 #pragma unroll
       for (int t = 0; t < C / 16; ++t) {
@@ -1363,24 +1424,21 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
 // ---------------------------------------------------------------- k_scan_bwd
 // grid B*H*(D/DVT) (XCD-remapped), max(C,D)/16 waves. G [D x DVT] in the accumulators of
 // waves < D/16, chunks reversed (pallas_tpu_v2.py:272-291). Also writes, per chunk and tile,
-// <G_after, S_after> (the last token's d gamma term: sum d_kws kws + d_carry carry). As in the
-// forward scan, every global input of a step is held in registers and refilled with the
-// previous chunk's values once used.
+// <G_after, S_before> (d carry, pallas_tpu_v2.py:288). As in the forward scan, every global
+// input of a step is held in registers and refilled with the previous chunk's values once used.
 template <int C, int D, int DVT, int NT, class TIO>
 struct ScanBwdIn {
   PairGates<C> gt;                // wave 0: grow and beta grow of the lane's row pair, and the carry
-  AccVals<DVT / 16> snext;        // S after the chunk, at G's accumulator layout (waves < D/16)
+  AccVals<DVT / 16> sbef;         // S before the chunk, at G's accumulator layout (waves < D/16)
   RegsIO<C, DVT, NT, TIO> dov;    // do columns of the tile, staged as do^T
   StripT<C> qk;                   // the wave's 16 columns of q, staged as (q grow)^T; then of k,
                                   // as (-k beta grow)^T (waves < D/16)
   StripA<D> kt;                   // Kt rows of this wave's strip (waves < C/16)
   AccVals<DVT / 16> xl;           // X_loc at the strip's accumulator layout
   // Loads without branches (a fixed count of memory operations per wave): waves past the
-  // D/16 (C/16) strips load a strip they do not use, and the last chunk loads S before it in
-  // place of the S after it, which does not exist (its partial is 0).
-  __device__ __forceinline__ void fetch_snext(const GdnArgs& A, int bh, int n, int j0) {
-    const int nn = n + 1 < A.N ? n + 1 : n;
-    snext.fetch(A.states + ((size_t)bh * A.N + nn) * D * D + j0, D, 16 * (wave() % (D / 16)));
+  // D/16 (C/16) strips load a strip they do not use.
+  __device__ __forceinline__ void fetch_sbef(const GdnArgs& A, int bh, int n, int j0) {
+    sbef.fetch(A.states + ((size_t)bh * A.N + n) * D * D + j0, D, 16 * (wave() % (D / 16)));
   }
   __device__ __forceinline__ void fetch_do(const GdnArgs& A, int b, int h, int n, int j0) {
     const TIO* dout = reinterpret_cast<const TIO*>(A.d_out);
@@ -1444,7 +1502,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
       in.put_gates(sgate[n & 1]);
       in.gt.fetch(A, b, h, n > n0 ? n - 1 : n, lane() % (C / 2));
     }
-    in.fetch_snext(A, bh, n, j0);
+    in.fetch_sbef(A, bh, n, j0);
     in.fetch_do(A, b, h, n, j0);
     in.fetch_qk(A.qn + hoff(A, b, hk, A.Hk, n, C, D));
     in.fetch_kt(A, b, h, n);
@@ -1456,8 +1514,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
   for (int n = ne; n >= n0; --n) {
     const int nx = n > n0 ? n - 1 : n;  // the last step refetches its own chunk (unused)
     const bool emit = n < n1;           // the replayed chunk n1 only rebuilds G
-    const bool has_next = n + 1 < A.N;
-    float part = 0.f;
+    float part = 0.f;                   // <G after the chunk, S before it> (0 after the last chunk)
     if (NW == D / 16 || w < D / 16) {
       float* gdst = A.gg + ((size_t)bh * A.N + n) * D * D;
 #pragma unroll
@@ -1466,11 +1523,11 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
         for (int rr = 0; rr < 4; ++rr) {
           const float g = accG[t][rr];
           og.put(16 * t + acc_col(), 16 * w + acc_row(rr), g);
-          part += has_next ? g * in.snext.v[t][rr] : 0.f;
+          part += g * in.sbef.v[t][rr];
         }
         if (emit) st_tile(gdst + 16 * w * D + j0 + 16 * t, D, accG[t]);
       }
-      in.fetch_snext(A, bh, nx, j0);
+      in.fetch_sbef(A, bh, nx, j0);
     }
     part = sum64(part);
     if (lane() == 0) red[w] = part;
@@ -1530,25 +1587,38 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
 //   dkb = m1 k - (grow . X) S^T                    dq  = m2 k + (grow . do) S^T
 //   dk' = m1^T (beta k) + m2^T q + (kws . v_new) G^T
 //   dk  = dk' + beta dkb    d beta = rows(dkb, k) + rows(X, v)
-//   d gamma = rows(beta k, dkb) + rows(q, dq) - rows(k, dk')  (+ <G_after, S_after> at the
-//   chunk's last token) -- pallas_tpu_v2.py:272-318 regrouped by shared operands. dkb is folded
-// into dk once complete (rows(k, dk') taken before, and from m2^T q kept apart).
-// rows(X, v) is added by k_post, which rebuilds v. Every input is read from global memory once:
-// each wave holds the X, do and v_new rows of its 16-row strip in registers (the A operands of
-// two products each; v_new's rows are also its share of the B operand of m1 and m2), and the k
-// and q rows of its strip at the accumulator layout (its share of the transposed k and q
-// operands, kept for the row sums). Stages: S, v_new, G, k^T, q^T through one LDS operand
-// region; m1, then m2, in fp32 LDS (read by rows and by columns).
+// (pallas_tpu_v2.py:272-318 regrouped by shared operands; rows(X, v) is added by k_post, which
+// rebuilds v). The gradient of the log decays g is emitted as three per-token terms, combined
+// by k_post in fp64:
+//   dg_t = sum_{s >= t in the chunk} a_s + sum_{s < t} f_s + x_t
+//   a = rows(beta k, dkb) + rows(q, (grow do) S^T) - rows(k, m1^T beta k)
+//   f = rows(k, (kws v_new) G^T)
+//   x_t = sum over token pairs i >= t > j of strict(m2)_ij (q_i . k_j), plus carry <S_before, G_after>
+// This is the reference's d gamma (pallas_tpu_v2.py:306-317) reverse-summed over the chunk,
+// with terms that cancel in that sum left out: the kws terms (f at its token against their sum
+// at the chunk's last), and m2's decay pairs (a pair's row sum against its column sum, summed
+// directly over the pairs across t, with q k^T from k_bwd_local). In fp32 those cancelling
+// terms leave rounding noise in dg that the sums d A_log = sum dg g amplify; m1's pairs, whose
+// noise is an order of magnitude smaller, keep the row-sum form.
+// Every input is read from global memory once: each wave holds the X, do and v_new rows of its
+// 16-row strip in registers (the A operands of two products each; v_new's rows are also the
+// wave's share of the B operand of m1 and m2), and its k and q rows at the accumulator layout
+// (its share of the transposed k and q operands, kept for the row sums). Stages: S, v_new, G,
+// k^T, q^T through one LDS operand region; m1, then m2, in fp32 LDS (read by rows and by
+// columns); the per-token sums through LDS.
 template <int C, int D, int PI, int PS, class TIO>
 __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
   constexpr int NT = C * 4;
   constexpr int LA = C + 4;
   constexpr int M = C > D ? C : D;
   constexpr int TD = D / 16;
+  constexpr int TC = C / 16;
   using TB = OpTile<PI, M, M>;
   __shared__ float sA[C * LA];
   __shared__ __align__(16) char sB[TB::BYTES];
   __shared__ Ctx<C> cx;
+  __shared__ float sga[C], sgf[C], sgb[C];  // a, f and d beta per token
+  __shared__ float sxc[TC * C];             // per wave: its rows' share of x_t for the tokens t of its tiles
   const Op<PI> ob = TB::at(sB);
   const int id = blockIdx.x;
   const int n = id % A.N, bh = id / A.N, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
@@ -1573,14 +1643,14 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
   __syncthreads();
   vn.put_rows(ob, i0);  // v_new: B(dv, j) = v_new[j][dv]
   __syncthreads();
-  f32x4 m2[C / 16];
+  f32x4 m2[TC];
   {  // m1 -> LDS, m2 -> registers
-    f32x4 acc[C / 16];
+    f32x4 acc[TC];
     zero(acc);
     const StripDecay<C> sd(cx, i0);
     xs.template product<PI>(acc, ob, 0, w + 1);
 #pragma unroll
-    for (int t = 0; t < C / 16; ++t) {
+    for (int t = 0; t < TC; ++t) {
       float d[4];
       sd.tile(cx, i0, t, w, d);
 #pragma unroll
@@ -1589,14 +1659,31 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
         lds_st(sA + i * LA + j, i > j ? -acc[t][rr] * d[rr] : 0.f);
       }
     }
+    AccVals<TC> qk;  // q k^T of the strip from k_bwd_local (tiles past the diagonal: the diagonal again)
+    {
+      const float* g = A.qk + ((size_t)bh * A.N + n) * C * C;
+#pragma unroll
+      for (int t = 0; t < TC; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) qk.v[t][rr] = g[(size_t)(i0 + acc_row(rr)) * C + 16 * (t < w ? t : w) + acc_col()];
+    }
     zero(m2);
     dos.template product<exact_a<PI, sizeof(TIO) == 2>()>(m2, ob, 0, w + 1);  // do: bf16 exact
+    float rp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < C / 16; ++t) {
+    for (int t = 0; t < TC; ++t) {
       float d[4];
       sd.tile(cx, i0, t, w, d);
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) m2[t][rr] *= d[rr];
+      if (t <= w) {  // x's pairs: strict(m2) . (q k^T)
+        f32x4 e;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) e[rr] = (t < w || acc_row(rr) > acc_col()) ? m2[t][rr] * qk.v[t][rr] : 0.f;
+        float cp = 0.f;
+        cross_tile(e, t == w, rp, cp);
+        if (lane() < 16) sxc[w * C + 16 * t + lane()] = cp;
+      }
     }
   }
   __syncthreads();
@@ -1611,68 +1698,93 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
 #pragma unroll
   for (int t = 0; t < TD; ++t)  // k^T: B(c, j) = k[c][j]
     ob.put4(16 * t + acc_col(), i0 + acc_row(0), kk.v[t][0], kk.v[t][1], kk.v[t][2], kk.v[t][3]);
+  {  // f = rows(k, (kws v_new) G^T), before m1^T beta k joins dk' (per token, in LDS)
+    float rf[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < TD; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) rf[rr] += kk.v[t][rr] * dk[t][rr];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      rf[rr] = sum16(rf[rr]);
+      if (acc_col() == 0) sgf[i0 + acc_row(rr)] = rf[rr];
+    }
+  }
   __syncthreads();
   strip_mma<PI, C, TD>(dkb, krow(sA, LA), i0, ob, 0, 0, tri_end<C>(i0));                  // m1 k
   strip_mma<PI, C, TD>(dk, scale_k(kcol(sA, LA), cx.beta), i0, ob, 0, tri_begin(i0), C);  // m1^T beta k
-  // dkb is complete: its row sums with k, those of dk' so far, then dkb folded into dk
-  float r3[4] = {0.f, 0.f, 0.f, 0.f}, r4[4] = {0.f, 0.f, 0.f, 0.f};
+  // dkb is complete: its row sums with k (d beta) and those of dk' so far, then dkb folded
+  // into dk. a = rows(beta k, dkb) + rows(q, (grow do) S^T) - rows(k, m1^T beta k): the
+  // e^gamma terms and m1's decay pairs (pallas_tpu_v2.py:306-310) as row sums
+  {
+    float r4[4] = {0.f, 0.f, 0.f, 0.f}, r3[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int t = 0; t < TD; ++t)
+    for (int t = 0; t < TD; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        r4[rr] += dkb[t][rr] * kk.v[t][rr];
+        r3[rr] += kk.v[t][rr] * dk[t][rr];
+        dk[t][rr] += cx.beta[i0 + acc_row(rr)] * dkb[t][rr];
+      }
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      r4[rr] += dkb[t][rr] * kk.v[t][rr];
-      r3[rr] += kk.v[t][rr] * dk[t][rr];
-      dk[t][rr] += cx.beta[i0 + acc_row(rr)] * dkb[t][rr];
+      r4[rr] = sum16(r4[rr]);
+      r3[rr] = sum16(r3[rr]);
+      const int i = i0 + acc_row(rr);
+      if (acc_col() == 0) {
+        sgb[i] = r4[rr];
+        sga[i] = cx.beta[i] * r4[rr] - (r3[rr] - sgf[i]);
+      }
     }
+  }
   __syncthreads();
 #pragma unroll
-  for (int t = 0; t < C / 16; ++t)
+  for (int t = 0; t < TC; ++t)
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) lds_st(sA + (i0 + acc_row(rr)) * LA + 16 * t + acc_col(), m2[t][rr]);
   AccVals<TD> qq;
   qq.fetch(qg, D, i0);
   __syncthreads();
+  {  // a's rows(q, (grow do) S^T), before m2 k joins dq
+    float ra[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < TD; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) ra[rr] += qq.v[t][rr] * dq[t][rr];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      ra[rr] = sum16(ra[rr]);
+      if (acc_col() == 0) sga[i0 + acc_row(rr)] += ra[rr];
+    }
+  }
   strip_mma<PI, C, TD>(dq, krow(sA, LA), i0, ob, 0, 0, tri_end<C>(i0));  // m2 k
   __syncthreads();
 #pragma unroll
   for (int t = 0; t < TD; ++t)  // q^T
     ob.put4(16 * t + acc_col(), i0 + acc_row(0), qq.v[t][0], qq.v[t][1], qq.v[t][2], qq.v[t][3]);
   __syncthreads();
-  f32x4 dk2[TD];  // kept apart from dk, whose rows(k, .) would cancel the folded beta dkb
+  f32x4 dk2[TD];
   zero(dk2);
   strip_mma<PI, C, TD>(dk2, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // m2^T q
-  // epilogue: row sums and the per-value-head dq, dk
-  float r2[4] = {0.f, 0.f, 0.f, 0.f};
+  // epilogue: the per-value-head dq, dk and the per-token gate terms
 #pragma unroll
   for (int t = 0; t < TD; ++t)
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-      r2[rr] += qq.v[t][rr] * dq[t][rr];
-      r3[rr] += kk.v[t][rr] * dk2[t][rr];
       A.dqh[off + i * D + j] = dq[t][rr];
       A.dkh[off + i * D + j] = dk[t][rr] + dk2[t][rr];
     }
-#pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    r2[rr] = sum16(r2[rr]);
-    r3[rr] = sum16(r3[rr]);
-    r4[rr] = sum16(r4[rr]);
-  }
-  if (acc_col() == 0) {
-    const size_t tok = (size_t)bh * A.Tp + (size_t)n * C;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int i = i0 + acc_row(rr);
-      float dgm = cx.beta[i] * r4[rr] + r2[rr] - r3[rr];
-      if (i == C - 1) {
-        float s = 0.f;
-        for (int q = 0; q < A.ntiles; ++q) s += A.gsp[((size_t)bh * A.N + n) * A.ntiles + q];
-        dgm += s;
-      }
-      A.dgam[tok + i] = dgm;
-      A.dbet[tok + i] = r4[rr];
-    }
+  const size_t tok = (size_t)bh * A.Tp + (size_t)n * C;
+  if (threadIdx.x < C) {  // the per-token terms; x_t: the waves' pair sums and the carry term
+    const int t = threadIdx.x;
+    float x = 0.f, dcarry = 0.f;
+    for (int v = t / 16; v < TC; ++v) x += sxc[v * C + t];
+    for (int q = 0; q < A.ntiles; ++q) dcarry += A.gsp[((size_t)bh * A.N + n) * A.ntiles + q];
+    A.dgam[tok + t] = sga[t];
+    A.dkws[tok + t] = sgf[t];
+    A.dbet[tok + t] = sgb[t];
+    A.dcross[tok + t] = x + cx.carry * dcarry;
   }
 }
 
@@ -1713,7 +1825,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   constexpr int E = (C + 63) / 64;
   const bool gate_wave = kind == 2 && threadIdx.x < 64;
   const size_t tok = (size_t)(b * A.H + head) * A.Tp + (size_t)n * C;
-  float gdg[E], gdb[E], gav[E], gbv[E];
+  float gdg[E], gdk[E], gdx[E], gdb[E], gav[E], gbv[E];
   if (gate_wave) {
     const TG* ga = reinterpret_cast<const TG*>(A.ga);
     const TG* gb = reinterpret_cast<const TG*>(A.gb);
@@ -1722,6 +1834,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
       const int i = threadIdx.x * E + q, t = n * C + i;
       const int ic = i < C ? i : C - 1, tc = t < A.T ? t : A.T - 1;
       gdg[q] = A.dgam[tok + ic];
+      gdk[q] = A.dkws[tok + ic];
+      gdx[q] = A.dcross[tok + ic];
       gdb[q] = A.dbet[tok + ic];
       gav[q] = ldf(ga + ((size_t)b * A.T + tc) * A.H + head);
       gbv[q] = ldf(gb + ((size_t)b * A.T + tc) * A.H + head);
@@ -1917,21 +2031,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     TG* da = reinterpret_cast<TG*>(A.d_a);
     TG* db = reinterpret_cast<TG*>(A.d_b);
     const float ea = expf(A.a_log[head]), dtb = A.dt_bias[head];
-    // dg = reverse in-chunk cumsum of d gamma, and the A_log / dt_bias partial sums, in fp64
-    double dgv[E], run = 0.0;
-#pragma unroll
-    for (int q = E - 1; q >= 0; --q) {
-      const int i = l * E + q;
-      run += i < C ? (double)gdg[q] : 0.0;
-      dgv[q] = run;  // inclusive suffix within the lane
-    }
-    double inc = run;  // inclusive suffix scan of lane totals
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const double dn = __shfl_down(inc, d);
-      if (l + d < 64) inc += dn;
-    }
-    const double excl = inc - run;
+    // dg from its three per-token terms, and the A_log / dt_bias partial sums, in fp64
+    double dgv[E];
+    chunk_dg<C, E>(gdg, gdk, gdx, dgv);
     double sa = 0.0, sd = 0.0;
 #pragma unroll
     for (int q = 0; q < E; ++q) {
@@ -1940,7 +2042,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         const bool in = t < A.T;
         const float av = in ? gav[q] : 0.f;
         const float bv = in ? gbv[q] : 0.f;
-        const double dg = excl + dgv[q];
+        const double dg = dgv[q];
         const float xg = av + dtb;
         const float g = -ea * softplusf_(xg);
         const double dad = dg * (double)(-ea * sigmoidf_(xg));

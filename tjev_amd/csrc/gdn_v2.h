@@ -137,25 +137,21 @@ __global__ __launch_bounds__(256) void k_post_v2(GdnArgs A) {
     TG* dg = reinterpret_cast<TG*>(A.d_g2);
     TG* db = reinterpret_cast<TG*>(A.d_b2);
     const size_t tok = (size_t)(b * A.H + head) * A.Tp + (size_t)n * C;
-    double dgv[E], run = 0.0;
+    float ta[E], tf[E], tx[E];
 #pragma unroll
-    for (int q = E - 1; q >= 0; --q) {
-      const int i = l * E + q;
-      run += i < C ? (double)A.dgam[tok + i] : 0.0;
-      dgv[q] = run;
+    for (int q = 0; q < E; ++q) {
+      const int ic = l * E + q < C ? l * E + q : C - 1;
+      ta[q] = A.dgam[tok + ic];
+      tf[q] = A.dkws[tok + ic];
+      tx[q] = A.dcross[tok + ic];
     }
-    double inc = run;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const double dn = __shfl_down(inc, d);
-      if (l + d < 64) inc += dn;
-    }
-    const double excl = inc - run;
+    double dgv[E];
+    chunk_dg<C, E>(ta, tf, tx, dgv);
 #pragma unroll
     for (int q = 0; q < E; ++q) {
       const int i = l * E + q, t = n * C + i;
       if (i < C && t < A.T) {
-        stf(dg + ((size_t)b * A.T + t) * A.H + head, (float)(excl + dgv[q]));
+        stf(dg + ((size_t)b * A.T + t) * A.H + head, (float)dgv[q]);
         stf(db + ((size_t)b * A.T + t) * A.H + head, A.dbet[tok + i] + sxv[i]);
       }
     }
