@@ -111,6 +111,39 @@ int tjev_gdn_mega2_fwd_state(const tjev_gdn_params* p, void* stream, const void*
                              float* final_state, void* conv_state, void* workspace,
                              size_t workspace_bytes);
 
+/* A sequence continued from an earlier call (a long prompt prefilled in pieces, a prefill that
+ * resumes a cached state): the chunked rule with an initial state (xla.py:170-262,
+ * `initial_state`; test_gated_delta_rule.py:61-73), and the conv over the rows before token 0.
+ * initial_state [B, H, Dk, Dv] fp32: the state before token 0, read by chunk 0's tokens of token
+ * 0's segment (chunk 0's "token before" is token 0's id instead of -2, xla.py:214-216);
+ * initial_conv [B, K-1, W] io_dtype: the raw rows before token 0, oldest first, read by the
+ * conv of token 0's segment (as conv_state below returns them). Either may be null (a fresh
+ * start: state 0; no rows before the row). final_state and conv_state as for
+ * tjev_gdn_mega2_fwd_state (null: not written). With both inputs null this is
+ * tjev_gdn_mega2_fwd_state. No counterpart in the megakernel, which starts every row fresh. */
+int tjev_gdn_mega2_fwd_cont(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a,
+                            const void* b, const float* a_log, const float* dt_bias,
+                            const float* conv_w, const int32_t* seg, const float* initial_state,
+                            const void* initial_conv, void* out, float* residuals,
+                            float* final_state, void* conv_state, void* workspace,
+                            size_t workspace_bytes);
+
+/* The backward of tjev_gdn_mega2_fwd_cont: initial_state and initial_conv as given to the forward
+ * (initial_state's values are in the residuals; only whether it is null matters here);
+ * d_final_state [B, H, Dk, Dv] fp32, the gradient of the forward's final_state (null: 0; needs
+ * a length that is a multiple of the kernels' chunk, else TJEV_GDN_EUNSUPPORTED). Writes, beside
+ * tjev_gdn_mega2_bwd's outputs, d_initial_state [B, H, Dk, Dv] fp32 and d_initial_conv
+ * [B, K-1, W] io_dtype when not null (each needs its input). The gradient of the forward's
+ * conv_state is that of rows of qkv or initial_conv: the caller adds it there. */
+int tjev_gdn_mega2_bwd_cont(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a,
+                            const void* b, const float* a_log, const float* dt_bias,
+                            const float* conv_w, const int32_t* seg, const float* initial_state,
+                            const void* initial_conv, const float* residuals, const void* d_out,
+                            const float* d_final_state, void* d_qkv, void* d_a, void* d_b,
+                            float* d_a_log, float* d_dt_bias, float* d_conv_w,
+                            float* d_initial_state, void* d_initial_conv, void* workspace,
+                            size_t workspace_bytes);
+
 /* One decode step, T = 1 token per row (p->length == 1; chunk and residuals are ignored):
  * the reference's token recurrence (xla.py:141-167, its "T=1 decode step") on the
  * megakernel's inputs, with the conv over the kept rows (HF causal_conv1d_update). qkv [B, W]
@@ -137,6 +170,23 @@ int tjev_gdn_v2_bwd(const tjev_gdn_params* p, void* stream, const void* q, const
                     const void* g, const void* beta, const int32_t* seg, const float* residuals,
                     const void* d_out, void* d_q, void* d_k, void* d_v, void* d_g, void* d_beta,
                     void* workspace, size_t workspace_bytes);
+
+/* The v2 operator with a state in and out: the reference's chunked rule
+ * chunk_gated_delta_rule(q, k, v, g, beta, segment_ids, initial_state) -> (out, final_state)
+ * (xla.py:170-262) on the v2 operator's inputs. initial_state [B, H, Dk, Dv] fp32 or null (as
+ * for tjev_gdn_mega2_fwd_cont); final_state [B, H, Dk, Dv] fp32 or null: the state after token
+ * T-1. The backward takes initial_state as given to the forward, d_final_state (null: 0; a length
+ * that is a multiple of the kernels' chunk) and writes d_initial_state when not null. */
+int tjev_gdn_v2_fwd_cont(const tjev_gdn_params* p, void* stream, const void* q, const void* k,
+                         const void* v, const void* g, const void* beta, const int32_t* seg,
+                         const float* initial_state, void* out, float* residuals,
+                         float* final_state, void* workspace, size_t workspace_bytes);
+int tjev_gdn_v2_bwd_cont(const tjev_gdn_params* p, void* stream, const void* q, const void* k,
+                         const void* v, const void* g, const void* beta, const int32_t* seg,
+                         const float* initial_state, const float* residuals, const void* d_out,
+                         const float* d_final_state, void* d_q, void* d_k, void* d_v, void* d_g,
+                         void* d_beta, float* d_initial_state, void* workspace,
+                         size_t workspace_bytes);
 
 /* backward: replaces pallas_call "gdn_mega2_bwd" (pallas_tpu_mega.py:471-524) plus the XLA sums
  * of _core_bwd (:563-571): d_qkv (io_dtype), d_a, d_b (gate_dtype), d_a_log and d_dt_bias ([H] fp32), and,

@@ -249,7 +249,11 @@ def test_ds_check_flags_the_miscompiled_merge_only():
 
 def test_decode_step_validation():
     """The decode step's checks, before any launch: one token per row, grouped heads, a
-    history buffer distinct from the one it reads, non-null and 16-byte aligned tensors."""
+    history buffer distinct from the one it reads, non-null and 16-byte aligned tensors. The
+    buffers are made-up addresses (the calls must fail validation): not run where a GPU is
+    visible, so that a regressed check cannot launch on them."""
+    if torch.cuda.is_available():
+        pytest.skip("host-side validation with made-up device addresses: CPU only")
     from tjev_amd import _lib
 
     lib = _lib.load()
@@ -310,3 +314,62 @@ def test_kernel_roofline_takes_the_longer_ideal_time():
     r = kernel_roofline(w["gdn_bwd_grads"], 338e-6, PEAK_FP32_TFLOPS)
     assert r["bound"] == "mfma" and r["unit"] == "TFLOP/s" and r["frac"] == r["mfma_frac"]
     assert kernel_roofline(w["gdn_post"], 270e-6, PEAK_FP32_TFLOPS)["bound"] == "hbm"
+
+
+def test_state_entry_points_validate_before_launch():
+    """The continued-sequence entry points (an initial state and conv history in, the final
+    ones out): their checks come before the workspace's, and every call here passes no
+    workspace, so none can launch: a conv history needs a conv of 2+ taps, a gradient needs its
+    input, the final state's gradient needs whole chunks, state tensors are 16-byte aligned."""
+    from tjev_amd import _lib
+
+    lib = _lib.load()
+    vp = lambda i: ctypes.c_void_p(4096 * (i + 1))  # noqa: E731  (256-byte aligned, never dereferenced)
+    ws = ctypes.c_void_p(4096 * 64)
+
+    def fwd(p, init=None, hist=None, final=None, cs=None):
+        return lib.tjev_gdn_mega2_fwd_cont(ctypes.byref(p), None, *[vp(i) for i in range(7)], init, hist, vp(8),
+                                           vp(9), final, cs, ws, 0)
+
+    def bwd(p, init=None, hist=None, d_final=None, d_init=None, d_hist=None):
+        return lib.tjev_gdn_mega2_bwd_cont(ctypes.byref(p), None, *[vp(i) for i in range(7)], init, hist, vp(9),
+                                           vp(10), d_final, *[vp(11 + i) for i in range(6)], d_init, d_hist, ws, 0)
+
+    p = _params(length=96, chunk=16)
+    assert fwd(p) == 3 and "workspace" in lib.tjev_gdn_last_error().decode()  # all checks passed
+    assert fwd(p, init=vp(20), hist=vp(21), final=vp(22), cs=vp(23)) == 3
+    assert fwd(_params(taps=1), hist=vp(21)) == 1 and "2 or more taps" in lib.tjev_gdn_last_error().decode()
+    assert fwd(_params(taps=0), cs=vp(23)) == 1
+    assert fwd(p, init=ctypes.c_void_p(4096 * 20 + 8)) == 1
+    assert "16-byte aligned" in lib.tjev_gdn_last_error().decode()
+    assert bwd(p, init=vp(20), hist=vp(21), d_final=vp(22), d_init=vp(23), d_hist=vp(24)) == 3
+    assert bwd(p, d_init=vp(23)) == 1 and "needs the initial state" in lib.tjev_gdn_last_error().decode()
+    assert bwd(p, init=vp(20), d_hist=vp(24)) == 1 and "needs the conv history" in lib.tjev_gdn_last_error().decode()
+    assert bwd(_params(length=100, chunk=16), d_final=vp(22)) == 2
+    assert "multiple of the chunk" in lib.tjev_gdn_last_error().decode()
+    # the v2 forms
+    p0 = _params(taps=0, length=96, chunk=16)
+    assert lib.tjev_gdn_v2_fwd_cont(ctypes.byref(p0), None, *[vp(i) for i in range(6)], vp(20), vp(7), vp(8),
+                                    vp(9), ws, 0) == 3
+    assert lib.tjev_gdn_v2_bwd_cont(ctypes.byref(p0), None, *[vp(i) for i in range(6)], None, vp(8), vp(9),
+                                    None, *[vp(10 + i) for i in range(5)], vp(16), ws, 0) == 1
+    assert "needs the initial state" in lib.tjev_gdn_last_error().decode()
+    assert lib.tjev_gdn_v2_bwd_cont(ctypes.byref(_params(taps=0, length=90, chunk=16)), None,
+                                    *[vp(i) for i in range(6)], vp(20), vp(8), vp(9), vp(21),
+                                    *[vp(10 + i) for i in range(5)], vp(16), ws, 0) == 2
+
+
+def test_state_operators_reject_cpu_tensors_and_bad_shapes():
+    from tjev_amd import gdn_megakernel
+    from tjev_amd.v2 import chunk_gated_delta_rule
+
+    x = torch.zeros(1, 16, 2 * 16 + 2 * 16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        gdn_megakernel(x, torch.zeros(1, 16, 2), torch.zeros(1, 16, 2), torch.zeros(2), torch.zeros(2),
+                       torch.zeros(4, 64), torch.ones(1, 16, dtype=torch.int32), key_heads=1, key_dim=16,
+                       value_heads=2, value_dim=16, initial_state=torch.zeros(1, 2, 16, 16))
+    q = torch.zeros(1, 16, 2, 16)
+    with pytest.raises(ValueError, match="inverse in"):
+        chunk_gated_delta_rule(q, q, q, torch.zeros(1, 16, 2), torch.zeros(1, 16, 2), inverse="lu")
+    with pytest.raises(RuntimeError, match="GPU"):
+        chunk_gated_delta_rule(q, q, q, torch.zeros(1, 16, 2), torch.zeros(1, 16, 2))

@@ -27,9 +27,13 @@ EXPORTS = (
     "tjev_gdn_workspace_bytes",
     "tjev_gdn_mega2_fwd",
     "tjev_gdn_mega2_fwd_state",
+    "tjev_gdn_mega2_fwd_cont",
+    "tjev_gdn_mega2_bwd_cont",
     "tjev_gdn_decode_step",
     "tjev_gdn_v2_fwd",
     "tjev_gdn_v2_bwd",
+    "tjev_gdn_v2_fwd_cont",
+    "tjev_gdn_v2_bwd_cont",
     "tjev_gdn_mega2_bwd",
     "tjev_gdn_norm_workspace_bytes",
     "tjev_gdn_gated_rmsnorm_fwd",
@@ -92,6 +96,14 @@ def load() -> ctypes.CDLL:
     lib.tjev_gdn_mega2_fwd.restype = i32
     lib.tjev_gdn_mega2_fwd_state.argtypes = [pp, vp] + [vp] * 12 + [sz]
     lib.tjev_gdn_mega2_fwd_state.restype = i32
+    lib.tjev_gdn_mega2_fwd_cont.argtypes = [pp, vp] + [vp] * 14 + [sz]
+    lib.tjev_gdn_mega2_fwd_cont.restype = i32
+    lib.tjev_gdn_mega2_bwd_cont.argtypes = [pp, vp] + [vp] * 21 + [sz]
+    lib.tjev_gdn_mega2_bwd_cont.restype = i32
+    lib.tjev_gdn_v2_fwd_cont.argtypes = [pp, vp] + [vp] * 11 + [sz]
+    lib.tjev_gdn_v2_fwd_cont.restype = i32
+    lib.tjev_gdn_v2_bwd_cont.argtypes = [pp, vp] + [vp] * 17 + [sz]
+    lib.tjev_gdn_v2_bwd_cont.restype = i32
     lib.tjev_gdn_decode_step.argtypes = [pp, vp] + [vp] * 11
     lib.tjev_gdn_decode_step.restype = i32
     lib.tjev_gdn_v2_fwd.argtypes = [pp, vp] + [vp] * 9 + [sz]

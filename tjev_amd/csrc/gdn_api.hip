@@ -307,14 +307,34 @@ size_t tjev_gdn_workspace_bytes(const tjev_gdn_params* p, int backward) {
   return layout(p, backward).total;
 }
 
-int tjev_gdn_mega2_fwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
-                       const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg, void* out,
-                       float* residuals, void* workspace, size_t workspace_bytes) {
+// the state arguments of a continued sequence, shared by the _cont entry points
+int check_state(const tjev_gdn_params* p, const void* initial_state, const void* initial_conv, const void* d_final,
+                const void* d_initial_state, const void* d_initial_conv) {
+  if (p->taps <= 1 && (initial_conv || d_initial_conv))
+    return fail(TJEV_GDN_EINVAL, "a conv history needs a conv of 2 or more taps");
+  if (d_initial_conv && !initial_conv)
+    return fail(TJEV_GDN_EINVAL, "the conv history's gradient needs the conv history");
+  if (d_initial_state && !initial_state)
+    return fail(TJEV_GDN_EINVAL, "the initial state's gradient needs the initial state");
+  for (const void* q : {initial_state, initial_conv, d_final, d_initial_state, d_initial_conv})
+    if (q && !aligned(q, 16)) return fail(TJEV_GDN_EINVAL, "state tensors must be 16-byte aligned");
+  if (d_final && p->length % kernel_chunk(p))
+    return fail(TJEV_GDN_EUNSUPPORTED, "the final state's gradient needs a length that is a multiple of the chunk (" +
+                                           std::to_string(kernel_chunk(p)) + ")");
+  return 0;
+}
+
+int tjev_gdn_mega2_fwd_cont(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
+                            const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg,
+                            const float* initial_state, const void* initial_conv, void* out, float* residuals,
+                            float* final_state, void* conv_state, void* workspace, size_t workspace_bytes) {
   if (int s = validate(p)) return s;
   if (!qkv || !a || !b || !a_log || !dt_bias || !seg || !out || !residuals || (p->taps > 0 && !conv_w))
     return fail(TJEV_GDN_EINVAL, "null tensor argument");
   if (!aligned(qkv, 16) || !aligned(out, 16) || !aligned(residuals, 256) || !aligned(workspace, 256))
     return fail(TJEV_GDN_EINVAL, "qkv and out must be 16-byte aligned, the residuals and workspace 256-byte aligned");
+  if (int s = check_state(p, initial_state, initial_conv, nullptr, nullptr, nullptr)) return s;
+  if (p->taps <= 1 && conv_state) return fail(TJEV_GDN_EINVAL, "a conv history needs a conv of 2 or more taps");
   const Layout L = layout(p, 0);
   if (!workspace || workspace_bytes < L.total)
     return fail(TJEV_GDN_EWORKSPACE, "forward workspace needs " + std::to_string(L.total) + " bytes");
@@ -328,45 +348,38 @@ int tjev_gdn_mega2_fwd(const tjev_gdn_params* p, void* stream, const void* qkv, 
   A.seg = seg;
   A.out = out;
   bind_residuals(p, residuals, A);
+  A.init_state = initial_state;
+  A.init_conv = initial_conv;
+  A.final_state = final_state;
+  A.conv_state = conv_state;
   return run(p, stream, A, 0);
+}
+
+int tjev_gdn_mega2_fwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
+                       const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg, void* out,
+                       float* residuals, void* workspace, size_t workspace_bytes) {
+  return tjev_gdn_mega2_fwd_cont(p, stream, qkv, a, b, a_log, dt_bias, conv_w, seg, nullptr, nullptr, out, residuals,
+                                 nullptr, nullptr, workspace, workspace_bytes);
 }
 
 int tjev_gdn_mega2_fwd_state(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
                              const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg,
                              void* out, float* residuals, float* final_state, void* conv_state, void* workspace,
                              size_t workspace_bytes) {
-  if (int s = validate(p)) return s;
-  if (!qkv || !a || !b || !a_log || !dt_bias || !seg || !out || !residuals || (p->taps > 0 && !conv_w))
-    return fail(TJEV_GDN_EINVAL, "null tensor argument");
-  if (!aligned(qkv, 16) || !aligned(out, 16) || !aligned(residuals, 256) || !aligned(workspace, 256))
-    return fail(TJEV_GDN_EINVAL, "qkv and out must be 16-byte aligned, the residuals and workspace 256-byte aligned");
-  const Layout L = layout(p, 0);
-  if (!workspace || workspace_bytes < L.total)
-    return fail(TJEV_GDN_EWORKSPACE, "forward workspace needs " + std::to_string(L.total) + " bytes");
-  gdn::GdnArgs A = base_args(p, workspace, L);
-  A.qkv = qkv;
-  A.ga = a;
-  A.gb = b;
-  A.a_log = a_log;
-  A.dt_bias = dt_bias;
-  A.conv_w = conv_w;
-  A.seg = seg;
-  A.out = out;
-  bind_residuals(p, residuals, A);
-  A.final_state = final_state;
-  A.conv_state = conv_state;
-  return run(p, stream, A, 0);
+  return tjev_gdn_mega2_fwd_cont(p, stream, qkv, a, b, a_log, dt_bias, conv_w, seg, nullptr, nullptr, out, residuals,
+                                 final_state, conv_state, workspace, workspace_bytes);
 }
 
-int tjev_gdn_v2_fwd(const tjev_gdn_params* p, void* stream, const void* q, const void* k, const void* v,
-                    const void* g, const void* beta, const int32_t* seg, void* out, float* residuals, void* workspace,
-                    size_t workspace_bytes) {
+int tjev_gdn_v2_fwd_cont(const tjev_gdn_params* p, void* stream, const void* q, const void* k, const void* v,
+                         const void* g, const void* beta, const int32_t* seg, const float* initial_state, void* out,
+                         float* residuals, float* final_state, void* workspace, size_t workspace_bytes) {
   if (int s = validate(p)) return s;
   if (p->taps != 0) return fail(TJEV_GDN_EINVAL, "the v2 operator has no conv: taps must be 0");
   if (!q || !k || !v || !g || !beta || !seg || !out || !residuals) return fail(TJEV_GDN_EINVAL, "null tensor argument");
   if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16) || !aligned(residuals, 256) ||
       !aligned(workspace, 256))
     return fail(TJEV_GDN_EINVAL, "q, k, v and out must be 16-byte aligned, the residuals and workspace 256-byte aligned");
+  if (int s = check_state(p, initial_state, nullptr, nullptr, nullptr, nullptr)) return s;
   const Layout L = layout(p, 0);
   if (!workspace || workspace_bytes < L.total)
     return fail(TJEV_GDN_EWORKSPACE, "forward workspace needs " + std::to_string(L.total) + " bytes");
@@ -379,13 +392,23 @@ int tjev_gdn_v2_fwd(const tjev_gdn_params* p, void* stream, const void* q, const
   A.seg = seg;
   A.out = out;
   bind_residuals(p, residuals, A);
+  A.init_state = initial_state;
+  A.final_state = final_state;
   return run_v2(p, stream, A, 0);
 }
 
-int tjev_gdn_v2_bwd(const tjev_gdn_params* p, void* stream, const void* q, const void* k, const void* v,
-                    const void* g, const void* beta, const int32_t* seg, const float* residuals, const void* d_out,
-                    void* d_q, void* d_k, void* d_v, void* d_g, void* d_beta, void* workspace,
+int tjev_gdn_v2_fwd(const tjev_gdn_params* p, void* stream, const void* q, const void* k, const void* v,
+                    const void* g, const void* beta, const int32_t* seg, void* out, float* residuals, void* workspace,
                     size_t workspace_bytes) {
+  return tjev_gdn_v2_fwd_cont(p, stream, q, k, v, g, beta, seg, nullptr, out, residuals, nullptr, workspace,
+                              workspace_bytes);
+}
+
+int tjev_gdn_v2_bwd_cont(const tjev_gdn_params* p, void* stream, const void* q, const void* k, const void* v,
+                         const void* g, const void* beta, const int32_t* seg, const float* initial_state,
+                         const float* residuals, const void* d_out, const float* d_final_state, void* d_q, void* d_k,
+                         void* d_v, void* d_g, void* d_beta, float* d_initial_state, void* workspace,
+                         size_t workspace_bytes) {
   if (int s = validate(p)) return s;
   if (p->taps != 0) return fail(TJEV_GDN_EINVAL, "the v2 operator has no conv: taps must be 0");
   if (!q || !k || !v || !g || !beta || !seg || !residuals || !d_out || !d_q || !d_k || !d_v || !d_g || !d_beta)
@@ -393,6 +416,7 @@ int tjev_gdn_v2_bwd(const tjev_gdn_params* p, void* stream, const void* q, const
   if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(d_out, 16) || !aligned(d_q, 16) ||
       !aligned(d_k, 16) || !aligned(d_v, 16) || !aligned(residuals, 256) || !aligned(workspace, 256))
     return fail(TJEV_GDN_EINVAL, "tensors must be 16-byte aligned, the residuals and workspace 256-byte aligned");
+  if (int s = check_state(p, initial_state, nullptr, d_final_state, d_initial_state, nullptr)) return s;
   const Layout L = layout(p, 1);
   if (!workspace || workspace_bytes < L.total)
     return fail(TJEV_GDN_EWORKSPACE, "backward workspace needs " + std::to_string(L.total) + " bytes");
@@ -410,13 +434,26 @@ int tjev_gdn_v2_bwd(const tjev_gdn_params* p, void* stream, const void* q, const
   A.d_v2 = d_v;
   A.d_g2 = d_g;
   A.d_b2 = d_beta;
+  A.init_state = initial_state;
+  A.d_final = d_final_state;
+  A.d_init_state = d_initial_state;
   return run_v2(p, stream, A, 1);
 }
 
-int tjev_gdn_mega2_bwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
-                       const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg,
-                       const float* residuals, const void* d_out, void* d_qkv, void* d_a, void* d_b, float* d_a_log,
-                       float* d_dt_bias, float* d_conv_w, void* workspace, size_t workspace_bytes) {
+int tjev_gdn_v2_bwd(const tjev_gdn_params* p, void* stream, const void* q, const void* k, const void* v,
+                    const void* g, const void* beta, const int32_t* seg, const float* residuals, const void* d_out,
+                    void* d_q, void* d_k, void* d_v, void* d_g, void* d_beta, void* workspace,
+                    size_t workspace_bytes) {
+  return tjev_gdn_v2_bwd_cont(p, stream, q, k, v, g, beta, seg, nullptr, residuals, d_out, nullptr, d_q, d_k, d_v, d_g,
+                              d_beta, nullptr, workspace, workspace_bytes);
+}
+
+int tjev_gdn_mega2_bwd_cont(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
+                            const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg,
+                            const float* initial_state, const void* initial_conv, const float* residuals,
+                            const void* d_out, const float* d_final_state, void* d_qkv, void* d_a, void* d_b,
+                            float* d_a_log, float* d_dt_bias, float* d_conv_w, float* d_initial_state,
+                            void* d_initial_conv, void* workspace, size_t workspace_bytes) {
   if (int s = validate(p)) return s;
   if (!qkv || !a || !b || !a_log || !dt_bias || !seg || !residuals || !d_out || !d_qkv || !d_a || !d_b || !d_a_log ||
       !d_dt_bias || (p->taps > 0 && !conv_w))
@@ -425,6 +462,7 @@ int tjev_gdn_mega2_bwd(const tjev_gdn_params* p, void* stream, const void* qkv, 
   if (!aligned(qkv, 16) || !aligned(d_out, 16) || !aligned(d_qkv, 16) || !aligned(residuals, 256) ||
       !aligned(workspace, 256))
     return fail(TJEV_GDN_EINVAL, "tensors must be 16-byte aligned, the residuals and workspace 256-byte aligned");
+  if (int s = check_state(p, initial_state, initial_conv, d_final_state, d_initial_state, d_initial_conv)) return s;
   const Layout L = layout(p, 1);
   if (!workspace || workspace_bytes < L.total)
     return fail(TJEV_GDN_EWORKSPACE, "backward workspace needs " + std::to_string(L.total) + " bytes");
@@ -444,7 +482,21 @@ int tjev_gdn_mega2_bwd(const tjev_gdn_params* p, void* stream, const void* qkv, 
   A.d_a_log = d_a_log;
   A.d_dt_bias = d_dt_bias;
   A.d_conv_w = d_conv_w;
+  A.init_state = initial_state;
+  A.init_conv = initial_conv;
+  A.d_final = d_final_state;
+  A.d_init_state = d_initial_state;
+  A.d_init_conv = d_initial_conv;
   return run(p, stream, A, 1);
+}
+
+int tjev_gdn_mega2_bwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
+                       const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg,
+                       const float* residuals, const void* d_out, void* d_qkv, void* d_a, void* d_b, float* d_a_log,
+                       float* d_dt_bias, float* d_conv_w, void* workspace, size_t workspace_bytes) {
+  return tjev_gdn_mega2_bwd_cont(p, stream, qkv, a, b, a_log, dt_bias, conv_w, seg, nullptr, nullptr, residuals, d_out,
+                                 nullptr, d_qkv, d_a, d_b, d_a_log, d_dt_bias, d_conv_w, nullptr, nullptr, workspace,
+                                 workspace_bytes);
 }
 
 int tjev_gdn_profile_begin(void) {

@@ -25,6 +25,14 @@ struct GdnArgs {
   float* states;       // [B, H, N, Dk, Dv]
   float* final_state;  // [B, H, Dk, Dv] the state after token T-1 (or null)
   void* conv_state;    // [B, K-1, W] the raw rows before token T (or null)
+  // a sequence continued from an earlier call: the state before token 0 (chunk 0's tokens of
+  // token 0's segment read it) and the K-1 raw rows before token 0 (token 0's segment); null:
+  // a fresh start (state 0, chunk 0 reads nothing; no rows before the row)
+  const float* init_state;  // [B, H, Dk, Dv]
+  const void* init_conv;    // [B, K-1, W] io dtype
+  const float* d_final;     // [B, H, Dk, Dv] the gradient of final_state (or null: 0)
+  float* d_init_state;      // [B, H, Dk, Dv] (or null)
+  void* d_init_conv;        // [B, K-1, W] io dtype (or null)
   // the v2 operator's inputs q, k [B,T,Hk,D], v [B,T,H,D], g, beta [B,T,H] and their gradients
   const void* q2;
   const void* k2;

@@ -122,6 +122,7 @@ hipError_t run_v2(const GdnArgs& A, hipStream_t st, int backward, const Timer* t
     }
     GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd<C, D, DVT, PI, PS>), tiles, dim3(NS));
     GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO>), persist, dim3(C * 4));
+    if (A.final_state) GDN_LAUNCH(K_FINAL_STATE, (k_final_state<C, D>), dim3(A.B * A.H * (D / DVT)), dim3(256));
   } else {
     GDN_LAUNCH(K_PREP_BWD, (k_prep_v2<C, D, TIO, TQK, TG>), ends, dim3(256));
     if (A.res == 0) {

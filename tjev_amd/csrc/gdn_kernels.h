@@ -32,8 +32,9 @@ __device__ __forceinline__ size_t hoff(const GdnArgs& A, int b, int head, int he
 
 // ---------------------------------------------------------------- chunk context
 // Segment semantics (pallas_tpu_v2.py:226-241, pallas_tpu_mega.py:349-361): cont_i: token i
-// reads the incoming state (same id as the previous chunk's last token; -2 before chunk 0);
-// in_last_i: token i writes the outgoing state (same id as the chunk's last token).
+// reads the incoming state (same id as the previous chunk's last token; before chunk 0: -2, or
+// token 0's id when the sequence continues from an initial state, xla.py:214-216); in_last_i:
+// token i writes the outgoing state (same id as the chunk's last token).
 template <int C>
 struct Ctx {
   int seg[C];
@@ -112,7 +113,7 @@ template <int C>
 struct CtxRaw {
   int seg, before;
   float gam, gaml, beta;
-  bool first;  // chunk 0: the token before it is "-2" (the loaded value is not used)
+  bool first;  // chunk 0: the token before it is "-2", or token 0's id (loaded) with an initial state
   // Every thread loads (threads past C repeat token threadIdx.x % C), with no branch around the
   // loads: a fixed count of memory operations per wave lets the compiler wait for exactly the
   // loads it needs instead of for all outstanding ones.
@@ -124,7 +125,7 @@ struct CtxRaw {
     gaml = A.gaml[tok];
     beta = A.bet[tok];
     before = A.segp[(size_t)b * A.Tp + (n > 0 ? (size_t)n * C - 1 : 0)];
-    first = n == 0;
+    first = n == 0 && !A.init_state;
   }
   __device__ __forceinline__ void commit(Ctx<C>& cx) const {
     const int i = threadIdx.x;
@@ -332,6 +333,17 @@ __device__ __forceinline__ void lag_weights(const GdnArgs& A, int cc, float (&wl
     for (int e = 0; e < 8; ++e) wl[L][e] = (L < A.taps) ? A.conv_w[(size_t)(A.taps - 1 - L) * A.W + cc + e] : 0.f;
 }
 
+// Raw row tt (>= -(taps - 1)) of batch row b at channels cc..cc+7: rows before the row come
+// from the conv history of a continued sequence (A.init_conv, oldest first), or read row 0 (a
+// clamped address; the conv's tap masks drop them); rows past T read row T - 1 (padding).
+template <class TIO>
+__device__ __forceinline__ const TIO* halo_row(const GdnArgs& A, const TIO* x, int b, int tt, int cc) {
+  const int k1 = A.taps > 0 ? A.taps - 1 : 0;
+  const TIO* hist = reinterpret_cast<const TIO*>(A.init_conv);
+  if (tt < 0 && hist && tt >= -k1) return hist + ((size_t)b * k1 + (k1 + tt)) * A.W + cc;
+  return x + ((size_t)b * A.T + (tt < 0 ? 0 : (tt < A.T ? tt : A.T - 1))) * A.W + cc;
+}
+
 // ---------------------------------------------------------------- k_prep
 // grid (B*N, 2*Hk + H), 256 threads. Slot y: q head y (< Hk), k head y - Hk, v head y - 2Hk.
 // Every (token, 8 channels) is independent: D/8 lanes per token row. l2norm of xla.py:42-53.
@@ -367,9 +379,8 @@ __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
 #pragma unroll
     for (int i = 0; i < RG + HW; ++i) {
       const int tt = n * C + r0 - HW + i;
-      const int tc = tt < 0 ? 0 : (tt < A.T ? tt : A.T - 1);
-      raw[i].load(x + ((size_t)b * A.T + tc) * A.W + cc);
-      sgv[i] = sg[tc];
+      raw[i].load(halo_row<TIO>(A, x, b, tt, cc));
+      sgv[i] = sg[tt < 0 ? 0 : (tt < A.T ? tt : A.T - 1)];  // rows before the row: token 0's segment
     }
 #pragma unroll
     for (int i = 0; i < RG; ++i) {
@@ -387,7 +398,7 @@ __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
         for (int e = 0; e < 8; ++e) z[e] *= wl[0][e];
 #pragma unroll
         for (int L = 1; L <= HW; ++L) {
-          const bool keep = L < A.taps && t - L >= 0 && sgv[HW + i - L] == st;
+          const bool keep = L < A.taps && (t - L >= 0 || A.init_conv) && sgv[HW + i - L] == st;
           float xl[8];
           raw[HW + i - L].get(xl);
 #pragma unroll
@@ -702,7 +713,7 @@ struct PairGates {
     gc = A.gam[th + C - 1];
     lc = A.gaml[th + C - 1];
     prev = A.segp[n > 0 ? tb - 1 : tb];
-    first = n == 0;
+    first = n == 0 && !A.init_state;
   }
   __device__ __forceinline__ int before() const { return first ? -2 : prev; }
   // e^gamma . cont
@@ -1004,7 +1015,7 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
 
 // ---------------------------------------------------------------- scan partition
 // carry of chunk c: its last token continues the segment of the token before the chunk (-2
-// before chunk 0). Where a chunk does not carry, the state after it does not depend on the state
+// before chunk 0, or token 0's id with an initial state). Where a chunk does not carry, the state after it does not depend on the state
 // before it (its last segment starts inside it and reads no earlier state), and the state
 // gradient entering it does not depend on the one after it (the rows that read the earlier
 // state, and so feed that gradient, are in another segment than the rows that write the later
@@ -1013,19 +1024,18 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
 template <int C>
 __device__ __forceinline__ bool chunk_carries(const GdnArgs& A, int b, int c) {
   const int32_t* sp = A.segp + (size_t)b * A.Tp;
-  const int before = c == 0 ? -2 : sp[(size_t)c * C - 1];
+  const int before = c == 0 ? (A.init_state ? sp[0] : -2) : sp[(size_t)c * C - 1];
   return sp[(size_t)c * C + C - 1] == before;
 }
 // The first chunk s in [q, N) where a range starts, or N; forward ranges start at chunk 0 and
-// after chunks that do not carry, backward ranges at chunks that do not carry (chunk 0 never
-// carries). One candidate per thread, then the workgroup minimum (red: NT/64 ints of LDS).
+// after chunks that do not carry, backward ranges at chunk 0 and at chunks that do not carry. One candidate per thread, then the workgroup minimum (red: NT/64 ints of LDS).
 // Called by every thread of the workgroup.
 template <int C, int NT, bool FWD>
 __device__ __forceinline__ int part_start(const GdnArgs& A, int b, int q, int* red) {
   for (int base = q; base < A.N; base += NT) {
     const int s = base + (int)threadIdx.x;
     bool hit = false;
-    if (s < A.N) hit = FWD ? (s == 0 || !chunk_carries<C>(A, b, s - 1)) : !chunk_carries<C>(A, b, s);
+    if (s < A.N) hit = s == 0 || (FWD ? !chunk_carries<C>(A, b, s - 1) : !chunk_carries<C>(A, b, s));
     int m = hit ? s : A.N;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = min(m, __shfl_xor(m, off));
@@ -1100,6 +1110,13 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
   const int nb = n0 > 0 ? n0 - 1 : 0;
   f32x4 accS[DVT / 16];
   zero(accS);
+  if (n0 == 0 && A.init_state && (NW == D / 16 || w < D / 16)) {  // a continued sequence: S before chunk 0
+    const float* s0 = A.init_state + (size_t)bh * D * D + j0;
+#pragma unroll
+    for (int t = 0; t < DVT / 16; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) accS[t][rr] = s0[(size_t)(16 * w + acc_row(rr)) * D + 16 * t + acc_col()];
+  }
   ScanFwdIn<C, D, DVT, NT> in;
   in.gt.fetch(A, b, h, nb, RegsT<C, D, NT>::pair());
   in.fetch_k(A, b, hk, nb);
@@ -1269,7 +1286,7 @@ __global__ __launch_bounds__(256) void k_final_state(GdnArgs A) {
   const float gl = A.gam[th + last], ll = A.gaml[th + last];
   for (int t = threadIdx.x; t < cnt; t += 256)
     sw[t] = A.segp[tb + t0 + t] == sl ? expf((gl - A.gam[th + t0 + t]) + (ll - A.gaml[th + t0 + t])) : 0.f;
-  const int before = nl > 0 ? A.segp[tb + t0 - 1] : -2;
+  const int before = nl > 0 ? A.segp[tb + t0 - 1] : (A.init_state ? A.segp[tb] : -2);
   const float carry = sl == before ? expf(gl + ll) : 0.f;
   __syncthreads();
   const int j = threadIdx.x % DT, rg = threadIdx.x / DT;
@@ -1298,7 +1315,7 @@ __global__ __launch_bounds__(256) void k_final_state(GdnArgs A) {
 
 // ---------------------------------------------------------------- k_conv_state
 // grid B, 256 threads: the raw rows T-K+1 .. T-1 of each row (oldest first, [B, K-1, W]), zero
-// before the row's start or outside token T-1's segment: the conv history a decode step
+// outside token T-1's segment or before the row's start (there: the given history, if any): the conv history a decode step
 // continuing that segment reads (the tap masks of causal_conv1d.py:10-17).
 template <class TIO>
 __global__ __launch_bounds__(256) void k_conv_state(GdnArgs A) {
@@ -1306,10 +1323,12 @@ __global__ __launch_bounds__(256) void k_conv_state(GdnArgs A) {
   const TIO* x = reinterpret_cast<const TIO*>(A.qkv);
   TIO* dst = reinterpret_cast<TIO*>(A.conv_state) + (size_t)b * k1 * A.W;
   const int sl = A.seg[(size_t)b * A.T + last];
+  const TIO* hist = reinterpret_cast<const TIO*>(A.init_conv);
   for (int idx = threadIdx.x; idx < k1 * A.W; idx += 256) {
     const int r = idx / A.W, c = idx % A.W, t = last - k1 + 1 + r;
-    const bool keep = t >= 0 && A.seg[(size_t)b * A.T + (t >= 0 ? t : 0)] == sl;
-    dst[idx] = keep ? x[((size_t)b * A.T + t) * A.W + c] : TIO(0);
+    // rows before the row: the history of a continued sequence (token 0's segment)
+    const bool keep = A.seg[(size_t)b * A.T + (t >= 0 ? t : 0)] == sl && (t >= 0 || hist);
+    dst[idx] = !keep ? TIO(0) : t >= 0 ? x[((size_t)b * A.T + t) * A.W + c] : hist[((size_t)b * k1 + k1 + t) * A.W + c];
   }
 }
 
@@ -1494,6 +1513,13 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
   const int ne = n1 < A.N ? n1 : n1 - 1;
   f32x4 accG[DVT / 16];
   zero(accG);
+  if (n1 == A.N && A.d_final && (NW == D / 16 || w < D / 16)) {  // the final state's gradient: G after the last chunk
+    const float* g1 = A.d_final + (size_t)bh * D * D + j0;
+#pragma unroll
+    for (int t = 0; t < DVT / 16; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) accG[t][rr] = g1[(size_t)(16 * w + acc_row(rr)) * D + 16 * t + acc_col()];
+  }
   ScanBwdIn<C, D, DVT, NT, TIO> in;
   {
     const int n = ne;
@@ -1579,6 +1605,10 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
       strip_mma<PI, C, DVT / 16>(accG, oq, 16 * w, ox, 0);
     // no barrier here: the next step's writes before its first barrier go to G^T, do^T, the
     // wave's own q rows and red, none of which this product reads
+  }
+  if (n0 == 0 && A.d_init_state && (NW == D / 16 || w < D / 16)) {  // G before chunk 0: the initial state's gradient
+#pragma unroll
+    for (int t = 0; t < DVT / 16; ++t) st_tile(A.d_init_state + (size_t)bh * D * D + 16 * w * D + j0 + 16 * t, D, accG[t]);
   }
 }
 
@@ -1854,10 +1884,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
   for (int i = 0; i < RG + HW; ++i) {
     const int tt = n * C + r0 - HW + i;
-    const int tc = tt < 0 ? 0 : (tt < A.T ? tt : A.T - 1);
     const int ts = tt < 0 ? 0 : (tt < A.Tp ? tt : A.Tp - 1);
-    raw[i].load(x + ((size_t)b * A.T + tc) * A.W + cc);
-    sgv[i] = sp[ts];
+    raw[i].load(halo_row<TIO>(A, x, b, tt, cc));
+    sgv[i] = sp[ts];  // rows before the row: token 0's segment (the history of a continued sequence)
   }
   float dyv[RG][8], btv[RG];
 #pragma unroll
@@ -1927,7 +1956,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
       for (int e = 0; e < 8; ++e) z[e] *= wl[0][e];
 #pragma unroll
       for (int L = 1; L <= HW; ++L) {
-        const bool keep = L < taps && t - L >= 0 && sgv[HW + i - L] == st;
+        const bool keep = L < taps && (t - L >= 0 || A.init_conv) && sgv[HW + i - L] == st;
         float xl[8];
         raw[HW + i - L].get(xl);
 #pragma unroll
@@ -1982,6 +2011,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   __syncthreads();
 #pragma unroll
   for (int j = (RG > HW ? RG - HW : 0); j < RG; ++j) emit(j, true);
+  if (n == 0 && grp == 0 && A.d_init_conv && taps > 1) {
+    // the gradient of the history rows -p (p = 1 .. taps - 1): sum over lags L >= p of
+    // w[K-1-L] dz[L - p] on rows of token 0's segment (rows past the group's from LDS)
+    const int s0 = sp[0];
+#pragma unroll
+    for (int p = 1; p <= HW; ++p) {
+      if (p >= taps) break;
+      float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int L = p; L <= HW; ++L) {
+        if (L >= taps) break;
+        const int j = L - p;
+        if (j < RG) {
+          if (str[j] == s0) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] += wl[L][e] * dzr[j][e];
+          }
+        } else {
+          const int k = (j / RG) * HS + j % RG;
+          if (shs[k] == s0) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] += wl[L][e] * shd[k * LZ + cg * 8 + e];
+          }
+        }
+      }
+      st8_io(reinterpret_cast<TIO*>(A.d_init_conv) + ((size_t)b * (taps - 1) + (taps - 1 - p)) * A.W + cc, o);
+    }
+  }
   if constexpr (DW) {
     // d w[K-1-L] += keep_L[t] dz[t] x[t-L] over the group's rows of the chunk, from its raw rows
     // loaded again (cache hits) once the prefetched gradients are spent
@@ -1991,16 +2048,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
       for (int e = 0; e < 8; ++e) dwa[L][e] = 0.f;
 #pragma unroll
-    for (int i = 0; i < RG + HW; ++i) {
-      const int tt = n * C + r0 - HW + i;
-      raw[i].load(x + ((size_t)b * A.T + (tt < 0 ? 0 : (tt < A.T ? tt : A.T - 1))) * A.W + cc);
-    }
+    for (int i = 0; i < RG + HW; ++i) raw[i].load(halo_row<TIO>(A, x, b, n * C + r0 - HW + i, cc));
 #pragma unroll
     for (int i = 0; i < RG; ++i) {
       const int r = r0 + i, t = n * C + r;
 #pragma unroll
       for (int L = 0; L < NL; ++L) {
-        const bool keep = r < C && L < taps && t - L >= 0 && (L == 0 || sgv[HW + i - L] == str[i]);
+        const bool keep = r < C && L < taps && (t - L >= 0 || A.init_conv) && (L == 0 || sgv[HW + i - L] == str[i]);
         float xl[8];
         raw[HW + i - L].get(xl);
 #pragma unroll

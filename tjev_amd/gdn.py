@@ -150,6 +150,79 @@ class _Core(torch.autograd.Function):
         return None, d_qkv, d_a, d_b, d_a_log, d_dt_bias, d_w, None, None
 
 
+def _conv_state_grad(d_cs, seg, d_qkv, d_init_conv, length: int):
+    """Adds the gradient of the forward's conv_state (the raw rows T-K+1 .. T-1, zero outside
+    token T-1's segment; rows before the row from the conv history) to those rows' gradients."""
+    k1 = d_cs.shape[1]
+    last = seg[:, length - 1]
+    for r in range(k1):
+        t = length - k1 + r
+        if t >= 0:
+            keep = (seg[:, t] == last)[:, None]
+            d_qkv[:, t] += torch.where(keep, d_cs[:, r].to(d_qkv.dtype), torch.zeros((), dtype=d_qkv.dtype,
+                                                                                     device=d_qkv.device))
+        elif d_init_conv is not None:
+            keep = (seg[:, 0] == last)[:, None]
+            d_init_conv[:, k1 + t] += torch.where(keep, d_cs[:, r].to(d_init_conv.dtype),
+                                                  torch.zeros((), dtype=d_init_conv.dtype, device=d_qkv.device))
+
+
+class _CoreCont(torch.autograd.Function):
+    """``_Core`` for a sequence continued from a given state: the initial recurrent state and
+    conv history in, the final ones out, gradients through all four (tjev_gdn_mega2_fwd_cont /
+    _bwd_cont)."""
+
+    @staticmethod
+    def forward(ctx, plan: GdnPlan, qkv, a, b, a_log, dt_bias, conv_w, seg, init_state, init_conv, out_shape,
+                want_state):
+        ctx.set_materialize_grads(False)
+        dev = qkv.device
+        p = plan.params
+        out = torch.empty(out_shape, dtype=qkv.dtype, device=dev)
+        res = plan.residuals(dev)
+        ws = plan.workspace(False, dev)
+        final = conv_state = None
+        if want_state:
+            final = torch.empty((p.batch, p.value_heads, p.key_dim, p.value_dim), dtype=torch.float32, device=dev)
+            if p.taps > 1:
+                conv_state = torch.empty((p.batch, p.taps - 1, qkv.shape[-1]), dtype=qkv.dtype, device=dev)
+        _lib.check_status(plan.lib.tjev_gdn_mega2_fwd_cont(
+            ctypes.byref(p), plan._stream(dev), _ptr(qkv), _ptr(a), _ptr(b), _ptr(a_log), _ptr(dt_bias),
+            _ptr(conv_w), _ptr(seg), _ptr(init_state), _ptr(init_conv), _ptr(out), _ptr(res), _ptr(final),
+            _ptr(conv_state), _ptr(ws), ws.numel()))
+        ctx.plan = plan
+        ctx.save_for_backward(qkv, a, b, a_log, dt_bias, conv_w, seg, res, init_state, init_conv)
+        return out, final, conv_state
+
+    @staticmethod
+    def backward(ctx, d_out, d_final, d_cs):
+        plan: GdnPlan = ctx.plan
+        p = plan.params
+        qkv, a, b, a_log, dt_bias, conv_w, seg, res, init_state, init_conv = ctx.saved_tensors
+        if d_out is None:
+            d_out = torch.zeros((qkv.shape[0], qkv.shape[1], p.value_heads, p.value_dim), dtype=qkv.dtype,
+                                device=qkv.device)
+        d_out = d_out.to(qkv.dtype).contiguous()
+        d_final = None if d_final is None else d_final.to(torch.float32).contiguous()
+        d_qkv, d_a, d_b = torch.empty_like(qkv), torch.empty_like(a), torch.empty_like(b)
+        d_a_log, d_dt_bias = torch.empty_like(a_log), torch.empty_like(dt_bias)
+        want_dw = conv_w is not None and ctx.needs_input_grad[6]
+        d_w = torch.empty_like(conv_w) if want_dw else None
+        d_init = torch.empty_like(init_state) if init_state is not None and ctx.needs_input_grad[8] else None
+        want_hist = init_conv is not None and (ctx.needs_input_grad[9] or d_cs is not None)
+        d_hist = torch.empty_like(init_conv) if want_hist else None
+        ws = plan.workspace(True, qkv.device)
+        _lib.check_status(plan.lib.tjev_gdn_mega2_bwd_cont(
+            ctypes.byref(p), plan._stream(qkv.device), _ptr(qkv), _ptr(a), _ptr(b), _ptr(a_log), _ptr(dt_bias),
+            _ptr(conv_w), _ptr(seg), _ptr(init_state), _ptr(init_conv), _ptr(res), _ptr(d_out), _ptr(d_final),
+            _ptr(d_qkv), _ptr(d_a), _ptr(d_b), _ptr(d_a_log), _ptr(d_dt_bias), _ptr(d_w), _ptr(d_init), _ptr(d_hist),
+            _ptr(ws), ws.numel()))
+        if d_cs is not None:
+            _conv_state_grad(d_cs, seg, d_qkv, d_hist, qkv.shape[1])
+        return (None, d_qkv, d_a, d_b, d_a_log, d_dt_bias, d_w, None, d_init,
+                d_hist if init_conv is not None and ctx.needs_input_grad[9] else None, None, None)
+
+
 def _check(precision, inverse, chunk, width, key_heads, key_dim, value_heads, value_dim, heads_per_step,
            conv_weight):
     """gdn_megakernel's checks, in its order and wording (pallas_tpu_mega.py:597-615)."""
@@ -177,7 +250,8 @@ def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: t
                    dt_bias: torch.Tensor, conv_weight: torch.Tensor | None, segment_ids: torch.Tensor, *,
                    key_heads: int, key_dim: int, value_heads: int, value_dim: int, chunk: int = 64,
                    precision: str = "high", inverse: str = "doubling", heads_per_step: int = 0,
-                   vmem_fraction: float = 0.0, residuals: str = "states") -> torch.Tensor:
+                   vmem_fraction: float = 0.0, residuals: str = "states", initial_state: torch.Tensor | None = None,
+                   initial_conv: torch.Tensor | None = None, output_final_state: bool = False):
     """The GDN core from the projection outputs (pallas_tpu_mega.py:585-596).
 
     qkv [B, T, 2·Hk·Dk + H·Dv]: with ``conv_weight`` [K, 2·Hk·Dk + H·Dv] (mega2) the raw
@@ -189,7 +263,15 @@ def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: t
     (this build's, not the reference's) picks what the forward keeps for the backward: "states"
     (chunk-boundary states only), "tinv" (the reference's gdn_states + gdn_tinv) or "all" (and
     v_new); every choice gives the same gradients up to rounding ("tinv" and "states" bit for
-    bit)."""
+    bit).
+
+    Beyond the reference's megakernel, which starts every row fresh: ``initial_state``
+    [B, H, Dk, Dv] (fp32) and ``initial_conv`` [B, K-1, W] (qkv's dtype) continue a sequence
+    from an earlier call (the chunked rule's ``initial_state``, xla.py:170-262: token 0's segment
+    reads them), and ``output_final_state`` returns (out, final_state [B, H, Dk, Dv] fp32,
+    conv_state [B, K-1, W] or None), the state after token T-1 and the last K-1 raw rows of its
+    segment, which the next piece takes as its initial state and history. Gradients flow through
+    all of them (the final state's needs T a multiple of the chunk the kernels run)."""
     batch, length, width = qkv.shape
     taps = _check(precision, inverse, chunk, width, key_heads, key_dim, value_heads, value_dim, heads_per_step,
                   conv_weight)
@@ -201,20 +283,31 @@ def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: t
                    heads_per_step=heads_per_step, residuals=residuals)
     b = b.to(a.dtype)
     conv_w = None if conv_weight is None else conv_weight.to(torch.float32).contiguous()
-    out, _ = _Core.apply(plan, qkv.contiguous(), a.contiguous(), b.contiguous(),
-                         a_log.to(torch.float32).contiguous(), dt_bias.to(torch.float32).contiguous(), conv_w,
-                         segment_ids.to(torch.int32).contiguous(), (batch, length, value_heads, value_dim))
-    return out
+    args = (qkv.contiguous(), a.contiguous(), b.contiguous(), a_log.to(torch.float32).contiguous(),
+            dt_bias.to(torch.float32).contiguous(), conv_w, segment_ids.to(torch.int32).contiguous())
+    if initial_state is None and initial_conv is None and not output_final_state:
+        out, _ = _Core.apply(plan, *args, (batch, length, value_heads, value_dim))
+        return out
+    if initial_state is not None and initial_state.shape != (batch, value_heads, key_dim, value_dim):
+        raise ValueError(f"initial_state must be [{batch}, {value_heads}, {key_dim}, {value_dim}], "
+                         f"not {tuple(initial_state.shape)}")
+    if initial_conv is not None and (conv_weight is None or initial_conv.shape != (batch, taps - 1, width)):
+        raise ValueError(f"initial_conv must be [{batch}, {taps - 1}, {width}] (a conv of 2 or more taps)")
+    init = None if initial_state is None else initial_state.to(torch.float32).contiguous()
+    hist = None if initial_conv is None else initial_conv.to(qkv.dtype).contiguous()
+    out, final, conv_state = _CoreCont.apply(plan, *args, init, hist, (batch, length, value_heads, value_dim),
+                                             output_final_state)
+    return (out, final, conv_state) if output_final_state else out
 
 
 def gdn_core_mega(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_heads: int, key_dim: int,
                   value_heads: int, value_dim: int, chunk: int = 64, precision: str = "high",
                   inverse: str = "default", heads_per_step: int = 0, vmem_fraction: float = 0.0,
-                  residuals: str = "states"):
+                  residuals: str = "states", **state):
     """The dispatcher form (__init__.py:112-149): ``inverse`` "default" -> doubling. The
     reference shards rows over devices here (``batch_parallel_with``); this build runs one GPU,
     where that split is the identity."""
     return gdn_megakernel(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, key_heads=key_heads,
                           key_dim=key_dim, value_heads=value_heads, value_dim=value_dim, chunk=chunk,
                           precision=precision, inverse=kernel_inverse(inverse),
-                          heads_per_step=heads_per_step, vmem_fraction=vmem_fraction, residuals=residuals)
+                          heads_per_step=heads_per_step, vmem_fraction=vmem_fraction, residuals=residuals, **state)

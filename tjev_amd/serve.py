@@ -25,9 +25,11 @@ _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
 
 def gdn_prefill(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_heads: int, key_dim: int,
                 value_heads: int, value_dim: int, chunk: int = 64, precision: str = "high",
-                inverse: str = "doubling", heads_per_step: int = 0):
+                inverse: str = "doubling", heads_per_step: int = 0, initial_state=None, initial_conv=None):
     """The megakernel forward (``gdn_megakernel``'s arguments) and the decode state it leaves:
-    (out [B, T, H, Dv], state [B, H, Dk, Dv] fp32, conv_state [B, K-1, W] or None)."""
+    (out [B, T, H, Dv], state [B, H, Dk, Dv] fp32, conv_state [B, K-1, W] or None). With
+    ``initial_state`` / ``initial_conv`` (a previous prefill's state and conv_state) it
+    continues that prefill: a long prompt in pieces."""
     batch, length, width = qkv.shape
     taps = _check(precision, inverse, chunk, width, key_heads, key_dim, value_heads, value_dim, heads_per_step,
                   conv_weight)
@@ -48,9 +50,16 @@ def gdn_prefill(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_head
     conv_state = None
     if conv_weight is not None and taps > 1:
         conv_state = torch.empty((batch, taps - 1, width), dtype=qkv.dtype, device=dev)
-    status = plan.lib.tjev_gdn_mega2_fwd_state(
+    init = None if initial_state is None else initial_state.to(torch.float32).contiguous()
+    hist = None if initial_conv is None or conv_state is None else initial_conv.to(qkv.dtype).contiguous()
+    if init is not None and init.shape != state.shape:
+        raise ValueError(f"initial_state must be {list(state.shape)}, not {list(init.shape)}")
+    if hist is not None and hist.shape != conv_state.shape:
+        raise ValueError(f"initial_conv must be {list(conv_state.shape)}, not {list(hist.shape)}")
+    status = plan.lib.tjev_gdn_mega2_fwd_cont(
         ctypes.byref(plan.params), plan._stream(dev), _ptr(qkv), _ptr(a), _ptr(b), _ptr(a_log), _ptr(dt_bias),
-        _ptr(conv_w), _ptr(seg), _ptr(out), _ptr(res), _ptr(state), _ptr(conv_state), _ptr(ws), ws.numel())
+        _ptr(conv_w), _ptr(seg), _ptr(init), _ptr(hist), _ptr(out), _ptr(res), _ptr(state), _ptr(conv_state),
+        _ptr(ws), ws.numel())
     _lib.check_status(status)
     return out, state, conv_state
 
@@ -84,6 +93,9 @@ def gdn_decode_step(qkv, a, b, a_log, dt_bias, conv_weight, conv_state, state, *
     conv_w = None if conv_weight is None else conv_weight.to(torch.float32).contiguous()
     hist = None if taps <= 1 else conv_state.to(qkv.dtype).contiguous()
     hist_out = None if taps <= 1 else torch.empty_like(hist)
+    if inplace and (not state.is_contiguous() or state.data_ptr() % 16):
+        raise ValueError("inplace: the state must be a contiguous, 16-byte aligned fp32 tensor (a copy would "
+                         "leave the caller's cache unchanged)")
     state = state.contiguous()
     state_out = state if inplace else torch.empty_like(state)
     out = torch.empty((batch, value_heads, value_dim), dtype=qkv.dtype, device=dev)

@@ -51,11 +51,54 @@ class _V2(torch.autograd.Function):
         return None, d_q, d_k, d_v, d_g, d_beta, None
 
 
+class _V2Cont(torch.autograd.Function):
+    """``_V2`` with a state in and out (tjev_gdn_v2_fwd_cont / _bwd_cont)."""
+
+    @staticmethod
+    def forward(ctx, plan: GdnPlan, q, k, v, g, beta, seg, init_state, want_state):
+        ctx.set_materialize_grads(False)
+        p = plan.params
+        out = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+        res = plan.residuals(v.device)
+        ws = plan.workspace(False, v.device)
+        final = None
+        if want_state:
+            final = torch.empty((p.batch, p.value_heads, p.key_dim, p.value_dim), dtype=torch.float32, device=v.device)
+        _lib.check_status(plan.lib.tjev_gdn_v2_fwd_cont(
+            ctypes.byref(p), plan._stream(v.device), _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(seg),
+            _ptr(init_state), _ptr(out), _ptr(res), _ptr(final), _ptr(ws), ws.numel()))
+        ctx.plan = plan
+        ctx.save_for_backward(q, k, v, g, beta, seg, res, init_state)
+        return out, final
+
+    @staticmethod
+    def backward(ctx, d_out, d_final):
+        plan: GdnPlan = ctx.plan
+        q, k, v, g, beta, seg, res, init_state = ctx.saved_tensors
+        d_out = torch.zeros_like(v) if d_out is None else d_out.to(v.dtype).contiguous()
+        d_final = None if d_final is None else d_final.to(torch.float32).contiguous()
+        d_q, d_k, d_v = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        d_g, d_beta = torch.empty_like(g), torch.empty_like(beta)
+        d_init = torch.empty_like(init_state) if init_state is not None and ctx.needs_input_grad[7] else None
+        ws = plan.workspace(True, v.device)
+        _lib.check_status(plan.lib.tjev_gdn_v2_bwd_cont(
+            ctypes.byref(plan.params), plan._stream(v.device), _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta),
+            _ptr(seg), _ptr(init_state), _ptr(res), _ptr(d_out), _ptr(d_final), _ptr(d_q), _ptr(d_k), _ptr(d_v),
+            _ptr(d_g), _ptr(d_beta), _ptr(d_init), _ptr(ws), ws.numel()))
+        return None, d_q, d_k, d_v, d_g, d_beta, None, d_init, None
+
+
 def chunk_gated_delta_rule_v2(q, k, v, g, beta, segment_ids=None, *, chunk: int = 64, precision: str = "high",
                               inverse: str = "doubling", heads_per_step: int = 0, vmem_fraction: float = 0.0,
-                              residuals: str = "states") -> torch.Tensor:
+                              residuals: str = "states", initial_state: torch.Tensor | None = None,
+                              output_final_state: bool = False):
     """q, k [B,T,Hk,Dk] (Hk divides H), v [B,T,H,Dv], g, beta [B,T,H] -> out [B,T,H,Dv] in v's
-    dtype (pallas_tpu_v2.py:541-582). T is padded to whole chunks with segment-0 tokens."""
+    dtype (pallas_tpu_v2.py:541-582). T is padded to whole chunks with segment-0 tokens.
+
+    Beyond the reference's v2 kernel: ``initial_state`` [B, H, Dk, Dv] fp32 continues a sequence
+    (xla.py:170-262's ``initial_state``: token 0's segment reads it), and ``output_final_state``
+    returns (out, final_state [B, H, Dk, Dv] fp32), the state after token T-1; gradients flow
+    through both (the final state's needs T a multiple of the kernels' chunk)."""
     if precision not in PRECISIONS:
         raise ValueError(f"precision in {PRECISIONS}")
     if inverse not in INVERSE_BLOCKS:
@@ -81,5 +124,29 @@ def chunk_gated_delta_rule_v2(q, k, v, g, beta, segment_ids=None, *, chunk: int 
                    precision=precision, inverse=inverse, heads_per_step=heads_per_step, residuals=residuals)
     plan.params.qk_dtype = _DTYPES[qk_dtype]
     gd = torch.bfloat16 if plan.params.gate_dtype == _lib.BF16 else torch.float32
-    return _V2.apply(plan, q.to(qk_dtype).contiguous(), k.to(qk_dtype).contiguous(), v.contiguous(),
-                     g.to(gd).contiguous(), beta.to(gd).contiguous(), segment_ids.to(torch.int32).contiguous())
+    args = (q.to(qk_dtype).contiguous(), k.to(qk_dtype).contiguous(), v.contiguous(), g.to(gd).contiguous(),
+            beta.to(gd).contiguous(), segment_ids.to(torch.int32).contiguous())
+    if initial_state is None and not output_final_state:
+        return _V2.apply(plan, *args)
+    if initial_state is not None and initial_state.shape != (batch, heads, dk, dv):
+        raise ValueError(f"initial_state must be [{batch}, {heads}, {dk}, {dv}], not {tuple(initial_state.shape)}")
+    init = None if initial_state is None else initial_state.to(torch.float32).contiguous()
+    out, final = _V2Cont.apply(plan, *args, init, output_final_state)
+    return (out, final) if output_final_state else out
+
+
+def chunk_gated_delta_rule(q, k, v, g, beta, segment_ids=None, initial_state=None, chunk: int = 64,
+                           precision: str = "highest", inverse: str = "solve"):
+    """The reference's chunked rule with its state I/O (src/tjev/kernels/gated_delta_rule/
+    xla.py:170-262): (out [B,T,H,Dv], final_state [B,H,Dk,Dv]) from q, k [B,T,H or Hk,Dk], v,
+    g, beta and an optional initial_state, on the v2 operator's kernels. ``inverse`` "solve"
+    (the reference's triangular solve), "doubling" or "blocked": the kernels' inverse is exact
+    in each case (xla.py:190-195 lists the same three). Unlike xla.py, v keeps its dtype in the
+    output (fp32 inputs give fp32, as there)."""
+    if inverse not in ("solve", "doubling", "blocked"):
+        raise ValueError(f"precision in {PRECISIONS}, inverse in ('solve', 'doubling', 'blocked')")
+    if precision not in PRECISIONS:
+        raise ValueError(f"precision in {PRECISIONS}, inverse in ('solve', 'doubling', 'blocked')")
+    return chunk_gated_delta_rule_v2(q, k, v, g, beta, segment_ids, chunk=chunk, precision=precision,
+                                     inverse="blocked" if inverse == "solve" else inverse,
+                                     initial_state=initial_state, output_final_state=True)
