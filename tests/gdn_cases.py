@@ -13,7 +13,7 @@ NAMES = ("qkv", "a", "b", "A_log", "dt_bias", "w")
 
 def rel(p: torch.Tensor, q: torch.Tensor) -> float:
     """max|p - q| / max|q| (test_gdn_mega.py:71-72)."""
-    p, q = p.double(), q.double()
+    p, q = p.detach().double(), q.detach().double()
     return float((p - q).abs().max() / (q.abs().max() + 1e-30))
 
 
