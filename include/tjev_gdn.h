@@ -144,6 +144,22 @@ int tjev_gdn_mega2_bwd_cont(const tjev_gdn_params* p, void* stream, const void* 
                             float* d_initial_state, void* d_initial_conv, void* workspace,
                             size_t workspace_bytes);
 
+/* tjev_gdn_mega2_fwd_cont without a workspace argument and without any allocation: no
+ * counterpart in the reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops that prefill prompt pieces, harnesses that forbid hipMalloc). The
+ * workspace is a static device array of TJEV_GDN_SCRATCH_BYTES on each GPU the library runs on,
+ * held until the process ends: a problem whose forward workspace (tjev_gdn_workspace_bytes(p, 0))
+ * exceeds it gets TJEV_GDN_EWORKSPACE (at the 0.8B head shape, 16 key and value heads of 128,
+ * that is about 2,700 tokens per call). Nothing in it needs to start at zero. Every call on one
+ * GPU uses that GPU's one array: calls that overlap on a GPU (other streams, other threads)
+ * race, so order them on one stream. */
+#define TJEV_GDN_SCRATCH_BYTES (128u << 20)
+int tjev_gdn_mega2_fwd_cont_noalloc(const tjev_gdn_params* p, void* stream, const void* qkv,
+                                    const void* a, const void* b, const float* a_log,
+                                    const float* dt_bias, const float* conv_w, const int32_t* seg,
+                                    const float* initial_state, const void* initial_conv, void* out,
+                                    float* residuals, float* final_state, void* conv_state);
+
 /* One decode step, T = 1 token per row (p->length == 1; chunk and residuals are ignored):
  * the reference's token recurrence (xla.py:141-167, its "T=1 decode step") on the
  * megakernel's inputs, with the conv over the kept rows (HF causal_conv1d_update). qkv [B, W]

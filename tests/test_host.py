@@ -30,6 +30,9 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert lib.tjev_gdn_version() >> 16 == 0
     assert lib.tjev_gdn_kernel_name(0) == b"gdn_prep_fwd"
+    text = (ROOT / "include" / "tjev_gdn.h").read_text()
+    m = re.search(r"#define TJEV_GDN_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.SCRATCH_BYTES
 
 
 def _params(**kw):

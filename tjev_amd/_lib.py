@@ -29,6 +29,7 @@ EXPORTS = (
     "tjev_gdn_mega2_fwd_state",
     "tjev_gdn_mega2_fwd_cont",
     "tjev_gdn_mega2_bwd_cont",
+    "tjev_gdn_mega2_fwd_cont_noalloc",
     "tjev_gdn_decode_step",
     "tjev_gdn_v2_fwd",
     "tjev_gdn_v2_bwd",
@@ -45,6 +46,7 @@ EXPORTS = (
     "tjev_gdn_version",
 )
 N_KERNELS = 16  # TJEV_GDN_KERNELS
+SCRATCH_BYTES = 128 << 20  # TJEV_GDN_SCRATCH_BYTES
 
 
 class Params(ctypes.Structure):
@@ -100,6 +102,8 @@ def load() -> ctypes.CDLL:
     lib.tjev_gdn_mega2_fwd_cont.restype = i32
     lib.tjev_gdn_mega2_bwd_cont.argtypes = [pp, vp] + [vp] * 21 + [sz]
     lib.tjev_gdn_mega2_bwd_cont.restype = i32
+    lib.tjev_gdn_mega2_fwd_cont_noalloc.argtypes = [pp, vp] + [vp] * 13
+    lib.tjev_gdn_mega2_fwd_cont_noalloc.restype = i32
     lib.tjev_gdn_v2_fwd_cont.argtypes = [pp, vp] + [vp] * 11 + [sz]
     lib.tjev_gdn_v2_fwd_cont.restype = i32
     lib.tjev_gdn_v2_bwd_cont.argtypes = [pp, vp] + [vp] * 17 + [sz]

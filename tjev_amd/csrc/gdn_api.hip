@@ -5,6 +5,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <utility>
 #include <vector>
@@ -353,6 +354,46 @@ int tjev_gdn_mega2_fwd_cont(const tjev_gdn_params* p, void* stream, const void* 
   A.final_state = final_state;
   A.conv_state = conv_state;
   return run(p, stream, A, 0);
+}
+
+// The workspace of tjev_gdn_mega2_fwd_cont_noalloc: one array per GPU, held until the process
+// ends. Host code uses its per-device address from hipGetSymbolAddress, never the name.
+static __device__ __align__(256) char scratch[TJEV_GDN_SCRATCH_BYTES];
+
+// scratch's address on the current device, looked up once per device
+int scratch_address(void** out) {
+  static std::mutex mu;
+  static void* addr[64] = {};
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(TJEV_GDN_EHIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
+  if (dev < 0 || dev >= 64) return fail(TJEV_GDN_EHIP, "device index out of range for the scratch table");
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t r = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (r != hipSuccess || !ptr)
+      return fail(TJEV_GDN_EHIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(r));
+    addr[dev] = ptr;
+  }
+  *out = addr[dev];
+  return 0;
+}
+
+int tjev_gdn_mega2_fwd_cont_noalloc(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a,
+                                    const void* b, const float* a_log, const float* dt_bias, const float* conv_w,
+                                    const int32_t* seg, const float* initial_state, const void* initial_conv,
+                                    void* out, float* residuals, float* final_state, void* conv_state) {
+  if (int s = validate(p)) return s;
+  const size_t need = layout(p, 0).total;
+  if (need > TJEV_GDN_SCRATCH_BYTES)
+    return fail(TJEV_GDN_EWORKSPACE, "the forward needs " + std::to_string(need) + " bytes of workspace, more than the " +
+                                         std::to_string((size_t)TJEV_GDN_SCRATCH_BYTES) +
+                                         " of the static scratch: use tjev_gdn_mega2_fwd_cont");
+  void* ws = nullptr;
+  if (int s = scratch_address(&ws)) return s;
+  return tjev_gdn_mega2_fwd_cont(p, stream, qkv, a, b, a_log, dt_bias, conv_w, seg, initial_state, initial_conv, out,
+                                 residuals, final_state, conv_state, ws, TJEV_GDN_SCRATCH_BYTES);
 }
 
 int tjev_gdn_mega2_fwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
