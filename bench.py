@@ -42,22 +42,54 @@ def _args(argv=None):
     ap.add_argument("--residuals", default="states", choices=("states", "tinv", "all"),
                     help="what the forward keeps for the backward (default: the chunk-boundary states only)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=1, help="rows of the workload in the CPU baseline sample")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum timed CPU work of the baseline")
+    ap.add_argument("--cpu-rows", type=int, default=0, help="rows of the workload in the CPU baseline (0: all)")
     ap.add_argument("--details", default=None, help="also write the full report to this JSON file")
     return ap.parse_args(argv)
 
 
-def _cpu_baseline(cfg, precision_dtype, rows: int, min_seconds: float, norm: bool) -> dict:
-    """The oracle's fwd+bwd on the CPU over ``rows`` full-length rows of the workload (its
-    per-token cost does not depend on the batch), with the gated RMSNorm epilogue when the GPU
-    step has it: one warm-up pass, then passes until at least ``min_seconds`` of timed work;
-    tokens/s over all timed passes."""
+def _cpu_cores() -> tuple[int, int, str]:
+    """(os.cpu_count(), the cores this process may run on, the lscpu model name)."""
+    import subprocess
+
+    total = os.cpu_count() or 1
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = total
+    model = "unknown"
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return total, usable, model
+
+
+def _cpu_median(one_pass, reps: int = 3) -> tuple[float, list[float]]:
+    """One warm-up pass, then the median of ``reps`` timed passes (BASELINE's CPU timing)."""
+    one_pass()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        one_pass()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), times
+
+
+def _cpu_baseline(cfg, precision_dtype, rows: int, norm: bool) -> dict:
+    """The oracle's fwd+bwd on the CPU over ``rows`` rows of the workload (all of them by
+    default), with the gated RMSNorm epilogue when the GPU step has it, on every core the
+    process may use: one warm-up pass, then the median of 3 passes (tokens/s)."""
     import torch
 
     from oracle.gdn_oracle import gated_rmsnorm, reference_core
     from tjev_amd.testing import cotangent, gdn_inputs
 
+    total, usable, model = _cpu_cores()
+    torch.set_num_threads(usable)
     threads = torch.get_num_threads()
     T, H, D = cfg["length"], cfg["value_heads"], cfg["dim"]
     inputs = gdn_inputs(batch=rows, length=T, key_heads=cfg["key_heads"], value_heads=H, dim=D,
@@ -76,18 +108,14 @@ def _cpu_baseline(cfg, precision_dtype, rows: int, min_seconds: float, norm: boo
             out = gated_rmsnorm(out, z, norm_w)
         torch.autograd.grad(torch.sum(out * cot), leaves)
 
-    one_pass()
-    passes, total = 0, 0.0
-    while total < min_seconds or passes < 1:
-        t0 = time.perf_counter()
-        one_pass()
-        total += time.perf_counter() - t0
-        passes += 1
+    med, times = _cpu_median(one_pass)
     what = "GDN core + gated RMSNorm" if norm else "GDN core"
-    return {"value": passes * rows * T / total, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": (f"oracle (CPU restatement of tjev's XLA chunked path, fp32, torch autograd) {what} "
-                       f"fwd+bwd on B={rows} T={T} rows of the same workload (its heads, dims, chunk, segments), "
-                       f"{passes} passes after 1 warm-up, {total:.1f} s timed, {threads} threads")}
+    return {"value": rows * T / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu_count": total, "usable_cores": usable, "threads": threads, "cpu_model": model,
+            "sample": (f"CPU restatement of tjev's XLA chunked path (the oracle, fp32, torch autograd) {what} "
+                       f"fwd+bwd on B={rows} T={T} of the same workload (its heads, dims, chunk, segments): "
+                       f"1 warm-up, median of 3 passes ({', '.join(f'{t:.2f}' for t in times)} s), "
+                       f"{threads} threads on {model} (os.cpu_count() {total}, {usable} usable)")}
 
 
 def _traffic(config: str, precision: str, kernel: str):
@@ -201,19 +229,16 @@ def _block_bench(args) -> dict:
             out = gdn_block(xl, sc, ps, key_heads=Hk, key_dim=Dk, value_heads=H, value_dim=Dv, chunk=c["chunk"])
             torch.autograd.grad((out * dyc).sum(), [xl] + [t for v in ps.values() if isinstance(v, tuple) for t in v[1:3]])
 
-        one_pass()
-        passes, total = 0, 0.0
-        while total < args.cpu_seconds or passes < 1:
-            t0 = time.perf_counter()
-            one_pass()
-            total += time.perf_counter() - t0
-            passes += 1
+        total_cores, usable, model = _cpu_cores()
+        torch.set_num_threads(usable)
         threads = torch.get_num_threads()
+        med, times = _cpu_median(one_pass)
         report["cpu_baseline"] = {
-            "value": passes * sample_t / total, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "value": sample_t / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu_count": total_cores, "usable_cores": usable, "threads": threads, "cpu_model": model,
             "sample": (f"oracle gdn_block (CPU restatement of tjev's GatedDeltaNet with merged LoRA, fp32, torch "
-                       f"autograd) fwd+bwd on B=1 T={sample_t} of the same block, {passes} passes after 1 "
-                       f"warm-up, {total:.1f} s timed, {threads} threads")}
+                       f"autograd) fwd+bwd on B=1 T={sample_t} of the same block: 1 warm-up, median of 3 passes "
+                       f"({', '.join(f'{t:.2f}' for t in times)} s), {threads} threads on {model}")}
     return report
 
 
@@ -458,7 +483,7 @@ def main(argv=None) -> int:
         "wall_s_timed": t_wall,
     }
     if not args.no_cpu_baseline:
-        report["cpu_baseline"] = _cpu_baseline(cfg, dtype, min(args.cpu_rows, B), args.cpu_seconds, norm)
+        report["cpu_baseline"] = _cpu_baseline(cfg, dtype, min(args.cpu_rows, B) if args.cpu_rows > 0 else B, norm)
     if args.details:
         with open(args.details, "w") as f:
             json.dump(report, f, indent=1)
