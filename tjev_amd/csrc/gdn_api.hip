@@ -3,7 +3,9 @@
 // (chunk, head dim, precision, dtype) kernel sequences.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -264,6 +266,35 @@ void prof_mark(void*, int kernel, int end, hipStream_t st) {
 
 const gdn::Timer g_timer{prof_mark, nullptr};
 
+// ---- the poison debug mode: with TJEV_GDN_POISON=1 in the environment, every forward fills its
+// workspace and residual buffer, and every backward its workspace, with NaN on the stream before
+// its kernels run, so a read of memory the kernels did not write reaches the outputs (the
+// reference's interpret mode poisons uninitialised scratch the same way)
+__global__ void k_poison(uint32_t* p, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = 0x7FC00000u;  // quiet NaN
+}
+
+bool poison_on() {
+  const char* e = getenv("TJEV_GDN_POISON");
+  return e && e[0] == '1';
+}
+
+int poison(void* ptr, size_t bytes, void* stream) {
+  if (!ptr || bytes < 4) return 0;
+  const size_t n = bytes / 4;
+  const unsigned grid = (unsigned)std::min<size_t>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(k_poison, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), static_cast<uint32_t*>(ptr), n);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : fail(TJEV_GDN_EHIP, std::string("poison fill: ") + hipGetErrorString(e));
+}
+
+int poison_buffers(const tjev_gdn_params* p, void* stream, void* workspace, float* residuals, int backward) {
+  if (!poison_on()) return 0;
+  if (int s = poison(workspace, layout(p, backward).total, stream)) return s;
+  return backward ? 0 : poison(residuals, residual_layout(p).total, stream);
+}
+
 int run(const tjev_gdn_params* p, void* stream, gdn::GdnArgs& A, int backward) {
   const gdn::ShapeTable* t = lookup(kernel_chunk(p), p->key_dim);
   const gdn::GdnFn fn = t->fn[p->precision][p->io_dtype][p->gate_dtype];
@@ -353,6 +384,7 @@ int tjev_gdn_mega2_fwd_cont(const tjev_gdn_params* p, void* stream, const void* 
   A.init_conv = initial_conv;
   A.final_state = final_state;
   A.conv_state = conv_state;
+  if (int s = poison_buffers(p, stream, workspace, residuals, 0)) return s;
   return run(p, stream, A, 0);
 }
 
@@ -435,6 +467,7 @@ int tjev_gdn_v2_fwd_cont(const tjev_gdn_params* p, void* stream, const void* q, 
   bind_residuals(p, residuals, A);
   A.init_state = initial_state;
   A.final_state = final_state;
+  if (int s = poison_buffers(p, stream, workspace, residuals, 0)) return s;
   return run_v2(p, stream, A, 0);
 }
 
@@ -478,6 +511,7 @@ int tjev_gdn_v2_bwd_cont(const tjev_gdn_params* p, void* stream, const void* q, 
   A.init_state = initial_state;
   A.d_final = d_final_state;
   A.d_init_state = d_initial_state;
+  if (int s = poison_buffers(p, stream, workspace, nullptr, 1)) return s;
   return run_v2(p, stream, A, 1);
 }
 
@@ -528,6 +562,7 @@ int tjev_gdn_mega2_bwd_cont(const tjev_gdn_params* p, void* stream, const void* 
   A.d_final = d_final_state;
   A.d_init_state = d_initial_state;
   A.d_init_conv = d_initial_conv;
+  if (int s = poison_buffers(p, stream, workspace, nullptr, 1)) return s;
   return run(p, stream, A, 1);
 }
 
