@@ -64,7 +64,8 @@ struct GdnArgs {
   float* ww;      // [B, H, Tp, D]   w = T kbe               (forward)
   float* vnew;    // [B, H, Tp, D]   v_new
   float* tt;      // [B, H, N, C, C] T = (I+L)^-1           (backward)
-  float* qk;      // [B, H, N, C, C] q k^T on and below the diagonal tiles (backward)
+  float* qk;      // [B, H, N, C/16, C/16, 256] q k^T's 16 x 16 tiles on and below the diagonal, in
+                  // accumulator order (backward)
   float* xl;      // [B, H, Tp, D]   X_loc, then X
   float* kt;      // [B, H, Tp, D]   T^T k_write
   float* gg;      // [B, H, N, D, D] G after each chunk

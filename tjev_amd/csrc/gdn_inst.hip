@@ -53,7 +53,8 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
     mark(id, 1);                                           \
   } while (0)
   if (!backward) {
-    GDN_LAUNCH(K_PREP_FWD, (k_prep<C, D, TIO, TG>), prep, dim3(256));
+    if (A.taps <= 4) GDN_LAUNCH(K_PREP_FWD, (k_prep<C, D, TIO, TG, 3>), prep, dim3(256));
+    else GDN_LAUNCH(K_PREP_FWD, (k_prep<C, D, TIO, TG, 4>), prep, dim3(256));
     if (A.res == 0) {
       GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0>), persist, dim3(C * 4));
     } else {  // T kept for the backward
@@ -65,7 +66,8 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
     if (A.conv_state && A.taps > 1) GDN_LAUNCH(K_FINAL_STATE, (k_conv_state<TIO>), dim3(A.B), dim3(256));
   } else {
     const int wouts = A.d_conv_w ? A.taps * A.W : 0;  // one workgroup per head, then the conv weights
-    GDN_LAUNCH(K_PREP_BWD, (k_prep<C, D, TIO, TG>), prep, dim3(256));
+    if (A.taps <= 4) GDN_LAUNCH(K_PREP_BWD, (k_prep<C, D, TIO, TG, 3>), prep, dim3(256));
+    else GDN_LAUNCH(K_PREP_BWD, (k_prep<C, D, TIO, TG, 4>), prep, dim3(256));
     if (A.res == 0) {  // T and v_new rebuilt
       GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 1>), persist, dim3(C * 4));
     } else if (A.res == 1) {  // v_new from the saved T

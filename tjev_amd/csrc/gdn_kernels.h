@@ -348,8 +348,9 @@ __device__ __forceinline__ const TIO* halo_row(const GdnArgs& A, const TIO* x, i
 // grid (B*N, 2*Hk + H), 256 threads. Slot y: q head y (< Hk), k head y - Hk, v head y - 2Hk.
 // Every (token, 8 channels) is independent: D/8 lanes per token row. l2norm of xla.py:42-53.
 // Slot 0 first writes the padded segment ids of the chunk (read by every later kernel).
-template <int C, int D, class TIO, class TG>
+template <int C, int D, class TIO, class TG, int K1 = 4>
 __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
+  static_assert(K1 >= 1 && K1 <= 4, "conv lags 1..K1 (launched with K1 >= taps - 1)");
   constexpr int CG = D / 8;
   constexpr int RPP = 256 / CG;
   const int b = blockIdx.x / A.N, n = blockIdx.x % A.N;
@@ -377,32 +378,32 @@ __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
     Raw8<TIO> raw[RG + HW];
     int sgv[RG + HW];
 #pragma unroll
-    for (int i = 0; i < RG + HW; ++i) {
+    for (int i = HW - K1; i < RG + HW; ++i) {  // the rows of lags past K1 are not read
       const int tt = n * C + r0 - HW + i;
       raw[i].load(halo_row<TIO>(A, x, b, tt, cc));
       sgv[i] = sg[tt < 0 ? 0 : (tt < A.T ? tt : A.T - 1)];  // rows before the row: token 0's segment
     }
+    // every raw row converted to fp32 once (each is read by up to K1 + 1 rows' conv)
+    float xr[RG + HW][8];
+#pragma unroll
+    for (int i = HW - K1; i < RG + HW; ++i) raw[i].get(xr[i]);
 #pragma unroll
     for (int i = 0; i < RG; ++i) {
       const int r = r0 + i, t = n * C + r;
       const int st = t < A.T ? sgv[HW + i] : 0;  // the padded tail: segment 0
       float act[8];
       if (A.taps == 0) {  // mega1: qkv is already the activation (zero on the tail)
-        raw[HW + i].get(act);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) act[e] = t < A.T ? act[e] : 0.f;
+        for (int e = 0; e < 8; ++e) act[e] = t < A.T ? xr[HW + i][e] : 0.f;
       } else {  // z = sum over lags of keep * x[t-L] * w[K-1-L], lag 0 first (causal_conv1d.py:42-45)
         float z[8];
-        raw[HW + i].get(z);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) z[e] *= wl[0][e];
+        for (int e = 0; e < 8; ++e) z[e] = xr[HW + i][e] * wl[0][e];
 #pragma unroll
-        for (int L = 1; L <= HW; ++L) {
+        for (int L = 1; L <= K1; ++L) {
           const bool keep = L < A.taps && (t - L >= 0 || A.init_conv) && sgv[HW + i - L] == st;
-          float xl[8];
-          raw[HW + i - L].get(xl);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) z[e] = keep ? z[e] + xl[e] * wl[L][e] : z[e];
+          for (int e = 0; e < 8; ++e) z[e] = keep ? z[e] + xr[HW + i - L][e] * wl[L][e] : z[e];
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) act[e] = st > 0 ? z[e] * sigmoid_io<TIO>(z[e]) : 0.f;
@@ -1396,10 +1397,12 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
       zero(acc);
       in.q.template product<PI>(acc, ob, 0, w + 1);
       in.fetch_q(A, y, i0);
-      float* qkg = A.qk + ((size_t)x.bh * A.N + x.n) * C * C + (size_t)i0 * C;
+      // q k^T on and below the diagonal, for the decay gradient's pair sums: tile (w, t) as 256
+      // floats in accumulator order, one 16-byte piece per lane
+      float4* qkg = reinterpret_cast<float4*>(A.qk + (((size_t)x.bh * A.N + x.n) * (C / 16) + w) * (C / 16) * 256);
 #pragma unroll
-      for (int t = 0; t < C / 16; ++t)  // q k^T below the diagonal, for the decay gradient's pair sums
-        if (t <= w) st_tile(qkg + 16 * t, C, acc[t]);
+      for (int t = 0; t < C / 16; ++t)
+        if (t <= w) qkg[t * 64 + lane()] = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
       const StripDecay<C> sd(cx, i0);
 #pragma unroll
       for (int t = 0; t < C / 16; ++t) {
@@ -1691,11 +1694,15 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
     }
     AccVals<TC> qk;  // q k^T of the strip from k_bwd_local (tiles past the diagonal: the diagonal again)
     {
-      const float* g = A.qk + ((size_t)bh * A.N + n) * C * C;
+      const float4* g = reinterpret_cast<const float4*>(A.qk + (((size_t)bh * A.N + n) * TC + w) * TC * 256);
 #pragma unroll
-      for (int t = 0; t < TC; ++t)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) qk.v[t][rr] = g[(size_t)(i0 + acc_row(rr)) * C + 16 * (t < w ? t : w) + acc_col()];
+      for (int t = 0; t < TC; ++t) {
+        const float4 v = g[(t < w ? t : w) * 64 + lane()];
+        qk.v[t][0] = v.x;
+        qk.v[t][1] = v.y;
+        qk.v[t][2] = v.z;
+        qk.v[t][3] = v.w;
+      }
     }
     zero(m2);
     dos.template product<exact_a<PI, sizeof(TIO) == 2>()>(m2, ob, 0, w + 1);  // do: bf16 exact
