@@ -27,6 +27,7 @@ CASES = [
     ((1, 256, 2, 4), 128, None, {"inverse": "blocked"}),
     ((1, 200, 4, 8), 64, None, {"heads_per_step": 4}),
     ((1, 256, 16, 32), 128, [100, 177], {"heads_per_step": 16, "inverse": "blocked"}),
+    ((1, 256, 16, 32), 128, [100, 177], {"heads_per_step": 32, "inverse": "blocked"}),  # one head group
     ((1, 256, 8, 16), 128, [100, 177], {"heads_per_step": 16, "inverse": "blocked"}),
 ]
 
@@ -63,6 +64,30 @@ def test_hip_conv_widths_fp32(taps):
     got = hip_outputs(inputs, cot, chunk=32, precision="highest", **shape)
     want = oracle_outputs(inputs, cot, **shape)
     errors = {k: rel(got[k], want[k]) for k in got}
+    assert all(bool(torch.isfinite(v).all()) for v in got.values())
+    for name, err in errors.items():
+        assert err < TOL[name], (name, errors)
+
+
+# every (chunk, head dim) pair with kernels beyond the d = 16 cases above: chunks below the head
+# dim (16 and 32 at 128), chunk 128 over head dim 64, and the small pairs
+SHAPE_GRID = [(16, 32), (32, 32), (64, 32), (16, 64), (32, 64), (128, 64), (16, 128), (32, 128), (64, 128)]
+
+
+@pytest.mark.parametrize("chunk,d", SHAPE_GRID, ids=[f"C{c}D{d}" for c, d in SHAPE_GRID])
+def test_hip_shape_grid_fp32(chunk, d):
+    """The chunk and head-dim pairs the reference accepts (pallas_tpu_mega.py:597-615: any
+    power-of-two chunk; Dk = Dv here), each against the oracle at the fp32 bar, with segment
+    cuts inside the first chunks and a ragged tail."""
+    hk, h = 2, 4
+    length = 3 * chunk + 5
+    inputs, cot = case_inputs(1, length, hk, h, d, cuts=[chunk - 1, chunk + 2, 2 * chunk + 1])
+    shape = dict(key_heads=hk, key_dim=d, value_heads=h, value_dim=d, conv=True)
+    print(f"shape grid chunk={chunk} d={d}", flush=True)
+    got = hip_outputs(inputs, cot, chunk=chunk, precision="highest", **shape)
+    want = oracle_outputs(inputs, cot, **shape)
+    errors = {k: rel(got[k], want[k]) for k in got}
+    print({k: f"{v:.1e}" for k, v in errors.items()})
     assert all(bool(torch.isfinite(v).all()) for v in got.values())
     for name, err in errors.items():
         assert err < TOL[name], (name, errors)

@@ -426,6 +426,26 @@ __device__ __forceinline__ void strip_mma(f32x4 (&acc)[TN], const AV& A, int i0,
   }
 }
 
+// acc[t] += sum over k < K of A(i0 + 16t + lane%16, k) * B(k, j0 + lane%16) for TM 16-row tiles
+// t of one 16-column tile: each B fragment is read once for the TM products.
+template <int P, int K, int TM, class AV, class BV>
+__device__ __forceinline__ void col_mma(f32x4 (&acc)[TM], const AV& A, int i0, const BV& B, int j0) {
+  constexpr int PA = a_prec<P>(), PB = b_prec<P>();
+  const int l = lane();
+  const int r = l & 15;
+  const int kg = (l >> 4) << 3;
+#pragma unroll
+  for (int k = 0; k < K; k += 32) {
+    const bool ok = (K % 32 == 0) || (k + kg < K);
+    const Frag<PB> fb = ok ? B.template frag<PB>(j0 + r, k + kg) : zero_frag<PB>();
+    Frag<PA> fa[TM];
+#pragma unroll
+    for (int t = 0; t < TM; ++t) fa[t] = ok ? A.template frag<PA>(i0 + 16 * t + r, k + kg) : zero_frag<PA>();
+#pragma unroll
+    for (int t = 0; t < TM; ++t) mma<P>(acc[t], fa[t], fb);
+  }
+}
+
 template <int TN>
 __device__ __forceinline__ void zero(f32x4 (&acc)[TN]) {
 #pragma unroll

@@ -763,6 +763,22 @@ struct StripA {
       tile_row<P, TN>(acc, fa, B, j0, 32 * s + kg, ok, tn);
     }
   }
+  // the transposed product: acc[t] += B(i0 + 16t .., .) (strip)^T for the tiles t < TM, B a view
+  // or operand tile whose rows are the M index (the strip is the B operand, its rows the N index)
+  template <int P, int TM, class AV>
+  __device__ __forceinline__ void product_t(f32x4 (&acc)[TM], const AV& B, int i0) const {
+    const int l = lane(), r = l & 15, kg = (l >> 4) << 3;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const bool ok = (K % 32 == 0) || (32 * s + kg < K);
+      const Frag<b_prec<P>()> fb = make_frag<b_prec<P>()>(x[s]);
+      Frag<a_prec<P>()> fa[TM];
+#pragma unroll
+      for (int t = 0; t < TM; ++t) fa[t] = ok ? B.template frag<a_prec<P>()>(i0 + 16 * t + r, 32 * s + kg) : zero_frag<a_prec<P>()>();
+#pragma unroll
+      for (int t = 0; t < TM; ++t) mma<P>(acc[t], fa[t], fb);
+    }
+  }
   // the strip as stored into an operand tile: op(i0 + r, k) = A(i0 + r, k)
   template <int P>
   __device__ __forceinline__ void put_rows(const Op<P>& op, int i0) const {
@@ -1064,17 +1080,20 @@ struct ScanIx {
 };
 
 // ---------------------------------------------------------------- k_scan_fwd
-// grid B*H*(D/DVT) (XCD-remapped), max(C,D)/16 waves. The state tile S [D x DVT] lives in
-// the accumulators of waves < D/16; chunks in order (pallas_tpu_v2.py:254-269). None of a
-// chunk step's global inputs depends on S, so each is held in registers and refilled with the
-// next chunk's values as soon as it has been used: those loads run during the rest of the
-// step (its products and barriers) instead of stalling the next one. Two barriers per step.
+// grid B*H*(D/DVT) (XCD-remapped), max(C,D)/16 waves; chunks in order (pallas_tpu_v2.py:254-269).
+// The products run transposed, v_new^T = u^T - S^T w^T and S^T = carry S^T + v_new^T (k kws),
+// so that an accumulator lane holds 4 consecutive value columns of one token (one dk row of
+// S): u is loaded and v_new and the states are stored as 16-byte vectors. S^T lives in the
+// accumulators of waves < D/16 (wave w: dk columns 16w .. 16w + 15, all DVT value rows). None
+// of a chunk step's global inputs depends on S, so each is held in registers and refilled
+// with the next chunk's values as soon as it has been used: those loads run during the rest of
+// the step (its products and barriers) instead of stalling the next one. Two barriers per step.
 template <int C, int D, int DVT, int NT>
 struct ScanFwdIn {
   PairGates<C> gt;     // kws of the thread's k rows, and the carry
   RegsT<C, D, NT> k;   // k rows, staged as (k kws)^T
-  StripA<D> wa;        // w rows of this wave's strip (waves < C/16)
-  AccVals<DVT / 16> u; // u at the strip's accumulator layout
+  StripA<D> wa;        // w rows of this wave's 16 tokens (the B operand of S^T w^T)
+  float4 u[DVT / 16];  // u[token][j0 + 16t + 4 (lane/16) ..] of the lane's token
   __device__ __forceinline__ void fetch_k(const GdnArgs& A, int b, int hk, int n) {
     k.fetch(A.kn + hoff(A, b, hk, A.Hk, n, C, D), D);
   }
@@ -1083,7 +1102,10 @@ struct ScanFwdIn {
     wa.fetch(A.ww + hoff(A, b, h, A.H, n, C, D), D, 16 * (wave() % (C / 16)));
   }
   __device__ __forceinline__ void fetch_u(const GdnArgs& A, int b, int h, int n, int j0) {
-    u.fetch(A.uu + hoff(A, b, h, A.H, n, C, D) + j0, D, 16 * (wave() % (C / 16)));
+    const float* g = A.uu + hoff(A, b, h, A.H, n, C, D) + (size_t)(16 * (wave() % (C / 16)) + acc_col()) * D + j0 +
+                     4 * (lane() >> 4);
+#pragma unroll
+    for (int t = 0; t < DVT / 16; ++t) u[t] = *reinterpret_cast<const float4*>(g + 16 * t);
   }
 };
 
@@ -1091,9 +1113,10 @@ template <int C, int D, int DVT, int PI, int PS>
 __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
   constexpr int NT = (C > D ? C : D) * 4;
   constexpr int NW = NT / 64;  // wave conditions below are compile-time when every wave takes part
-  using TS = OpTile<PI, DVT, D>;   // S^T: B(k=dk, j) = S[dk][j]
-  using TK = OpTile<PI, D, C>;     // (k kws)^T: A(i=dk, k=c)
-  using TV = OpTile<PI, DVT, C>;   // v_new^T: B(k=c, j)
+  constexpr int TJ = DVT / 16;
+  using TS = OpTile<PI, DVT, D>;   // S^T: A(i = j, k = dk)
+  using TK = OpTile<PI, D, C>;     // (k kws): B(k = c, j = dk), stored as (k kws)^T
+  using TV = OpTile<PI, DVT, C>;   // v_new^T: A(i = j, k = c)
   __shared__ __align__(16) char sS[TS::BYTES];
   __shared__ __align__(16) char sK[TK::BYTES];
   __shared__ __align__(16) char sV[TV::BYTES];
@@ -1104,19 +1127,21 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
   const int h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
   const int j0 = tile * DVT;
   const int w = wave();
+  const int jl = 4 * (lane() >> 4);  // the lane's first value column within a 16-column tile
   // this workgroup's chunks [n0, n1); from n0 - 1 (not stored) when the range starts after chunk 0
   const int n0 = part_start<C, NT, true>(A, b, (int)((long)part * A.N / A.parts), red);
   const int n1 = part_start<C, NT, true>(A, b, (int)((long)(part + 1) * A.N / A.parts), red);
   if (n0 >= n1) return;
   const int nb = n0 > 0 ? n0 - 1 : 0;
-  f32x4 accS[DVT / 16];
+  f32x4 accS[TJ];  // accS[t][rr] = S[16w + acc_col()][j0 + 16t + jl + rr]
   zero(accS);
   if (n0 == 0 && A.init_state && (NW == D / 16 || w < D / 16)) {  // a continued sequence: S before chunk 0
-    const float* s0 = A.init_state + (size_t)bh * D * D + j0;
+    const float* s0 = A.init_state + (size_t)bh * D * D + (size_t)(16 * w + acc_col()) * D + j0 + jl;
 #pragma unroll
-    for (int t = 0; t < DVT / 16; ++t)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) accS[t][rr] = s0[(size_t)(16 * w + acc_row(rr)) * D + 16 * t + acc_col()];
+    for (int t = 0; t < TJ; ++t) {
+      const float4 v = *reinterpret_cast<const float4*>(s0 + 16 * t);
+      accS[t] = f32x4{v.x, v.y, v.z, v.w};
+    }
   }
   ScanFwdIn<C, D, DVT, NT> in;
   in.gt.fetch(A, b, h, nb, RegsT<C, D, NT>::pair());
@@ -1126,34 +1151,32 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
   for (int n = nb; n < n1; ++n) {
     const int nx = n + 1 < n1 ? n + 1 : n;  // the last step refetches its own chunk (unused)
     const bool emit = n >= n0;              // the replayed chunk n0 - 1 only rebuilds the state
-    float* sg = A.states + ((size_t)bh * A.N + n) * D * D;
     if (NW == D / 16 || w < D / 16) {
+      const int dk = 16 * w + acc_col();
+      float* sg = A.states + ((size_t)bh * A.N + n) * D * D + (size_t)dk * D + j0 + jl;
 #pragma unroll
-      for (int t = 0; t < DVT / 16; ++t)
+      for (int t = 0; t < TJ; ++t) {
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
-          os.put(j, i, accS[t][rr]);
-          if (emit) sg[i * D + j0 + j] = accS[t][rr];
-        }
+        for (int rr = 0; rr < 4; ++rr) os.put(16 * t + jl + rr, dk, accS[t][rr]);
+        if (emit) *reinterpret_cast<float4*>(sg + 16 * t) = make_float4(accS[t][0], accS[t][1], accS[t][2], accS[t][3]);
+      }
     }
     const float carry = in.gt.carry();
     __syncthreads();
-    if (NW == C / 16 || w < C / 16) {  // v_new = u - w S
-      f32x4 acc[DVT / 16];
+    if (NW == C / 16 || w < C / 16) {  // v_new^T = u^T - S^T w^T for the wave's 16 tokens
+      f32x4 acc[TJ];
       zero(acc);
-      in.wa.template product<PS>(acc, os, 0);
+      in.wa.template product_t<PS>(acc, os, 0);
       in.fetch_w(A, b, h, nx);
-      const size_t off = hoff(A, b, h, A.H, n, C, D);
+      const int i = 16 * w + acc_col();
+      float* vg = A.vnew + hoff(A, b, h, A.H, n, C, D) + (size_t)i * D + j0 + jl;
 #pragma unroll
-      for (int t = 0; t < DVT / 16; ++t)
+      for (int t = 0; t < TJ; ++t) {
+        const float vn[4] = {in.u[t].x - acc[t][0], in.u[t].y - acc[t][1], in.u[t].z - acc[t][2], in.u[t].w - acc[t][3]};
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int i = 16 * w + acc_row(rr), j = 16 * t + acc_col();
-          const float vn = in.u.v[t][rr] - acc[t][rr];
-          ov.put(j, i, vn);
-          if (emit) A.vnew[off + (size_t)i * D + j0 + j] = vn;
-        }
+        for (int rr = 0; rr < 4; ++rr) ov.put(16 * t + jl + rr, i, vn[rr]);
+        if (emit) *reinterpret_cast<float4*>(vg + 16 * t) = make_float4(vn[0], vn[1], vn[2], vn[3]);
+      }
       in.fetch_u(A, b, h, nx, j0);
     }
     // (k kws)^T after the product, so one wave's staging overlaps the other's MFMA work
@@ -1161,10 +1184,10 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
     in.fetch_k(A, b, hk, nx);
     in.gt.fetch(A, b, h, nx, RegsT<C, D, NT>::pair());
     __syncthreads();
-    if (NW == D / 16 || w < D / 16) {  // S = carry S + k_write^T v_new
+    if (NW == D / 16 || w < D / 16) {  // S^T = carry S^T + v_new^T (k kws)
 #pragma unroll
-      for (int t = 0; t < DVT / 16; ++t) accS[t] *= carry;
-      strip_mma<PI, C, DVT / 16>(accS, ok, 16 * w, ov, 0);
+      for (int t = 0; t < TJ; ++t) accS[t] *= carry;
+      col_mma<PI, C, TJ>(accS, ov, 0, ok, 16 * w);
     }
     // no barrier here: the next step's first writes go to the S tile, which this product
     // does not read, and the k and v_new tiles are rewritten only after its first barrier

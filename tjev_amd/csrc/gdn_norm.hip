@@ -36,7 +36,7 @@ struct NormArgs {
 
 constexpr int kThreads = 256;
 constexpr int kMaxBwdBlocks = 2048;
-constexpr int kFwdRows = 4;  // rows per lane group in the forward
+constexpr int kFwdRows = 2;  // rows per lane group in the forward (measured: 4 and 8 are slower)
 
 // round to the storage type and back (what astype(dtype).astype(float32) does)
 template <class T>
