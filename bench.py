@@ -3,9 +3,11 @@
 
 A step is one forward and one backward pass of the GDN layer core over one batch of synthetic
 inputs already resident in HBM (the HIP library called through its C ABI, no autograd): the
-megakernel's out and chunk states, the gated RMSNorm y of out with gate z, then under a fixed
-upstream gradient of y the norm's backward (d out, d z) and the megakernel's d(qkv), d(a),
-d(b), d(A_log), d(dt_bias). ``--no-norm`` times the megakernel alone. W untimed warm-up steps, then K timed steps between device synchronizations;
+megakernel's out and chunk states, the gated RMSNorm y of out with gate z (its own kernel;
+``--fused-norm``: in the megakernel's output kernel), then under a fixed upstream gradient of y
+the norm's backward (d out, d z) and the megakernel's d(qkv), d(a), d(b), d(A_log),
+d(dt_bias). ``--no-norm`` times the megakernel alone. W untimed warm-up steps, then K timed
+steps between device synchronizations;
 ``value`` = B*T / (seconds per step). A second, event-profiled pass of K steps gives every
 kernel's average duration (HIP events on the launch stream) for the dominant kernel's
 roofline. The CPU baseline is the oracle (a CPU restatement of tjev's XLA chunked path, fp32,
@@ -39,6 +41,9 @@ def _args(argv=None):
     ap.add_argument("--config", default="0.8B")
     ap.add_argument("--precision", default=None, help="override the config's precision")
     ap.add_argument("--no-norm", action="store_true", help="time the GDN core alone, without the gated RMSNorm")
+    ap.add_argument("--fused-norm", action="store_true",
+                    help="run the norm's forward in the core's output kernel (tjev_gdn_mega2_fwd_normed) instead "
+                         "of as its own kernel (measured: the same step time)")
     ap.add_argument("--residuals", default="states", choices=("states", "tinv", "all"),
                     help="what the forward keeps for the backward (default: the chunk-boundary states only)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -416,10 +421,16 @@ def main(argv=None) -> int:
     d_qkv, d_a, d_b = torch.empty_like(qkv), torch.empty_like(a), torch.empty_like(b)
     d_alog, d_dtb = torch.empty_like(a_log), torch.empty_like(dt_bias)
 
+    fused = norm and args.fused_norm
+
     def step():
-        plan.forward(qkv, a, b, a_log, dt_bias, w, seg, out, states, ws)
+        if fused:  # the norm's forward in the core's output kernel
+            plan.forward_normed(qkv, a, b, a_log, dt_bias, w, seg, z, norm_w, 1e-6, out, y, states, ws)
+        else:
+            plan.forward(qkv, a, b, a_log, dt_bias, w, seg, out, states, ws)
+            if norm:
+                norm_forward(norm_p, out, z, norm_w, seg, y)
         if norm:
-            norm_forward(norm_p, out, z, norm_w, seg, y)
             norm_backward(norm_p, out, z, norm_w, seg, d_y, d_out, d_z, None, None)
         plan.backward(qkv, a, b, a_log, dt_bias, w, seg, states, d_out, d_qkv, d_a, d_b, d_alog, d_dtb, None, ws)
 
@@ -443,7 +454,7 @@ def main(argv=None) -> int:
     per_kernel = {k: kt.ms[k] / kt.launches[k] for k in kt.ms if kt.launches[k]}
     io_bytes = 2 if dtype == torch.bfloat16 else 4
     shape = dict(batch=B, length=T, key_heads=Hk, value_heads=H, dim=D, chunk=C, io_bytes=io_bytes)
-    work = kernel_work(**shape, residuals=args.residuals)
+    work = kernel_work(**shape, residuals=args.residuals, fused_norm=fused)
     shape["norm"] = norm
     peak_mfma = PEAK_FP32_TFLOPS if precision == "highest" else PEAK_BF16_TFLOPS
     kernels = {name: {"ms": avg_ms, **kernel_roofline(work[name], avg_ms * 1e-3, peak_mfma)}
@@ -469,7 +480,8 @@ def main(argv=None) -> int:
         "config": {"workload": f"{args.config} GDN layer core (mega2) fwd+bwd", "batch": B, "seq_len": T,
                    "key_heads": Hk, "value_heads": H, "head_dim": D, "chunk": C, "conv_taps": int(w.shape[0]),
                    "precision": precision, "segments": cfg["segments"],
-                   "epilogue": "gated_rmsnorm" if norm else None, "residuals": args.residuals},
+                   "epilogue": ("gated_rmsnorm (forward in the output kernel)" if fused else "gated_rmsnorm")
+                   if norm else None, "residuals": args.residuals},
         "roofline": {"kernel": dominant, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
                      "unit": dk["unit"], "frac": dk["frac"], "traffic": traffic,
                      "hbm_frac": dk["hbm_frac"], "mfma_frac": dk["mfma_frac"]},

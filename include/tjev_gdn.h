@@ -128,6 +128,21 @@ int tjev_gdn_mega2_fwd_cont(const tjev_gdn_params* p, void* stream, const void* 
                             float* final_state, void* conv_state, void* workspace,
                             size_t workspace_bytes);
 
+/* tjev_gdn_mega2_fwd_cont followed by the gated RMSNorm of its output, replacing the pair of
+ * calls GatedDeltaNet.__call__ makes (src/tjev/model/gdn.py:126-164: core_mega, then
+ * GatedRMSNorm, src/tjev/model/norms.py:36-62) with the norm in the output kernel's epilogue:
+ * y [B, T, H, Dv] io_dtype = weight * round(x rsqrt(mean x^2 + eps)) * silu(gate), x = out as
+ * stored, 0 on padding tokens (seg <= 0) -- what tjev_gdn_gated_rmsnorm_fwd(out, gate, weight,
+ * seg) writes, up to the summation order of mean x^2 (a rare last-bit difference). out is still
+ * written (the norm's backward, tjev_gdn_gated_rmsnorm_bwd, reads it). gate [B, T, H, Dv]
+ * io_dtype and y are 16-byte aligned; norm_weight [Dv] fp32; eps >= 0. */
+int tjev_gdn_mega2_fwd_normed(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a,
+                              const void* b, const float* a_log, const float* dt_bias,
+                              const float* conv_w, const int32_t* seg, const float* initial_state,
+                              const void* initial_conv, const void* gate, const float* norm_weight,
+                              float eps, void* out, void* y, float* residuals, float* final_state,
+                              void* conv_state, void* workspace, size_t workspace_bytes);
+
 /* The backward of tjev_gdn_mega2_fwd_cont: initial_state and initial_conv as given to the forward
  * (initial_state's values are in the residuals; only whether it is null matters here);
  * d_final_state [B, H, Dk, Dv] fp32, the gradient of the forward's final_state (null: 0; needs

@@ -128,6 +128,21 @@ int main() {
                                  (const float*)f[5], (const int32_t*)f[6], (const float*)odd(20), nullptr, fake(7),
                                  (float*)fake(8), nullptr, nullptr, ws, 0),
          TJEV_GDN_EINVAL, "fwd_cont misaligned state");
+  expect(tjev_gdn_mega2_fwd_normed(&p, nullptr, f[0], f[1], f[2], (const float*)f[3], (const float*)f[4],
+                                   (const float*)f[5], (const int32_t*)f[6], nullptr, nullptr, fake(24),
+                                   (const float*)fake(25), 1e-6f, fake(7), fake(26), (float*)fake(8), nullptr, nullptr,
+                                   ws, 0),
+         TJEV_GDN_EWORKSPACE, "fwd_normed");
+  expect(tjev_gdn_mega2_fwd_normed(&p, nullptr, f[0], f[1], f[2], (const float*)f[3], (const float*)f[4],
+                                   (const float*)f[5], (const int32_t*)f[6], nullptr, nullptr, odd(24),
+                                   (const float*)fake(25), 1e-6f, fake(7), fake(26), (float*)fake(8), nullptr, nullptr,
+                                   ws, 0),
+         TJEV_GDN_EINVAL, "fwd_normed misaligned gate");
+  expect(tjev_gdn_mega2_fwd_normed(&p, nullptr, f[0], f[1], f[2], (const float*)f[3], (const float*)f[4],
+                                   (const float*)f[5], (const int32_t*)f[6], nullptr, nullptr, fake(24),
+                                   (const float*)fake(25), -1.f, fake(7), fake(26), (float*)fake(8), nullptr, nullptr,
+                                   ws, 0),
+         TJEV_GDN_EINVAL, "fwd_normed negative eps");
   expect(tjev_gdn_mega2_bwd_cont(&p, nullptr, f[0], f[1], f[2], (const float*)f[3], (const float*)f[4],
                                  (const float*)f[5], (const int32_t*)f[6], nullptr, nullptr, (const float*)f[8], f[9],
                                  (const float*)fake(22), fake(10), fake(11), fake(12), (float*)fake(13),

@@ -149,3 +149,62 @@ def test_norm_zero_tokens():
     torch.cuda.synchronize()
     assert y.shape == (0, 2, 64)
     assert dw is not None and bool((dw == 0).all())
+
+
+FUSED_CASES = [
+    # (B, T, Hk, H, D, chunk, dtype): the model's head shape in bf16, and small fp32 shapes
+    (2, 300, 2, 4, 128, 128, torch.bfloat16),
+    (1, 150, 2, 4, 16, 32, torch.float32),
+    (1, 200, 2, 4, 64, 64, torch.float32),
+]
+
+
+@pytest.mark.parametrize("case", FUSED_CASES, ids=[f"D{c[4]}C{c[5]}-{str(c[6])[6:]}" for c in FUSED_CASES])
+def test_norm_in_the_output_kernel_equals_the_separate_norm(case):
+    """gdn_megakernel_normed (the gated RMSNorm's forward in the core's output kernel) against
+    gdn_megakernel followed by gated_rmsnorm, on inputs with segment cuts and trailing padding:
+    y equals the separate norm's up to the order of its sum of squares (fp32: 1e-6 relative;
+    bf16: at least 99.9% bit-identical, the rest one bf16 ulp apart); padding tokens exactly 0;
+    every gradient (the core's inputs, the gate, the norm weight) bitwise the same: the backward
+    is the same norm backward on the same saved out, so out is bitwise the same too."""
+    from gdn_cases import case_inputs
+    from tjev_amd import gdn_megakernel, gdn_megakernel_normed
+    from tjev_amd.norm import gated_rmsnorm
+
+    batch, length, hk, h, d, chunk, dtype = case
+    (qkv, a, b, a_log, dt_bias, w, seg), cot = case_inputs(batch, length, hk, h, d, dtype=dtype,
+                                                            cuts=[chunk - 1, chunk + 2])
+    gen = torch.Generator().manual_seed(3)
+    z = torch.randn((batch, length, h, d), generator=gen).to(dtype)
+    nw = 1 + 0.1 * torch.randn(d, generator=gen)
+    kw = dict(key_heads=hk, key_dim=d, value_heads=h, value_dim=d, chunk=chunk,
+              precision="high" if dtype == torch.bfloat16 else "highest")
+    print(f"fused norm case {case}", flush=True)
+
+    def leaves():
+        return [t.detach().clone().cuda().requires_grad_(t.is_floating_point())
+                for t in (qkv, a, b, a_log, dt_bias, w, z, nw)]
+
+    segc, dy = seg.cuda(), cot.to(dtype).cuda()
+    l1 = leaves()
+    y1 = gdn_megakernel_normed(*l1[:6], segc, l1[6], l1[7], 1e-6, **kw)
+    g1 = torch.autograd.grad(y1, l1, dy)
+    l2 = leaves()
+    out2 = gdn_megakernel(*l2[:6], segc, **kw)
+    y2 = gated_rmsnorm(out2, l2[6], l2[7], 1e-6, segment_ids=segc)
+    g2 = torch.autograd.grad(y2, l2, dy)
+    torch.cuda.synchronize()
+    y1, y2 = y1.detach(), y2.detach()
+    pad = seg.cuda() <= 0
+    assert bool((y1[pad] == 0).all())
+    if dtype == torch.float32:
+        assert rel(y1.cpu(), y2.cpu()) <= 1e-6
+    else:
+        same = (y1 == y2).float().mean().item()
+        ulp = (y2.float().abs().clamp_min(1e-30).log2().floor() - 7).exp2()
+        worst = float(((y1.float() - y2.float()).abs() / ulp).max())
+        print(f"bit-identical {same:.5f}, worst {worst:.2f} ulp")
+        assert same >= 0.999 and worst <= 1.0
+    names = ["qkv", "a", "b", "A_log", "dt_bias", "w", "gate", "norm_weight"]
+    for n, x1, x2 in zip(names, g1, g2):
+        assert torch.equal(x1, x2), n

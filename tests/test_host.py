@@ -376,3 +376,39 @@ def test_state_operators_reject_cpu_tensors_and_bad_shapes():
         chunk_gated_delta_rule(q, q, q, torch.zeros(1, 16, 2), torch.zeros(1, 16, 2), inverse="lu")
     with pytest.raises(RuntimeError, match="GPU"):
         chunk_gated_delta_rule(q, q, q, torch.zeros(1, 16, 2), torch.zeros(1, 16, 2))
+
+
+def test_normed_forward_validates_before_launch():
+    """tjev_gdn_mega2_fwd_normed (the core with the gated RMSNorm in its output kernel): y,
+    gate and the norm weight are required, gate and y 16-byte aligned, eps >= 0; with every
+    check passed and no workspace it stops at the workspace check, so nothing launches."""
+    from tjev_amd import _lib
+
+    lib = _lib.load()
+    vp = lambda i: ctypes.c_void_p(4096 * (i + 1))  # noqa: E731  (never dereferenced)
+    ws = ctypes.c_void_p(4096 * 64)
+
+    def fwd(gate=vp(12), nw=vp(13), eps=1e-6, y=vp(15)):
+        return lib.tjev_gdn_mega2_fwd_normed(ctypes.byref(_params(length=96, chunk=16)), None,
+                                             *[vp(i) for i in range(7)], None, None, gate, nw, ctypes.c_float(eps),
+                                             vp(14), y, vp(16), None, None, ws, 0)
+
+    assert fwd() == 3 and "workspace" in lib.tjev_gdn_last_error().decode()
+    assert fwd(y=None) == 1 and "null" in lib.tjev_gdn_last_error().decode()
+    assert fwd(gate=None) == 1 and "null" in lib.tjev_gdn_last_error().decode()
+    assert fwd(nw=None) == 1
+    assert fwd(gate=ctypes.c_void_p(4096 * 12 + 8)) == 1 and "16-byte" in lib.tjev_gdn_last_error().decode()
+    assert fwd(eps=-1.0) == 1 and "eps" in lib.tjev_gdn_last_error().decode()
+
+
+def test_normed_operator_checks_shapes_and_has_no_cpu_fallback():
+    from tjev_amd import gdn_megakernel_normed
+
+    x = torch.zeros(1, 16, 2 * 16 + 2 * 16)
+    g2 = torch.zeros(1, 16, 2)
+    args = (x, g2, g2, torch.zeros(2), torch.zeros(2), torch.zeros(4, 64), torch.ones(1, 16, dtype=torch.int32))
+    kw = dict(key_heads=1, key_dim=16, value_heads=2, value_dim=16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        gdn_megakernel_normed(*args, torch.zeros(1, 16, 2, 16), torch.ones(16), **kw)
+    with pytest.raises(ValueError, match="inverse"):
+        gdn_megakernel_normed(*args, torch.zeros(1, 16, 2, 16), torch.ones(16), inverse="lu", **kw)

@@ -28,6 +28,7 @@ EXPORTS = (
     "tjev_gdn_mega2_fwd",
     "tjev_gdn_mega2_fwd_state",
     "tjev_gdn_mega2_fwd_cont",
+    "tjev_gdn_mega2_fwd_normed",
     "tjev_gdn_mega2_bwd_cont",
     "tjev_gdn_mega2_fwd_cont_noalloc",
     "tjev_gdn_decode_step",
@@ -100,6 +101,8 @@ def load() -> ctypes.CDLL:
     lib.tjev_gdn_mega2_fwd_state.restype = i32
     lib.tjev_gdn_mega2_fwd_cont.argtypes = [pp, vp] + [vp] * 14 + [sz]
     lib.tjev_gdn_mega2_fwd_cont.restype = i32
+    lib.tjev_gdn_mega2_fwd_normed.argtypes = [pp, vp] + [vp] * 11 + [ctypes.c_float] + [vp] * 6 + [sz]
+    lib.tjev_gdn_mega2_fwd_normed.restype = i32
     lib.tjev_gdn_mega2_bwd_cont.argtypes = [pp, vp] + [vp] * 21 + [sz]
     lib.tjev_gdn_mega2_bwd_cont.restype = i32
     lib.tjev_gdn_mega2_fwd_cont_noalloc.argtypes = [pp, vp] + [vp] * 13

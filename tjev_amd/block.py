@@ -4,8 +4,8 @@ with merged-LoRA projections (src/tjev/model/lora.py:191-223 ``grouped``, :262-3
 
     x (padding rows zeroed) -> in_proj_qkv, in_proj_z, in_proj_b, in_proj_a (one input; each
     adapter merged per call, W' = W + s*A*B rounded once to the compute dtype) -> the GDN
-    megakernel core (HIP) -> the gated RMSNorm on the heads side by side with the padding
-    select (HIP) -> out_proj (merged LoRA)
+    megakernel core (HIP) with the gated RMSNorm of its output and the padding select in its
+    output kernel -> out_proj (merged LoRA)
 
 The projections are plain GEMMs on hipBLASLt (torch.mm). Their backward is the reference's
 custom VJP (lora.py:320-366): dx = sum_i dy_i W'_i^T, dA_i = s_i x^T (dy_i B_i^T),
@@ -21,8 +21,7 @@ import math
 
 import torch
 
-from .gdn import gdn_megakernel
-from .norm import gated_rmsnorm
+from .gdn import gdn_megakernel_normed
 
 
 def _mm32(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
@@ -149,9 +148,10 @@ class GatedDeltaNetBlock:
         valid = (segment_ids > 0)[..., None]
         x = torch.where(valid, x, torch.zeros((), dtype=x.dtype, device=x.device)).to(self.dtype)
         qkv, z, b, a = grouped(x, self.in_proj_qkv, self.in_proj_z, self.in_proj_b, self.in_proj_a)
-        out = gdn_megakernel(qkv, a, b, self.a_log, self.dt_bias, self.conv, segment_ids, key_heads=self.hk,
-                             key_dim=self.dk, value_heads=self.h, value_dim=self.dv, chunk=self.chunk,
-                             precision=self.precision, inverse=self.inverse, residuals=self.residuals)
-        out = out.reshape(batch, length, self.h * self.dv)
-        out = gated_rmsnorm(out, z, self.norm_weight, self.eps, heads=self.h, segment_ids=segment_ids)
-        return self.out_proj(out)
+        # the core and its gated RMSNorm (gdn.py:157-160), the norm in the core's output kernel
+        out = gdn_megakernel_normed(qkv, a, b, self.a_log, self.dt_bias, self.conv, segment_ids,
+                                    z.reshape(batch, length, self.h, self.dv), self.norm_weight, self.eps,
+                                    key_heads=self.hk, key_dim=self.dk, value_heads=self.h, value_dim=self.dv,
+                                    chunk=self.chunk, precision=self.precision, inverse=self.inverse,
+                                    residuals=self.residuals)
+        return self.out_proj(out.reshape(batch, length, self.h * self.dv))

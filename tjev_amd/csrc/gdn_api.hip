@@ -356,11 +356,18 @@ int check_state(const tjev_gdn_params* p, const void* initial_state, const void*
   return 0;
 }
 
-int tjev_gdn_mega2_fwd_cont(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
-                            const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg,
-                            const float* initial_state, const void* initial_conv, void* out, float* residuals,
-                            float* final_state, void* conv_state, void* workspace, size_t workspace_bytes) {
+// the megakernel forward, with the gated RMSNorm of its output in the output kernel when y is given
+static int mega2_fwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
+              const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg,
+              const float* initial_state, const void* initial_conv, void* out, float* residuals, float* final_state,
+              void* conv_state, const void* gate, const float* norm_weight, float eps, void* y, void* workspace,
+              size_t workspace_bytes) {
   if (int s = validate(p)) return s;
+  if (y) {
+    if (!gate || !norm_weight) return fail(TJEV_GDN_EINVAL, "null tensor argument");
+    if (!aligned(gate, 16) || !aligned(y, 16)) return fail(TJEV_GDN_EINVAL, "gate and y must be 16-byte aligned");
+    if (!(eps >= 0.f)) return fail(TJEV_GDN_EINVAL, "eps must be >= 0");
+  }
   if (!qkv || !a || !b || !a_log || !dt_bias || !seg || !out || !residuals || (p->taps > 0 && !conv_w))
     return fail(TJEV_GDN_EINVAL, "null tensor argument");
   if (!aligned(qkv, 16) || !aligned(out, 16) || !aligned(residuals, 256) || !aligned(workspace, 256))
@@ -384,8 +391,30 @@ int tjev_gdn_mega2_fwd_cont(const tjev_gdn_params* p, void* stream, const void* 
   A.init_conv = initial_conv;
   A.final_state = final_state;
   A.conv_state = conv_state;
+  A.nz = gate;
+  A.nw = norm_weight;
+  A.neps = eps;
+  A.ny = y;
   if (int s = poison_buffers(p, stream, workspace, residuals, 0)) return s;
   return run(p, stream, A, 0);
+}
+
+int tjev_gdn_mega2_fwd_cont(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
+                            const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg,
+                            const float* initial_state, const void* initial_conv, void* out, float* residuals,
+                            float* final_state, void* conv_state, void* workspace, size_t workspace_bytes) {
+  return mega2_fwd(p, stream, qkv, a, b, a_log, dt_bias, conv_w, seg, initial_state, initial_conv, out, residuals,
+                   final_state, conv_state, nullptr, nullptr, 0.f, nullptr, workspace, workspace_bytes);
+}
+
+int tjev_gdn_mega2_fwd_normed(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
+                              const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg,
+                              const float* initial_state, const void* initial_conv, const void* gate,
+                              const float* norm_weight, float eps, void* out, void* y, float* residuals,
+                              float* final_state, void* conv_state, void* workspace, size_t workspace_bytes) {
+  if (!y) return fail(TJEV_GDN_EINVAL, "null tensor argument");
+  return mega2_fwd(p, stream, qkv, a, b, a_log, dt_bias, conv_w, seg, initial_state, initial_conv, out, residuals,
+                   final_state, conv_state, gate, norm_weight, eps, y, workspace, workspace_bytes);
 }
 
 // The workspace of tjev_gdn_mega2_fwd_cont_noalloc: one array per GPU, held until the process

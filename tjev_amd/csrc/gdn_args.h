@@ -22,6 +22,12 @@ struct GdnArgs {
   const int32_t* seg;
   // forward outputs
   void* out;
+  // the gated RMSNorm of out computed in the output kernel (null ny: none): y = w rnd(x r) silu(z)
+  // with x = out as stored, r = rsqrt(mean x^2 + eps), 0 on padding tokens
+  const void* nz;    // [B, T, H, Dv] io dtype, the gate
+  const float* nw;   // [Dv]
+  float neps;
+  void* ny;          // [B, T, H, Dv] io dtype
   float* states;       // [B, H, N, Dk, Dv]
   float* final_state;  // [B, H, Dk, Dv] the state after token T-1 (or null)
   void* conv_state;    // [B, K-1, W] the raw rows before token T (or null)

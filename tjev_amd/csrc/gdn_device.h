@@ -119,6 +119,33 @@ template <> struct Raw8<uint16_t> {
   }
 };
 
+// 4 consecutive stored values held as loaded (8-byte aligned for bf16, 16-byte for fp32)
+template <class T> struct Raw4;
+template <> struct Raw4<float> {
+  float4 a;
+  __device__ __forceinline__ void load(const float* p) { a = *reinterpret_cast<const float4*>(p); }
+  __device__ __forceinline__ void get(float (&o)[4]) const { o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; }
+};
+template <> struct Raw4<uint16_t> {
+  uint2 a;
+  __device__ __forceinline__ void load(const uint16_t* p) { a = *reinterpret_cast<const uint2*>(p); }
+  __device__ __forceinline__ void get(float (&o)[4]) const {
+    o[0] = __uint_as_float(a.x << 16);
+    o[1] = __uint_as_float(a.x & 0xffff0000u);
+    o[2] = __uint_as_float(a.y << 16);
+    o[3] = __uint_as_float(a.y & 0xffff0000u);
+  }
+};
+// a value rounded to the storage type T and back (bf16: round to nearest even)
+template <class T>
+__device__ __forceinline__ float rnd_io(float v) {
+  if constexpr (sizeof(T) == 2) {
+    return bf2f(f2bf(v));
+  } else {
+    return v;
+  }
+}
+
 // ---------------------------------------------------------------- numerics
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 // The elementwise activations' forms on the hardware transcendentals (v_exp_f32, v_rcp_f32,

@@ -61,7 +61,8 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
       GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 2>), persist, dim3(C * 4));
     }
     GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd<C, D, DVT, PI, PS>), tiles, dim3(NS));
-    GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO>), persist, dim3(C * 4));
+    if (A.ny) GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO, true>), persist, dim3(C * 4));
+    else GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO>), persist, dim3(C * 4));
     if (A.final_state) GDN_LAUNCH(K_FINAL_STATE, (k_final_state<C, D>), dim3(A.B * A.H * (D / DVT)), dim3(256));
     if (A.conv_state && A.taps > 1) GDN_LAUNCH(K_FINAL_STATE, (k_conv_state<TIO>), dim3(A.B), dim3(256));
   } else {

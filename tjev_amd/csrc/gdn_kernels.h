@@ -1209,7 +1209,7 @@ struct OutIn {
   RegsT<D, D, NT> st;    // S_before rows, staged as S^T
 };
 
-template <int C, int D, int PI, int PS, class TIO>
+template <int C, int D, int PI, int PS, class TIO, bool NORM = false>
 __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
   constexpr int NT = C * 4;
   constexpr int LI = C + 4;
@@ -1218,6 +1218,10 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
   __shared__ float sI[C * LI];
   __shared__ __align__(16) char sB[TB::BYTES];
   __shared__ Ctx<C> cx;
+  __shared__ __align__(16) float snw[NORM ? D : 1];  // the norm's weight
+  if constexpr (NORM) {
+    for (int c = threadIdx.x; c < D; c += NT) snw[c] = A.nw[c];
+  }
   const Op<PI> ob = TB::at(sB);
   const int w = wave(), i0 = 16 * w;
   const int total = A.B * A.H * A.N;
@@ -1264,19 +1268,50 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
     in.v.fetch(A.vnew + hoff(A, y.b, y.h, A.H, y.n, C, D), D);
     __syncthreads();
     in.st.put_cols(ob);
+    // the lane's output row after the quad transposes below (4 consecutive columns per tile)
+    const int tok = x.n * C + i0 + ((lane() >> 4) << 2) + (lane() & 3);
+    const size_t orow = (((size_t)x.b * A.T + (tok < A.T ? tok : 0)) * A.H + x.h) * D + (lane() & 12);
+    Raw4<TIO> zr[NORM ? D / 16 : 1];  // the norm's gate, in flight during the last product
+    if constexpr (NORM) {
+#pragma unroll
+      for (int t = 0; t < D / 16; ++t) zr[t].load(reinterpret_cast<const TIO*>(A.nz) + orow + 16 * t);
+    }
     __syncthreads();
     in.q.template product<PS>(o, ob, 0, D / 16, cx.grow[i0 + (lane() & 15)]);
     in.q.fetch(A.qn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D, i0);
     in.st.fetch(A.states + ((size_t)y.b * A.H + y.h) * A.N * D * D + (size_t)y.n * D * D, D);
     TIO* out = reinterpret_cast<TIO*>(A.out);
     {  // quad transposes: each lane stores 4 consecutive columns of one row
-      const int tok = x.n * C + i0 + ((lane() >> 4) << 2) + (lane() & 3);
-      TIO* orow = out + (((size_t)x.b * A.T + (tok < A.T ? tok : 0)) * A.H + x.h) * D + (lane() & 12);
+      float ss = 0.f;
 #pragma unroll
       for (int t = 0; t < D / 16; ++t) {
         float v[4] = {o[t][0], o[t][1], o[t][2], o[t][3]};
         quad_transpose(v);
-        if (tok < A.T) st4_io(orow + 16 * t, v);
+        if (tok < A.T) st4_io(out + orow + 16 * t, v);
+        if constexpr (NORM) {  // the norm reads out as stored
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            o[t][e] = rnd_io<TIO>(v[e]);
+            ss += o[t][e] * o[t][e];
+          }
+        }
+      }
+      if constexpr (NORM) {  // gated RMSNorm (norms.py:13-15, 36-40) over the row's 4 lanes
+        ss += __shfl_xor(ss, 4);
+        ss += __shfl_xor(ss, 8);
+        const float r = rsqrt_io<TIO>(ss * (1.0f / D) + A.neps);
+        const bool valid = cx.seg[i0 + ((lane() >> 4) << 2) + (lane() & 3)] > 0;
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) {
+          float z[4], yv[4];
+          zr[t].get(z);
+          const float4 w = *reinterpret_cast<const float4*>(snw + 16 * t + (lane() & 12));
+          const float wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            yv[e] = valid ? wv[e] * rnd_io<TIO>(o[t][e] * r) * (z[e] * sigmoid_io<TIO>(z[e])) : 0.f;
+          if (tok < A.T) st4_io(reinterpret_cast<TIO*>(A.ny) + orow + 16 * t, yv);
+        }
       }
     }
     __syncthreads();  // cx and the operand region are rewritten by the next unit

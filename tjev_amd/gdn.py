@@ -24,6 +24,9 @@ import math
 import torch
 
 from . import _lib
+from .norm import _params as _norm_params
+from .norm import norm_backward
+from .norm import workspace_bytes as norm_workspace_bytes
 
 PRECISIONS = ("highest", "high", "bf16", "mixed")  # xla.py:23
 INVERSE_BLOCKS = {"doubling": 0, "blocked": 16}    # pallas_tpu_v2.py:141
@@ -106,6 +109,17 @@ class GdnPlan:
             workspace.numel())
         _lib.check_status(status)
 
+    def forward_normed(self, qkv, a, b, a_log, dt_bias, conv_w, seg, gate, norm_weight, eps: float, out, y,
+                       residuals, workspace) -> None:
+        """forward() with the gated RMSNorm of out into y in the output kernel
+        (tjev_gdn_mega2_fwd_normed)."""
+        status = self.lib.tjev_gdn_mega2_fwd_normed(
+            ctypes.byref(self.params), self._stream(qkv.device), _ptr(qkv), _ptr(a), _ptr(b), _ptr(a_log),
+            _ptr(dt_bias), _ptr(conv_w), _ptr(seg), None, None, _ptr(gate), _ptr(norm_weight),
+            ctypes.c_float(eps), _ptr(out), _ptr(y), _ptr(residuals), None, None, _ptr(workspace),
+            workspace.numel())
+        _lib.check_status(status)
+
     def backward(self, qkv, a, b, a_log, dt_bias, conv_w, seg, residuals, d_out, d_qkv, d_a, d_b, d_a_log,
                  d_dt_bias, d_conv_w, workspace) -> None:
         status = self.lib.tjev_gdn_mega2_bwd(
@@ -148,6 +162,48 @@ class _Core(torch.autograd.Function):
         plan.backward(qkv, a, b, a_log, dt_bias, conv_w, seg, res, d_out, d_qkv, d_a, d_b, d_a_log, d_dt_bias,
                       d_w, ws)
         return None, d_qkv, d_a, d_b, d_a_log, d_dt_bias, d_w, None, None
+
+
+class _CoreNormed(torch.autograd.Function):
+    """``_Core`` followed by the gated RMSNorm of its output (GatedDeltaNet.__call__,
+    model/gdn.py:157-160), the norm's forward in the output kernel; the backward is the norm's
+    backward on the saved out, then the core's."""
+
+    @staticmethod
+    def forward(ctx, plan: GdnPlan, qkv, a, b, a_log, dt_bias, conv_w, seg, gate, norm_weight, eps: float,
+                out_shape):
+        out = torch.empty(out_shape, dtype=qkv.dtype, device=qkv.device)
+        y = torch.empty(out_shape, dtype=qkv.dtype, device=qkv.device)
+        res = plan.residuals(qkv.device)
+        ws = plan.workspace(False, qkv.device)
+        plan.forward_normed(qkv, a, b, a_log, dt_bias, conv_w, seg, gate, norm_weight, eps, out, y, res, ws)
+        ctx.plan = plan
+        ctx.norm_p = _norm_params(out_shape[0] * out_shape[1], out_shape[2], out_shape[3], qkv.dtype, eps)
+        ctx.save_for_backward(qkv, a, b, a_log, dt_bias, conv_w, seg, res, out, gate, norm_weight)
+        return y
+
+    @staticmethod
+    def backward(ctx, d_y):
+        plan: GdnPlan = ctx.plan
+        qkv, a, b, a_log, dt_bias, conv_w, seg, res, out, gate, norm_weight = ctx.saved_tensors
+        d_y = d_y.to(qkv.dtype).contiguous()
+        d_out, d_gate = torch.empty_like(out), torch.empty_like(gate)
+        want_nw = ctx.needs_input_grad[9]
+        d_nw = torch.empty_like(norm_weight) if want_nw else None
+        nws = torch.empty(norm_workspace_bytes(ctx.norm_p, True), dtype=torch.uint8,
+                          device=qkv.device) if want_nw else None
+        norm_backward(ctx.norm_p, out, gate, norm_weight, seg, d_y, d_out, d_gate, d_nw, nws)
+        d_qkv = torch.empty_like(qkv)
+        d_a = torch.empty_like(a)
+        d_b = torch.empty_like(b)
+        d_a_log = torch.empty_like(a_log)
+        d_dt_bias = torch.empty_like(dt_bias)
+        want_dw = conv_w is not None and ctx.needs_input_grad[6]
+        d_w = torch.empty_like(conv_w) if want_dw else None
+        ws = plan.workspace(True, qkv.device)
+        plan.backward(qkv, a, b, a_log, dt_bias, conv_w, seg, res, d_out, d_qkv, d_a, d_b, d_a_log, d_dt_bias,
+                      d_w, ws)
+        return None, d_qkv, d_a, d_b, d_a_log, d_dt_bias, d_w, None, d_gate, d_nw, None, None
 
 
 def _conv_state_grad(d_cs, seg, d_qkv, d_init_conv, length: int):
@@ -298,6 +354,40 @@ def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: t
     out, final, conv_state = _CoreCont.apply(plan, *args, init, hist, (batch, length, value_heads, value_dim),
                                              output_final_state)
     return (out, final, conv_state) if output_final_state else out
+
+
+def gdn_megakernel_normed(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: torch.Tensor,
+                          dt_bias: torch.Tensor, conv_weight: torch.Tensor | None, segment_ids: torch.Tensor,
+                          gate: torch.Tensor, norm_weight: torch.Tensor, eps: float = 1e-6, *, key_heads: int,
+                          key_dim: int, value_heads: int, value_dim: int, chunk: int = 64, precision: str = "high",
+                          inverse: str = "doubling", heads_per_step: int = 0, residuals: str = "states"):
+    """gdn_megakernel followed by the gated RMSNorm of its output, as GatedDeltaNet.__call__
+    applies it (model/gdn.py:157-160, norms.py:36-62): gate [B, T, H, Dv] (the z projection,
+    qkv's dtype), norm_weight [Dv]. Returns y [B, T, H, Dv] in qkv's dtype, the values of
+    gated_rmsnorm(gdn_megakernel(...), gate, norm_weight, eps, segment_ids=segment_ids) up to the
+    summation order of the norm's mean square (rare last-bit differences); the norm's forward
+    runs in the megakernel's output kernel. Gradients flow to the megakernel's inputs, gate and
+    norm_weight."""
+    batch, length, width = qkv.shape
+    taps = _check(precision, inverse, chunk, width, key_heads, key_dim, value_heads, value_dim, heads_per_step,
+                  conv_weight)
+    if not qkv.is_cuda:
+        raise RuntimeError("gdn_megakernel_normed runs on the GPU (HIP); got a CPU tensor")
+    shape = (batch, length, value_heads, value_dim)
+    if tuple(gate.shape) != shape:
+        raise ValueError(f"gate must be [{batch}, {length}, {value_heads}, {value_dim}], not {tuple(gate.shape)}")
+    if tuple(norm_weight.shape) != (value_dim,):
+        raise ValueError(f"norm_weight must be [{value_dim}], not {tuple(norm_weight.shape)}")
+    plan = GdnPlan(batch=batch, length=length, key_heads=key_heads, key_dim=key_dim, value_heads=value_heads,
+                   value_dim=value_dim, taps=0 if conv_weight is None else taps, chunk=chunk,
+                   io_dtype=qkv.dtype, gate_dtype=a.dtype, precision=precision, inverse=inverse,
+                   heads_per_step=heads_per_step, residuals=residuals)
+    b = b.to(a.dtype)
+    conv_w = None if conv_weight is None else conv_weight.to(torch.float32).contiguous()
+    return _CoreNormed.apply(plan, qkv.contiguous(), a.contiguous(), b.contiguous(),
+                             a_log.to(torch.float32).contiguous(), dt_bias.to(torch.float32).contiguous(), conv_w,
+                             segment_ids.to(torch.int32).contiguous(), gate.to(qkv.dtype).contiguous(),
+                             norm_weight.to(torch.float32).contiguous(), float(eps), shape)
 
 
 def gdn_core_mega(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_heads: int, key_dim: int,

@@ -20,12 +20,13 @@ PEAK_HBM_GBS = 8000.0
 
 
 def kernel_work(*, batch: int, length: int, key_heads: int, value_heads: int, dim: int, chunk: int,
-                io_bytes: int, residuals: str = "states") -> dict[str, dict]:
+                io_bytes: int, residuals: str = "states", fused_norm: bool = False) -> dict[str, dict]:
     """Per-launch algorithmic work of each kernel: {"bytes": B, "flops": F}. Bytes are the
     minimal HBM traffic of the kernel's own inputs and outputs (each tensor read or written
     once); FLOPs count the dense chunk contractions once (zero for the elementwise kernels).
     ``residuals`` (states | tinv | all) sets what the forward's chunk kernel writes and what
-    the backward's reads, as the library's residual policy does."""
+    the backward's reads, as the library's residual policy does; ``fused_norm``: the output
+    kernel also reads the norm's gate and writes its y."""
     C, D = chunk, dim
     n = -(-length // C)
     tp = n * C
@@ -54,7 +55,8 @@ def kernel_work(*, batch: int, length: int, key_heads: int, value_heads: int, di
         # w, u, k -> v_new, S before each chunk
         "gdn_scan_fwd": {"bytes": tok_h * D * f32 * 4 + units * D * D * f32, "flops": 0},
         # q, k, v_new, S -> out
-        "gdn_out": {"bytes": 2 * act_k + act_v + mats + ctx + io, "flops": units * (2 * sq + sd)},
+        "gdn_out": {"bytes": 2 * act_k + act_v + mats + ctx + io * (3 if fused_norm else 1),
+                    "flops": units * (2 * sq + sd)},
         "gdn_prep_bwd": {"bytes": prep, "flops": 0},
         # k, v, S (and T under tinv) -> v_new = T (v beta - kbe S) (and T under states)
         "gdn_chunk_bwd": {"bytes": act_k + 2 * act_v + mats + tinv + ctx,
