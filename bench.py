@@ -3,8 +3,9 @@
 
 A step is one forward and one backward pass of the GDN layer core over one batch of synthetic
 inputs already resident in HBM (the HIP library called through its C ABI, no autograd): the
-megakernel's out and chunk states, the gated RMSNorm y of out with gate z (its own kernel;
-``--fused-norm``: in the megakernel's output kernel), then under a fixed upstream gradient of y
+megakernel's out and chunk states, the gated RMSNorm y of out with gate z (in the megakernel's
+output kernel, its backward in the same call as the megakernel's; ``--unfused-norm``: as their
+own calls), then under a fixed upstream gradient of y
 the norm's backward (d out, d z) and the megakernel's d(qkv), d(a), d(b), d(A_log),
 d(dt_bias). ``--no-norm`` times the megakernel alone. W untimed warm-up steps, then K timed
 steps between device synchronizations;
@@ -41,9 +42,9 @@ def _args(argv=None):
     ap.add_argument("--config", default="0.8B")
     ap.add_argument("--precision", default=None, help="override the config's precision")
     ap.add_argument("--no-norm", action="store_true", help="time the GDN core alone, without the gated RMSNorm")
-    ap.add_argument("--fused-norm", action="store_true",
-                    help="run the norm's forward in the core's output kernel (tjev_gdn_mega2_fwd_normed) instead "
-                         "of as its own kernel (measured: the same step time)")
+    ap.add_argument("--unfused-norm", action="store_true",
+                    help="the norm as its own forward and backward calls instead of in the megakernel's "
+                         "(tjev_gdn_mega2_fwd_normed / _bwd_normed: the forward in the output kernel)")
     ap.add_argument("--residuals", default="states", choices=("states", "tinv", "all"),
                     help="what the forward keeps for the backward (default: the chunk-boundary states only)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -421,16 +422,19 @@ def main(argv=None) -> int:
     d_qkv, d_a, d_b = torch.empty_like(qkv), torch.empty_like(a), torch.empty_like(b)
     d_alog, d_dtb = torch.empty_like(a_log), torch.empty_like(dt_bias)
 
-    fused = norm and args.fused_norm
+    fused = norm and not args.unfused_norm
+    if fused:
+        ws = torch.empty(max(plan.fwd_bytes, plan.normed_bwd_bytes(False)), dtype=torch.uint8, device=dev)
 
     def step():
-        if fused:  # the norm's forward in the core's output kernel
+        if fused:  # the norm's forward in the core's output kernel, its backward in the core's call
             plan.forward_normed(qkv, a, b, a_log, dt_bias, w, seg, z, norm_w, 1e-6, out, y, states, ws)
-        else:
-            plan.forward(qkv, a, b, a_log, dt_bias, w, seg, out, states, ws)
-            if norm:
-                norm_forward(norm_p, out, z, norm_w, seg, y)
+            plan.backward_normed(qkv, a, b, a_log, dt_bias, w, seg, states, out, z, norm_w, 1e-6, d_y, d_qkv, d_a,
+                                 d_b, d_alog, d_dtb, None, d_z, None, ws)
+            return
+        plan.forward(qkv, a, b, a_log, dt_bias, w, seg, out, states, ws)
         if norm:
+            norm_forward(norm_p, out, z, norm_w, seg, y)
             norm_backward(norm_p, out, z, norm_w, seg, d_y, d_out, d_z, None, None)
         plan.backward(qkv, a, b, a_log, dt_bias, w, seg, states, d_out, d_qkv, d_a, d_b, d_alog, d_dtb, None, ws)
 

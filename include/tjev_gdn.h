@@ -159,6 +159,24 @@ int tjev_gdn_mega2_bwd_cont(const tjev_gdn_params* p, void* stream, const void* 
                             float* d_initial_state, void* d_initial_conv, void* workspace,
                             size_t workspace_bytes);
 
+/* The backward of tjev_gdn_mega2_fwd_normed: the gated RMSNorm's backward (what
+ * tjev_gdn_gated_rmsnorm_bwd computes from out, gate, norm_weight, seg and d_y: d out, d_gate and,
+ * when not null, d_norm_weight [Dv] fp32), then tjev_gdn_mega2_bwd_cont's from that d out, in one
+ * call on the caller's stream (the backward of GatedDeltaNet.__call__'s core and norm,
+ * src/tjev/model/gdn.py:157-160). d out lives in the workspace, of
+ * tjev_gdn_workspace_bytes_normed(p, d_norm_weight != null) bytes. out, gate, d_y and d_gate
+ * [B, T, H, Dv] io_dtype, 16-byte aligned. */
+size_t tjev_gdn_workspace_bytes_normed(const tjev_gdn_params* p, int norm_weight_grad);
+int tjev_gdn_mega2_bwd_normed(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a,
+                              const void* b, const float* a_log, const float* dt_bias,
+                              const float* conv_w, const int32_t* seg, const float* initial_state,
+                              const void* initial_conv, const float* residuals, const void* out,
+                              const void* gate, const float* norm_weight, float eps,
+                              const void* d_y, const float* d_final_state, void* d_qkv, void* d_a,
+                              void* d_b, float* d_a_log, float* d_dt_bias, float* d_conv_w,
+                              float* d_initial_state, void* d_initial_conv, void* d_gate,
+                              float* d_norm_weight, void* workspace, size_t workspace_bytes);
+
 /* tjev_gdn_mega2_fwd_cont without a workspace argument and without any allocation: no
  * counterpart in the reference; for callers that cannot allocate device memory (code under HIP
  * graph capture, serving loops that prefill prompt pieces, harnesses that forbid hipMalloc). The

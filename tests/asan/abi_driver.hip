@@ -143,6 +143,22 @@ int main() {
                                    (const float*)fake(25), -1.f, fake(7), fake(26), (float*)fake(8), nullptr, nullptr,
                                    ws, 0),
          TJEV_GDN_EINVAL, "fwd_normed negative eps");
+  expect(tjev_gdn_mega2_bwd_normed(&p, nullptr, f[0], f[1], f[2], (const float*)f[3], (const float*)f[4],
+                                   (const float*)f[5], (const int32_t*)f[6], nullptr, nullptr, (const float*)f[8],
+                                   fake(7), fake(24), (const float*)fake(25), 1e-6f, fake(9), nullptr, fake(10),
+                                   fake(11), fake(12), (float*)fake(13), (float*)fake(14), nullptr, nullptr, nullptr,
+                                   fake(26), (float*)fake(27), ws, 0),
+         TJEV_GDN_EWORKSPACE, "bwd_normed");
+  expect(tjev_gdn_mega2_bwd_normed(&p, nullptr, f[0], f[1], f[2], (const float*)f[3], (const float*)f[4],
+                                   (const float*)f[5], (const int32_t*)f[6], nullptr, nullptr, (const float*)f[8],
+                                   nullptr, fake(24), (const float*)fake(25), 1e-6f, fake(9), nullptr, fake(10),
+                                   fake(11), fake(12), (float*)fake(13), (float*)fake(14), nullptr, nullptr, nullptr,
+                                   fake(26), nullptr, ws, 0),
+         TJEV_GDN_EINVAL, "bwd_normed null out");
+  if (tjev_gdn_workspace_bytes_normed(&p, 1) <= tjev_gdn_workspace_bytes(&p, 1)) {
+    std::printf("MISMATCH workspace_bytes_normed\n");
+    ++g_bad;
+  }
   expect(tjev_gdn_mega2_bwd_cont(&p, nullptr, f[0], f[1], f[2], (const float*)f[3], (const float*)f[4],
                                  (const float*)f[5], (const int32_t*)f[6], nullptr, nullptr, (const float*)f[8], f[9],
                                  (const float*)fake(22), fake(10), fake(11), fake(12), (float*)fake(13),

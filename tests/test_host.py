@@ -412,3 +412,33 @@ def test_normed_operator_checks_shapes_and_has_no_cpu_fallback():
         gdn_megakernel_normed(*args, torch.zeros(1, 16, 2, 16), torch.ones(16), **kw)
     with pytest.raises(ValueError, match="inverse"):
         gdn_megakernel_normed(*args, torch.zeros(1, 16, 2, 16), torch.ones(16), inverse="lu", **kw)
+
+
+def test_normed_backward_validates_before_launch():
+    """tjev_gdn_mega2_bwd_normed: out, gate, d_y and d_gate are required and 16-byte aligned,
+    eps >= 0, and its workspace (tjev_gdn_workspace_bytes_normed) holds the megakernel
+    backward's, d out and the norm's weight-gradient partials; with no workspace every valid
+    call stops at the workspace check, before the norm's backward is launched."""
+    from tjev_amd import _lib
+
+    lib = _lib.load()
+    vp = lambda i: ctypes.c_void_p(4096 * (i + 1))  # noqa: E731  (never dereferenced)
+    ws = ctypes.c_void_p(4096 * 64)
+    p = _params(length=96, chunk=16)
+    base = lib.tjev_gdn_workspace_bytes(ctypes.byref(p), 1)
+    dout = 1 * 96 * p.value_heads * p.value_dim * 4
+    assert lib.tjev_gdn_workspace_bytes_normed(ctypes.byref(p), 0) == base + dout
+    assert lib.tjev_gdn_workspace_bytes_normed(ctypes.byref(p), 1) > base + dout
+    assert lib.tjev_gdn_workspace_bytes_normed(ctypes.byref(_params(chunk=24)), 0) == 0
+
+    def bwd(out=vp(12), gate=vp(13), eps=1e-6, d_y=vp(15), d_gate=vp(26), d_nw=None):
+        return lib.tjev_gdn_mega2_bwd_normed(ctypes.byref(p), None, *[vp(i) for i in range(7)], None, None, vp(9),
+                                             out, gate, vp(14), ctypes.c_float(eps), d_y, None,
+                                             *[vp(16 + i) for i in range(5)], None, None, None, d_gate, d_nw, ws, 0)
+
+    assert bwd() == 3 and "workspace" in lib.tjev_gdn_last_error().decode()
+    assert bwd(d_nw=vp(27)) == 3
+    assert bwd(out=None) == 1 and "null" in lib.tjev_gdn_last_error().decode()
+    assert bwd(d_gate=None) == 1
+    assert bwd(d_y=ctypes.c_void_p(4096 * 15 + 4)) == 1 and "16-byte" in lib.tjev_gdn_last_error().decode()
+    assert bwd(eps=float("nan")) == 1 and "eps" in lib.tjev_gdn_last_error().decode()

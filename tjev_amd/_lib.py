@@ -29,6 +29,8 @@ EXPORTS = (
     "tjev_gdn_mega2_fwd_state",
     "tjev_gdn_mega2_fwd_cont",
     "tjev_gdn_mega2_fwd_normed",
+    "tjev_gdn_mega2_bwd_normed",
+    "tjev_gdn_workspace_bytes_normed",
     "tjev_gdn_mega2_bwd_cont",
     "tjev_gdn_mega2_fwd_cont_noalloc",
     "tjev_gdn_decode_step",
@@ -103,6 +105,10 @@ def load() -> ctypes.CDLL:
     lib.tjev_gdn_mega2_fwd_cont.restype = i32
     lib.tjev_gdn_mega2_fwd_normed.argtypes = [pp, vp] + [vp] * 11 + [ctypes.c_float] + [vp] * 6 + [sz]
     lib.tjev_gdn_mega2_fwd_normed.restype = i32
+    lib.tjev_gdn_mega2_bwd_normed.argtypes = [pp, vp] + [vp] * 13 + [ctypes.c_float] + [vp] * 13 + [sz]
+    lib.tjev_gdn_mega2_bwd_normed.restype = i32
+    lib.tjev_gdn_workspace_bytes_normed.argtypes = [pp, i32]
+    lib.tjev_gdn_workspace_bytes_normed.restype = sz
     lib.tjev_gdn_mega2_bwd_cont.argtypes = [pp, vp] + [vp] * 21 + [sz]
     lib.tjev_gdn_mega2_bwd_cont.restype = i32
     lib.tjev_gdn_mega2_fwd_cont_noalloc.argtypes = [pp, vp] + [vp] * 13

@@ -552,15 +552,47 @@ int tjev_gdn_v2_bwd(const tjev_gdn_params* p, void* stream, const void* q, const
                               d_beta, nullptr, workspace, workspace_bytes);
 }
 
-int tjev_gdn_mega2_bwd_cont(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
-                            const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg,
-                            const float* initial_state, const void* initial_conv, const float* residuals,
-                            const void* d_out, const float* d_final_state, void* d_qkv, void* d_a, void* d_b,
-                            float* d_a_log, float* d_dt_bias, float* d_conv_w, float* d_initial_state,
-                            void* d_initial_conv, void* workspace, size_t workspace_bytes) {
+// The gated RMSNorm's backward ahead of the megakernel's (tjev_gdn_mega2_bwd_normed): its
+// inputs, and where its d out goes (a part of the caller's workspace).
+struct NormBwd {
+  const void* out;
+  const void* gate;
+  const float* weight;
+  float eps;
+  const void* d_y;
+  void* d_gate;
+  float* d_weight;
+};
+
+// the extra workspace of tjev_gdn_mega2_bwd_normed after the megakernel backward's: d out, then
+// the norm's weight-gradient partials
+static size_t norm_bwd_extra(const tjev_gdn_params* p, int weight_grad, tjev_gdn_norm_params* np, size_t* dout_bytes) {
+  np->tokens = (int64_t)p->batch * p->length;
+  np->heads = p->value_heads;
+  np->dim = p->value_dim;
+  np->dtype = p->io_dtype;
+  np->eps = 0.f;
+  *dout_bytes = ((size_t)np->tokens * p->value_heads * p->value_dim * (p->io_dtype == TJEV_GDN_BF16 ? 2 : 4) + 255) &
+                ~size_t(255);
+  return *dout_bytes + tjev_gdn_norm_workspace_bytes(np, weight_grad);
+}
+
+static int mega2_bwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
+                     const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg,
+                     const float* initial_state, const void* initial_conv, const float* residuals, const void* d_out,
+                     const float* d_final_state, void* d_qkv, void* d_a, void* d_b, float* d_a_log, float* d_dt_bias,
+                     float* d_conv_w, float* d_initial_state, void* d_initial_conv, void* workspace,
+                     size_t workspace_bytes, const NormBwd* nb) {
   if (int s = validate(p)) return s;
-  if (!qkv || !a || !b || !a_log || !dt_bias || !seg || !residuals || !d_out || !d_qkv || !d_a || !d_b || !d_a_log ||
-      !d_dt_bias || (p->taps > 0 && !conv_w))
+  if (nb) {  // d out comes from the norm's backward, into the workspace after the megakernel's part
+    if (!nb->out || !nb->gate || !nb->weight || !nb->d_y || !nb->d_gate) return fail(TJEV_GDN_EINVAL, "null tensor argument");
+    if (!aligned(nb->out, 16) || !aligned(nb->gate, 16) || !aligned(nb->d_y, 16) || !aligned(nb->d_gate, 16))
+      return fail(TJEV_GDN_EINVAL, "out, gate, d_y and d_gate must be 16-byte aligned");
+    if (!(nb->eps >= 0.f)) return fail(TJEV_GDN_EINVAL, "eps must be >= 0");
+    d_out = workspace ? static_cast<char*>(workspace) + layout(p, 1).total : nullptr;
+  }
+  if (!qkv || !a || !b || !a_log || !dt_bias || !seg || !residuals || (!d_out && !nb) || !d_qkv || !d_a || !d_b ||
+      !d_a_log || !d_dt_bias || (p->taps > 0 && !conv_w))
     return fail(TJEV_GDN_EINVAL, "null tensor argument");
   if (p->taps == 0 && d_conv_w) return fail(TJEV_GDN_EINVAL, "no conv weight gradient without a conv (taps == 0)");
   if (!aligned(qkv, 16) || !aligned(d_out, 16) || !aligned(d_qkv, 16) || !aligned(residuals, 256) ||
@@ -568,8 +600,11 @@ int tjev_gdn_mega2_bwd_cont(const tjev_gdn_params* p, void* stream, const void* 
     return fail(TJEV_GDN_EINVAL, "tensors must be 16-byte aligned, the residuals and workspace 256-byte aligned");
   if (int s = check_state(p, initial_state, initial_conv, d_final_state, d_initial_state, d_initial_conv)) return s;
   const Layout L = layout(p, 1);
-  if (!workspace || workspace_bytes < L.total)
-    return fail(TJEV_GDN_EWORKSPACE, "backward workspace needs " + std::to_string(L.total) + " bytes");
+  tjev_gdn_norm_params np{};
+  size_t dout_bytes = 0;
+  const size_t need = L.total + (nb ? norm_bwd_extra(p, nb->d_weight != nullptr, &np, &dout_bytes) : 0);
+  if (!workspace || workspace_bytes < need)
+    return fail(TJEV_GDN_EWORKSPACE, "backward workspace needs " + std::to_string(need) + " bytes");
   gdn::GdnArgs A = base_args(p, workspace, L);
   A.qkv = qkv;
   A.ga = a;
@@ -592,7 +627,46 @@ int tjev_gdn_mega2_bwd_cont(const tjev_gdn_params* p, void* stream, const void* 
   A.d_init_state = d_initial_state;
   A.d_init_conv = d_initial_conv;
   if (int s = poison_buffers(p, stream, workspace, nullptr, 1)) return s;
+  if (!nb) return run(p, stream, A, 1);
+  // the norm's backward into d out, then the megakernel's, on the caller's stream
+  np.eps = nb->eps;
+  char* nws = static_cast<char*>(workspace) + L.total + dout_bytes;
+  if (int s = tjev_gdn_gated_rmsnorm_bwd(&np, stream, nb->out, nb->gate, nb->weight, seg, nb->d_y,
+                                         const_cast<void*>(d_out), nb->d_gate, nb->d_weight, nws,
+                                         workspace_bytes - L.total - dout_bytes))
+    return s;
   return run(p, stream, A, 1);
+}
+
+int tjev_gdn_mega2_bwd_cont(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
+                            const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg,
+                            const float* initial_state, const void* initial_conv, const float* residuals,
+                            const void* d_out, const float* d_final_state, void* d_qkv, void* d_a, void* d_b,
+                            float* d_a_log, float* d_dt_bias, float* d_conv_w, float* d_initial_state,
+                            void* d_initial_conv, void* workspace, size_t workspace_bytes) {
+  return mega2_bwd(p, stream, qkv, a, b, a_log, dt_bias, conv_w, seg, initial_state, initial_conv, residuals, d_out,
+                   d_final_state, d_qkv, d_a, d_b, d_a_log, d_dt_bias, d_conv_w, d_initial_state, d_initial_conv,
+                   workspace, workspace_bytes, nullptr);
+}
+
+size_t tjev_gdn_workspace_bytes_normed(const tjev_gdn_params* p, int norm_weight_grad) {
+  if (validate(p)) return 0;
+  tjev_gdn_norm_params np{};
+  size_t dout_bytes = 0;
+  return layout(p, 1).total + norm_bwd_extra(p, norm_weight_grad, &np, &dout_bytes);
+}
+
+int tjev_gdn_mega2_bwd_normed(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,
+                              const float* a_log, const float* dt_bias, const float* conv_w, const int32_t* seg,
+                              const float* initial_state, const void* initial_conv, const float* residuals,
+                              const void* out, const void* gate, const float* norm_weight, float eps, const void* d_y,
+                              const float* d_final_state, void* d_qkv, void* d_a, void* d_b, float* d_a_log,
+                              float* d_dt_bias, float* d_conv_w, float* d_initial_state, void* d_initial_conv,
+                              void* d_gate, float* d_norm_weight, void* workspace, size_t workspace_bytes) {
+  const NormBwd nb{out, gate, norm_weight, eps, d_y, d_gate, d_norm_weight};
+  return mega2_bwd(p, stream, qkv, a, b, a_log, dt_bias, conv_w, seg, initial_state, initial_conv, residuals, nullptr,
+                   d_final_state, d_qkv, d_a, d_b, d_a_log, d_dt_bias, d_conv_w, d_initial_state, d_initial_conv,
+                   workspace, workspace_bytes, &nb);
 }
 
 int tjev_gdn_mega2_bwd(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a, const void* b,

@@ -24,9 +24,6 @@ import math
 import torch
 
 from . import _lib
-from .norm import _params as _norm_params
-from .norm import norm_backward
-from .norm import workspace_bytes as norm_workspace_bytes
 
 PRECISIONS = ("highest", "high", "bf16", "mixed")  # xla.py:23
 INVERSE_BLOCKS = {"doubling": 0, "blocked": 16}    # pallas_tpu_v2.py:141
@@ -120,6 +117,22 @@ class GdnPlan:
             workspace.numel())
         _lib.check_status(status)
 
+    def normed_bwd_bytes(self, norm_weight_grad: bool) -> int:
+        return int(self.lib.tjev_gdn_workspace_bytes_normed(ctypes.byref(self.params), int(norm_weight_grad)))
+
+    def backward_normed(self, qkv, a, b, a_log, dt_bias, conv_w, seg, residuals, out, gate, norm_weight,
+                        eps: float, d_y, d_qkv, d_a, d_b, d_a_log, d_dt_bias, d_conv_w, d_gate, d_norm_weight,
+                        workspace) -> None:
+        """The backward of forward_normed: the norm's backward and the megakernel's in one call
+        (tjev_gdn_mega2_bwd_normed)."""
+        status = self.lib.tjev_gdn_mega2_bwd_normed(
+            ctypes.byref(self.params), self._stream(qkv.device), _ptr(qkv), _ptr(a), _ptr(b), _ptr(a_log),
+            _ptr(dt_bias), _ptr(conv_w), _ptr(seg), None, None, _ptr(residuals), _ptr(out), _ptr(gate),
+            _ptr(norm_weight), ctypes.c_float(eps), _ptr(d_y), None, _ptr(d_qkv), _ptr(d_a), _ptr(d_b),
+            _ptr(d_a_log), _ptr(d_dt_bias), _ptr(d_conv_w), None, None, _ptr(d_gate), _ptr(d_norm_weight),
+            _ptr(workspace), workspace.numel())
+        _lib.check_status(status)
+
     def backward(self, qkv, a, b, a_log, dt_bias, conv_w, seg, residuals, d_out, d_qkv, d_a, d_b, d_a_log,
                  d_dt_bias, d_conv_w, workspace) -> None:
         status = self.lib.tjev_gdn_mega2_bwd(
@@ -167,7 +180,7 @@ class _Core(torch.autograd.Function):
 class _CoreNormed(torch.autograd.Function):
     """``_Core`` followed by the gated RMSNorm of its output (GatedDeltaNet.__call__,
     model/gdn.py:157-160), the norm's forward in the output kernel; the backward is the norm's
-    backward on the saved out, then the core's."""
+    backward on the saved out, then the core's (one library call)."""
 
     @staticmethod
     def forward(ctx, plan: GdnPlan, qkv, a, b, a_log, dt_bias, conv_w, seg, gate, norm_weight, eps: float,
@@ -178,7 +191,7 @@ class _CoreNormed(torch.autograd.Function):
         ws = plan.workspace(False, qkv.device)
         plan.forward_normed(qkv, a, b, a_log, dt_bias, conv_w, seg, gate, norm_weight, eps, out, y, res, ws)
         ctx.plan = plan
-        ctx.norm_p = _norm_params(out_shape[0] * out_shape[1], out_shape[2], out_shape[3], qkv.dtype, eps)
+        ctx.eps = eps
         ctx.save_for_backward(qkv, a, b, a_log, dt_bias, conv_w, seg, res, out, gate, norm_weight)
         return y
 
@@ -187,12 +200,9 @@ class _CoreNormed(torch.autograd.Function):
         plan: GdnPlan = ctx.plan
         qkv, a, b, a_log, dt_bias, conv_w, seg, res, out, gate, norm_weight = ctx.saved_tensors
         d_y = d_y.to(qkv.dtype).contiguous()
-        d_out, d_gate = torch.empty_like(out), torch.empty_like(gate)
+        d_gate = torch.empty_like(gate)
         want_nw = ctx.needs_input_grad[9]
         d_nw = torch.empty_like(norm_weight) if want_nw else None
-        nws = torch.empty(norm_workspace_bytes(ctx.norm_p, True), dtype=torch.uint8,
-                          device=qkv.device) if want_nw else None
-        norm_backward(ctx.norm_p, out, gate, norm_weight, seg, d_y, d_out, d_gate, d_nw, nws)
         d_qkv = torch.empty_like(qkv)
         d_a = torch.empty_like(a)
         d_b = torch.empty_like(b)
@@ -200,9 +210,9 @@ class _CoreNormed(torch.autograd.Function):
         d_dt_bias = torch.empty_like(dt_bias)
         want_dw = conv_w is not None and ctx.needs_input_grad[6]
         d_w = torch.empty_like(conv_w) if want_dw else None
-        ws = plan.workspace(True, qkv.device)
-        plan.backward(qkv, a, b, a_log, dt_bias, conv_w, seg, res, d_out, d_qkv, d_a, d_b, d_a_log, d_dt_bias,
-                      d_w, ws)
+        ws = torch.empty(plan.normed_bwd_bytes(want_nw), dtype=torch.uint8, device=qkv.device)
+        plan.backward_normed(qkv, a, b, a_log, dt_bias, conv_w, seg, res, out, gate, norm_weight, ctx.eps, d_y,
+                             d_qkv, d_a, d_b, d_a_log, d_dt_bias, d_w, d_gate, d_nw, ws)
         return None, d_qkv, d_a, d_b, d_a_log, d_dt_bias, d_w, None, d_gate, d_nw, None, None
 
 
