@@ -93,6 +93,22 @@ def test_hip_shape_grid_fp32(chunk, d):
         assert err < TOL[name], (name, errors)
 
 
+@pytest.mark.parametrize("chunk,d", [(256, 16), (512, 64)], ids=["C256D16", "C512D64"])
+def test_hip_chunks_above_128_fp32(chunk, d):
+    """Chunks above 128 (the reference accepts any power of two) run the chunk-128 kernels: the
+    chunked form is exact for any chunk, so the result is the oracle's at the fp32 bar."""
+    hk, h = 2, 4
+    inputs, cot = case_inputs(1, 700, hk, h, d, cuts=[127, 300, 513])
+    shape = dict(key_heads=hk, key_dim=d, value_heads=h, value_dim=d, conv=True)
+    print(f"chunk {chunk} d={d}", flush=True)
+    got = hip_outputs(inputs, cot, chunk=chunk, precision="highest", **shape)
+    want = oracle_outputs(inputs, cot, **shape)
+    errors = {k: rel(got[k], want[k]) for k in got}
+    assert all(bool(torch.isfinite(v).all()) for v in got.values())
+    for name, err in errors.items():
+        assert err < TOL[name], (name, errors)
+
+
 @pytest.mark.parametrize("d,chunk,taps", [(16, 32, 4), (16, 128, 4), (64, 64, 4), (16, 32, 5)])
 def test_hip_frozen_conv_weight_fp32(d, chunk, taps):
     """The conv weight not differentiated (pallas_tpu_mega.py:548-571 emits no dz then), as in

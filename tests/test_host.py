@@ -442,3 +442,17 @@ def test_normed_backward_validates_before_launch():
     assert bwd(d_gate=None) == 1
     assert bwd(d_y=ctypes.c_void_p(4096 * 15 + 4)) == 1 and "16-byte" in lib.tjev_gdn_last_error().decode()
     assert bwd(eps=float("nan")) == 1 and "eps" in lib.tjev_gdn_last_error().decode()
+
+
+def test_chunks_above_128_run_the_128_kernels():
+    """Every power-of-two chunk >= 8 is accepted (pallas_tpu_mega.py:597-615): chunks above 128 run
+    the chunk-128 kernels, so their residual and workspace sizes are chunk 128's."""
+    from tjev_amd import _lib
+
+    lib = _lib.load()
+    for c in (256, 512, 1024):
+        p = _params(chunk=c, length=600)
+        assert lib.tjev_gdn_check(ctypes.byref(p)) == 0
+        q = _params(chunk=128, length=600)
+        assert lib.tjev_gdn_residual_bytes(ctypes.byref(p)) == lib.tjev_gdn_residual_bytes(ctypes.byref(q))
+        assert lib.tjev_gdn_workspace_bytes(ctypes.byref(p), 1) == lib.tjev_gdn_workspace_bytes(ctypes.byref(q), 1)

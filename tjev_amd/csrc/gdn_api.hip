@@ -42,9 +42,10 @@ std::string supported_shapes() {
   return s;
 }
 
-// The chunk the kernels run: the requested one, or 16 for chunks below 16 (the chunked form is
-// exact for any chunk, so only fp32 rounding depends on it).
-int kernel_chunk(const tjev_gdn_params* p) { return p->chunk < 16 ? 16 : p->chunk; }
+// The chunk the kernels run: the requested one, 16 for chunks below 16 and 128 for chunks above
+// 128 (the chunked form is exact for any chunk, so only fp32 rounding depends on it; a chunk's
+// C x C operands in LDS bound it at 128).
+int kernel_chunk(const tjev_gdn_params* p) { return p->chunk < 16 ? 16 : (p->chunk > 128 ? 128 : p->chunk); }
 
 // Validation in the order of gdn_megakernel (pallas_tpu_mega.py:597-615) and
 // heads_per_block (pallas_tpu_v2.py:518-525).

@@ -77,7 +77,7 @@ class GdnPlan:
         if status == 1:
             raise ValueError(self.lib.tjev_gdn_last_error().decode())
         _lib.check_status(status)
-        self.chunk_run = max(chunk, 16)
+        self.chunk_run = min(max(chunk, 16), 128)  # the kernels' chunk (tjev_gdn_params.chunk clamped)
         self.n_chunks = math.ceil(length / self.chunk_run)
         self.states_shape = (batch, value_heads, self.n_chunks, key_dim, value_dim)
         self.residual_bytes = self.lib.tjev_gdn_residual_bytes(ctypes.byref(self.params))
