@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""GDN megakernel fwd+bwd throughput on one MI355X (tjev's mega2, BASELINE.json's metric).
+"""GDN megakernel fwd+bwd throughput on one MI355X (tjev's mega2: fwd+bwd tokens/s of the GDN layer).
 
 A step is one forward and one backward pass of the GDN layer core over one batch of synthetic
 inputs already resident in HBM (the HIP library called through its C ABI, no autograd): the
@@ -16,7 +16,7 @@ torch autograd) on a bounded sample of the same workload.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 0.8B|9B|varlen|tiny|4B-block|decode|v2]
 
-``--config 4B-block`` times BASELINE's block config instead: the 4B-shaped GDN block with merged
+``--config 4B-block`` times the 4B block config instead: the 4B-shaped GDN block with merged
 LoRA r64 (projections on hipBLASLt, core and norm in the HIP library), with peak activation
 bytes; ``--config decode`` the serving path's one-token decode step (64 rows, 0.8B head shape);
 ``--config v2`` the v2 operator (pre-gated q, k, v, g, beta) fwd+bwd at the 0.8B layer shape.
@@ -75,7 +75,7 @@ def _cpu_cores() -> tuple[int, int, str]:
 
 
 def _cpu_median(one_pass, reps: int = 3) -> tuple[float, list[float]]:
-    """One warm-up pass, then the median of ``reps`` timed passes (BASELINE's CPU timing)."""
+    """One warm-up pass, then the median of ``reps`` timed passes (the CPU baseline's timing rule)."""
     one_pass()
     times = []
     for _ in range(reps):
@@ -141,7 +141,7 @@ BLOCK = dict(batch=2, length=8192, hidden=2560, key_heads=16, key_dim=128, value
 
 
 def _block_bench(args) -> dict:
-    """BASELINE's block config: the 4B-shaped GDN block (src/tjev/model/gdn.py:126-164) fwd+bwd
+    """The 4B block config: the 4B-shaped GDN block (src/tjev/model/gdn.py:126-164) fwd+bwd
     with merged LoRA r64 on every projection (tjev_amd/block.py), bf16, one segment per row.
     A step is the block's forward and the backward of sum(out * dy) to x and every adapter.
     Peak activation bytes: the step's allocator peak above what is resident before it
@@ -304,7 +304,7 @@ def _v2_bench(args) -> dict:
     ``gdn_impl=pallas_tpu_v2``) fwd+bwd at the 0.8B layer shape (B=4, T=4096, Hk=H=16, D=128,
     chunk 128, precision high, one segment per row): q and k l2-normalised with q scaled by
     Dk^-1/2 (as gdn.py:90-92 passes them), v ~ N(0, 1) in bf16; g = -exp(A_log) softplus(a +
-    dt_bias) and beta = sigmoid(b) in fp32 from BASELINE's distributions. A step is the forward
+    dt_bias) and beta = sigmoid(b) in fp32 from the benchmark's input distributions. A step is the forward
     and the backward of sum(out * dy) to q, k, v, g and beta. The chunk, scan and gradient kernels
     are the megakernel's (the roofline object is the dominant one's); the ends are v2's own."""
     import math

@@ -4,7 +4,7 @@ The reference commits no GDN arrays (its tests are differential on jax.random in
 fixtures come from this repository's oracle in float64 (the chunked form, equal to the token
 recurrence to ~1e-12 as tests/test_oracle.py pins): inputs, the fixed upstream gradient, and
 the expected output and gradients of qkv, a, b, A_log, dt_bias and the conv weight. Shapes
-mirror the reference's tests (tests/kernels/test_gdn_mega.py:96-111) and BASELINE config 1.
+mirror the reference's tests (tests/kernels/test_gdn_mega.py:96-111) and the tiny fp32 benchmark config.
 
     python tests/golden/make_golden.py
 """

@@ -9,7 +9,7 @@ norm, merged LoRA on every projection) against the oracle's ``gdn_block`` with t
 - bf16 (precision "high"): against the oracle on the same bf16 values with the activations
   stored in bf16 between the stages as the reference's bf16 layer stores them (the core in
   fp32), the output's max abs error beyond its own bf16 rounding <= 2e-2 RMS and gradient
-  cosine >= 0.9999; at BASELINE's block shape (hidden 2560, 16/32 heads of 128, r64) the
+  cosine >= 0.9999; at the 4B block benchmark shape (hidden 2560, 16/32 heads of 128, r64) the
   output's error beyond one bf16 spacing of each element <= 2e-2 RMS.
 """
 
@@ -136,7 +136,7 @@ def test_block_bf16_matches_oracle():
 
 
 def test_block_bf16_config5_shape():
-    """BASELINE's block config at its own shape (src/tjev/model/gdn.py:126-164 with the LoRA
+    """The 4B block benchmark config at its own shape (src/tjev/model/gdn.py:126-164 with the LoRA
     layouts of campaign/bench.py:383-390): hidden 2560, Hk/H 16/32, Dk = Dv = C = 128, merged
     LoRA r64 on all five projections (A ~ N(0, 1/r), B ~ N(0, 0.01)), precision "high", one row
     of 512 tokens with packed segments and padding, against the oracle block on the same bf16

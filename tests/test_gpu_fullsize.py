@@ -1,4 +1,4 @@
-"""GPU parity at BASELINE's full sizes (0.8B: B=4, T=4096, 16/16 heads; 9B: B=2, T=8192, 16/32
+"""GPU parity at the benchmark's full sizes (0.8B: B=4, T=4096, 16/16 heads; 9B: B=2, T=8192, 16/32
 heads; varlen: B=1, T=16384 packed segments), all D = 128, chunk 128, bf16, precision high,
 through the C ABI.
 

@@ -84,7 +84,7 @@ def test_norm_bf16_matches_oracle_roundings(shape):
     assert bool(((y.float() - oy.float()).abs() <= ulp).all())
     for name, g, h in (("d_x", dx, odx), ("d_gate", dz, odz), ("d_weight", dw, odw)):
         assert cosine(g, h) >= 0.99999, (name, cosine(g, h))
-    # the BASELINE bf16 bar against the reference's semantics (the oracle at bf16)
+    # the benchmark's bf16 bar against the reference's semantics (the oracle at bf16)
     assert float((y.double() - oy.double()).abs().max()) <= 2e-2 * float(oy.double().pow(2).mean().sqrt())
     # against fp64 truth of the same bf16 inputs: no worse than the reference's own roundings
     # (its intermediate cast of the normalized value to bf16 costs up to a bf16 ulp before the

@@ -128,7 +128,7 @@ def test_hip_frozen_conv_weight_fp32(d, chunk, taps):
 
 
 def test_hip_tiny_config_fp32():
-    """BASELINE config 1 (B=1, T=512, Hk=H=4, D=64, chunk 64, fp32 "highest", one segment).
+    """The tiny benchmark config (B=1, T=512, Hk=H=4, D=64, chunk 64, fp32 "highest", one segment).
     Output and every gradient: max relative error <= 1e-5 against the fp32 reference path, and
     <= 5e-5 on the sums over every token (A_log, dt_bias: test_gdn_mega.py:89-91); gradient
     cosine >= 0.999999. The sums are also held to the fp32 reference path's own error against

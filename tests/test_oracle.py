@@ -220,7 +220,7 @@ def test_gated_rmsnorm_backward_matches_hf(dtype):
 
 
 # ------------------------------------------------------------------ gates and the core's inputs
-# (a, dt_bias, A_log, b) points: ordinary values, the BASELINE A_log range end (ln 16), large
+# (a, dt_bias, A_log, b) points: ordinary values, the end of the benchmark configs' A_log range (ln 16), large
 # |a + dt_bias| where a naive log(1 + e^x) overflows or loses everything, and saturated b
 GATE_POINTS = [(0.3, -0.5, 0.4, 0.1), (-2.0, 1.5, 2.772588722239781, -3.0), (25.0, 0.0, 0.0, 40.0),
                (-30.0, -5.0, 1.0, -40.0), (0.0, 0.0, -1.5, 0.0), (700.0, 10.0, 0.5, 5.0)]
@@ -325,7 +325,7 @@ def _hf_core(inputs, cot, *, key_heads, key_dim, value_heads, value_dim, monkeyp
 
 def _hf_vs_oracle(monkeypatch, seed=21):
     """Relative max errors of the oracle's composed core against HF's Qwen3_5GatedDeltaNet on
-    one segment (T = 45, not a multiple of the chunk 16; GQA 2 -> 4 heads; BASELINE's gate
+    one segment (T = 45, not a multiple of the chunk 16; GQA 2 -> 4 heads; the benchmark configs' gate
     spreads, A_log ~ U(0, ln 16)): the rule's inputs, the output and every gradient."""
     from tjev_amd.testing import cotangent, gdn_inputs
 

@@ -100,7 +100,7 @@ def grouped(x: torch.Tensor, *linears: LoRALinear) -> list[torch.Tensor]:
 class GatedDeltaNetBlock:
     """The block with every projection adapted (rank ``rank``, merged) and the flat norm
     (``compute.gdn_norm=flat``, ``compute.lora_impl=merged``), random weights of the given
-    shape (no checkpoint is loaded). ``init``: the adapters as BASELINE's block config draws
+    shape (no checkpoint is loaded). ``init``: the adapters as the 4B block benchmark config draws
     them (A ~ N(0, 1/r), B ~ N(0, 0.01)), base kernels ~ N(0, 1/fan_in), conv ~ N(0, 0.5),
     A_log ~ U(0, ln 16), dt_bias ~ N(0, 1), norm weight 1."""
 

@@ -1,4 +1,4 @@
-"""Seeded synthetic inputs of the GDN megakernel: BASELINE's configurations and the
+"""Seeded synthetic inputs of the GDN megakernel: the benchmark configurations and the
 reference tests' shapes (tests/kernels/test_gdn_mega.py:25-41).
 
 numpy PCG64 streams (jax.random's threefry streams cannot be regenerated without jax): seed 0
@@ -53,7 +53,7 @@ def gdn_inputs(*, batch: int, length: int, key_heads: int, value_heads: int, dim
                style: str = "baseline", device="cpu"):
     """(qkv, a, b, a_log, dt_bias, conv_w, segment_ids) as torch tensors.
 
-    style "baseline": qkv, a, b, dt_bias ~ N(0,1), A_log ~ U(0, ln 16),
+    style "baseline" (the benchmark configurations): qkv, a, b, dt_bias ~ N(0,1), A_log ~ U(0, ln 16),
     conv w ~ N(0, 0.5). style "reference" (test_gdn_mega.py:25-41): A_log, dt_bias ~ 0.5 N(0,1).
     ``segments``: "one" (id 1 everywhere), "geometric" (varlen packing), "cuts" (``cuts``,
     plus ``trailing_pad`` segment-0 tokens) or "random4" (4 random cuts per row, as the
