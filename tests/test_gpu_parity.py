@@ -234,3 +234,42 @@ def test_hip_bf16_model_heads(hk, h):
     assert err - floor <= 2e-2 and l2 <= 2e-2
     for k, c in cos.items():
         assert c >= 0.9999, (k, cos)
+
+
+@pytest.mark.parametrize("length", [1, 5, 63, 65])
+def test_hip_rows_shorter_than_a_chunk_fp32(length):
+    """Rows shorter than one chunk (and one token past it): the padded tail of the only chunk
+    reads and writes nothing, at the fp32 bar against the fp64 oracle (the fp32 oracle is itself
+    4.5e-5 from fp64 on d A_log at T = 65)."""
+    d, hk, h = 16, 2, 4
+    inputs, cot = case_inputs(2, length, hk, h, d, trailing_pad=0, segments="one")
+    shape = dict(key_heads=hk, key_dim=d, value_heads=h, value_dim=d, conv=True)
+    print(f"short row T={length}", flush=True)
+    got = hip_outputs(inputs, cot, chunk=64, precision="highest", **shape)
+    want = oracle_outputs(inputs, cot, dtype=torch.float64, **shape)
+    assert all(bool(torch.isfinite(v).all()) for v in got.values())
+    for name in got:
+        if not bool(want[name].any()):  # one token: no decay reaches anything, d a = 0 exactly
+            assert not bool(got[name].any()), name
+        else:
+            assert rel(got[name], want[name]) < TOL[name], (name, rel(got[name], want[name]))
+
+
+def test_hip_all_padding_row_fp32():
+    """A batch row that is padding throughout (segment ids all 0) beside a packed row: the padded
+    row's output and every gradient of its inputs are exact zeros, and the other row's match the
+    fp64 oracle at the fp32 bar."""
+    d, hk, h = 16, 2, 4
+    inputs, cot = case_inputs(2, 150, hk, h, d, cuts=[31, 64, 65, 98])
+    qkv, a, b, a_log, dt_bias, w, seg = inputs
+    seg = seg.clone()
+    seg[0] = 0
+    inputs = (qkv, a, b, a_log, dt_bias, w, seg)
+    shape = dict(key_heads=hk, key_dim=d, value_heads=h, value_dim=d, conv=True)
+    got = hip_outputs(inputs, cot, chunk=32, precision="highest", **shape)
+    want = oracle_outputs(inputs, cot, dtype=torch.float64, **shape)
+    for name in ("out", "qkv", "a", "b"):
+        assert bool((got[name][0] == 0).all()), name
+    errors = {k: rel(got[k], want[k]) for k in got}
+    for name, err in errors.items():
+        assert err < TOL[name], (name, errors)
