@@ -945,17 +945,24 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
         f32x4 acc[C / 16];
         zero(acc);
         strip_mma<PI, D, C / 16>(acc, ob, i0, ob, 0, 0, D, w + 1);
+        // every tile's values first, then the stores: the single stores' memory clobber would
+        // otherwise keep the next tile's context reads (LDS) behind them
         const StripDecay<C> sd(cx, i0);
+        float bt[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) bt[rr] = cx.beta[i0 + acc_row(rr)];
 #pragma unroll
         for (int t = 0; t < C / 16; ++t) {
           float d[4];
           sd.tile(cx, i0, t, w, d);
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
-            lds_st(sT + i * LT + j, i > j ? cx.beta[i] * acc[t][rr] * d[rr] : 0.f);
-          }
+          for (int rr = 0; rr < 4; ++rr)
+            acc[t][rr] = i0 + acc_row(rr) > 16 * t + acc_col() ? bt[rr] * acc[t][rr] * d[rr] : 0.f;
         }
+#pragma unroll
+        for (int t = 0; t < C / 16; ++t)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) lds_st(sT + (i0 + acc_row(rr)) * LT + 16 * t + acc_col(), acc[t][rr]);
       }
       if constexpr (!FWD) {  // in flight during the inverse
         sc.fetch(A.states + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * D * D, D);
