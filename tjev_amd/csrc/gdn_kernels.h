@@ -1747,10 +1747,12 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
     zero(acc);
     const StripDecay<C> sd(cx, i0);
     xs.template product<PI>(acc, ob, 0, w + 1);
+    float dn[4];  // the next tile's decays, read before this tile's stores (their memory clobber)
+    sd.tile(cx, i0, 0, w, dn);
 #pragma unroll
     for (int t = 0; t < TC; ++t) {
-      float d[4];
-      sd.tile(cx, i0, t, w, d);
+      const float d[4] = {dn[0], dn[1], dn[2], dn[3]};
+      if (t + 1 < TC) sd.tile(cx, i0, t + 1, w, dn);
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int i = i0 + acc_row(rr), j = 16 * t + acc_col();
