@@ -1,4 +1,4 @@
-"""Build libtjev_gdn.so for gfx950 in-tree: one hipcc job per (chunk, head dim) pair of
+"""Build libtjev_gdn.so for gfx950 in-tree: PARTS hipcc jobs per (chunk, head dim) pair of
 csrc/gdn_shapes.def plus the C ABI, linked with ``hipcc -shared``.
 
     python -m tjev_amd.build [-j JOBS]
@@ -30,6 +30,9 @@ FLAGS = [
 
 # units built once: the C ABI, the gated RMSNorm and the decode step
 EXTRA_UNITS = ("gdn_api", "gdn_norm", "gdn_decode")
+# object files per (chunk, head dim) pair: the launch sequences with the small kernels (part 0),
+# then one per large kernel family (gdn_inst.hip's GDN_PART)
+PARTS = 6
 
 
 def shapes() -> list[tuple[int, int]]:
@@ -60,9 +63,10 @@ def build(jobs: int | None = None, verbose: bool = False, verify: bool = True) -
     OUT.mkdir(exist_ok=True)
     units = []
     for c, d in shapes():
-        obj = OUT / f"gdn_inst_c{c}_d{d}.o"
-        units.append([hipcc, *FLAGS, f"-DGDN_C={c}", f"-DGDN_D={d}", "-c", str(CSRC / "gdn_inst.hip"),
-                      "-o", str(obj)])
+        for part in range(PARTS):
+            obj = OUT / f"gdn_inst_c{c}_d{d}_p{part}.o"
+            units.append([hipcc, *FLAGS, f"-DGDN_C={c}", f"-DGDN_D={d}", f"-DGDN_PART={part}", "-c",
+                          str(CSRC / "gdn_inst.hip"), "-o", str(obj)])
     for name in EXTRA_UNITS:
         units.append([hipcc, *FLAGS, "-c", str(CSRC / f"{name}.hip"), "-o", str(OUT / f"{name}.o")])
     t0 = time.time()
@@ -71,7 +75,7 @@ def build(jobs: int | None = None, verbose: bool = False, verify: bool = True) -
         if verify:
             from .ds_check import check_source, check_unit
 
-            checks = [pool.submit(check_unit, c, d) for c, d in shapes()]
+            checks = [pool.submit(check_unit, c, d, part) for c, d in shapes() for part in range(PARTS)]
             checks += [pool.submit(check_source, CSRC / f"{name}.hip") for name in EXTRA_UNITS]
         list(pool.map(_run, units))
         bad = [line for f in checks for line in f.result()]

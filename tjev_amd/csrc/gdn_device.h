@@ -33,6 +33,19 @@ template <int P, bool EXACT_A> constexpr int exact_a() { return P == P_BF16X3 &&
 
 __device__ __forceinline__ int lane() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave() { return threadIdx.x >> 6; }
+// The 16-row strip of a wave in the kernels with one strip per wave (NW = C/16 waves), as a
+// wave-uniform value. A workgroup's waves w and w + 4 run on one SIMD (gfx950 gives the first
+// four waves one SIMD each, in an order that rotates between workgroups, and the next four the
+// same SIMDs in the same order), and strip s carries s + 1 tiles of a product over the
+// triangle's rows (NW - s of one over its columns). PAIR puts strips s and NW - 1 - s on one
+// SIMD, which then carries NW + 1 tiles of every such product (without it: 6, 8, 10 and 12 for
+// NW = 8). readfirstlane marks the value uniform: the strip-dependent loop bounds and branches
+// are otherwise compiled as divergent code.
+template <int NW, bool PAIR>
+__device__ __forceinline__ int wave_strip() {
+  const int w = wave();
+  return __builtin_amdgcn_readfirstlane(PAIR && NW == 8 && w >= 4 ? 11 - w : w);
+}
 
 // ---------------------------------------------------------------- bf16 storage
 // bf16 tensors are held as uint16_t; conversion rounds to nearest even (as torch does).

@@ -1,14 +1,83 @@
 // One (chunk, head dim) instantiation of the kernel sequences, built once per GDN_SHAPE in
-// gdn_shapes.def with -DGDN_C=<chunk> -DGDN_D=<head dim>.
+// gdn_shapes.def with -DGDN_C=<chunk> -DGDN_D=<head dim>, in six object files
+// (-DGDN_PART=0 .. 5): part 0 holds the launch sequences, the shape's table and the small
+// kernels; parts 1 .. 5 each instantiate one family of the large kernels (explicit
+// instantiations, declared extern in the other parts). A kernel's code then depends only on its
+// own family's source: the register allocation of one family, which runs close to the 256
+// VGPRs of two waves per SIMD, no longer moves when another family's code changes.
 #include "gdn_kernels.h"
 #include "gdn_launch.h"
 #include "gdn_v2.h"
 
 #ifndef GDN_C
-#error "build with -DGDN_C=<chunk> -DGDN_D=<head dim>"
+#error "build with -DGDN_C=<chunk> -DGDN_D=<head dim> -DGDN_PART=<part>"
+#endif
+#ifndef GDN_PART
+#error "build with -DGDN_PART=<part> (0 .. 5)"
 #endif
 
 namespace gdn {
+
+// the explicit instantiations of parts 1 .. 5 (definitions in their own part, declarations
+// elsewhere), over every (A-side, state-side) precision pair the shape table holds
+#if GDN_PART == 1
+#define GDN_KW_1 template
+#else
+#define GDN_KW_1 extern template
+#endif
+#if GDN_PART == 2
+#define GDN_KW_2 template
+#else
+#define GDN_KW_2 extern template
+#endif
+#if GDN_PART == 3
+#define GDN_KW_3 template
+#else
+#define GDN_KW_3 extern template
+#endif
+#if GDN_PART == 4
+#define GDN_KW_4 template
+#else
+#define GDN_KW_4 extern template
+#endif
+#if GDN_PART == 5
+#define GDN_KW_5 template
+#else
+#define GDN_KW_5 extern template
+#endif
+constexpr int kDVT = GDN_D < 32 ? GDN_D : 32;
+#define GDN_EACH_PAIR(M) M(P_F32, P_F32) M(P_BF16X3, P_BF16X3) M(P_BF16, P_BF16) M(P_BF16X3, P_BF16)
+#define GDN_EACH_IO(M, PI, PS) M(PI, PS, float) M(PI, PS, uint16_t)
+// part 1: k_chunk, its four modes
+#define GDN_CHUNK(PI, PS)                                                  \
+  GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 0>(GdnArgs);      \
+  GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 1>(GdnArgs);      \
+  GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 2>(GdnArgs);      \
+  GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 3>(GdnArgs);
+GDN_EACH_PAIR(GDN_CHUNK)
+// part 2: the scans
+#define GDN_SCAN_BWD(PI, PS, TIO) GDN_KW_2 __global__ void k_scan_bwd<GDN_C, GDN_D, kDVT, PI, PS, TIO>(GdnArgs);
+#define GDN_SCANS(PI, PS)                                                  \
+  GDN_KW_2 __global__ void k_scan_fwd<GDN_C, GDN_D, kDVT, PI, PS>(GdnArgs); \
+  GDN_EACH_IO(GDN_SCAN_BWD, PI, PS)
+GDN_EACH_PAIR(GDN_SCANS)
+// part 3: k_out, without and with the norm
+#define GDN_OUT_IO(PI, PS, TIO)                                            \
+  GDN_KW_3 __global__ void k_out<GDN_C, GDN_D, PI, PS, TIO, false>(GdnArgs); \
+  GDN_KW_3 __global__ void k_out<GDN_C, GDN_D, PI, PS, TIO, true>(GdnArgs);
+#define GDN_OUT(PI, PS) GDN_EACH_IO(GDN_OUT_IO, PI, PS)
+GDN_EACH_PAIR(GDN_OUT)
+// part 4: k_bwd_local (one A-side precision each: the pairs' first members, once)
+#define GDN_LOCAL_IO(PI, PS, TIO) GDN_KW_4 __global__ void k_bwd_local<GDN_C, GDN_D, PI, TIO>(GdnArgs);
+GDN_EACH_IO(GDN_LOCAL_IO, P_F32, 0)
+GDN_EACH_IO(GDN_LOCAL_IO, P_BF16X3, 0)
+GDN_EACH_IO(GDN_LOCAL_IO, P_BF16, 0)
+// part 5: k_bwd_grads
+#define GDN_GRADS_IO(PI, PS, TIO) GDN_KW_5 __global__ void k_bwd_grads<GDN_C, GDN_D, PI, PS, TIO>(GdnArgs);
+#define GDN_GRADS(PI, PS) GDN_EACH_IO(GDN_GRADS_IO, PI, PS)
+GDN_EACH_PAIR(GDN_GRADS)
+
+#if GDN_PART == 0
 namespace {
 
 // compute units of the current device (queried once per device): the persistent kernels run
@@ -185,5 +254,6 @@ const ShapeTable* GDN_CAT(table_, GDN_C, GDN_D)() {
   static const ShapeTable t = make();
   return &t;
 }
+#endif  // GDN_PART == 0
 
 }  // namespace gdn

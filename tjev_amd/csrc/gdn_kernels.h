@@ -1230,7 +1230,7 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
     for (int c = threadIdx.x; c < D; c += NT) snw[c] = A.nw[c];
   }
   const Op<PI> ob = TB::at(sB);
-  const int w = wave(), i0 = 16 * w;
+  const int w = wave_strip<C / 16, false>(), i0 = 16 * w;
   const int total = A.B * A.H * A.N;
   OutIn<C, D, NT> in;
   {
@@ -1438,7 +1438,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
   __shared__ __align__(16) char sB[TB::BYTES];
   __shared__ Ctx<C> cx;
   const Op<PI> ob = TB::at(sB);
-  const int w = wave(), i0 = 16 * w;
+  const int w = wave_strip<C / 16, true>(), i0 = 16 * w;
   const int total = A.B * A.H * A.N;
   LocalIn<C, D, NT, TIO> in;
   {
@@ -1720,7 +1720,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
   const Op<PI> ob = TB::at(sB);
   const int id = blockIdx.x;
   const int n = id % A.N, bh = id / A.N, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
-  const int w = wave(), i0 = 16 * w, r = lane() & 15;
+  const int w = wave_strip<C / 16, true>(), i0 = 16 * w, r = lane() & 15;
   const float* qg = A.qn + hoff(A, b, hk, A.Hk, n, C, D);
   const float* kg = A.kn + hoff(A, b, hk, A.Hk, n, C, D);
   const size_t off = hoff(A, b, h, A.H, n, C, D);

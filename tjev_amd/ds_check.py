@@ -17,7 +17,7 @@ import re
 import subprocess
 import sys
 
-from .build import CSRC, FLAGS, _hipcc, shapes
+from .build import CSRC, FLAGS, PARTS, _hipcc, shapes
 
 _SINGLE = re.compile(r"DS_(WRITE|READ)_B(32|64)\w*\s(%\d+)[^,]*,.*?,\s*(\d+),\s*0,\s*implicit"
                      r".*?(?:into|from) %ir\.([\w.]+)")
@@ -25,9 +25,10 @@ _PAIR = re.compile(r"DS_(WRITE|READ)2(ST64)?_B(32|64)\w*\s.*?,\s*(\d+),\s*(\d+),
                    r".*?(?:into|from) %ir\.([\w.]+).*?(?:into|from) %ir\.([\w.]+)")
 
 
-def check_unit(c: int, d: int) -> list[str]:
-    """Wrongly merged LDS accesses of the (chunk c, head dim d) kernel unit (empty if none)."""
-    return check_source(CSRC / "gdn_inst.hip", [f"-DGDN_C={c}", f"-DGDN_D={d}"])
+def check_unit(c: int, d: int, part: int) -> list[str]:
+    """Wrongly merged LDS accesses of one part of the (chunk c, head dim d) kernel unit (empty
+    if none)."""
+    return check_source(CSRC / "gdn_inst.hip", [f"-DGDN_C={c}", f"-DGDN_D={d}", f"-DGDN_PART={part}"])
 
 
 def check_source(src, defines=()) -> list[str]:
@@ -63,7 +64,7 @@ def main(argv: list[str] | None = None) -> int:
     units = [(int(argv[i]), int(argv[i + 1])) for i in range(0, len(argv), 2)] if argv else shapes()
     failed = 0
     for c, d in units:
-        bad = check_unit(c, d)
+        bad = [line for part in range(PARTS) for line in check_unit(c, d, part)]
         print(f"chunk {c} dim {d}: {len(bad)} wrongly merged LDS accesses")
         for line in bad[:5]:
             print("   ", line)
