@@ -57,8 +57,13 @@ constexpr int kDVT = GDN_D < 32 ? GDN_D : 32;
 GDN_EACH_PAIR(GDN_CHUNK)
 // part 2: the scans
 #define GDN_SCAN_BWD(PI, PS, TIO) GDN_KW_2 __global__ void k_scan_bwd<GDN_C, GDN_D, kDVT, PI, PS, TIO>(GdnArgs);
-#define GDN_SCANS(PI, PS)                                                  \
-  GDN_KW_2 __global__ void k_scan_fwd<GDN_C, GDN_D, kDVT, PI, PS>(GdnArgs); \
+#if GDN_C == 128 && GDN_D == 128
+#define GDN_SCAN_FWD(PI, PS) GDN_KW_2 __global__ void k_scan_fwd_split<PI, PS>(GdnArgs);
+#else
+#define GDN_SCAN_FWD(PI, PS) GDN_KW_2 __global__ void k_scan_fwd<GDN_C, GDN_D, kDVT, PI, PS>(GdnArgs);
+#endif
+#define GDN_SCANS(PI, PS) \
+  GDN_SCAN_FWD(PI, PS)    \
   GDN_EACH_IO(GDN_SCAN_BWD, PI, PS)
 GDN_EACH_PAIR(GDN_SCANS)
 // part 3: k_out, without and with the norm
@@ -129,7 +134,8 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
     } else {  // T kept for the backward
       GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 2>), persist, dim3(C * 4));
     }
-    GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd<C, D, DVT, PI, PS>), tiles, dim3(NS));
+    if constexpr (C == 128 && D == 128) GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd_split<PI, PS>), tiles, dim3(512));
+    else GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd<C, D, DVT, PI, PS>), tiles, dim3(NS));
     if (A.ny) GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO, true>), persist, dim3(C * 4));
     else GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO>), persist, dim3(C * 4));
     if (A.final_state) GDN_LAUNCH(K_FINAL_STATE, (k_final_state<C, D>), dim3(A.B * A.H * (D / DVT)), dim3(256));
@@ -192,7 +198,8 @@ hipError_t run_v2(const GdnArgs& A, hipStream_t st, int backward, const Timer* t
     } else {
       GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 2>), persist, dim3(C * 4));
     }
-    GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd<C, D, DVT, PI, PS>), tiles, dim3(NS));
+    if constexpr (C == 128 && D == 128) GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd_split<PI, PS>), tiles, dim3(512));
+    else GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd<C, D, DVT, PI, PS>), tiles, dim3(NS));
     GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO>), persist, dim3(C * 4));
     if (A.final_state) GDN_LAUNCH(K_FINAL_STATE, (k_final_state<C, D>), dim3(A.B * A.H * (D / DVT)), dim3(256));
   } else {

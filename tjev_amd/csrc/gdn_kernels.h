@@ -1201,6 +1201,252 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
   }
 }
 
+// ---------------------------------------------------------------- k_scan_fwd_split
+// The forward scan at C = D = 128 with its two products chained in registers. Two compute
+// waves each own 16 value columns of the 32-column Dv tile: S[:, cols] (Dk x 16, 8 accumulator
+// tiles, rows dk) and v_new[:, cols] (C x 16, 8 tiles, rows tokens). Per chunk:
+//   P1  v_new = u + (-w) S             A: -w (LDS, rows tokens), B: S from the accumulators
+//   P2  S = carry S + k^T (kws v_new)  A: k^T (LDS, rows dk), B: v_new from the accumulators,
+//                                      its rows (tokens) scaled by kws
+// A product's B operand has the contraction index along the other product's accumulator rows:
+// two accumulator tiles (rows 0-15, 16-31) become one 32-deep B fragment by one permlane32 and
+// one permlane16 swap per register (lane group kq then holds rows 8kq .. 8kq + 7 of its
+// column), so neither result goes through LDS and the products need no barrier between them.
+// The other six waves stage the LDS operands a product ahead: k^T of chunk n during P1 of
+// chunk n, -w, u^T and the gates of chunk n + 1 during P2 of chunk n, each from registers loaded
+// one product earlier. Two barriers per chunk. Same chunk ranges, replays and outputs as
+// k_scan_fwd.
+struct ScanSplitBuf {
+  static constexpr int C = 128, D = 128, DVT = 32, LU = C + 4;
+};
+
+// B fragment values (rows 8 (lane/16) .. + 7 of the 32-row contraction step, column lane % 16)
+// from accumulator tiles t0 (rows 0-15) and t1 (rows 16-31)
+__device__ __forceinline__ void acc_pair_to_b(const f32x4& t0, const f32x4& t1, float (&v)[8]) {
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    // (the element values are copied out first: __builtin_bit_cast of a vector element
+    // subscript reads element 0 whatever the index, with this compiler)
+    const float a = t0[rr], c = t1[rr];
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(c), false, false);
+    const unsigned p0 = p[0], p1 = p[1];
+    const auto q = __builtin_amdgcn_permlane16_swap(p0, p1, false, false);
+    const unsigned q0 = q[0], q1 = q[1];
+    v[rr] = __uint_as_float(q0);
+    v[4 + rr] = __uint_as_float(q1);
+  }
+}
+
+// acc[t] += A(16 t + lane % 16, k) B(k, lane % 16) over a 128-deep contraction: A from an LDS
+// operand tile (8 row tiles), B from the accumulator tiles bsrc (two per 32-deep step). Each
+// step's eight A fragments are read one step ahead, so the LDS latency runs under the previous
+// step's MFMAs.
+template <int P, class OP>
+__device__ __forceinline__ void split_product(f32x4 (&acc)[8], const OP& a, const f32x4 (&bsrc)[8],
+                                              const float* bscale = nullptr) {
+  const int r = lane() & 15, kg = (lane() >> 4) << 3;
+  Frag<a_prec<P>()> fa[2][8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) fa[0][t] = a.template frag<a_prec<P>()>(16 * t + r, kg);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if (s + 1 < 4) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) fa[(s + 1) & 1][t] = a.template frag<a_prec<P>()>(16 * t + r, 32 * (s + 1) + kg);
+    }
+    // the scheduler would otherwise sink these reads next to their MFMAs (register pressure)
+    __builtin_amdgcn_sched_barrier(0);
+    float bv[8];
+    acc_pair_to_b(bsrc[2 * s], bsrc[2 * s + 1], bv);
+    if (bscale) {  // B(k, .) scaled by bscale[k]: the lane's 8 contraction rows
+      const float4 s0 = *reinterpret_cast<const float4*>(bscale + 32 * s + kg);
+      const float4 s1 = *reinterpret_cast<const float4*>(bscale + 32 * s + kg + 4);
+      bv[0] *= s0.x; bv[1] *= s0.y; bv[2] *= s0.z; bv[3] *= s0.w;
+      bv[4] *= s1.x; bv[5] *= s1.y; bv[6] *= s1.z; bv[7] *= s1.w;
+    }
+    const Frag<b_prec<P>()> fb = make_frag<b_prec<P>()>(bv);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) mma<P>(acc[t], fa[s & 1][t], fb);
+  }
+}
+
+template <int PI, int PS>
+__global__ __launch_bounds__(512) void k_scan_fwd_split(GdnArgs A) {
+  constexpr int C = 128, D = 128, DVT = 32, NT = 512, LU = C + 4;
+  constexpr int NL = NT - 128;      // loader threads (waves 2 .. 7)
+  using TW = OpTile<PI, C, D>;      // -w: A(i = token, k = dk)
+  using TK = OpTile<PI, D, C>;      // k^T: A(i = dk, k = token)
+  __shared__ __align__(16) char sW[TW::BYTES];
+  __shared__ __align__(16) char sK[TK::BYTES];
+  __shared__ __align__(16) float sU[DVT * LU];  // u^T: [value column][token]
+  __shared__ __align__(16) float skws[2][C];    // kws per token, by chunk parity
+  __shared__ float scarry[2];
+  __shared__ int red[NT / 64];
+  const Op<PI> ow = TW::at(sW), okt = TK::at(sK);
+  const ScanIx ix(A);
+  const int tile = ix.tile, bh = ix.bh, part = ix.part;
+  const int h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
+  const int j0 = tile * DVT;
+  const int w = wave(), l = lane();
+  const int n0 = part_start<C, NT, true>(A, b, (int)((long)part * A.N / A.parts), red);
+  const int n1 = part_start<C, NT, true>(A, b, (int)((long)(part + 1) * A.N / A.parts), red);
+  if (n0 >= n1) return;
+  const int nb = n0 > 0 ? n0 - 1 : 0;
+  const bool compute = w < 2;  // wave-uniform
+  const int lt = (int)threadIdx.x - 128;  // loader thread index (>= 0 in waves 2 .. 7)
+  // ---- loader state: the next operands in registers
+  float4 wr[11];            // -w: 4096 float4 slots over 384 threads
+  float4 ka[6], kb[6];      // k rows 2j, 2j+1 at 4 dk columns: 2048 slots
+  float4 ur[3];             // u: 1024 float4 slots
+  int gs = 0, gsc = 0, gprev = 0;
+  float gg = 0.f, gl = 0.f, ggc = 0.f, glc = 0.f;
+  auto fetch_w = [&](int n) {
+    const float* g = A.ww + hoff(A, b, h, A.H, n, C, D);
+#pragma unroll
+    for (int it = 0; it < 11; ++it) {
+      const int idx = min(lt + it * NL, 4095);
+      wr[it] = *reinterpret_cast<const float4*>(g + (size_t)(idx >> 5) * D + 4 * (idx & 31));
+    }
+  };
+  auto fetch_u = [&](int n) {
+    const float* g = A.uu + hoff(A, b, h, A.H, n, C, D) + j0;
+#pragma unroll
+    for (int it = 0; it < 3; ++it) {
+      const int idx = min(lt + it * NL, 1023);
+      ur[it] = *reinterpret_cast<const float4*>(g + (size_t)(idx >> 3) * D + 4 * (idx & 7));
+    }
+  };
+  auto fetch_k = [&](int n) {
+    const float* g = A.kn + hoff(A, b, hk, A.Hk, n, C, D);
+#pragma unroll
+    for (int it = 0; it < 6; ++it) {
+      const int idx = min(lt + it * NL, 2047), q = idx & 7, rest = idx >> 3, j = rest & 63;
+      const int c = 4 * (q + 8 * (rest >> 6));
+      ka[it] = *reinterpret_cast<const float4*>(g + (size_t)(2 * j) * D + c);
+      kb[it] = *reinterpret_cast<const float4*>(g + (size_t)(2 * j + 1) * D + c);
+    }
+  };
+  // the gates of chunk n: token lt's segment and gamma (lt < C), the chunk's last token and the
+  // token before it
+  auto fetch_g = [&](int n) {
+    const size_t tb = (size_t)b * A.Tp + (size_t)n * C, th = (size_t)(b * A.H + h) * A.Tp + (size_t)n * C;
+    const int t = lt < C ? lt : C - 1;
+    gs = A.segp[tb + t];
+    gg = A.gam[th + t];
+    gl = A.gaml[th + t];
+    gsc = A.segp[tb + C - 1];
+    ggc = A.gam[th + C - 1];
+    glc = A.gaml[th + C - 1];
+    gprev = A.segp[n > 0 ? tb - 1 : tb];
+  };
+  auto put_gates = [&](int n) {  // kws and carry of chunk n into the parity buffers
+    const int before = (n == 0 && !A.init_state) ? -2 : gprev;
+    if (lt < C) skws[n & 1][lt] = gs == gsc ? expf((ggc - gg) + (glc - gl)) : 0.f;
+    if (lt == 0) scarry[n & 1] = gsc == before ? expf(ggc + glc) : 0.f;
+  };
+  auto put_w = [&]() {
+#pragma unroll
+    for (int it = 0; it < 11; ++it) {
+      const int idx = lt + it * NL;
+      if (idx < 4096) ow.put4(idx >> 5, 4 * (idx & 31), -wr[it].x, -wr[it].y, -wr[it].z, -wr[it].w);
+    }
+  };
+  auto put_u = [&]() {
+#pragma unroll
+    for (int it = 0; it < 3; ++it) {
+      const int idx = lt + it * NL;
+      if (idx < 1024) {
+        const int tk = idx >> 3, c = 4 * (idx & 7);
+        sU[(c + 0) * LU + tk] = ur[it].x;
+        sU[(c + 1) * LU + tk] = ur[it].y;
+        sU[(c + 2) * LU + tk] = ur[it].z;
+        sU[(c + 3) * LU + tk] = ur[it].w;
+      }
+    }
+  };
+  auto put_k = [&]() {  // k^T: op(dk, token) = k[token][dk] as 32-bit token pairs (kws is applied
+                        // to v_new's rows on the compute side)
+#pragma unroll
+    for (int it = 0; it < 6; ++it) {
+      const int idx = lt + it * NL;
+      if (idx < 2048) {
+        const int q = idx & 7, rest = idx >> 3, j = rest & 63, c = 4 * (q + 8 * (rest >> 6));
+        okt.put2(c + 0, 2 * j, ka[it].x, kb[it].x);
+        okt.put2(c + 1, 2 * j, ka[it].y, kb[it].y);
+        okt.put2(c + 2, 2 * j, ka[it].z, kb[it].z);
+        okt.put2(c + 3, 2 * j, ka[it].w, kb[it].w);
+      }
+    }
+  };
+  // Each role runs its own loop (their registers are then never live together), with the same
+  // barriers: one before the first chunk, two per chunk.
+  if (compute) {
+    const int jt = w & 1;          // the wave's 16 value columns
+    const int col = j0 + 16 * jt;  // first value column of the wave
+    f32x4 accS[8];  // S[16 dt + 4 (lane/16) + rr][col + lane % 16]
+    f32x4 accV[8];  // v_new[16 rt + 4 (lane/16) + rr][col + lane % 16]
+    zero(accS);
+    if (n0 == 0 && A.init_state) {
+      const float* s0 = A.init_state + (size_t)bh * D * D + col + acc_col();
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) accS[dt][rr] = s0[(size_t)(16 * dt + acc_row(rr)) * D];
+    }
+    __syncthreads();  // chunk nb's -w, u^T and gates staged
+    for (int n = nb; n < n1; ++n) {
+      const bool emit = n >= n0;  // the replayed chunk n0 - 1 only rebuilds the state
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt) {  // v_new = u, then + (-w) S
+        const float4 v = *reinterpret_cast<const float4*>(sU + (16 * jt + acc_col()) * LU + 16 * rt + acc_row(0));
+        accV[rt] = f32x4{v.x, v.y, v.z, v.w};
+      }
+      split_product<PS>(accV, ow, accS);
+      // the stores go out while the product's MFMAs run: S before chunk n now (P1 leaves it as
+      // is), v_new after P2's issue (P2 only reads it)
+      if (emit) {
+        float* sg = A.states + ((size_t)bh * A.N + n) * D * D + col;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) st_tile(sg + (size_t)(16 * dt) * D, D, accS[dt]);
+      }
+      __syncthreads();  // (k kws)^T of chunk n staged
+      const float carry = scarry[n & 1];
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) accS[dt] *= carry;
+      split_product<PI>(accS, okt, accV, skws[n & 1]);  // S = carry S + k^T (kws v_new)
+      if (emit) {
+        float* vg = A.vnew + hoff(A, b, h, A.H, n, C, D) + col;
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt) st_tile(vg + (size_t)(16 * rt) * D, D, accV[rt]);
+      }
+      __syncthreads();  // the next chunk's -w, u^T and gates staged
+    }
+  } else {
+    fetch_g(nb);  // prologue: chunk nb's -w, u^T and gates staged, its k in registers
+    fetch_k(nb);
+    fetch_w(nb);
+    fetch_u(nb);
+    put_gates(nb);
+    put_w();
+    put_u();
+    __syncthreads();
+    for (int n = nb; n < n1; ++n) {
+      const int nx = n + 1 < n1 ? n + 1 : n;  // the last step refetches its own chunk (unused)
+      put_k();  // k^T of chunk n, for P2 (during P1)
+      fetch_g(nx);
+      fetch_w(nx);
+      fetch_u(nx);
+      __syncthreads();
+      fetch_k(nx);  // during P2: -w, u^T and the gates of the next chunk
+      put_w();
+      put_u();
+      if (nx != n) put_gates(nx);  // (the last step's would rewrite the carry being read)
+      __syncthreads();
+    }
+  }
+}
+
 // ---------------------------------------------------------------- k_out
 // Persistent: one workgroup per CU (grid <= number of units) loops over the (row, head, chunk)
 // units blockIdx.x, + gridDim.x, ...; C/16 waves. Per unit: o = ((q k^T) . D) v_new + q_read
