@@ -5,15 +5,21 @@
 // instantiations, declared extern in the other parts). A kernel's code then depends only on its
 // own family's source: the register allocation of one family, which runs close to the 256
 // VGPRs of two waves per SIMD, no longer moves when another family's code changes.
+#ifndef GDN_PART
+#error "build with -DGDN_PART=<part> (0 .. 5)"
+#endif
+// 32-bit lane offsets in the staging loads of the scans, k_out and k_bwd_local (measured:
+// k_bwd_local 222 -> 200 us, the others 2 us each); k_chunk and k_bwd_grads keep the widened
+// form (with 32-bit offsets they spill: +7 and +35 us)
+#if GDN_PART == 2 || GDN_PART == 3 || GDN_PART == 4
+#define GDN_LANE_OFF32 1
+#endif
 #include "gdn_kernels.h"
 #include "gdn_launch.h"
 #include "gdn_v2.h"
 
 #ifndef GDN_C
 #error "build with -DGDN_C=<chunk> -DGDN_D=<head dim> -DGDN_PART=<part>"
-#endif
-#ifndef GDN_PART
-#error "build with -DGDN_PART=<part> (0 .. 5)"
 #endif
 
 namespace gdn {

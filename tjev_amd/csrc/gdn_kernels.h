@@ -30,6 +30,24 @@ __device__ __forceinline__ size_t hoff(const GdnArgs& A, int b, int head, int he
   return ((size_t)(b * heads + head) * A.Tp + (size_t)n * C) * D;
 }
 
+// g + row * ld + col for a lane's element of a staged tile (all three small) from a wave-uniform
+// base g: with GDN_LANE_OFF32 as a 32-bit offset, so the loads take the scalar-base form (one
+// VGPR per address instead of a 64-bit pair), else widened before the multiply. Which form
+// allocates better is a property of the kernel (a spilled address reloaded from scratch waits
+// for every outstanding memory operation), so each object file of gdn_inst.hip sets it for its
+// kernel family.
+#ifndef GDN_LANE_OFF32
+#define GDN_LANE_OFF32 0
+#endif
+template <class T>
+__device__ __forceinline__ const T* lane_ptr(const T* g, int row, int ld, int col) {
+  if constexpr (GDN_LANE_OFF32) {
+    return g + (unsigned)(row * ld + col);
+  } else {
+    return g + (size_t)row * ld + col;
+  }
+}
+
 // ---------------------------------------------------------------- chunk context
 // Segment semantics (pallas_tpu_v2.py:226-241, pallas_tpu_mega.py:349-361): cont_i: token i
 // reads the incoming state (same id as the previous chunk's last token; before chunk 0: -2, or
@@ -486,7 +504,7 @@ struct Regs {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
       const int idx = threadIdx.x + it * NT;
-      if (live(it)) v[it] = *reinterpret_cast<const float4*>(g + (size_t)(idx / V) * ldg + 4 * (idx % V));
+      if (live(it)) v[it] = *reinterpret_cast<const float4*>(lane_ptr(g, idx / V, ldg, 4 * (idx % V)));
     }
   }
   // op(r, k) = g[r][k] * rs[r] * cst
@@ -556,8 +574,8 @@ struct RegsT {
     for (int it = 0; it < IT; ++it) {
       int q, j, c;
       slot(it, q, j, c);
-      a[it] = *reinterpret_cast<const float4*>(g + (size_t)(2 * j) * ldg + c);
-      b[it] = *reinterpret_cast<const float4*>(g + (size_t)(2 * j + 1) * ldg + c);
+      a[it] = *reinterpret_cast<const float4*>(lane_ptr(g, 2 * j, ldg, c));
+      b[it] = *reinterpret_cast<const float4*>(lane_ptr(g, 2 * j + 1, ldg, c));
     }
   }
   template <int P>
@@ -658,7 +676,7 @@ struct RegsIO {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int r = 2 * j + h;
-        x[it][h].load(g + (size_t)(r < rows ? r : rows - 1) * ldg + c);
+        x[it][h].load(lane_ptr(g, r < rows ? r : rows - 1, ldg, c));
       }
     }
   }
@@ -740,7 +758,7 @@ struct StripA {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       if ((K % 32 == 0) || (32 * s + kg < K)) {
-        ld8(g + (size_t)(i0 + r) * ld + 32 * s + kg, x[s]);
+        ld8(lane_ptr(g, i0 + r, ld, 32 * s + kg), x[s]);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[s][e] = 0.f;
@@ -801,7 +819,7 @@ struct StripIO {
     const int rr = i0 + r < rows ? i0 + r : rows - 1;
     valid = i0 + r < rows;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) x[s].load(g + (size_t)rr * ld + ((32 * s + kg) % K));
+    for (int s = 0; s < KS; ++s) x[s].load(lane_ptr(g, rr, ld, (32 * s + kg) % K));
   }
   template <int P, int TN, class BV>
   __device__ __forceinline__ void product(f32x4 (&acc)[TN], const BV& B, int j0, int tn = TN,
@@ -839,8 +857,8 @@ struct StripT {
 #pragma unroll
     for (int it = 0; it < U; ++it) {
       const int j = pair(it);
-      a[it] = *reinterpret_cast<const float4*>(g + (size_t)(2 * j) * ld + col);
-      b[it] = *reinterpret_cast<const float4*>(g + (size_t)(2 * j + 1) * ld + col);
+      a[it] = *reinterpret_cast<const float4*>(lane_ptr(g, 2 * j, ld, col));
+      b[it] = *reinterpret_cast<const float4*>(lane_ptr(g, 2 * j + 1, ld, col));
     }
   }
   // op(c0 + e, r) = g[r][c0 + e] * sc[r] for the held rows r
@@ -869,7 +887,7 @@ struct AccVals {
 #pragma unroll
     for (int t = 0; t < TN; ++t)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) v[t][rr] = g[(size_t)(i0 + acc_row(rr)) * ld + 16 * t + acc_col()];
+      for (int rr = 0; rr < 4; ++rr) v[t][rr] = *lane_ptr(g, i0 + acc_row(rr), ld, 16 * t + acc_col());
   }
   __device__ __forceinline__ void clear() {
 #pragma unroll
@@ -1306,7 +1324,7 @@ __global__ __launch_bounds__(512) void k_scan_fwd_split(GdnArgs A) {
 #pragma unroll
     for (int it = 0; it < 11; ++it) {
       const int idx = min(lt + it * NL, 4095);
-      wr[it] = *reinterpret_cast<const float4*>(g + (size_t)(idx >> 5) * D + 4 * (idx & 31));
+      wr[it] = *reinterpret_cast<const float4*>(lane_ptr(g, idx >> 5, D, 4 * (idx & 31)));
     }
   };
   auto fetch_u = [&](int n) {
@@ -1314,7 +1332,7 @@ __global__ __launch_bounds__(512) void k_scan_fwd_split(GdnArgs A) {
 #pragma unroll
     for (int it = 0; it < 3; ++it) {
       const int idx = min(lt + it * NL, 1023);
-      ur[it] = *reinterpret_cast<const float4*>(g + (size_t)(idx >> 3) * D + 4 * (idx & 7));
+      ur[it] = *reinterpret_cast<const float4*>(lane_ptr(g, idx >> 3, D, 4 * (idx & 7)));
     }
   };
   auto fetch_k = [&](int n) {
@@ -1323,8 +1341,8 @@ __global__ __launch_bounds__(512) void k_scan_fwd_split(GdnArgs A) {
     for (int it = 0; it < 6; ++it) {
       const int idx = min(lt + it * NL, 2047), q = idx & 7, rest = idx >> 3, j = rest & 63;
       const int c = 4 * (q + 8 * (rest >> 6));
-      ka[it] = *reinterpret_cast<const float4*>(g + (size_t)(2 * j) * D + c);
-      kb[it] = *reinterpret_cast<const float4*>(g + (size_t)(2 * j + 1) * D + c);
+      ka[it] = *reinterpret_cast<const float4*>(lane_ptr(g, 2 * j, D, c));
+      kb[it] = *reinterpret_cast<const float4*>(lane_ptr(g, 2 * j + 1, D, c));
     }
   };
   // the gates of chunk n: token lt's segment and gamma (lt < C), the chunk's last token and the
