@@ -33,7 +33,7 @@ import sys
 from collections import defaultdict
 from pathlib import Path
 
-_FIXED = [("k_scan_fwd<", "gdn_scan_fwd"), ("k_out<", "gdn_out"), ("k_bwd_local<", "gdn_bwd_local"),
+_FIXED = [("k_scan_fwd<", "gdn_scan_fwd"), ("k_scan_fwd_split<", "gdn_scan_fwd"), ("k_out<", "gdn_out"), ("k_bwd_local<", "gdn_bwd_local"),
           ("k_scan_bwd<", "gdn_scan_bwd"), ("k_bwd_grads<", "gdn_bwd_grads"), ("k_post<", "gdn_post"),
           ("k_reduce<", "gdn_reduce"), ("k_norm_fwd<", "gdn_norm_fwd"), ("k_norm_bwd<", "gdn_norm_bwd"),
           ("k_norm_reduce", "gdn_norm_reduce"), ("k_decode<", "gdn_decode"),
