@@ -227,12 +227,28 @@ struct StripDecay {
 template <int R, int D, int NT>
 __device__ __forceinline__ void load_tile(float* s, int LD, const float* g);
 
+// The order in which a persistent kernel walks its units (workgroup i takes units i, i + grid,
+// ...). A kernel's last units are still in the L2 and memory-side caches when the next kernel
+// starts, so a producer whose consumer is a scan ends on the chunks the scan reads first:
+//   BY_HEAD      all chunks of a (row, head) together
+//   CHUNKS_DOWN  one chunk of every (row, head) at a time, the last chunk first (k_chunk: the
+//                forward scan and k_bwd_local start from chunk 0)
+//   CHUNKS_UP    the same, chunk 0 first (k_bwd_local: the backward scan starts from the last)
+enum UnitOrder { BY_HEAD, CHUNKS_DOWN, CHUNKS_UP };
+
 // indices of the (row, head, chunk) unit u of the chunk-parallel kernels
+template <UnitOrder O>
 struct UnitIx {
   int n, bh, h, b, hk;
   __device__ __forceinline__ UnitIx(const GdnArgs& A, int u) {
-    n = u % A.N;
-    bh = u / A.N;
+    if constexpr (O == BY_HEAD) {
+      n = u % A.N;
+      bh = u / A.N;
+    } else {
+      const int nbh = A.B * A.H, c = u / nbh;
+      bh = u - c * nbh;
+      n = O == CHUNKS_DOWN ? A.N - 1 - c : c;
+    }
     h = bh % A.H;
     b = bh / A.H;
     hk = h / A.ratio;
@@ -933,13 +949,13 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
   CtxRaw<C> rc;
   RegsT<C, D, NT> kk;  // k: staged as rows (A and B of k k^T), then as kbe^T
   {
-    const UnitIx x(A, blockIdx.x);
+    const UnitIx<CHUNKS_DOWN> x(A, blockIdx.x);
     rc.fetch(A, x.b, x.h, x.n);
     kk.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D);
   }
   for (int u = blockIdx.x; u < total; u += gridDim.x) {
-    const UnitIx x(A, u);
-    const UnitIx y(A, u + gridDim.x < total ? u + gridDim.x : u);  // the next unit (or this one again)
+    const UnitIx<CHUNKS_DOWN> x(A, u);
+    const UnitIx<CHUNKS_DOWN> y(A, u + gridDim.x < total ? u + gridDim.x : u);  // the next unit (or this one again)
     const size_t off = hoff(A, x.b, x.h, A.H, x.n, C, D);
     float* tg = A.tt + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * C * C;
     rc.commit(cx);
@@ -1498,7 +1514,7 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
   const int total = A.B * A.H * A.N;
   OutIn<C, D, NT> in;
   {
-    const UnitIx x(A, blockIdx.x);
+    const UnitIx<BY_HEAD> x(A, blockIdx.x);
     in.cx.fetch(A, x.b, x.h, x.n);
     in.k.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D);
     in.q.fetch(A.qn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D, i0);
@@ -1506,8 +1522,8 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
     in.st.fetch(A.states + ((size_t)x.b * A.H + x.h) * A.N * D * D + (size_t)x.n * D * D, D);
   }
   for (int u = blockIdx.x; u < total; u += gridDim.x) {
-    const UnitIx x(A, u);
-    const UnitIx y(A, u + gridDim.x < total ? u + gridDim.x : u);  // the next unit (or this one again)
+    const UnitIx<BY_HEAD> x(A, u);
+    const UnitIx<BY_HEAD> y(A, u + gridDim.x < total ? u + gridDim.x : u);  // the next unit (or this one again)
     in.cx.commit(cx);
     in.cx.fetch(A, y.b, y.h, y.n);
     in.k.put_rows(ob);
@@ -1677,17 +1693,21 @@ struct LocalIn {
   StripA<D> q;                // this wave's q rows (A operand of q k^T)
   RegsIO<C, D, NT, TIO> dov;  // do rows, staged as do^T
   Regs<C, C, NT> tt;          // T rows
-  __device__ __forceinline__ void fetch_k(const GdnArgs& A, const UnitIx& y) {
+  template <class U>
+  __device__ __forceinline__ void fetch_k(const GdnArgs& A, const U& y) {
     k.fetch(A.kn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D);
   }
-  __device__ __forceinline__ void fetch_q(const GdnArgs& A, const UnitIx& y, int i0) {
+  template <class U>
+  __device__ __forceinline__ void fetch_q(const GdnArgs& A, const U& y, int i0) {
     q.fetch(A.qn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D, i0);
   }
-  __device__ __forceinline__ void fetch_do(const GdnArgs& A, const UnitIx& y) {
+  template <class U>
+  __device__ __forceinline__ void fetch_do(const GdnArgs& A, const U& y) {
     const TIO* dout = reinterpret_cast<const TIO*>(A.d_out);
     dov.fetch(dout + (((size_t)y.b * A.T + (size_t)y.n * C) * A.H + y.h) * D, A.H * D, A.T - y.n * C);
   }
-  __device__ __forceinline__ void fetch_t(const GdnArgs& A, const UnitIx& y) {
+  template <class U>
+  __device__ __forceinline__ void fetch_t(const GdnArgs& A, const U& y) {
     tt.fetch(A.tt + ((size_t)y.bh * A.N + y.n) * C * C, C);
   }
 };
@@ -1706,14 +1726,14 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
   const int total = A.B * A.H * A.N;
   LocalIn<C, D, NT, TIO> in;
   {
-    const UnitIx x(A, blockIdx.x);
+    const UnitIx<CHUNKS_UP> x(A, blockIdx.x);
     in.cx.fetch(A, x.b, x.h, x.n);
     in.fetch_k(A, x);
     in.fetch_q(A, x, i0);
   }
   for (int u = blockIdx.x; u < total; u += gridDim.x) {
-    const UnitIx x(A, u);
-    const UnitIx y(A, u + gridDim.x < total ? u + gridDim.x : u);  // the next unit (or this one again)
+    const UnitIx<CHUNKS_UP> x(A, u);
+    const UnitIx<CHUNKS_UP> y(A, u + gridDim.x < total ? u + gridDim.x : u);  // the next unit (or this one again)
     in.cx.commit(cx);
     in.cx.fetch(A, y.b, y.h, y.n);
     in.fetch_do(A, x);
