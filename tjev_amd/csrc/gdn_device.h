@@ -521,14 +521,13 @@ __device__ __forceinline__ void quad_transpose(float (&v)[4]) {
   v[3] = hi ? n3 : u1;
 }
 
-// A 16 x 16 accumulator tile stored row-major at p (its element (0, 0); row stride ld, fp32
-// or bf16): a quad transpose, then 4 consecutive columns of one row per lane.
-template <class T>
-__device__ __forceinline__ void st_tile(T* p, size_t ld, const f32x4& a) {
-  float v[4] = {a[0], a[1], a[2], a[3]};
-  quad_transpose(v);
-  const int l = lane();
-  st4_io(p + (size_t)(((l >> 4) << 2) + (l & 3)) * ld + (l & 12), v);
+// A 16 x 16 fp32 accumulator tile stored row-major at p (its element (0, 0); row stride ld) as
+// it lies: 4 rows of one column per lane, 64-byte row segments per store. (A quad transpose
+// first would make them 16-byte stores of 4 columns, at 14 VALU instructions per tile: slower
+// wherever the storing wave's VALU work is on the kernel's critical path, as in the scans.)
+__device__ __forceinline__ void st_tile(float* p, int ld, const f32x4& a) {
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) p[(unsigned)(acc_row(rr) * ld + acc_col())] = a[rr];
 }
 
 // sum over each aligned group of N consecutive lanes (N a power of two <= 64), in every lane
