@@ -1248,8 +1248,10 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
 // column), so neither result goes through LDS and the products need no barrier between them.
 // The other six waves stage the LDS operands a product ahead: k^T of chunk n during P1 of
 // chunk n, -w, u^T and the gates of chunk n + 1 during P2 of chunk n, each from registers loaded
-// one product earlier. Two barriers per chunk. Same chunk ranges, replays and outputs as
-// k_scan_fwd.
+// one product earlier. They also store the states: a compute wave leaves S before chunk n in
+// its columns of the u^T buffer once it has read u from there, and in P2 each loader thread
+// stores the values it then overwrites with the next u^T. Two barriers per chunk. Same chunk
+// ranges, replays and outputs as k_scan_fwd.
 struct ScanSplitBuf {
   static constexpr int C = 128, D = 128, DVT = 32, LU = C + 4;
 };
@@ -1386,6 +1388,19 @@ __global__ __launch_bounds__(512) void k_scan_fwd_split(GdnArgs A) {
       if (idx < 4096) ow.put4(idx >> 5, 4 * (idx & 31), -wr[it].x, -wr[it].y, -wr[it].z, -wr[it].w);
     }
   };
+  auto store_s = [&](int n) {  // S before chunk n, from sU, where put_u writes next
+    float* sg = A.states + ((size_t)bh * A.N + n) * D * D + j0;
+#pragma unroll
+    for (int it = 0; it < 3; ++it) {
+      const int idx = lt + it * NL;
+      if (idx < 1024) {
+        const int dk = idx >> 3, c = 4 * (idx & 7);
+        const float4 v = make_float4(sU[(c + 0) * LU + dk], sU[(c + 1) * LU + dk], sU[(c + 2) * LU + dk],
+                                     sU[(c + 3) * LU + dk]);
+        *reinterpret_cast<float4*>(sg + (unsigned)(dk * D + c)) = v;
+      }
+    }
+  };
   auto put_u = [&]() {
 #pragma unroll
     for (int it = 0; it < 3; ++it) {
@@ -1436,14 +1451,13 @@ __global__ __launch_bounds__(512) void k_scan_fwd_split(GdnArgs A) {
         const float4 v = *reinterpret_cast<const float4*>(sU + (16 * jt + acc_col()) * LU + 16 * rt + acc_row(0));
         accV[rt] = f32x4{v.x, v.y, v.z, v.w};
       }
-      split_product<PS>(accV, ow, accS);
-      // the stores go out while the product's MFMAs run: S before chunk n now (P1 leaves it as
-      // is), v_new after P2's issue (P2 only reads it)
-      if (emit) {
-        float* sg = A.states + ((size_t)bh * A.N + n) * D * D + col;
+      // S before chunk n into the wave's own columns of sU (just read as u^T there): the loaders
+      // store it in the next phase, each thread before it stages the next u^T at those places
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) st_tile(sg + (size_t)(16 * dt) * D, D, accS[dt]);
-      }
+      for (int dt = 0; dt < 8; ++dt)
+        *reinterpret_cast<float4*>(sU + (16 * jt + acc_col()) * LU + 16 * dt + acc_row(0)) =
+            make_float4(accS[dt][0], accS[dt][1], accS[dt][2], accS[dt][3]);
+      split_product<PS>(accV, ow, accS);
       __syncthreads();  // (k kws)^T of chunk n staged
       const float carry = scarry[n & 1];
 #pragma unroll
@@ -1474,6 +1488,7 @@ __global__ __launch_bounds__(512) void k_scan_fwd_split(GdnArgs A) {
       __syncthreads();
       fetch_k(nx);  // during P2: -w, u^T and the gates of the next chunk
       put_w();
+      if (n >= n0) store_s(n);
       put_u();
       if (nx != n) put_gates(nx);  // (the last step's would rewrite the carry being read)
       __syncthreads();
