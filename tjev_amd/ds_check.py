@@ -17,7 +17,7 @@ import re
 import subprocess
 import sys
 
-from .build import CSRC, FLAGS, PARTS, _hipcc, shapes
+from .build import CSRC, FLAGS, PARTS, _hipcc, shapes, unit_flags
 
 _SINGLE = re.compile(r"DS_(WRITE|READ)_B(32|64)\w*\s(%\d+)[^,]*,.*?,\s*(\d+),\s*0,\s*implicit"
                      r".*?(?:into|from) %ir\.([\w.]+)")
@@ -28,7 +28,7 @@ _PAIR = re.compile(r"DS_(WRITE|READ)2(ST64)?_B(32|64)\w*\s.*?,\s*(\d+),\s*(\d+),
 def check_unit(c: int, d: int, part: int) -> list[str]:
     """Wrongly merged LDS accesses of one part of the (chunk c, head dim d) kernel unit (empty
     if none)."""
-    return check_source(CSRC / "gdn_inst.hip", [f"-DGDN_C={c}", f"-DGDN_D={d}", f"-DGDN_PART={part}"])
+    return check_source(CSRC / "gdn_inst.hip", unit_flags(c, d, part))
 
 
 def check_source(src, defines=()) -> list[str]:
