@@ -41,6 +41,15 @@ __device__ __forceinline__ int wave() { return threadIdx.x >> 6; }
 // SIMD, which then carries NW + 1 tiles of every such product (without it: 6, 8, 10 and 12 for
 // NW = 8). readfirstlane marks the value uniform: the strip-dependent loop bounds and branches
 // are otherwise compiled as divergent code.
+// A wave-uniform value made opaque to the optimiser at this point (it stays in a scalar
+// register). Inside a persistent kernel's unit loop, the strip index taken through it keeps the
+// conditions on it (tile t below, on or above the strip's diagonal ...) from being computed
+// once before the loop and held across it as 64-bit lane masks, which run the kernel out of
+// scalar registers and spill them to vector lanes.
+__device__ __forceinline__ int opaque_uniform(int v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
 template <int NW, bool PAIR>
 __device__ __forceinline__ int wave_strip() {
   const int w = wave();

@@ -1525,18 +1525,19 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
     for (int c = threadIdx.x; c < D; c += NT) snw[c] = A.nw[c];
   }
   const Op<PI> ob = TB::at(sB);
-  const int w = wave_strip<C / 16, false>(), i0 = 16 * w;
+  const int ws = wave_strip<C / 16, false>();
   const int total = A.B * A.H * A.N;
   OutIn<C, D, NT> in;
   {
     const UnitIx<BY_HEAD> x(A, blockIdx.x);
     in.cx.fetch(A, x.b, x.h, x.n);
     in.k.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D);
-    in.q.fetch(A.qn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D, i0);
+    in.q.fetch(A.qn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D, 16 * ws);
     in.v.fetch(A.vnew + hoff(A, x.b, x.h, A.H, x.n, C, D), D);
     in.st.fetch(A.states + ((size_t)x.b * A.H + x.h) * A.N * D * D + (size_t)x.n * D * D, D);
   }
   for (int u = blockIdx.x; u < total; u += gridDim.x) {
+    const int w = opaque_uniform(ws), i0 = 16 * w;  // conditions on w stay in the loop
     const UnitIx<BY_HEAD> x(A, u);
     const UnitIx<BY_HEAD> y(A, u + gridDim.x < total ? u + gridDim.x : u);  // the next unit (or this one again)
     in.cx.commit(cx);
@@ -1737,16 +1738,17 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
   __shared__ __align__(16) char sB[TB::BYTES];
   __shared__ Ctx<C> cx;
   const Op<PI> ob = TB::at(sB);
-  const int w = wave_strip<C / 16, true>(), i0 = 16 * w;
+  const int ws = wave_strip<C / 16, true>();
   const int total = A.B * A.H * A.N;
   LocalIn<C, D, NT, TIO> in;
   {
     const UnitIx<CHUNKS_UP> x(A, blockIdx.x);
     in.cx.fetch(A, x.b, x.h, x.n);
     in.fetch_k(A, x);
-    in.fetch_q(A, x, i0);
+    in.fetch_q(A, x, 16 * ws);
   }
   for (int u = blockIdx.x; u < total; u += gridDim.x) {
+    const int w = opaque_uniform(ws), i0 = 16 * w;  // conditions on w stay in the loop
     const UnitIx<CHUNKS_UP> x(A, u);
     const UnitIx<CHUNKS_UP> y(A, u + gridDim.x < total ? u + gridDim.x : u);  // the next unit (or this one again)
     in.cx.commit(cx);
