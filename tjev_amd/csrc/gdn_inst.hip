@@ -111,7 +111,7 @@ template <int C, int D, int PI, int PS, class TIO, class TG>
 hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) {
   constexpr int DVT = D < 32 ? D : 32;
   constexpr int NS = (C > D ? C : D) * 4;
-  const dim3 prep(A.B * A.N, 2 * A.Hk + A.H);
+  const dim3 prep(A.B * A.N * (2 * A.Hk + A.H));  // the slot fastest (k_prep, k_post)
   const dim3 chunks(A.B * A.H * A.N);
   // the scans: (row, head, Dv tile) chains, each split into up to `parts` chunk ranges at
   // segment resets (rows without resets leave the extra ranges empty)

@@ -379,7 +379,8 @@ __device__ __forceinline__ const TIO* halo_row(const GdnArgs& A, const TIO* x, i
 }
 
 // ---------------------------------------------------------------- k_prep
-// grid (B*N, 2*Hk + H), 256 threads. Slot y: q head y (< Hk), k head y - Hk, v head y - 2Hk.
+// grid B*N*(2*Hk + H), 256 threads, the slot fastest: the workgroups of one chunk run together
+// and read its token rows whole. Slot y: q head y (< Hk), k head y - Hk, v head y - 2Hk.
 // Every (token, 8 channels) is independent: D/8 lanes per token row. l2norm of xla.py:42-53.
 // Slot 0 first writes the padded segment ids of the chunk (read by every later kernel).
 template <int C, int D, class TIO, class TG, int K1 = 4>
@@ -387,8 +388,9 @@ __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
   static_assert(K1 >= 1 && K1 <= 4, "conv lags 1..K1 (launched with K1 >= taps - 1)");
   constexpr int CG = D / 8;
   constexpr int RPP = 256 / CG;
-  const int b = blockIdx.x / A.N, n = blockIdx.x % A.N;
-  const int slot = blockIdx.y;
+  const int slots = 2 * A.Hk + A.H, bn = blockIdx.x / slots;
+  const int b = bn / A.N, n = bn % A.N;
+  const int slot = blockIdx.x % slots;
   const int cg = threadIdx.x % CG;
   int kind, head, c0;
   if (slot < A.Hk) { kind = 0; head = slot; c0 = slot * D; }
@@ -2194,7 +2196,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
 }
 
 // ---------------------------------------------------------------- k_post
-// grid (B*N, 2*Hk + H), 256 threads: the activations' gradients back to d(qkv) -- GQA sums,
+// grid B*N*(2*Hk + H) as k_prep's, 256 threads: the activations' gradients back to d(qkv) -- GQA sums,
 // l2norm backward (pallas_tpu_mega.py:101-103), SiLU and the anti-causal conv backward with
 // segment masks (pallas_tpu_mega.py:161-179, 306-319) -- and, for the value heads, the gate
 // backward (pallas_tpu_mega.py:129-145): dg = reverse in-chunk cumsum of d gamma, and d beta
@@ -2213,8 +2215,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   __shared__ int shs[NG * HS];                  // and their segment ids
   __shared__ float sxv[C];                      // value heads: rows(X, v) of the chunk's tokens
   __shared__ float sdw[DW ? 4 * NL * D : 1];    // per-wave sums of d(conv w)
-  const int b = blockIdx.x / A.N, n = blockIdx.x % A.N;
-  const int slot = blockIdx.y;
+  const int slots = 2 * A.Hk + A.H, bn = blockIdx.x / slots;
+  const int b = bn / A.N, n = bn % A.N;
+  const int slot = blockIdx.x % slots;
   const int cg = threadIdx.x % CG, grp = threadIdx.x / CG;
   int kind, head, c0;
   if (slot < A.Hk) { kind = 0; head = slot; c0 = slot * D; }
