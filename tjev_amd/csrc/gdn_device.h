@@ -114,6 +114,22 @@ __device__ __forceinline__ void st8_io(uint16_t* p, const float (&v)[8]) {
   for (int e = 0; e < 4; ++e) w[e] = (uint32_t)f2bf(v[2 * e]) | ((uint32_t)f2bf(v[2 * e + 1]) << 16);
   *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
 }
+// Nontemporal forms for the step's final outputs, which no later kernel of the step reads:
+// they are not kept in the caches the next kernels' inputs go through
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void st8_io_nt(float* p, const float (&v)[8]) {
+  const f32x4 a = {v[0], v[1], v[2], v[3]}, b = {v[4], v[5], v[6], v[7]};
+  __builtin_nontemporal_store(a, reinterpret_cast<f32x4*>(p));
+  __builtin_nontemporal_store(b, reinterpret_cast<f32x4*>(p) + 1);
+}
+__device__ __forceinline__ void st8_io_nt(uint16_t* p, const float (&v)[8]) {
+  u32x4 w;
+  w.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+  w.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+  w.z = (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16);
+  w.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
+}
 
 // 8 consecutive stored values held as loaded (bf16 stays packed), converted when used
 template <class T> struct Raw8;

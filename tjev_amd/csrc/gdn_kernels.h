@@ -2316,7 +2316,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         }
       }
     }
-    st8_io(dx + ((size_t)b * A.T + t) * A.W + cc, o);
+    st8_io_nt(dx + ((size_t)b * A.T + t) * A.W + cc, o);  // d(qkv): read by no later kernel
   };
 #pragma unroll
   for (int i = 0; i < RG; ++i) {
