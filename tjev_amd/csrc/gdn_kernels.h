@@ -525,6 +525,29 @@ struct Regs {
       if (live(it)) v[it] = *reinterpret_cast<const float4*>(lane_ptr(g, idx / V, ldg, 4 * (idx % V)));
     }
   }
+  // a lower triangular tile: only the 16 x 16 tiles on and below the diagonal are read. The
+  // slots above go to the row's first tile (a line the same instruction fetches anyway), so
+  // every slot still issues one load and the count stays static; put_lds_lower writes them as
+  // zeros (the condition recomputed there, not held across the loads' latency).
+  __device__ __forceinline__ static bool upper(int it) {
+    const int idx = threadIdx.x + it * NT;
+    return ((idx % V) >> 2) > ((idx / V) >> 4);
+  }
+  __device__ __forceinline__ void fetch_lower(const float* g, int ldg) {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int idx = threadIdx.x + it * NT, c4 = idx % V;
+      if (live(it)) v[it] = *reinterpret_cast<const float4*>(lane_ptr(g, idx / V, ldg, 4 * (upper(it) ? (c4 & 3) : c4)));
+    }
+  }
+  __device__ __forceinline__ void put_lds_lower(float* s, int ld) const {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      if (!live(it)) continue;
+      const int idx = threadIdx.x + it * NT;
+      *reinterpret_cast<float4*>(s + (idx / V) * ld + 4 * (idx % V)) = upper(it) ? make_float4(0.f, 0.f, 0.f, 0.f) : v[it];
+    }
+  }
   // op(r, k) = g[r][k] * rs[r] * cst
   template <int P>
   __device__ __forceinline__ void put_rows(const Op<P>& op, const float* rs = nullptr, float cst = 1.f) const {
@@ -1033,9 +1056,16 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
       f32x4 vn[D / 16];
       zero(vn);
       strip_mma<PI, C, D / 16>(vn, krow(sT, LT), i0, ob, 0, 0, tri_end<C>(i0));
-      if constexpr (STORE_T) {
-        for (int idx = threadIdx.x; idx < C * C; idx += NT)  // lower triangle (the rest is scratch)
-          tg[idx] = idx % C <= idx / C ? sT[(idx / C) * LT + idx % C] : 0.f;
+      if constexpr (STORE_T) {  // for k_bwd_local (fetch_lower): the tiles on and below the diagonal
+#pragma unroll 2
+        for (int idx = threadIdx.x; idx < C * C / 4; idx += NT) {
+          const int r = idx / (C / 4), c = 4 * (idx % (C / 4));
+          if ((c >> 4) <= (r >> 4)) {  // the lower triangle (the rest of sT is scratch)
+            const float4 t = *reinterpret_cast<const float4*>(sT + r * LT + c);
+            *reinterpret_cast<float4*>(tg + r * C + c) =
+                make_float4(c <= r ? t.x : 0.f, c + 1 <= r ? t.y : 0.f, c + 2 <= r ? t.z : 0.f, c + 3 <= r ? t.w : 0.f);
+          }
+        }
       }
 #pragma unroll
       for (int t = 0; t < D / 16; ++t)
@@ -1726,7 +1756,7 @@ struct LocalIn {
   }
   template <class U>
   __device__ __forceinline__ void fetch_t(const GdnArgs& A, const U& y) {
-    tt.fetch(A.tt + ((size_t)y.bh * A.N + y.n) * C * C, C);
+    tt.fetch_lower(A.tt + ((size_t)y.bh * A.N + y.n) * C * C, C);
   }
 };
 
@@ -1789,7 +1819,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
     strip_mma<PDO, C, D / 16>(acc, kcol(sA, LA), i0, ob, 0, tri_begin(i0), C);  // dv_loc = intra^T do
     in.fetch_t(A, x);
     __syncthreads();
-    in.tt.put_lds(sA, LA);
+    in.tt.put_lds_lower(sA, LA);
 #pragma unroll
     for (int t = 0; t < D / 16; ++t)  // dv_loc^T: B(c, j) = dv_loc[c][j]
       ob.put4(16 * t + acc_col(), i0 + acc_row(0), acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
