@@ -301,7 +301,8 @@ def test_serving_rejects_cpu_tensors():
 def test_kernel_roofline_takes_the_longer_ideal_time():
     """The bound is the resource whose ideal time is longer: the 0.8B chunk kernels are HBM-bound
     against the bf16 peak and MFMA-bound against the fp32 one; bytes of every kernel are the sum
-    of its operand tensors (bwd grads: q, k, X, v_new, dq, dk, S, G, d out and the context)."""
+    of its operand tensors (bwd grads: q, k, X, v_new, dq, dk, S, G, d out and the context; T,
+    unit lower triangular, counts as its strictly lower triangle)."""
     from tjev_amd.roofline import PEAK_BF16_TFLOPS, PEAK_FP32_TFLOPS, kernel_roofline, kernel_work
 
     w = kernel_work(batch=4, length=4096, key_heads=16, value_heads=16, dim=128, chunk=128, io_bytes=2)
@@ -309,8 +310,9 @@ def test_kernel_roofline_takes_the_longer_ideal_time():
     ctx = 4 * 4096 * 4 + 3 * 4 * 16 * 4096 * 4
     assert w["gdn_bwd_grads"]["bytes"] == 6 * act + 2 * mat + io + ctx + 2 * 4 * 16 * 4096 * 4
     assert w["gdn_chunk_fwd"]["bytes"] == 4 * act + ctx
+    tri = 4 * 16 * 32 * (128 * 127 // 2) * 4  # T: its strictly lower triangle per chunk
     assert kernel_work(batch=4, length=4096, key_heads=16, value_heads=16, dim=128, chunk=128, io_bytes=2,
-                       residuals="tinv")["gdn_chunk_fwd"]["bytes"] == 4 * act + ctx + mat
+                       residuals="tinv")["gdn_chunk_fwd"]["bytes"] == 4 * act + ctx + tri
     r = kernel_roofline(w["gdn_bwd_grads"], 338e-6, PEAK_BF16_TFLOPS)
     assert r["bound"] == "hbm" and r["unit"] == "GB/s" and abs(r["frac"] - r["hbm_frac"]) < 1e-12
     assert abs(r["achieved"] - w["gdn_bwd_grads"]["bytes"] / 338e-6 / 1e9) < 1e-6

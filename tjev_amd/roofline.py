@@ -42,7 +42,7 @@ def kernel_work(*, batch: int, length: int, key_heads: int, value_heads: int, di
     act_k = tok_k * D * f32                    # q or k (key heads), fp32
     act_v = tok_h * D * f32                    # v, w, u, v_new, X, Kt, dq / dk per value head, fp32
     mats = units * D * D * f32                 # chunk-boundary states S or their gradients G
-    tinv = units * C * C * f32                 # T per chunk
+    tinv = units * C * (C - 1) // 2 * f32      # T per chunk: its strictly lower triangle (unit lower triangular)
     io = tok_h * D * io_bytes                  # out or d out
     ctx = batch * tp * 4 + 3 * tok_h * f32     # segment ids, gamma (hi, lo), beta
     prep = tokens * (width + 2 * value_heads) * io_bytes + (2 * tok_k + tok_h) * D * f32 + 3 * tok_h * f32
