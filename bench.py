@@ -50,6 +50,8 @@ def _args(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=0, help="rows of the workload in the CPU baseline (0: all)")
     ap.add_argument("--details", default=None, help="also write the full report to this JSON file")
+    ap.add_argument("--no-9b", action="store_true",
+                    help="with the default 0.8B config, skip the 9B config timed after it in the same run")
     return ap.parse_args(argv)
 
 
@@ -382,13 +384,6 @@ def main(argv=None) -> int:
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import torch
 
-    from tjev_amd import _lib
-    from tjev_amd.gdn import GdnPlan
-    from tjev_amd.norm import _params as _norm_params
-    from tjev_amd.norm import norm_backward, norm_forward
-    from tjev_amd.roofline import PEAK_BF16_TFLOPS, PEAK_FP32_TFLOPS, kernel_roofline, kernel_work, operator_work
-    from tjev_amd.testing import CONFIGS, cotangent, gdn_inputs
-
     if args.config in ("4B-block", "decode", "v2"):
         report = {"4B-block": _block_bench, "decode": _decode_bench, "v2": _v2_bench}[args.config](args)
         if args.details:
@@ -396,7 +391,42 @@ def main(argv=None) -> int:
                 json.dump(report, f, indent=1)
         print(json.dumps(report), flush=True)
         return 0
-    cfg = dict(CONFIGS[args.config])
+    report = _layer_bench(args, args.config)
+    if args.config == "0.8B" and not args.no_9b:
+        # the metric names both layer shapes (campaign/bench.py:359-380 times (16,16) and (16,32)):
+        # the 9B config in the same process, after the 0.8B buffers are released
+        torch.cuda.empty_cache()
+        nine = _layer_bench(args, "9B", cpu=False)
+        report["config_9B"] = {
+            "workload": nine["config"]["workload"], "value": nine["value"], "unit": "tokens/s",
+            "ms_per_step": nine["ms_per_step"], "batch": nine["config"]["batch"], "seq_len": nine["config"]["seq_len"],
+            "key_heads": nine["config"]["key_heads"], "value_heads": nine["config"]["value_heads"],
+            "operator_roofline_frac": nine["operator_roofline"]["frac"],
+            "operator_ceiling_tokens_per_s": nine["operator_roofline"]["ceiling_tokens_per_s"],
+            "roofline": {k: nine["roofline"][k] for k in ("kernel", "bound", "achieved", "peak", "unit", "frac")},
+            "kernels_ms": {k: v["ms"] for k, v in nine["kernels"].items()},
+            "finite": nine["finite"], "wall_s_timed": nine["wall_s_timed"],
+        }
+    if args.details:
+        with open(args.details, "w") as f:
+            json.dump(report, f, indent=1)
+    print(json.dumps(report), flush=True)
+    return 0
+
+
+def _layer_bench(args, config: str, cpu: bool = True) -> dict:
+    """One layer config (0.8B, 9B, varlen, tiny): the report of its timed steps, per-kernel
+    rooflines and (with ``cpu``) the CPU baseline."""
+    import torch
+
+    from tjev_amd import _lib
+    from tjev_amd.gdn import GdnPlan
+    from tjev_amd.norm import _params as _norm_params
+    from tjev_amd.norm import norm_backward, norm_forward
+    from tjev_amd.roofline import PEAK_BF16_TFLOPS, PEAK_FP32_TFLOPS, kernel_roofline, kernel_work, operator_work
+    from tjev_amd.testing import CONFIGS, cotangent, gdn_inputs
+
+    cfg = dict(CONFIGS[config])
     precision = args.precision or cfg["precision"]
     dtype = cfg["dtype"]
     dev = torch.device("cuda", 0)
@@ -465,7 +495,7 @@ def main(argv=None) -> int:
                for name, avg_ms in per_kernel.items()}
     dominant = max(kernels, key=lambda k: kernels[k]["ms"])
     dk = kernels[dominant]
-    traffic = _traffic(args.config, precision, dominant)
+    traffic = _traffic(config, precision, dominant)
     op = operator_work(**shape)
     value = B * T / (ms * 1e-3)
     report = {
@@ -481,7 +511,7 @@ def main(argv=None) -> int:
         "vs_baseline": None,
         "dtype": "bf16" if dtype == torch.bfloat16 else "f32",
         "data": "synthetic",
-        "config": {"workload": f"{args.config} GDN layer core (mega2) fwd+bwd", "batch": B, "seq_len": T,
+        "config": {"workload": f"{config} GDN layer core (mega2) fwd+bwd", "batch": B, "seq_len": T,
                    "key_heads": Hk, "value_heads": H, "head_dim": D, "chunk": C, "conv_taps": int(w.shape[0]),
                    "precision": precision, "segments": cfg["segments"],
                    "epilogue": ("gated_rmsnorm (forward in the output kernel)" if fused else "gated_rmsnorm")
@@ -498,13 +528,9 @@ def main(argv=None) -> int:
         "finite": finite,
         "wall_s_timed": t_wall,
     }
-    if not args.no_cpu_baseline:
+    if cpu and not args.no_cpu_baseline:
         report["cpu_baseline"] = _cpu_baseline(cfg, dtype, min(args.cpu_rows, B) if args.cpu_rows > 0 else B, norm)
-    if args.details:
-        with open(args.details, "w") as f:
-            json.dump(report, f, indent=1)
-    print(json.dumps(report), flush=True)
-    return 0
+    return report
 
 
 if __name__ == "__main__":

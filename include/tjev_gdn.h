@@ -24,8 +24,10 @@
  *                v_new  [B, H, ceil(T/C)*C, Dv]    u - w S of each token, when
  *                                                   residuals == TJEV_GDN_SAVE_ALL
  *              (C: the chunk the kernels run, max(chunk, 16))
- * T need not be a multiple of the chunk: the tail is treated as segment-0 padding with zero
- * qkv, a and b, as the reference pads (pallas_tpu_mega.py:616-621).
+ * T need not be a multiple of the chunk: the kernels pad the tail with zero q, k, v and beta,
+ * g = 0 and the last token's segment id (xla.py:198-204), so the padding changes no output
+ * (pallas_tpu_mega.py:616-621 pads with segment 0: the same outputs) and carries the state after
+ * token T-1 unchanged to the end of the last chunk.
  */
 #ifndef TJEV_GDN_H
 #define TJEV_GDN_H
@@ -104,7 +106,8 @@ int tjev_gdn_mega2_fwd(const tjev_gdn_params* p, void* stream, const void* qkv, 
  * xla.py:170-262): final_state [B, H, Dk, Dv] fp32, the recurrent state after token T-1
  * (xla.py:141-167 run to the last token: restarted where the segment id changes), and
  * conv_state [B, K-1, W] io_dtype, the raw rows T-K+1 .. T-1 (oldest first), zero before the
- * row or outside token T-1's segment. Either may be null. */
+ * row or outside token T-1's segment. Either may be null; a conv of 0 or 1 taps has no history:
+ * a non-null conv_state then returns TJEV_GDN_EINVAL. */
 int tjev_gdn_mega2_fwd_state(const tjev_gdn_params* p, void* stream, const void* qkv, const void* a,
                              const void* b, const float* a_log, const float* dt_bias,
                              const float* conv_w, const int32_t* seg, void* out, float* residuals,
@@ -145,8 +148,8 @@ int tjev_gdn_mega2_fwd_normed(const tjev_gdn_params* p, void* stream, const void
 
 /* The backward of tjev_gdn_mega2_fwd_cont: initial_state and initial_conv as given to the forward
  * (initial_state's values are in the residuals; only whether it is null matters here);
- * d_final_state [B, H, Dk, Dv] fp32, the gradient of the forward's final_state (null: 0; needs
- * a length that is a multiple of the kernels' chunk, else TJEV_GDN_EUNSUPPORTED). Writes, beside
+ * d_final_state [B, H, Dk, Dv] fp32, the gradient of the forward's final_state (null: 0; any
+ * length: the padded tail carries the state unchanged). Writes, beside
  * tjev_gdn_mega2_bwd's outputs, d_initial_state [B, H, Dk, Dv] fp32 and d_initial_conv
  * [B, K-1, W] io_dtype when not null (each needs its input). The gradient of the forward's
  * conv_state is that of rows of qkv or initial_conv: the caller adds it there. */
@@ -224,8 +227,8 @@ int tjev_gdn_v2_bwd(const tjev_gdn_params* p, void* stream, const void* q, const
  * chunk_gated_delta_rule(q, k, v, g, beta, segment_ids, initial_state) -> (out, final_state)
  * (xla.py:170-262) on the v2 operator's inputs. initial_state [B, H, Dk, Dv] fp32 or null (as
  * for tjev_gdn_mega2_fwd_cont); final_state [B, H, Dk, Dv] fp32 or null: the state after token
- * T-1. The backward takes initial_state as given to the forward, d_final_state (null: 0; a length
- * that is a multiple of the kernels' chunk) and writes d_initial_state when not null. */
+ * T-1. The backward takes initial_state as given to the forward, d_final_state (null: 0; any
+ * length) and writes d_initial_state when not null. */
 int tjev_gdn_v2_fwd_cont(const tjev_gdn_params* p, void* stream, const void* q, const void* k,
                          const void* v, const void* g, const void* beta, const int32_t* seg,
                          const float* initial_state, void* out, float* residuals,

@@ -47,9 +47,11 @@ def test_golden_inputs_are_the_seeded_generator(name):
         assert np.array_equal(fx[k], again[k]), (name, k)
 
 
-# per-token terms at the fp32 level; the A_log / dt_bias sums over every token are judged
-# against the fp64 truth at 1e-4 (the fp32 reference path itself is 3e-5 off it at config 1)
-TOL32 = {"out": 1e-5, "qkv": 1e-5, "a": 1e-5, "b": 1e-5, "A_log": 1e-4, "dt_bias": 1e-4, "w": 1e-5}
+# every output and gradient within the fp32 tolerance (test_gdn_mega.py:89-91) of the fp64
+# truth, the A_log / dt_bias sums over every token included (the kernels form the decay
+# gradient without its cancelling terms: ~3e-6 there, where the fp32 reference path itself is
+# 3e-5 off the truth at config 1)
+TOL32 = {"out": 1e-5, "qkv": 1e-5, "a": 1e-5, "b": 1e-5, "A_log": 1e-5, "dt_bias": 1e-5, "w": 1e-5}
 
 
 @pytest.mark.gpu
@@ -65,7 +67,7 @@ def test_hip_matches_golden(name):
     want = {k: torch.from_numpy(fx["want_" + k]).double() for k in got}
     if str(fx["dtype"]) == "float32":
         errors = {k: rel(got[k], want[k]) for k in got}
-        print(errors)
+        print(name, {k: f"{v:.2e}" for k, v in errors.items()}, flush=True)
         for k, e in errors.items():
             assert e < TOL32[k], (k, errors)
     else:

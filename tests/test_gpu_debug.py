@@ -118,3 +118,28 @@ def test_nan_input_stays_where_the_recurrence_carries_it():
         assert torch.isfinite(out[0, :, hh]).all(), hh        # the other value heads
     for g in grads[:3]:
         assert torch.isfinite(g[1].cpu()).all()               # the other row's gradients
+
+
+@pytest.mark.parametrize("weight_grad", [False, True], ids=["frozen-weight", "weight-grad"])
+def test_poisoned_buffers_normed_path(weight_grad):
+    """The core with its gated RMSNorm (tjev_gdn_mega2_fwd_normed / _bwd_normed, the bench's and
+    the block's path) under the poison mode: the backward's whole workspace is poisoned, the
+    norm's d out and weight partials after the megakernel's part included."""
+    from tjev_amd import gdn_megakernel_normed
+
+    (qkv, a, b, a_log, dt_bias, w, seg), cot = case_inputs(1, 400, 2, 4, 128, cuts=[100, 177], dtype=torch.bfloat16,
+                                                           style="baseline")
+    gen = torch.Generator().manual_seed(6)
+    z = torch.randn((1, 400, 4, 128), generator=gen).to(torch.bfloat16)
+    nw = 1 + 0.1 * torch.randn(128, generator=gen)
+    print(f"poison normed weight_grad={weight_grad}", flush=True)
+
+    def run():
+        leaves = [x.cuda().requires_grad_(x.is_floating_point()) for x in (qkv, a, b, a_log, dt_bias, z)]
+        wt = nw.cuda().requires_grad_(weight_grad)
+        y = gdn_megakernel_normed(*leaves[:5], w.cuda(), seg.cuda(), leaves[5], wt, key_heads=2, key_dim=128,
+                                  value_heads=4, value_dim=128, chunk=128, precision="high")
+        grads = torch.autograd.grad((y.float() * cot.cuda()).sum(), leaves + ([wt] if weight_grad else []))
+        return {"y": y.detach(), **{f"d{i}": g for i, g in enumerate(grads)}}
+
+    _same(*_both(run), f"normed weight_grad={weight_grad}")

@@ -24,16 +24,18 @@ def _leaves(*xs):
     return [x.detach().clone().cuda().requires_grad_(x.is_floating_point()) for x in xs]
 
 
+@pytest.mark.parametrize("t1", [96, 77], ids=["whole-chunks", "ragged"])
 @pytest.mark.parametrize("cuts", [None, [30, 110, 130]], ids=["one-segment", "cuts"])
 @pytest.mark.parametrize("conv", [True, False], ids=["mega2", "mega1"])
-def test_megakernel_in_two_pieces_equals_one_run(conv, cuts):
+def test_megakernel_in_two_pieces_equals_one_run(conv, cuts, t1):
+    """The first piece ends after whole chunks (96) or inside a chunk (77 = 4 * 16 + 13: the
+    kernels' padded tail carries its final state, and the final state's gradient enters there)."""
     from tjev_amd import gdn_megakernel
 
     (qkv, a, b, a_log, dt_bias, w, seg), cot = case_inputs(2, 141, 2, 4, 16, cuts=cuts, trailing_pad=3 if cuts else 0,
                                                            segments="cuts" if cuts else "one")
     kw = dict(key_heads=2, key_dim=16, value_heads=4, value_dim=16, chunk=16, precision="highest")
-    t1 = 96  # whole chunks: the final state's gradient crosses to the first piece
-    print(f"pieces conv={conv} cuts={cuts}", flush=True)
+    print(f"pieces conv={conv} cuts={cuts} t1={t1}", flush=True)
     lv = _leaves(qkv, a, b, a_log, dt_bias, w)
     wl = lv[5] if conv else None
     segc, cotc = seg.cuda(), cot.cuda()
@@ -56,18 +58,21 @@ def test_megakernel_in_two_pieces_equals_one_run(conv, cuts):
         assert e <= (5e-5 if n in ("A_log", "dt_bias") else TOL), (n, errs)
 
 
-def test_v2_initial_state_matches_the_oracle():
+@pytest.mark.parametrize("T", [128, 141], ids=["whole-chunks", "ragged"])
+def test_v2_initial_state_matches_the_oracle(T):
     """chunk_gated_delta_rule(q, k, v, g, beta, seg, initial_state) -> (out, final_state) against
     the fp64 chunked rule with the same state (xla.py:170-262), with segment cuts (the state is
-    read by token 0's segment only) and GQA; every gradient, the initial state's included."""
+    read by token 0's segment only) and GQA; every gradient, the initial state's and the one
+    through the final state included, also at a length inside a chunk (141 = 8 * 16 + 13)."""
     import numpy as np
 
     from oracle.gdn_oracle import chunk_gated_delta_rule as ref_rule
     from oracle.gdn_oracle import l2norm
     from tjev_amd.v2 import chunk_gated_delta_rule
 
+    print(f"v2 with an initial state, T={T}", flush=True)
     rng = np.random.default_rng(5)
-    B, T, H, D = 2, 128, 4, 16
+    B, H, D = 2, 4, 16
     f = lambda *s: torch.from_numpy(rng.standard_normal(s).astype(np.float32))  # noqa: E731
     q, k = l2norm(f(B, T, H, D)) * D ** -0.5, l2norm(f(B, T, H, D))
     v = f(B, T, H, D)

@@ -54,6 +54,9 @@ def _params(**kw):
     (dict(key_dim=48, value_dim=48), 2, "no kernels"),
     (dict(value_dim=32), 2, "key_dim == value_dim"),
     (dict(residuals=3), 1, "residuals"),
+    # B*T*W = 2^27 * 48 passes the size bound, but the flat prep grid would hold 2^23 * 3
+    # workgroups of 256 work-items: more than one launch takes
+    (dict(length=1 << 27, key_heads=1, value_heads=1), 2, "too large for one launch"),
 ])
 def test_c_abi_validation(bad, status, msg):
     from tjev_amd import _lib
@@ -325,7 +328,7 @@ def test_state_entry_points_validate_before_launch():
     """The continued-sequence entry points (an initial state and conv history in, the final
     ones out): their checks come before the workspace's, and every call here passes no
     workspace, so none can launch: a conv history needs a conv of 2+ taps, a gradient needs its
-    input, the final state's gradient needs whole chunks, state tensors are 16-byte aligned."""
+    input (the final state's gradient any length), state tensors are 16-byte aligned."""
     from tjev_amd import _lib
 
     lib = _lib.load()
@@ -350,8 +353,9 @@ def test_state_entry_points_validate_before_launch():
     assert bwd(p, init=vp(20), hist=vp(21), d_final=vp(22), d_init=vp(23), d_hist=vp(24)) == 3
     assert bwd(p, d_init=vp(23)) == 1 and "needs the initial state" in lib.tjev_gdn_last_error().decode()
     assert bwd(p, init=vp(20), d_hist=vp(24)) == 1 and "needs the conv history" in lib.tjev_gdn_last_error().decode()
-    assert bwd(_params(length=100, chunk=16), d_final=vp(22)) == 2
-    assert "multiple of the chunk" in lib.tjev_gdn_last_error().decode()
+    # a length inside a chunk: the final state's gradient is accepted (the padded tail carries it)
+    assert bwd(_params(length=100, chunk=16), d_final=vp(22)) == 3
+    assert "workspace" in lib.tjev_gdn_last_error().decode()
     # the v2 forms
     p0 = _params(taps=0, length=96, chunk=16)
     assert lib.tjev_gdn_v2_fwd_cont(ctypes.byref(p0), None, *[vp(i) for i in range(6)], vp(20), vp(7), vp(8),
@@ -361,7 +365,7 @@ def test_state_entry_points_validate_before_launch():
     assert "needs the initial state" in lib.tjev_gdn_last_error().decode()
     assert lib.tjev_gdn_v2_bwd_cont(ctypes.byref(_params(taps=0, length=90, chunk=16)), None,
                                     *[vp(i) for i in range(6)], vp(20), vp(8), vp(9), vp(21),
-                                    *[vp(10 + i) for i in range(5)], vp(16), ws, 0) == 2
+                                    *[vp(10 + i) for i in range(5)], vp(16), ws, 0) == 3
 
 
 def test_state_operators_reject_cpu_tensors_and_bad_shapes():

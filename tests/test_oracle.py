@@ -630,6 +630,152 @@ def test_gdn_block_zero_adapters_reduce_to_the_base_layer():
     assert torch.all(got[0, 9:] == 0)
 
 
+def _block_case(seed=31):
+    """A small GDN block in fp64 (hidden 8 = H * Dv, so a norm after out_proj is expressible as
+    a slip; GQA 1 -> 2 heads of 4; nonzero adapters on all five projections, rsLoRA-sized
+    scale), an input x [2, 23, 8], a cotangent, and per-row valid lengths (row 1 starts with
+    three padding tokens). A_log is chosen so that its float32 exponential, as HF evaluates it,
+    is exact in float64."""
+    rng = np.random.default_rng(seed)
+    f = lambda *s: torch.from_numpy(rng.standard_normal(s))  # noqa: E731
+    hidden, hk, h, d, r = 8, 1, 2, 4, 2
+    width = 2 * hk * d + h * d
+    names = {"in_proj_qkv": width, "in_proj_z": h * d, "in_proj_b": h, "in_proj_a": h}
+    p = {n: (f(hidden, o) * 0.4, f(hidden, r) / r ** 0.5, f(r, o) * 0.1, 1.5) for n, o in names.items()}
+    p["out_proj"] = (f(h * d, hidden) * 0.4, f(h * d, r) / r ** 0.5, f(r, hidden) * 0.1, 1.5)
+    a_log = torch.log(torch.from_numpy(rng.uniform(1.0, 16.0, h)).float().to(F64))
+    p.update(conv=f(4, width) * 0.5, a_log=a_log, dt_bias=f(h), norm=1 + 0.2 * f(d))
+    x = f(2, 23, hidden)
+    seg = torch.ones((2, 23), dtype=torch.int32)
+    seg[1, :3] = 0
+    return dict(hidden=hidden, key_heads=hk, key_dim=d, value_heads=h, value_dim=d), p, x, seg, f(2, 23, hidden)
+
+
+def _hf_block(shape, p, x, seg, cot, monkeypatch):
+    """HF transformers' whole Qwen3_5GatedDeltaNet layer (modeling_qwen3_5.py:432-545: input
+    mask, in_proj_qkv/z/b/a, conv + SiLU, split, gates, l2norm and q scale, the delta rule,
+    the gated RMSNorm per head with gate z, out_proj) in float64 with its Linear weights set to
+    the block's merged kernels W + s A B and its conv, A_log, dt_bias and norm weight to the
+    block's; the padding rows go in as HF's attention mask. Its delta rule is replaced by the
+    float64 token recurrence (HF's own casts to float32). HF still evaluates the norm and
+    e^{A_log} in float32. Returns the output and dx of sum(out * cot)."""
+    hf = pytest.importorskip("transformers.models.qwen3_5.modeling_qwen3_5")
+    from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5TextConfig
+
+    cfg = Qwen3_5TextConfig(hidden_size=shape["hidden"], linear_num_key_heads=shape["key_heads"],
+                            linear_num_value_heads=shape["value_heads"], linear_key_head_dim=shape["key_dim"],
+                            linear_value_head_dim=shape["value_dim"], linear_conv_kernel_dim=4, num_hidden_layers=1,
+                            layer_types=["linear_attention"], hidden_act="silu", rms_norm_eps=1e-6)
+    torch.manual_seed(0)
+    m = hf.Qwen3_5GatedDeltaNet(cfg, 0).double()
+    with torch.no_grad():
+        for name in ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a", "out_proj"):
+            w, la, lb, s = p[name]
+            getattr(m, name).weight.copy_((w + s * (la @ lb)).T)
+        m.conv1d.weight.copy_(p["conv"].T[:, None, :])
+        m.A_log.copy_(p["a_log"])
+        m.dt_bias.copy_(p["dt_bias"])
+        m.norm.weight.copy_(p["norm"])
+
+    def rule64(query, key, value, g, beta, chunk_size=64, initial_state=None, output_final_state=False,
+               use_qk_l2norm_in_kernel=False, **kw):
+        if use_qk_l2norm_in_kernel:
+            query, key = hf.l2norm(query, dim=-1, eps=1e-6), hf.l2norm(key, dim=-1, eps=1e-6)
+        query = query * query.shape[-1] ** -0.5
+        out, state = O.recurrent_gated_delta_rule(query, key, value, g, beta)
+        return out, (state if output_final_state else None)
+
+    monkeypatch.setattr(hf, "torch_chunk_gated_delta_rule", rule64)
+    xl = x.clone().requires_grad_(True)
+    out = m(xl, attention_mask=(seg > 0).to(F64))
+    (dx,) = torch.autograd.grad((out * cot).sum(), [xl])
+    return out.detach(), dx
+
+
+def _oracle_block(shape, p, x, seg, cot, block=None):
+    kw = {k: v for k, v in shape.items() if k != "hidden"}
+    xl = x.clone().requires_grad_(True)
+    out = (block or O.gdn_block)(xl, seg, p, dtype=F64, chunk=8, **kw)
+    (dx,) = torch.autograd.grad((out * cot).sum(), [xl])
+    return out.detach(), dx
+
+
+def _block_slip(kind):
+    """gdn_block with one plausible slip in its composition (model/gdn.py:126-164 is the order
+    being pinned): the norm's gate taken from the value part of in_proj_qkv instead of
+    in_proj_z; the norm applied after out_proj; the RMS taken over all heads at once (one flat
+    row) instead of per head; the input's padding mask dropped."""
+    def block(x, segment_ids, params, *, key_heads, key_dim, value_heads, value_dim, dtype, chunk):
+        batch, length, _ = x.shape
+        valid = (segment_ids > 0)[..., None]
+        if kind != "input mask dropped":
+            x = torch.where(valid, x, torch.zeros((), dtype=x.dtype))
+        proj = lambda t, n: O.merged_projection(t, *params[n], dtype)  # noqa: E731
+        qkv, z, b, a = (proj(x, n) for n in ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a"))
+        if kind == "gate from in_proj_qkv":
+            z = qkv[..., 2 * key_heads * key_dim:]
+        core = O.reference_core(qkv, a, b, params["a_log"], params["dt_bias"], params["conv"], segment_ids,
+                                key_heads=key_heads, key_dim=key_dim, value_heads=value_heads,
+                                value_dim=value_dim, chunk=chunk, dtype=dtype)
+        zh = z.reshape(batch, length, value_heads, value_dim)
+        if kind == "norm after out_proj":
+            y = proj(core.reshape(batch, length, -1), "out_proj").reshape(batch, length, value_heads, value_dim)
+            y = O.gated_rmsnorm(y, zh, params["norm"]).reshape(batch, length, -1)
+            return torch.where(valid, y, torch.zeros((), dtype=y.dtype))
+        if kind == "one RMS over all heads":
+            flat = core.reshape(batch, length, 1, -1)
+            normed = O.gated_rmsnorm(flat, z.reshape(batch, length, 1, -1), params["norm"].repeat(value_heads))
+        else:
+            normed = O.gated_rmsnorm(core, zh, params["norm"])
+        y = torch.where(valid, normed.reshape(batch, length, -1), torch.zeros((), dtype=dtype))
+        return proj(y, "out_proj")
+    return block
+
+
+def _max_rel(a, b):
+    return float((a - b).abs().max() / b.abs().max())
+
+
+def test_gdn_block_matches_hf_layer(monkeypatch):
+    """The oracle's whole block (``gdn_block``: input mask, merged-LoRA projections, core,
+    per-head gated RMSNorm with gate z, padding select, out_proj; model/gdn.py:126-164) against
+    HF's Qwen3_5GatedDeltaNet layer (an independent implementation of the same layer order)
+    in float64 with the same parameters: output and dx agree to float32 rounding (HF evaluates
+    the norm and e^{A_log} in float32: 1e-7), on a row without padding and on a row whose
+    first three tokens are padding (HF's attention mask)."""
+    shape, p, x, seg, cot = _block_case()
+    hf_out, hf_dx = _hf_block(shape, p, x, seg, cot, monkeypatch)
+    out, dx = _oracle_block(shape, p, x, seg, cot)
+    err = {"out": _max_rel(out, hf_out), "dx": _max_rel(dx, hf_dx)}
+    assert max(err.values()) < 2e-6, err
+    assert torch.all(out[1, :3] == 0) and torch.all(dx[1, :3] == 0)
+
+
+@pytest.mark.parametrize("kind", ["gate from in_proj_qkv", "norm after out_proj", "one RMS over all heads"])
+def test_gdn_block_slips_fail_the_hf_layer(monkeypatch, kind):
+    """Each composition slip, planted in a copy of the block, moves out or dx far beyond the
+    float32 rounding at which the oracle agrees with HF."""
+    shape, p, x, seg, cot = _block_case()
+    hf_out, hf_dx = _hf_block(shape, p, x, seg, cot, monkeypatch)
+    out, dx = _oracle_block(shape, p, x, seg, cot, block=_block_slip(kind))
+    assert max(_max_rel(out, hf_out), _max_rel(dx, hf_dx)) > 1e-2, kind
+
+
+def test_gdn_block_input_mask_is_redundant():
+    """Dropping the block's input mask (gdn.py:126-164 masks x before the projections) changes
+    neither out nor dx: every path from a padding token's x is masked downstream (its conv
+    output by valid, its own output by the padding select, its gates cancel in the decay
+    differences of the segment after it). So that mask cannot be pinned by any comparison of
+    outputs; the HF comparison above pins the rest of the order."""
+    shape, p, x, seg, cot = _block_case()
+    out, dx = _oracle_block(shape, p, x, seg, cot)
+    out2, dx2 = _oracle_block(shape, p, x, seg, cot, block=_block_slip("input mask dropped"))
+    assert _max_rel(out2, out) < 1e-13 and _max_rel(dx2, dx) < 1e-13
+    # the slips' copy of the block without a slip is the oracle's block itself
+    out0, dx0 = _oracle_block(shape, p, x, seg, cot, block=_block_slip("none"))
+    assert torch.equal(out0, out) and torch.equal(dx0, dx)
+
+
 # ------------------------------------------------------------------ decode
 def test_decode_step_continues_the_recurrence():
     """test_gated_delta_rule.py:61-73's continuation on the megakernel's inputs: the token

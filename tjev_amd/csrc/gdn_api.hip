@@ -81,6 +81,12 @@ int validate(const tjev_gdn_params* p) {
   const long w = 2L * p->key_heads * p->key_dim + (long)p->value_heads * p->value_dim;
   if (w > (1L << 30) || (long)p->batch * p->length * w > (1L << 40))
     return fail(TJEV_GDN_EINVAL, "problem too large");
+  // the flat grids: k_prep / k_post launch B * N * (2 Hk + H) workgroups of 256 work-items and
+  // k_bwd_grads B * H * N of 4 C; a launch holds fewer than 2^32 work-items along x
+  const long C = kernel_chunk(p), n = (p->length + C - 1) / C;
+  const long slots = 2L * p->key_heads + p->value_heads;
+  if ((long)p->batch * n * slots * 256 >= (1L << 32) || (long)p->batch * p->value_heads * n * 4 * C >= (1L << 32))
+    return fail(TJEV_GDN_EUNSUPPORTED, "batch * chunks * heads too large for one launch of this build's grids");
   return 0;
 }
 
@@ -351,9 +357,6 @@ int check_state(const tjev_gdn_params* p, const void* initial_state, const void*
     return fail(TJEV_GDN_EINVAL, "the initial state's gradient needs the initial state");
   for (const void* q : {initial_state, initial_conv, d_final, d_initial_state, d_initial_conv})
     if (q && !aligned(q, 16)) return fail(TJEV_GDN_EINVAL, "state tensors must be 16-byte aligned");
-  if (d_final && p->length % kernel_chunk(p))
-    return fail(TJEV_GDN_EUNSUPPORTED, "the final state's gradient needs a length that is a multiple of the chunk (" +
-                                           std::to_string(kernel_chunk(p)) + ")");
   return 0;
 }
 
@@ -627,7 +630,9 @@ static int mega2_bwd(const tjev_gdn_params* p, void* stream, const void* qkv, co
   A.d_final = d_final_state;
   A.d_init_state = d_initial_state;
   A.d_init_conv = d_initial_conv;
-  if (int s = poison_buffers(p, stream, workspace, nullptr, 1)) return s;
+  // the poison mode fills the whole workspace: with the norm, its d out and weight partials too
+  if (poison_on())
+    if (int s = poison(workspace, need, stream)) return s;
   if (!nb) return run(p, stream, A, 1);
   // the norm's backward into d out, then the megakernel's, on the caller's stream
   np.eps = nb->eps;

@@ -426,7 +426,7 @@ __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
 #pragma unroll
     for (int i = 0; i < RG; ++i) {
       const int r = r0 + i, t = n * C + r;
-      const int st = t < A.T ? sgv[HW + i] : 0;  // the padded tail: segment 0
+      const int st = t < A.T ? sgv[HW + i] : 0;  // the padded tail: no activation
       float act[8];
       if (A.taps == 0) {  // mega1: qkv is already the activation (zero on the tail)
 #pragma unroll
@@ -459,10 +459,10 @@ __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
       o[1] = make_float4(act[4], act[5], act[6], act[7]);
     }
   }
-  if (slot == 0) {
+  if (slot == 0) {  // the padded tail takes the last token's id (edge mode, xla.py:198-204)
     for (int i = threadIdx.x; i < C; i += 256) {
       const int t = n * C + i;
-      A.segp[(size_t)b * A.Tp + t] = t < A.T ? sg[t] : 0;
+      A.segp[(size_t)b * A.Tp + t] = sg[t < A.T ? t : A.T - 1];
     }
   }
   if (kind == 2 && threadIdx.x < 64) {  // gates of value head `head` (pallas_tpu_mega.py:106-127)
@@ -480,9 +480,9 @@ __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
       const bool in = i < C && t < A.T;
       const float av = in ? ldf(ga + ((size_t)b * A.T + t) * A.H + head) : 0.f;
       const float bv = in ? ldf(gb + ((size_t)b * A.T + t) * A.H + head) : 0.f;
-      run += i < C ? (double)(-alog * softplusf_(av + dtb)) : 0.0;
+      run += in ? (double)(-alog * softplusf_(av + dtb)) : 0.0;  // the padded tail: g = 0, beta = 0
       g[q] = run;  // inclusive within the lane
-      bt[q] = sigmoidf_(bv);
+      bt[q] = in ? sigmoidf_(bv) : 0.f;
     }
     double inc = run;  // inclusive scan of lane totals
 #pragma unroll
@@ -2511,8 +2511,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         const float dav = (float)dad;
         const float bt = sigmoidf_(bv);
         const float dbv = (gdb[q] + sxv[i]) * bt * (1.f - bt);
-        sa += dg * (double)g;
-        sd += dad;
+        // the padded tail's g is the constant 0 (no function of A_log, dt_bias): its dg, which the
+        // final state's gradient makes nonzero, enters neither sum
+        sa += in ? dg * (double)g : 0.0;
+        sd += in ? dad : 0.0;
         if (in) {
           stf(da + ((size_t)b * A.T + t) * A.H + head, dav);
           stf(db + ((size_t)b * A.T + t) * A.H + head, dbv);

@@ -45,7 +45,7 @@ __global__ __launch_bounds__(256) void k_prep_v2(GdnArgs A) {
   if (slot == 0) {
     for (int i = threadIdx.x; i < C; i += 256) {
       const int t = n * C + i;
-      A.segp[(size_t)b * A.Tp + t] = t < A.T ? A.seg[(size_t)b * A.T + t] : 0;
+      A.segp[(size_t)b * A.Tp + t] = A.seg[(size_t)b * A.T + (t < A.T ? t : A.T - 1)];  // edge mode
     }
   }
   if (kind == 2 && threadIdx.x < 64) {  // gamma = in-chunk inclusive cumsum of g (fp64), beta

@@ -337,7 +337,7 @@ def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: t
     reads them), and ``output_final_state`` returns (out, final_state [B, H, Dk, Dv] fp32,
     conv_state [B, K-1, W] or None), the state after token T-1 and the last K-1 raw rows of its
     segment, which the next piece takes as its initial state and history. Gradients flow through
-    all of them (the final state's needs T a multiple of the chunk the kernels run)."""
+    all of them, for any T."""
     batch, length, width = qkv.shape
     taps = _check(precision, inverse, chunk, width, key_heads, key_dim, value_heads, value_dim, heads_per_step,
                   conv_weight)
