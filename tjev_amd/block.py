@@ -25,10 +25,27 @@ from .gdn import gdn_megakernel_normed
 
 
 def _mm32(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    """a @ b accumulated and returned in fp32 (the reference's preferred_element_type=f32)."""
+    """a @ b accumulated and returned in fp32 (the reference's preferred_element_type=f32).
+    Transposed views are read in place (the GEMM's transpose flags), never copied."""
     if a.dtype == torch.float32:
         return a @ b.to(torch.float32)
     return torch.mm(a, b, out_dtype=torch.float32)
+
+
+def _addmm32(c: torch.Tensor, a: torch.Tensor, b: torch.Tensor, alpha: float = 1.0) -> torch.Tensor:
+    """c + alpha a @ b in fp32 (c fp32), the product accumulated in fp32: one GEMM with c as its
+    addend where the backend has the mixed-precision form, else a product and an add."""
+    if a.dtype == torch.float32:
+        return torch.addmm(c, a, b.to(torch.float32), alpha=alpha)
+    if a.is_cuda:
+        return torch.addmm(c, a, b, alpha=alpha, out_dtype=torch.float32)
+    return c + alpha * _mm32(a, b)
+
+
+def _merge(w: torch.Tensor, a: torch.Tensor, b: torch.Tensor, s: float, dtype) -> torch.Tensor:
+    """W' = (W + s A B) rounded once to ``dtype``, A and B rounded to it first and their product
+    accumulated in fp32 (lora.py:284-295, ``_merge``)."""
+    return _addmm32(w.to(torch.float32), a.to(dtype), b.to(dtype), alpha=s).to(dtype)
 
 
 class _MergedLoRA(torch.autograd.Function):
@@ -41,8 +58,7 @@ class _MergedLoRA(torch.autograd.Function):
         n = len(scales)
         ws, a_s, b_s = params[:n], params[n:2 * n], params[2 * n:]
         dtype = x.dtype
-        merged = [(w.to(torch.float32) + s * _mm32(a.to(dtype), b.to(dtype))).to(dtype)
-                  for w, a, b, s in zip(ws, a_s, b_s, scales)]
+        merged = [_merge(w, a, b, s, dtype) for w, a, b, s in zip(ws, a_s, b_s, scales)]
         ys = tuple(x @ m for m in merged)
         ctx.scales = scales
         ctx.save_for_backward(x, *merged, *a_s, *b_s)
@@ -57,17 +73,28 @@ class _MergedLoRA(torch.autograd.Function):
         dtype = x.dtype
         dys = [torch.zeros((x.shape[0], m.shape[1]), dtype=dtype, device=x.device) if dy is None
                else dy.to(dtype).contiguous() for dy, m in zip(dys, merged)]
-        # dx = sum_i dy_i W'_i^T: one product over the concatenated outputs (fp32 accumulation)
-        dx = torch.cat(dys, dim=1) @ torch.cat(merged, dim=1).t().contiguous()
+        # dx = sum_i dy_i W'_i^T, each product and the sum in fp32, rounded once (lora.py:333-338);
+        # W'^T read in place. The narrow projections (b, a) as one product over their joined
+        # outputs (a small copy), the wide ones each with the running sum as its addend.
+        wide = [i for i in range(n) if merged[i].shape[1] >= 256]
+        narrow = [i for i in range(n) if merged[i].shape[1] < 256]
+        dx = None
+        if narrow:
+            dyn = dys[narrow[0]] if len(narrow) == 1 else torch.cat([dys[i] for i in narrow], dim=1)
+            mn = merged[narrow[0]] if len(narrow) == 1 else torch.cat([merged[i] for i in narrow], dim=1)
+            dx = _mm32(dyn, mn.t())
+        for i in wide:
+            dx = _mm32(dys[i], merged[i].t()) if dx is None else _addmm32(dx, dys[i], merged[i].t())
+        dx = dx.to(dtype)
         # the adapters: one pass over x for every A, x^T [s_1 t_1 | s_2 t_2 | ...]
         ranks = [a.shape[1] for a in a_s]
-        xa = x @ torch.cat([a.to(dtype) for a in a_s], dim=1)
-        t = torch.cat([(s * _mm32(dy, b.to(dtype).t().contiguous())).to(dtype)
-                       for dy, b, s in zip(dys, b_s, scales)], dim=1)
-        xt = x.t().contiguous()
-        da = torch.split(_mm32(xt, t), ranks, dim=1)
+        a_cat = a_s[0].to(dtype) if n == 1 else torch.cat([a.to(dtype) for a in a_s], dim=1)
+        xa = x @ a_cat
+        ts = [(s * _mm32(dy, b.to(dtype).t())).to(dtype) for dy, b, s in zip(dys, b_s, scales)]
+        t = ts[0] if n == 1 else torch.cat(ts, dim=1)
+        da = torch.split(_mm32(x.t(), t), ranks, dim=1)
         xas = torch.split(xa, ranks, dim=1)
-        db = [s * _mm32(xai.t().contiguous(), dy) for xai, dy, s in zip(xas, dys, scales)]
+        db = [s * _mm32(xai.t(), dy) for xai, dy, s in zip(xas, dys, scales)]
         return (dx, None, *([None] * n), *[d.to(a.dtype) for d, a in zip(da, a_s)],
                 *[d.to(b.dtype) for d, b in zip(db, b_s)])
 
