@@ -47,6 +47,8 @@ def _args(argv=None):
                          "(tjev_gdn_mega2_fwd_normed / _bwd_normed: the forward in the output kernel)")
     ap.add_argument("--residuals", default="states", choices=("states", "tinv", "all"),
                     help="what the forward keeps for the backward (default: the chunk-boundary states only)")
+    ap.add_argument("--inverse", default="doubling", choices=("doubling", "blocked"),
+                    help="the in-chunk inverse (the reference's default: pure doubling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=0, help="rows of the workload in the CPU baseline (0: all)")
     ap.add_argument("--details", default=None, help="also write the full report to this JSON file")
@@ -159,7 +161,7 @@ def _block_bench(args) -> dict:
     blk = GatedDeltaNetBlock(hidden=hid, key_heads=c["key_heads"], key_dim=c["key_dim"],
                              value_heads=c["value_heads"], value_dim=c["value_dim"], rank=c["rank"],
                              dtype=torch.bfloat16, chunk=c["chunk"], precision=c["precision"],
-                             residuals=args.residuals)
+                             inverse=args.inverse, residuals=args.residuals)
     gen = torch.Generator().manual_seed(21)
     x = torch.randn((B, T, hid), generator=gen).to(torch.bfloat16).cuda().requires_grad_(True)
     seg = torch.ones((B, T), dtype=torch.int32, device="cuda")
@@ -211,7 +213,7 @@ def _block_bench(args) -> dict:
         "config": {"workload": "4B-shaped GDN block fwd+bwd (merged LoRA r64, flat gated RMSNorm)", "batch": B,
                    "seq_len": T, "hidden": hid, "key_heads": Hk, "value_heads": H, "head_dim": Dk, "lora_rank": r,
                    "chunk": c["chunk"], "precision": c["precision"], "segments": "one",
-                   "residuals": args.residuals},
+                   "inverse": args.inverse, "residuals": args.residuals},
         "peak_activation_bytes": peak,
         "roofline": {"kernel": "projections (hipBLASLt GEMMs, merge and glue: the step less the HIP library's kernels)",
                      "bound": "mfma", "achieved": ach, "peak": 2500.0, "unit": "TFLOP/s", "frac": ach / 2500.0,
@@ -334,7 +336,8 @@ def _v2_bench(args) -> dict:
     dy = rn(B, T, H, D).to(torch.bfloat16).cuda()
 
     def step():
-        out = chunk_gated_delta_rule_v2(*leaves, seg, chunk=C, precision="high", residuals=args.residuals)
+        out = chunk_gated_delta_rule_v2(*leaves, seg, chunk=C, precision="high", inverse=args.inverse,
+                                        residuals=args.residuals)
         return torch.autograd.grad(out, leaves, dy)
 
     for _ in range(args.warmup):
@@ -365,7 +368,7 @@ def _v2_bench(args) -> dict:
         "dtype": "bf16", "data": "synthetic",
         "config": {"workload": "0.8B GDN layer core, v2 operator (pre-gated q, k, v, g, beta) fwd+bwd", "batch": B,
                    "seq_len": T, "key_heads": Hk, "value_heads": H, "head_dim": D, "chunk": C, "precision": "high",
-                   "segments": "one", "residuals": args.residuals},
+                   "segments": "one", "inverse": args.inverse, "residuals": args.residuals},
         "roofline": {"kernel": dominant, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
                      "unit": dk["unit"], "frac": dk["frac"], "traffic": None, "hbm_frac": dk["hbm_frac"],
                      "mfma_frac": dk["mfma_frac"]},
@@ -445,7 +448,8 @@ def _layer_bench(args, config: str, cpu: bool = True) -> dict:
     else:
         d_out = d_y
     plan = GdnPlan(batch=B, length=T, key_heads=Hk, key_dim=D, value_heads=H, value_dim=D, taps=w.shape[0],
-                   chunk=C, io_dtype=dtype, gate_dtype=dtype, precision=precision, residuals=args.residuals)
+                   chunk=C, io_dtype=dtype, gate_dtype=dtype, precision=precision, inverse=args.inverse,
+                   residuals=args.residuals)
     ws = torch.empty(max(plan.fwd_bytes, plan.bwd_bytes), dtype=torch.uint8, device=dev)
     out = torch.empty((B, T, H, D), dtype=dtype, device=dev)
     states = plan.residuals(dev)
@@ -515,7 +519,7 @@ def _layer_bench(args, config: str, cpu: bool = True) -> dict:
                    "key_heads": Hk, "value_heads": H, "head_dim": D, "chunk": C, "conv_taps": int(w.shape[0]),
                    "precision": precision, "segments": cfg["segments"],
                    "epilogue": ("gated_rmsnorm (forward in the output kernel)" if fused else "gated_rmsnorm")
-                   if norm else None, "residuals": args.residuals},
+                   if norm else None, "inverse": args.inverse, "residuals": args.residuals},
         "roofline": {"kernel": dominant, "bound": dk["bound"], "achieved": dk["achieved"], "peak": dk["peak"],
                      "unit": dk["unit"], "frac": dk["frac"], "traffic": traffic,
                      "hbm_frac": dk["hbm_frac"], "mfma_frac": dk["mfma_frac"]},

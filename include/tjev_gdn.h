@@ -50,7 +50,9 @@ enum tjev_gdn_precision {
   TJEV_GDN_MIXED = 3
 };
 
-/* the reference's `inverse` (pallas_tpu_v2.py:141) */
+/* the reference's `inverse` (pallas_tpu_v2.py:141-193): (I + L)^-1 of each chunk by the pure
+ * doubling from T = I, every level's products at the intra-chunk precision, or with its 16 x 16
+ * diagonal blocks inverted exactly (forward substitution in fp32) before the doubling levels */
 enum tjev_gdn_inverse { TJEV_GDN_DOUBLING = 0, TJEV_GDN_BLOCKED = 1 };
 
 /* what the forward keeps for the backward (the reference's remat residual contract names

@@ -114,12 +114,20 @@ def doubling_masks(size: int) -> list[np.ndarray]:
     return out
 
 
-def unit_lower_inverse(lower: torch.Tensor, block: int = 0) -> torch.Tensor:
+def unit_lower_inverse(lower: torch.Tensor, block: int = 0, bf16_operands: bool = False) -> torch.Tensor:
     """(I + L)^-1 for strictly lower-triangular L [..., C, C] (C a power of two).
 
     ``block`` 0: recursive doubling from T = I (xla.py:82-100). ``block`` > 1: the exact
     block x block diagonal inverse by forward substitution first, then the remaining
-    doubling levels (pallas_tpu_v2.py:144-193, ``inverse="blocked"``)."""
+    doubling levels (pallas_tpu_v2.py:144-193, ``inverse="blocked"``). ``bf16_operands``: each
+    doubling product's operands rounded to bf16 first, the product accumulated in the input
+    dtype (``mm`` / ``_dot`` at mode "bf16", xla.py:55-62, pallas_tpu_v2.py:88-93)."""
+
+    def mm(a, b):
+        if bf16_operands:
+            a, b = a.to(torch.bfloat16).to(a.dtype), b.to(torch.bfloat16).to(b.dtype)
+        return a @ b
+
     c = lower.shape[-1]
     row = torch.arange(c)[:, None]
     col = torch.arange(c)[None, :]
@@ -141,7 +149,7 @@ def unit_lower_inverse(lower: torch.Tensor, block: int = 0) -> torch.Tensor:
     while s < c:
         mask = ((row // (2 * s)) == (col // (2 * s))) & ((row // s) % 2 == 1) & ((col // s) % 2 == 0)
         off = torch.where(mask, lower, 0.0)
-        tinv = tinv - (tinv @ off) @ tinv
+        tinv = tinv - mm(mm(tinv, off), tinv)
         s *= 2
     return tinv
 

@@ -4,7 +4,9 @@ pallas_tpu_mega.py:444-449, 543-548): what the forward keeps changes no result b
 - "tinv" and "states" give the same output and gradients bit for bit: the forward's T comes
   from the same code as the backward's rebuilt one, and v_new from it by the same code;
 - "all" (v_new from the forward's scan) matches "states" to rounding;
-- the kept T is each chunk's (I + L)^-1: the oracle's ``chunk_tinv`` on the same inputs.
+- the kept T is each chunk's (I + L)^-1: the oracle's ``chunk_tinv`` on the same inputs, under
+  either form of the inverse; the pure doubling's diagonal blocks follow the oracle's doubling
+  at the products' precision, the blocked form's are exact.
 """
 
 from __future__ import annotations
@@ -38,27 +40,88 @@ def test_residual_policies_agree(precision, dtype):
                 assert rel(runs["all"][k], runs["states"][k]) <= 1e-5, k
 
 
-def test_kept_tinv_is_the_chunk_inverse():
-    from oracle.gdn_oracle import chunk_tinv, core_inputs
+def _kept_tinv(inputs, C, precision, inverse):
+    """The forward's kept T [B, H, N, C, C] (residuals "tinv") at the SHAPE heads."""
     from tjev_amd.gdn import GdnPlan
 
-    inputs, _ = case_inputs(1, 200, 2, 4, 64, dtype=torch.float32, seed=4)
     qkv, a, b, a_log, dt_bias, w, seg = (x.cuda().contiguous() for x in inputs)
     B, T, _ = qkv.shape
-    C = 64
     plan = GdnPlan(batch=B, length=T, key_heads=2, key_dim=64, value_heads=4, value_dim=64, taps=w.shape[0],
-                   chunk=C, io_dtype=torch.float32, gate_dtype=torch.float32, precision="highest", residuals="tinv")
+                   chunk=C, io_dtype=torch.float32, gate_dtype=torch.float32, precision=precision,
+                   inverse=inverse, residuals="tinv")
     res = plan.residuals("cuda")
     out = torch.empty((B, T, 4, 64), device="cuda")
     plan.forward(qkv, a, b, a_log, dt_bias, w, seg, out, res, plan.workspace(False, "cuda"))
     torch.cuda.synchronize()
     n = math.ceil(T / C)
     start = (math.prod(plan.states_shape) + 63) // 64 * 64  # the states part, 256-byte aligned
-    got = res[start:start + B * 4 * n * C * C].view(B, 4, n, C, C).double().cpu()
+    return res[start:start + B * 4 * n * C * C].view(B, 4, n, C, C).double().cpu()
+
+
+def _chunk_lower(inputs, C):
+    """L of every chunk [B, H, N, C, C] in fp64 from the oracle."""
+    from oracle.gdn_oracle import _chunk_terms, core_inputs
+
     _, k, _, g, beta, sg = core_inputs(*(x.double() if x.is_floating_point() else x for x in inputs),
                                        key_heads=2, key_dim=64, value_heads=4, value_dim=64, dtype=torch.float64)
+    z = torch.zeros_like(k)
+    return k, g, beta, sg, _chunk_terms(z, k, z, g, beta, sg, None, C)["lower"]
+
+
+@pytest.mark.parametrize("inverse", ["doubling", "blocked"])
+def test_kept_tinv_is_the_chunk_inverse(inverse):
+    from oracle.gdn_oracle import chunk_tinv
+
+    inputs, _ = case_inputs(1, 200, 2, 4, 64, dtype=torch.float32, seed=4)
+    C = 64
+    got = _kept_tinv(inputs, C, "highest", inverse)
+    k, g, beta, sg, _ = _chunk_lower(inputs, C)
     want = chunk_tinv(k, g, beta, sg, chunk=C)
     err = float((got - want).abs().max()) / float(want.abs().max())
-    print(f"kept T vs oracle: max rel {err:.2e}", flush=True)
+    print(f"kept T ({inverse}) vs oracle: max rel {err:.2e}", flush=True)
     assert err <= 1e-5
     assert torch.all(got.triu(1) == 0) and torch.all(got.diagonal(dim1=-2, dim2=-1) == 1)
+
+
+@pytest.mark.parametrize("C", [64, 128])
+def test_doubling_inverse_runs_products_on_the_diagonal_blocks(C):
+    """inverse="doubling" is the reference's pure doubling from T = I (pallas_tpu_v2.py:168-193
+    with no diagonal blocks; xla.py:82-100). With one-pass bf16 products (precision "bf16", L
+    itself then from bf16 k) the 16 x 16 diagonal blocks of its T carry the bf16 products'
+    rounding and follow the oracle's doubling with bf16 operands on that L, where the blocked
+    form's diagonal blocks are its exact inverse (substitution in fp32). Compared by quantiles
+    over the blocks' strictly lower entries: an fp32 difference in k (the kernel's against the
+    oracle's) could move a bf16 rounding now and then. Only the diagonal blocks are compared with
+    the emulation: above 16 the kernels associate each level's product as T_BR (L_LL T_TL),
+    the reference as (T_BR L_LL) T_TL, another bf16 rounding."""
+    from oracle.gdn_oracle import _chunk_terms, core_inputs, unit_lower_inverse
+
+    inputs, _ = case_inputs(1, 2 * C, 2, 4, 64, dtype=torch.float32, seed=6)
+    _, k, _, g, beta, sg = core_inputs(*(x.double() if x.is_floating_point() else x for x in inputs),
+                                       key_heads=2, key_dim=64, value_heads=4, value_dim=64, dtype=torch.float64)
+    z = torch.zeros_like(k)
+    t = _chunk_terms(z, k, z, g, beta, sg, None, C)
+    kb = t["k"].to(torch.bfloat16).double()
+    lower = torch.tril(t["beta"][..., None] * (kb @ kb.transpose(-1, -2)) * t["decay"], -1)  # L from bf16 k
+    exact = torch.linalg.inv(torch.eye(C, dtype=torch.float64) + lower)
+    emulated = unit_lower_inverse(lower.float(), 0, bf16_operands=True).double()
+    strict = torch.tril(torch.ones(16, 16, dtype=torch.bool), -1)
+
+    def entries(x):  # the strictly lower entries of every 16 x 16 diagonal block
+        return torch.cat([x[..., 16 * i:16 * i + 16, 16 * i:16 * i + 16][..., strict].reshape(-1)
+                          for i in range(C // 16)])
+
+    scale = float(entries(exact).abs().max())
+    dbl, blk = (entries(_kept_tinv(inputs, C, "bf16", inv)) for inv in ("doubling", "blocked"))
+    q = torch.tensor([0.5, 0.99], dtype=torch.float64)
+    e_blk = torch.quantile((blk - entries(exact)).abs() / scale, q)
+    e_dbl = torch.quantile((dbl - entries(exact)).abs() / scale, q)
+    e_emu = torch.quantile((dbl - entries(emulated)).abs() / scale, q)
+    print(f"C={C} diagonal blocks (median, 99%): blocked vs exact {e_blk.tolist()}, doubling vs exact "
+          f"{e_dbl.tolist()}, doubling vs the bf16 doubling {e_emu.tolist()}", flush=True)
+    # measured at C = 64: blocked 2.7e-8, doubling 3.9e-4 and against the emulation 0 (bitwise)
+    # at the 99th percentile (many entries are decayed to a few ulps of the scale: the medians
+    # are small for all three)
+    assert float(e_blk[1]) <= 1e-6
+    assert float(e_dbl[1]) >= 1e-5
+    assert float(e_emu[0]) <= 1e-7 and float(e_emu[1]) <= 1e-6

@@ -126,6 +126,29 @@ def test_inverse_matches_dense_inverse_correlated_keys(size, block):
     assert float((got - exact).abs().max()) < 1e-9 * float(exact.abs().max())
 
 
+def test_inverse_bf16_operands_round_each_product():
+    """The doubling with bf16 product operands (mode "bf16"): on a lower triangle whose every
+    intermediate is a short dyadic (exact in bf16) it is the exact inverse; on correlated keys
+    it leaves the fp32 doubling by about the bf16 rounding (2^-9 relative), not by 0 and not by
+    more than a few times that."""
+    size = 16
+    lower = torch.zeros((size, size), dtype=torch.float32)
+    for i in range(1, size):
+        lower[i, i - 1] = 0.5  # T[i][j] = (-1/2)^(i-j): one significant bit each
+    exact = torch.linalg.inv(torch.eye(size) + lower)
+    assert torch.equal(O.unit_lower_inverse(lower, 0, bf16_operands=True), exact)
+    rng = np.random.default_rng(5)
+    kk = torch.from_numpy(rng.standard_normal((4, size, 32)).astype(np.float32)) + 2.0
+    kk = kk / kk.norm(dim=-1, keepdim=True)
+    lower = torch.tril(0.9 * kk @ kk.transpose(-1, -2), -1)
+    plain = O.unit_lower_inverse(lower, 0)
+    rounded = O.unit_lower_inverse(lower, 0, bf16_operands=True)
+    err = float((rounded - plain).abs().max()) / float(plain.abs().max())
+    assert 2.0 ** -12 < err < 2.0 ** -5, err
+    blocked = O.unit_lower_inverse(lower, 16, bf16_operands=True)  # one block: substitution only
+    assert float((blocked - plain).abs().max()) < 1e-5 * float(plain.abs().max())
+
+
 # ------------------------------------------------------------------ l2norm, conv, norms
 def test_l2norm_known_answer():
     """test_gated_delta_rule.py:172-183: a zero row maps to 0 with zero gradient; elsewhere the

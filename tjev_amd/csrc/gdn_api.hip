@@ -219,6 +219,7 @@ gdn::GdnArgs base_args(const tjev_gdn_params* p, void* ws, const Layout& L) {
   A.pd = at<double>(ws, L.pd);
   A.dwp = at<float>(ws, L.dwp);
   A.res = p->residuals;
+  A.inv = p->inverse;
   return A;
 }
 

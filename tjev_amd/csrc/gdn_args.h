@@ -11,6 +11,7 @@ struct GdnArgs {
   int ntiles;  // Dv tiles of the scans
   int parts;   // chunk ranges per (row, head, tile) of the scans, split where a segment resets
   int res;     // residuals kept by the forward: 0 states, 1 and T, 2 and v_new
+  int inv;     // the in-chunk inverse: 0 pure doubling, 1 diagonal blocks by substitution + doubling
   float scale; // Dk^-1/2
   // inputs
   const void* qkv;

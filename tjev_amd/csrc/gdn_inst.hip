@@ -54,12 +54,15 @@ namespace gdn {
 constexpr int kDVT = GDN_D < 32 ? GDN_D : 32;
 #define GDN_EACH_PAIR(M) M(P_F32, P_F32) M(P_BF16X3, P_BF16X3) M(P_BF16, P_BF16) M(P_BF16X3, P_BF16)
 #define GDN_EACH_IO(M, PI, PS) M(PI, PS, float) M(PI, PS, uint16_t)
-// part 1: k_chunk, its four modes
-#define GDN_CHUNK(PI, PS)                                                  \
-  GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 0>(GdnArgs);      \
-  GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 1>(GdnArgs);      \
-  GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 2>(GdnArgs);      \
-  GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 3>(GdnArgs);
+// part 1: k_chunk, its four modes (the three that invert with either form of the inverse)
+#define GDN_CHUNK_INV(PI, PS, DBL)                                             \
+  GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 0, DBL>(GdnArgs);     \
+  GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 1, DBL>(GdnArgs);     \
+  GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 2, DBL>(GdnArgs);
+#define GDN_CHUNK(PI, PS)          \
+  GDN_CHUNK_INV(PI, PS, true)      \
+  GDN_CHUNK_INV(PI, PS, false)     \
+  GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 3, false>(GdnArgs);
 GDN_EACH_PAIR(GDN_CHUNK)
 // part 2: the scans
 #define GDN_SCAN_BWD(PI, PS, TIO) GDN_KW_2 __global__ void k_scan_bwd<GDN_C, GDN_D, kDVT, PI, PS, TIO>(GdnArgs);
@@ -136,9 +139,11 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
     if (A.taps <= 4) GDN_LAUNCH(K_PREP_FWD, (k_prep<C, D, TIO, TG, 3>), prep, dim3(256));
     else GDN_LAUNCH(K_PREP_FWD, (k_prep<C, D, TIO, TG, 4>), prep, dim3(256));
     if (A.res == 0) {
-      GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0>), persist, dim3(C * 4));
+      if (A.inv == 0) GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0, true>), persist, dim3(C * 4));
+      else GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0, false>), persist, dim3(C * 4));
     } else {  // T kept for the backward
-      GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 2>), persist, dim3(C * 4));
+      if (A.inv == 0) GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 2, true>), persist, dim3(C * 4));
+      else GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 2, false>), persist, dim3(C * 4));
     }
     if constexpr (C == 128 && D == 128) GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd_split<PI, PS>), tiles, dim3(512));
     else GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd<C, D, DVT, PI, PS>), tiles, dim3(NS));
@@ -151,9 +156,10 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
     if (A.taps <= 4) GDN_LAUNCH(K_PREP_BWD, (k_prep<C, D, TIO, TG, 3>), prep, dim3(256));
     else GDN_LAUNCH(K_PREP_BWD, (k_prep<C, D, TIO, TG, 4>), prep, dim3(256));
     if (A.res == 0) {  // T and v_new rebuilt
-      GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 1>), persist, dim3(C * 4));
+      if (A.inv == 0) GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 1, true>), persist, dim3(C * 4));
+      else GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 1, false>), persist, dim3(C * 4));
     } else if (A.res == 1) {  // v_new from the saved T
-      GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 3>), persist, dim3(C * 4));
+      GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 3, false>), persist, dim3(C * 4));
     }  // else both saved
     GDN_LAUNCH(K_BWD_LOCAL, (k_bwd_local<C, D, PI, TIO>), persist, dim3(C * 4));
     GDN_LAUNCH(K_SCAN_BWD, (k_scan_bwd<C, D, DVT, PI, PS, TIO>), tiles, dim3(NS));
@@ -200,9 +206,11 @@ hipError_t run_v2(const GdnArgs& A, hipStream_t st, int backward, const Timer* t
   if (!backward) {
     GDN_LAUNCH(K_PREP_FWD, (k_prep_v2<C, D, TIO, TQK, TG>), ends, dim3(256));
     if (A.res == 0) {
-      GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0>), persist, dim3(C * 4));
+      if (A.inv == 0) GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0, true>), persist, dim3(C * 4));
+      else GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0, false>), persist, dim3(C * 4));
     } else {
-      GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 2>), persist, dim3(C * 4));
+      if (A.inv == 0) GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 2, true>), persist, dim3(C * 4));
+      else GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 2, false>), persist, dim3(C * 4));
     }
     if constexpr (C == 128 && D == 128) GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd_split<PI, PS>), tiles, dim3(512));
     else GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd<C, D, DVT, PI, PS>), tiles, dim3(NS));
@@ -211,9 +219,10 @@ hipError_t run_v2(const GdnArgs& A, hipStream_t st, int backward, const Timer* t
   } else {
     GDN_LAUNCH(K_PREP_BWD, (k_prep_v2<C, D, TIO, TQK, TG>), ends, dim3(256));
     if (A.res == 0) {
-      GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 1>), persist, dim3(C * 4));
+      if (A.inv == 0) GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 1, true>), persist, dim3(C * 4));
+      else GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 1, false>), persist, dim3(C * 4));
     } else if (A.res == 1) {
-      GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 3>), persist, dim3(C * 4));
+      GDN_LAUNCH(K_CHUNK_BWD, (k_chunk<C, D, PI, PS, 3, false>), persist, dim3(C * 4));
     }
     GDN_LAUNCH(K_BWD_LOCAL, (k_bwd_local<C, D, PI, TIO>), persist, dim3(C * 4));
     GDN_LAUNCH(K_SCAN_BWD, (k_scan_bwd<C, D, DVT, PI, PS, TIO>), tiles, dim3(NS));

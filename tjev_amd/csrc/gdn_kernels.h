@@ -256,10 +256,12 @@ struct UnitIx {
 };
 
 // ---------------------------------------------------------------- inverse
-// (I + L)^-1 in place for the strictly lower-triangular L in sT (C x C, row stride LT):
-// exact 16x16 diagonal blocks by forward substitution (one wave per block, on the VALU),
-// then doubling levels s = 16 .. C/2 on MFMA, T_LL = -T_BR (L_LL T_TL) (pallas_tpu_v2.py:144-193;
-// xla.py:82-100). sTT (C x LT floats) keeps T transposed as it is built, so the right
+// (I + L)^-1 in place for the strictly lower-triangular L in sT (C x C, row stride LT): the
+// 16x16 diagonal blocks first (one wave per block), then doubling levels s = 16 .. C/2 on
+// MFMA, T_LL = -T_BR (L_LL T_TL) (pallas_tpu_v2.py:144-193; xla.py:82-100). The diagonal
+// blocks either by the doubling levels s = 1, 2, 4, 8 from T = I at the products' precision
+// (inverse "doubling": the whole inverse is the pure doubling) or exactly by forward
+// substitution on the VALU (inverse "blocked"). sTT (C x LT floats) keeps T transposed as it is built, so the right
 // operand T_TL is read by rows. A level's product L_LL T_TL is kept transposed in the pair's
 // upper-right block of sT (unused by a lower-triangular T) and read by rows in turn. Products
 // with a triangular operand run over whole 32-wide contraction steps, so they read the upper
@@ -316,10 +318,79 @@ __device__ __forceinline__ void doubling_level(float* sT, float* sTT, int LT) {
   }
 }
 
+// One 16 x 16 x 16 product at precision P of tiles held at the accumulator layout (lane l: rows
+// 4 (l / 16) + e, column l % 16): a[e] = A(l % 16, 4 (l / 16) + e), b[e] = B(4 (l / 16) + e, l % 16).
+// A tile X at that layout is thus both the B operand X and the A operand X^T. The contraction's
+// 16 values fill the first four of each lane group's eight slots of a 32-deep step; the rest
+// are zero.
+template <int P>
+__device__ __forceinline__ f32x4 mma16(const float (&a)[4], const float (&b)[4]) {
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (P == P_F32) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], acc, 0, 0, 0);
+  } else {
+    const float xa[8] = {a[0], a[1], a[2], a[3], 0.f, 0.f, 0.f, 0.f};
+    const float xb[8] = {b[0], b[1], b[2], b[3], 0.f, 0.f, 0.f, 0.f};
+    mma<P>(acc, make_frag<a_prec<P>()>(xa), make_frag<b_prec<P>()>(xb));
+  }
+  return acc;
+}
+
+// (I + L_d)^-1 of one 16 x 16 diagonal block by the doubling levels s = 1, 2, 4, 8 from T = I
+// (xla.py:82-100, pallas_tpu_v2.py:168-193): T <- T - (T off) T, off the lower-left s x s block
+// of every 2s x 2s block of L, each product at precision P and rounded to fp32 as the
+// reference's. lo, t and tt at the accumulator layout (L, T and T^T): P^T = off^T T^T, then
+// Q = P T and Q^T = T^T P^T, every operand already in registers.
+template <int P>
+__device__ __forceinline__ void diag_doubling(const float (&lo)[4], float (&t)[4], float (&tt)[4]) {
+  const int j = lane() & 15, i0 = (lane() >> 4) << 2;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) t[r] = tt[r] = i0 + r == j ? 1.f : 0.f;
+#pragma unroll
+  for (int lv = 0; lv < 4; ++lv) {
+    float off[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = i0 + r;
+      const bool m = (i >> (lv + 1)) == (j >> (lv + 1)) && ((i >> lv) & 1) && !((j >> lv) & 1);
+      off[r] = m ? lo[r] : 0.f;
+    }
+    const f32x4 pv = mma16<P>(off, tt);
+    const float pt[4] = {pv[0], pv[1], pv[2], pv[3]};
+    const f32x4 q = mma16<P>(pt, t);
+    const f32x4 qt = mma16<P>(t, pt);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      t[r] -= q[r];
+      tt[r] -= qt[r];
+    }
+  }
+}
+
 template <int C, int P>
-__device__ __forceinline__ void invert_unit_lower(float* sT, int LT, float* sTT) {
+__device__ __forceinline__ void invert_unit_lower(float* sT, int LT, float* sTT, bool doubling) {
   const int w = wave(), l = lane();
-  if (l < 16) {  // diagonal block w: lane l owns column l, X[i] = e_i - sum_{r<i} L[i][r] X[r]
+  if (doubling) {  // the wave's diagonal block in registers; sT and sTT get T and T^T
+    const int j = l & 15, i0 = (l >> 4) << 2;
+    float* blk = sT + 16 * w * LT + 16 * w;
+    float* blkT = sTT + 16 * w * LT + 16 * w;
+    float lo[4], t[4], tt[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) lo[r] = blk[(i0 + r) * LT + j];
+    diag_doubling<P>(lo, t, tt);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      lds_st(blk + (i0 + r) * LT + j, t[r]);
+      lds_st(blkT + (i0 + r) * LT + j, tt[r]);
+    }
+    if (w % 2 == 1) {  // zeros in sTT's lower 16 x 16 corner of the 32 x 32 diagonal block
+      for (int idx = l; idx < 256; idx += 64) {
+        const int r = idx >> 4, k = idx & 15;
+        sTT[(16 * w + r) * LT + 16 * (w - 1) + k] = 0.f;
+      }
+    }
+  } else if (l < 16) {  // diagonal block w: lane l owns column l, X[i] = e_i - sum_{r<i} L[i][r] X[r]
     const float* blk = sT + 16 * w * LT + 16 * w;
     float x[16];
 #pragma unroll
@@ -954,8 +1025,9 @@ __device__ __forceinline__ void load_tile(float* s, int LD, const float* g) {
 // for k, kbe^T, (v beta)^T, S^T and Y^T (and T^T during the inverse). The next unit's context
 // and k rows are loaded at this unit's start and end; the forward's k (again) and v, and the
 // backward's S and k strip, during the inverse; the backward's v after it (held across the
-// inverse, it would spill).
-template <int C, int D, int PI, int PS, int MODE>
+// inverse, it would spill). DBL: the inverse's diagonal blocks by doubling (else by substitution;
+// a template argument: both forms in one kernel take 17 more VGPRs and spill in MODE 1).
+template <int C, int D, int PI, int PS, int MODE, bool DBL>
 __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
   constexpr bool FWD = MODE == 0 || MODE == 2;  // writes w and u (else v_new)
   constexpr bool LOAD_T = MODE == 3;            // T from the residuals
@@ -1032,7 +1104,7 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
         vc.fetch(A.vv + off, D);
       }
       __syncthreads();
-      invert_unit_lower<C, PI>(sT, LT, reinterpret_cast<float*>(sB));
+      invert_unit_lower<C, PI>(sT, LT, reinterpret_cast<float*>(sB), DBL);
       if constexpr (!FWD) {
         va.fetch(A.vv + off, D, i0);
       }

@@ -139,10 +139,11 @@ def chunk_gated_delta_rule(q, k, v, g, beta, segment_ids=None, initial_state=Non
                            precision: str = "highest", inverse: str = "solve"):
     """The reference's chunked rule with its state I/O (src/tjev/kernels/gated_delta_rule/
     xla.py:170-262): (out [B,T,H,Dv], final_state [B,H,Dk,Dv]) from q, k [B,T,H or Hk,Dk], v,
-    g, beta and an optional initial_state, on the v2 operator's kernels. ``inverse`` "solve"
-    (the reference's triangular solve), "doubling" or "blocked": the kernels' inverse is exact
-    in each case (xla.py:190-195 lists the same three). Unlike xla.py, v keeps its dtype in the
-    output (fp32 inputs give fp32, as there)."""
+    g, beta and an optional initial_state, on the v2 operator's kernels. ``inverse`` (xla.py:190-195
+    lists the same three): "doubling" the pure doubling from T = I at the products' precision,
+    "blocked" exact 16 x 16 diagonal blocks then doubling levels, and "solve" (the reference's
+    triangular solve) runs the blocked form, the kernels' closest to an exact solve. Unlike
+    xla.py, v keeps its dtype in the output (fp32 inputs give fp32, as there)."""
     if inverse not in ("solve", "doubling", "blocked"):
         raise ValueError(f"precision in {PRECISIONS}, inverse in ('solve', 'doubling', 'blocked')")
     if precision not in PRECISIONS:
