@@ -300,6 +300,11 @@ const char* tjev_gdn_last_error(void);
 /* (major << 16) | minor */
 int tjev_gdn_version(void);
 
+/* 1 in the LDS-poison debug build (libtjev_gdn_lds_poison.so: every kernel fills its LDS with NaN
+ * bytes before its own code runs, the counterpart of the reference's interpret-mode run with
+ * uninitialized_memory="nan", tests/kernels/test_gdn_mega.py:161-178), 0 in the library */
+int tjev_gdn_lds_poison(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,7 +5,11 @@ uninitialised scratch read as NaN (tests/kernels/test_gdn_mega.py:161-178):
   and every backward its workspace, with NaN before its kernels run; outputs and gradients are
   then bit for bit those of an ordinary run (and finite), so no kernel reads memory that no
   kernel wrote -- over segment cuts at chunk offsets, padding, GQA, every residual policy, the
-  conv weight's gradient, a continued sequence with its state gradients, and the v2 operator;
+  conv weight's gradient, a continued sequence with its state gradients, the gated RMSNorm
+  path and the v2 operator;
+- poisoned LDS: the same cases through the LDS-poison debug library (libtjev_gdn_lds_poison.so,
+  every kernel fills its LDS arrays with NaN bytes before its own code runs; both forms of the
+  inverse), bit for bit the ordinary library's results: no kernel reads LDS it did not write;
 - NaN inputs: a NaN in one value head's input returns normally (status 0) and stays where the
   recurrence carries it: the other row, the chunks before it and the other heads' outputs are
   finite.
@@ -21,10 +25,22 @@ from gdn_cases import case_inputs, hip_outputs
 pytestmark = pytest.mark.gpu
 
 
-def _both(fn):
-    """fn() without and with the poison mode."""
+POISONS = ["buffers", "lds"]
+
+
+def _both(fn, kind="buffers"):
+    """fn() plainly and under a poison: "buffers" (TJEV_GDN_POISON=1: the workspace and residual
+    buffers filled with NaN before the kernels run) or "lds" (the calls go through the LDS-poison
+    debug library, whose kernels fill their LDS with NaN before their own code runs)."""
+    from tjev_amd import _lib
+
     os.environ.pop("TJEV_GDN_POISON", None)
     plain = fn()
+    if kind == "lds":
+        with _lib.library(_lib.LDS_POISON_PATH) as lib:
+            assert lib.tjev_gdn_lds_poison() == 1
+            poisoned = fn()
+        return plain, poisoned
     os.environ["TJEV_GDN_POISON"] = "1"
     try:
         poisoned = fn()
@@ -48,21 +64,24 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("kind", POISONS)
 @pytest.mark.parametrize("case", CASES, ids=[f"D{c[0][4]}-C{c[1]}-{c[4]}-{c[5]}" for c in CASES])
 @pytest.mark.parametrize("conv", [True, False], ids=["mega2", "mega1"])
-def test_poisoned_buffers_change_nothing(case, conv):
+def test_poisoned_buffers_change_nothing(case, conv, kind):
     (b, t, hk, h, d), chunk, cuts, dtype, precision, residuals = case
     inputs, cot = case_inputs(b, t, hk, h, d, cuts=cuts, dtype=dtype, style="baseline" if d == 128 else "reference")
     shape = dict(key_heads=hk, key_dim=d, value_heads=h, value_dim=d, conv=conv)
-    print(f"poison {case} conv={conv}", flush=True)
-    plain, poisoned = _both(lambda: hip_outputs(inputs, cot, chunk=chunk, precision=precision, residuals=residuals,
-                                                **shape))
-    _same(plain, poisoned, case)
+    print(f"poison {kind} {case} conv={conv}", flush=True)
+    for inverse in ("doubling", "blocked") if kind == "lds" else ("doubling",):
+        plain, poisoned = _both(lambda: hip_outputs(inputs, cot, chunk=chunk, precision=precision,
+                                                    residuals=residuals, inverse=inverse, **shape), kind)
+        _same(plain, poisoned, (case, inverse))
 
 
-def test_poisoned_buffers_continued_sequence_and_v2():
+@pytest.mark.parametrize("kind", POISONS)
+def test_poisoned_buffers_continued_sequence_and_v2(kind):
     """The _cont entry points (an initial state and conv history, the final state's gradient)
-    and the v2 operator under the poison mode."""
+    and the v2 operator under the poison modes."""
     from tjev_amd import gdn_megakernel
     from tjev_amd.v2 import chunk_gated_delta_rule
 
@@ -82,7 +101,7 @@ def test_poisoned_buffers_continued_sequence_and_v2():
         return {"out": out.detach(), "final": fin.detach(), "conv": cs.detach(),
                 **{f"d{i}": g for i, g in enumerate(grads)}}
 
-    _same(*_both(mega), "megakernel continued")
+    _same(*_both(mega, kind), "megakernel continued")
 
     def v2():
         g = torch.Generator().manual_seed(4)
@@ -94,7 +113,7 @@ def test_poisoned_buffers_continued_sequence_and_v2():
         grads = torch.autograd.grad((out * cot.cuda()).sum() + (fin * d_final).sum(), [q, k, v, gg, be, s0])
         return {"out": out.detach(), "final": fin.detach(), **{f"d{i}": x for i, x in enumerate(grads)}}
 
-    _same(*_both(v2), "v2 with a state")
+    _same(*_both(v2, kind), "v2 with a state")
 
 
 def test_nan_input_stays_where_the_recurrence_carries_it():
@@ -120,8 +139,9 @@ def test_nan_input_stays_where_the_recurrence_carries_it():
         assert torch.isfinite(g[1].cpu()).all()               # the other row's gradients
 
 
+@pytest.mark.parametrize("kind", POISONS)
 @pytest.mark.parametrize("weight_grad", [False, True], ids=["frozen-weight", "weight-grad"])
-def test_poisoned_buffers_normed_path(weight_grad):
+def test_poisoned_buffers_normed_path(weight_grad, kind):
     """The core with its gated RMSNorm (tjev_gdn_mega2_fwd_normed / _bwd_normed, the bench's and
     the block's path) under the poison mode: the backward's whole workspace is poisoned, the
     norm's d out and weight partials after the megakernel's part included."""
@@ -132,7 +152,7 @@ def test_poisoned_buffers_normed_path(weight_grad):
     gen = torch.Generator().manual_seed(6)
     z = torch.randn((1, 400, 4, 128), generator=gen).to(torch.bfloat16)
     nw = 1 + 0.1 * torch.randn(128, generator=gen)
-    print(f"poison normed weight_grad={weight_grad}", flush=True)
+    print(f"poison {kind} normed weight_grad={weight_grad}", flush=True)
 
     def run():
         leaves = [x.cuda().requires_grad_(x.is_floating_point()) for x in (qkv, a, b, a_log, dt_bias, z)]
@@ -142,4 +162,4 @@ def test_poisoned_buffers_normed_path(weight_grad):
         grads = torch.autograd.grad((y.float() * cot.cuda()).sum(), leaves + ([wt] if weight_grad else []))
         return {"y": y.detach(), **{f"d{i}": g for i, g in enumerate(grads)}}
 
-    _same(*_both(run), f"normed weight_grad={weight_grad}")
+    _same(*_both(run, kind), f"normed weight_grad={weight_grad}")

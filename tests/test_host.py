@@ -29,10 +29,21 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert lib.tjev_gdn_version() >> 16 == 0
+    assert lib.tjev_gdn_lds_poison() == 0
     assert lib.tjev_gdn_kernel_name(0) == b"gdn_prep_fwd"
     text = (ROOT / "include" / "tjev_gdn.h").read_text()
     m = re.search(r"#define TJEV_GDN_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
     assert m and int(m.group(1)) << int(m.group(2)) == _lib.SCRATCH_BYTES
+
+
+def test_lds_poison_library_exports_the_same_symbols():
+    """The LDS-poison debug build: the same ABI, and it says what it is."""
+    from tjev_amd import _lib
+
+    lib = _lib.open_library(_lib.LDS_POISON_PATH)
+    for name in _lib.EXPORTS:
+        assert hasattr(lib, name), name
+    assert lib.tjev_gdn_lds_poison() == 1
 
 
 def _params(**kw):

@@ -7,12 +7,15 @@ torch is imported first so that the library shares torch's HIP runtime (same son
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from pathlib import Path
 
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = Path(__file__).resolve().parent / "libtjev_gdn.so"
+# the debug build whose kernels first fill their LDS with NaN (python -m tjev_amd.build --lds-poison)
+LDS_POISON_PATH = Path(__file__).resolve().parent / "libtjev_gdn_lds_poison.so"
 
 F32, BF16 = 0, 1
 PRECISION = {"highest": 0, "high": 1, "bf16": 2, "mixed": 3}
@@ -47,6 +50,7 @@ EXPORTS = (
     "tjev_gdn_kernel_name",
     "tjev_gdn_last_error",
     "tjev_gdn_version",
+    "tjev_gdn_lds_poison",
 )
 N_KERNELS = 16  # TJEV_GDN_KERNELS
 SCRATCH_BYTES = 128 << 20  # TJEV_GDN_SCRATCH_BYTES
@@ -79,14 +83,38 @@ class GdnLibraryError(RuntimeError):
 _LIB: ctypes.CDLL | None = None
 
 
+_OPENED: dict[str, ctypes.CDLL] = {}
+
+
 def load() -> ctypes.CDLL:
     """The loaded library (raises if it is not built)."""
     global _LIB
-    if _LIB is not None:
-        return _LIB
-    if not LIB_PATH.exists():
-        raise RuntimeError(f"{LIB_PATH} is not built: run `python -m tjev_amd.build` (hipcc, gfx950)")
-    lib = ctypes.CDLL(str(LIB_PATH))
+    if _LIB is None:
+        _LIB = open_library(LIB_PATH)
+    return _LIB
+
+
+@contextlib.contextmanager
+def library(path: Path):
+    """Every call made inside the block (plans built inside it) goes through the library at
+    ``path``: the LDS-poison debug build in its tests. The default library comes back after."""
+    global _LIB
+    saved = _LIB
+    _LIB = open_library(path)
+    try:
+        yield _LIB
+    finally:
+        _LIB = saved
+
+
+def open_library(path: Path) -> ctypes.CDLL:
+    """The library at ``path`` with the ABI's argument types bound (opened once per path)."""
+    key = str(path)
+    if key in _OPENED:
+        return _OPENED[key]
+    if not Path(path).exists():
+        raise RuntimeError(f"{path} is not built: run `python -m tjev_amd.build` (hipcc, gfx950)")
+    lib = ctypes.CDLL(key)
     vp, sz, i32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
     pp = ctypes.POINTER(Params)
     lib.tjev_gdn_check.argtypes = [pp]
@@ -142,7 +170,9 @@ def load() -> ctypes.CDLL:
     lib.tjev_gdn_last_error.restype = ctypes.c_char_p
     lib.tjev_gdn_version.argtypes = []
     lib.tjev_gdn_version.restype = i32
-    _LIB = lib
+    lib.tjev_gdn_lds_poison.argtypes = []
+    lib.tjev_gdn_lds_poison.restype = i32
+    _OPENED[key] = lib
     return lib
 
 

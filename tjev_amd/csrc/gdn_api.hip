@@ -721,4 +721,12 @@ const char* tjev_gdn_last_error(void) { return g_error.c_str(); }
 
 int tjev_gdn_version(void) { return (0 << 16) | 1; }
 
+int tjev_gdn_lds_poison(void) {
+#ifdef GDN_LDS_POISON
+  return 1;
+#else
+  return 0;
+#endif
+}
+
 }  // extern "C"

@@ -56,6 +56,29 @@ __device__ __forceinline__ int wave_strip() {
   return __builtin_amdgcn_readfirstlane(PAIR && NW == 8 && w >= 4 ? 11 - w : w);
 }
 
+// ---------------------------------------------------------------- debug: poisoned LDS
+// Built with -DGDN_LDS_POISON (the debug library libtjev_gdn_lds_poison.so), every kernel first
+// fills each LDS array it declares with all-ones bytes (NaN as fp32 and as bf16, -1 as an int)
+// and synchronises, so a read of LDS that the kernel did not write carries NaN into its results
+// (the reference's interpret-mode run with uninitialized_memory="nan", pallas_tpu.py:209-219).
+// Without the flag the macro is empty.
+#ifdef GDN_LDS_POISON
+__device__ __forceinline__ void poison_bytes(void* p, unsigned n) {
+  uint32_t* w = static_cast<uint32_t*>(p);
+  for (unsigned i = threadIdx.x; i < n / 4; i += blockDim.x) w[i] = 0xffffffffu;
+  unsigned char* c = static_cast<unsigned char*>(p);
+  for (unsigned i = n / 4 * 4 + threadIdx.x; i < n; i += blockDim.x) c[i] = 0xff;
+}
+template <class... Ts>
+__device__ __forceinline__ void poison_lds(Ts&... xs) {
+  (poison_bytes(static_cast<void*>(&xs), (unsigned)sizeof(xs)), ...);
+  __syncthreads();
+}
+#define GDN_POISON_LDS(...) ::gdn::poison_lds(__VA_ARGS__)
+#else
+#define GDN_POISON_LDS(...) ((void)0)
+#endif
+
 // ---------------------------------------------------------------- bf16 storage
 // bf16 tensors are held as uint16_t; conversion rounds to nearest even (as torch does).
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }

@@ -1040,6 +1040,7 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
   __shared__ __align__(16) float sT[C * LT];
   __shared__ __align__(16) char sB[RB];
   __shared__ Ctx<C> cx;
+  GDN_POISON_LDS(sT, sB, cx);
   const int w = wave(), i0 = 16 * w;
   const Op<PI> ob = TB::at(sB);
   const int total = A.B * A.H * A.N;
@@ -1267,6 +1268,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
   __shared__ __align__(16) char sV[TV::BYTES];
   const Op<PI> os = TS::at(sS), ok = TK::at(sK), ov = TV::at(sV);
   __shared__ int red[NW];
+  GDN_POISON_LDS(sS, sK, sV, red);
   const ScanIx ix(A);
   const int tile = ix.tile, bh = ix.bh, part = ix.part;
   const int h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
@@ -1423,6 +1425,7 @@ __global__ __launch_bounds__(512) void k_scan_fwd_split(GdnArgs A) {
   __shared__ __align__(16) float skws[2][C];    // kws per token, by chunk parity
   __shared__ float scarry[2];
   __shared__ int red[NT / 64];
+  GDN_POISON_LDS(sW, sK, sU, skws, scarry, red);
   const Op<PI> ow = TW::at(sW), okt = TK::at(sK);
   const ScanIx ix(A);
   const int tile = ix.tile, bh = ix.bh, part = ix.part;
@@ -1625,6 +1628,7 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
   __shared__ __align__(16) char sB[TB::BYTES];
   __shared__ Ctx<C> cx;
   __shared__ __align__(16) float snw[NORM ? D : 1];  // the norm's weight
+  GDN_POISON_LDS(sI, sB, cx, snw);
   if constexpr (NORM) {
     for (int c = threadIdx.x; c < D; c += NT) snw[c] = A.nw[c];
   }
@@ -1741,6 +1745,7 @@ __global__ __launch_bounds__(256) void k_final_state(GdnArgs A) {
   __shared__ float sk[C * D];
   __shared__ float sv[C * DT];
   __shared__ float sw[C];
+  GDN_POISON_LDS(sk, sv, sw);
   const int tile = blockIdx.x % NTL, bh = blockIdx.x / NTL, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
   const int last = A.T - 1, nl = last / C, t0 = nl * C, cnt = last - t0 + 1;
   const size_t tb = (size_t)b * A.Tp, th = (size_t)bh * A.Tp;
@@ -1841,6 +1846,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
   __shared__ float sA[C * LA];
   __shared__ __align__(16) char sB[TB::BYTES];
   __shared__ Ctx<C> cx;
+  GDN_POISON_LDS(sA, sB, cx);
   const Op<PI> ob = TB::at(sB);
   const int ws = wave_strip<C / 16, true>();
   const int total = A.B * A.H * A.N;
@@ -1971,6 +1977,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
   __shared__ float red[NW];
   __shared__ int red_i[NW];
   __shared__ float sgate[2][3][C];  // per chunk parity: grow, -beta grow, the carry (written by wave 0)
+  GDN_POISON_LDS(sG, sQ, sDo, sX, red, red_i, sgate);
   const Op<PI> og = TG_::at(sG), oq = TQ::at(sQ), odo = TD::at(sDo), ox = TD::at(sX);
   const ScanIx ix(A);
   const int tile = ix.tile, bh = ix.bh, part = ix.part;
@@ -2122,6 +2129,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
   __shared__ Ctx<C> cx;
   __shared__ float sga[C], sgf[C], sgb[C];  // a, f and d beta per token
   __shared__ float sxc[TC * C];             // per wave: its rows' share of x_t for the tokens t of its tiles
+  GDN_POISON_LDS(sA, sB, cx, sga, sgf, sgb, sxc);
   const Op<PI> ob = TB::at(sB);
   const int id = blockIdx.x;
   const int n = id % A.N, bh = id / A.N, h = bh % A.H, b = bh / A.H, hk = h / A.ratio;
@@ -2317,6 +2325,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   __shared__ int shs[NG * HS];                  // and their segment ids
   __shared__ float sxv[C];                      // value heads: rows(X, v) of the chunk's tokens
   __shared__ float sdw[DW ? 4 * NL * D : 1];    // per-wave sums of d(conv w)
+  GDN_POISON_LDS(shd, shs, sxv, sdw);
   const int slots = 2 * A.Hk + A.H, bn = blockIdx.x / slots;
   const int b = bn / A.N, n = bn % A.N;
   const int slot = blockIdx.x % slots;
@@ -2612,6 +2621,7 @@ __global__ __launch_bounds__(256) void k_reduce(GdnArgs A) {
   const int bn = A.B * A.N;
   if ((int)blockIdx.x < A.H) {
     __shared__ double ra[256], rd[256];
+    GDN_POISON_LDS(ra, rd);
     const int h = blockIdx.x;
     double sa = 0.0, sd = 0.0;
     for (int q = threadIdx.x; q < bn; q += 256) {
