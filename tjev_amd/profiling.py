@@ -53,8 +53,8 @@ class _Namer:
         if "k_prep<" in symbol:
             self.preps += 1
             return "gdn_prep_fwd" if self.preps % 2 else "gdn_prep_bwd"
-        m = re.search(r"k_chunk<.*,\s*(\d)>", symbol)
-        if m:  # modes 0 and 2 run in the forward, 1 and 3 in the backward
+        m = re.search(r"k_chunk<(?:[^,<>]+,\s*){4}(\d)\s*[,>]", symbol)
+        if m:  # k_chunk<C, D, PI, PS, MODE, inverse form>: modes 0 and 2 run in the forward, 1 and 3 in the backward
             return "gdn_chunk_fwd" if m.group(1) in "02" else "gdn_chunk_bwd"
         return symbol
 
