@@ -16,12 +16,15 @@
  *   conv_w     [K, 2*Hk*Dk + H*Dv]     fp32       (K = taps; ignored when taps == 0)
  *   seg        [B, T] int32            segment ids, 0 = padding
  *   out        [B, T, H, Dv]           io_dtype
- *   residuals  fp32, tjev_gdn_residual_bytes(p) bytes, the forward's output for the backward,
+ *   residuals  tjev_gdn_residual_bytes(p) bytes, the forward's output for the backward,
  *              each part 256-byte aligned, in this order:
- *                states [B, H, ceil(T/C), Dk, Dv]  the state before each chunk (gdn_states)
- *                tinv   [B, H, ceil(T/C), C, C]    (I + L)^-1 of each chunk (gdn_tinv), when
+ *                states [B, H, ceil(T/C), Dk, Dv]  the state before each chunk (gdn_states):
+ *                                                   fp32, or bf16 under TJEV_GDN_MIXED and
+ *                                                   TJEV_GDN_ONE_PASS_BF16 (the reference's
+ *                                                   _state_dtypes, pallas_tpu_mega.py:425-426)
+ *                tinv   [B, H, ceil(T/C), C, C]    fp32 (I + L)^-1 of each chunk (gdn_tinv), when
  *                                                   residuals >= TJEV_GDN_SAVE_TINV
- *                v_new  [B, H, ceil(T/C)*C, Dv]    u - w S of each token, when
+ *                v_new  [B, H, ceil(T/C)*C, Dv]    fp32 u - w S of each token, when
  *                                                   residuals == TJEV_GDN_SAVE_ALL
  *              (C: the chunk the kernels run, max(chunk, 16))
  * T need not be a multiple of the chunk: the kernels pad the tail with zero q, k, v and beta,

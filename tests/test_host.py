@@ -99,7 +99,18 @@ def test_c_abi_sizes():
         assert lib.tjev_gdn_states_bytes(ctypes.byref(p)) == part
     assert lib.tjev_gdn_workspace_bytes(ctypes.byref(p), 0) == fwd - part
     assert lib.tjev_gdn_workspace_bytes(ctypes.byref(p), 1) == bwd - 2 * part
-    # a ragged T is padded to whole chunks (segment-0 padding, as the reference pads)
+    # "mixed" and "bf16" keep the states in bf16 (the reference's _state_dtypes) and the forward
+    # workspace an fp32 copy of each row's state before its last chunk (the final state's source)
+    for precision in (2, 3):
+        q = _params(batch=4, length=4096, key_heads=16, key_dim=128, value_heads=16, value_dim=128, chunk=128,
+                    io_dtype=1, gate_dtype=1, precision=precision)
+        assert lib.tjev_gdn_states_bytes(ctypes.byref(q)) == part // 2
+        assert lib.tjev_gdn_residual_bytes(ctypes.byref(q)) == part // 2
+        assert lib.tjev_gdn_workspace_bytes(ctypes.byref(q), 0) == fwd + 4 * 16 * 128 * 128 * 4
+        assert lib.tjev_gdn_workspace_bytes(ctypes.byref(q), 1) == bwd
+        q.residuals = 1  # T stays fp32 after the bf16 states (256-byte aligned)
+        assert lib.tjev_gdn_residual_bytes(ctypes.byref(q)) == part // 2 + part
+    # a ragged T is padded to whole chunks (the last segment's id carried over, as the reference pads)
     p = _params(length=100, chunk=16)
     assert lib.tjev_gdn_states_bytes(ctypes.byref(p)) == 1 * 4 * 7 * 16 * 16 * 4
 

@@ -91,12 +91,18 @@ int validate(const tjev_gdn_params* p) {
 }
 
 struct Layout {
-  size_t segp, qn, kn, vv, gam, gaml, bet, uu, ww, vnew, tt, qk, xl, kt, gg, gsp, dqh, dkh, dgam, dkws, dcross, dbet, pa, pd,
-      dwp;
+  size_t segp, qn, kn, vv, gam, gaml, bet, uu, ww, vnew, s_last, tt, qk, xl, kt, gg, gsp, dqh, dkh, dgam, dkws, dcross,
+      dbet, pa, pd, dwp;
   size_t total;
 };
 
 size_t up(size_t x) { return (x + 255) & ~size_t(255); }
+
+// bytes per element of the chunk-boundary states: bf16 when the state-path products are one
+// bf16 pass (mixed, bf16), as the reference keeps them (pallas_tpu_mega.py:425-426)
+size_t state_elem(const tjev_gdn_params* p) {
+  return (p->precision == TJEV_GDN_MIXED || p->precision == TJEV_GDN_ONE_PASS_BF16) ? 2 : 4;
+}
 
 Layout layout(const tjev_gdn_params* p, int backward) {
   const size_t C = kernel_chunk(p), D = p->key_dim;
@@ -124,10 +130,12 @@ Layout layout(const tjev_gdn_params* p, int backward) {
   if (!backward) {
     L.uu = take(hv);
     L.ww = take(hv);
+    // bf16 states: the fp32 state before each row's last chunk, for the final state
+    L.s_last = state_elem(p) == 2 ? take(B * H * D * D * 4) : none;
     L.tt = L.qk = L.xl = L.kt = L.gg = L.gsp = L.dqh = L.dkh = L.dgam = L.dkws = L.dcross = L.dbet = L.pa = L.pd = L.dwp =
         none;
   } else {
-    L.uu = L.ww = none;
+    L.uu = L.ww = L.s_last = none;
     L.tt = p->residuals == TJEV_GDN_SAVE_STATES ? take(B * H * N * C * C * 4) : none;
     L.qk = take(B * H * N * C * C * 4);
     L.xl = take(hv);
@@ -160,7 +168,7 @@ Residuals residual_layout(const tjev_gdn_params* p) {
   const size_t none = ~size_t(0);
   Residuals R{};
   R.states = 0;
-  size_t o = up(B * H * N * D * D * 4);
+  size_t o = up(B * H * N * D * D * state_elem(p));
   R.tinv = R.vnew = none;
   if (p->residuals >= TJEV_GDN_SAVE_TINV) {
     R.tinv = o;
@@ -203,6 +211,7 @@ gdn::GdnArgs base_args(const tjev_gdn_params* p, void* ws, const Layout& L) {
   A.uu = at<float>(ws, L.uu);
   A.ww = at<float>(ws, L.ww);
   A.vnew = at<float>(ws, L.vnew);
+  A.s_last = at<float>(ws, L.s_last);
   A.tt = at<float>(ws, L.tt);
   A.qk = at<float>(ws, L.qk);
   A.xl = at<float>(ws, L.xl);
@@ -334,7 +343,7 @@ size_t tjev_gdn_states_bytes(const tjev_gdn_params* p) {
   if (validate(p)) return 0;
   const size_t C = kernel_chunk(p);
   const size_t N = (p->length + C - 1) / C;
-  return (size_t)p->batch * p->value_heads * N * p->key_dim * p->value_dim * 4;
+  return (size_t)p->batch * p->value_heads * N * p->key_dim * p->value_dim * state_elem(p);
 }
 
 size_t tjev_gdn_residual_bytes(const tjev_gdn_params* p) {

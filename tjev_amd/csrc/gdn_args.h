@@ -29,7 +29,10 @@ struct GdnArgs {
   const float* nw;   // [Dv]
   float neps;
   void* ny;          // [B, T, H, Dv] io dtype
-  float* states;       // [B, H, N, Dk, Dv]
+  void* states;        // [B, H, N, Dk, Dv] fp32, or bf16 when the state-path products are one bf16
+                       // pass (precisions mixed and bf16: StateT in gdn_kernels.h)
+  float* s_last;       // [B, H, Dk, Dv] fp32 copy of the state before the last chunk when the
+                       // states are bf16 (k_final_state reads it), else null
   float* final_state;  // [B, H, Dk, Dv] the state after token T-1 (or null)
   void* conv_state;    // [B, K-1, W] the raw rows before token T (or null)
   // a sequence continued from an earlier call: the state before token 0 (chunk 0's tokens of

@@ -16,6 +16,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace gdn {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -197,6 +199,15 @@ template <> struct Raw4<uint16_t> {
     o[3] = __uint_as_float(a.y & 0xffff0000u);
   }
 };
+// 4 consecutive stored values as loaded: a float4, or 4 bf16 packed in a uint2 (expanded exactly
+// when used, so the load's latency is not waited for at the load)
+template <class T>
+using Packed4 = std::conditional_t<sizeof(T) == 2, uint2, float4>;
+__device__ __forceinline__ float4 f4_of(const float4& v) { return v; }
+__device__ __forceinline__ float4 f4_of(const uint2& v) {
+  return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
+                     __uint_as_float(v.y & 0xffff0000u));
+}
 // a value rounded to the storage type T and back (bf16: round to nearest even)
 template <class T>
 __device__ __forceinline__ float rnd_io(float v) {

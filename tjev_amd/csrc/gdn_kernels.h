@@ -6,8 +6,8 @@
 //   k_prep      conv + SiLU + padding mask, l2norm(q, k), q * Dk^-1/2, gates beta, g and the
 //               in-chunk cumulative decay gamma; head-major fp32 tiles      (HBM-bound)
 //   k_chunk     per (row, head, chunk): L = strict(beta k k^T . D), T = (I+L)^-1 (16x16
-//               diagonal blocks by substitution, then doubling levels on MFMA),
-//               w = T kbe, u = T v beta                                       (MFMA)
+//               diagonal blocks by doubling or by substitution, then doubling levels on
+//               MFMA), w = T kbe, u = T v beta                                (MFMA)
 //   k_scan_fwd  per (row, head, Dv tile): the recurrent state S (Dk x Dv tile, fp32), chunks
 //               in order: S_before stored, v_new = u - w S, S = carry S + k_write^T v_new
 //   k_out       per chunk: o = q_read S_before + ((q k^T) . D) v_new        (MFMA)
@@ -24,7 +24,18 @@
 
 namespace gdn {
 
-
+// Storage of the chunk-boundary states (the residual S): bf16 when the state-path products are one
+// bf16 pass (precisions mixed and bf16), else fp32, as the reference keeps them
+// (pallas_tpu_mega.py:425-426, _state_dtypes). Every reader of S in those modes feeds it to a
+// one-pass bf16 product, which rounds it to bf16 anyway, except the carry's gradient
+// <G_after, S_before> (the reference reads its bf16 S there too) and the final state, which
+// k_final_state builds from an fp32 copy of the last chunk's S (GdnArgs::s_last).
+template <int PS>
+using StateT = std::conditional_t<PS == P_BF16, uint16_t, float>;
+template <int PS>
+__device__ __forceinline__ StateT<PS>* states_ptr(const GdnArgs& A) {
+  return static_cast<StateT<PS>*>(A.states);
+}
 
 __device__ __forceinline__ size_t hoff(const GdnArgs& A, int b, int head, int heads, int n, int C, int D) {
   return ((size_t)(b * heads + head) * A.Tp + (size_t)n * C) * D;
@@ -581,19 +592,19 @@ __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
 // An R x K fp32 tile held in registers, 4 consecutive values per slot: fetch() issues every
 // global load of the tile at once (one memory round trip), the put_* calls then write it to an
 // operand tile as stored (rows) or transposed (cols), scaled.
-template <int R, int K, int NT>
+template <int R, int K, int NT, class TS = float>
 struct Regs {
   static constexpr int V = K / 4;
   static constexpr int IT = (R * V + NT - 1) / NT;
-  float4 v[IT];
+  Packed4<TS> v[IT];  // as stored (fp32, or bf16 expanded when put)
   __device__ __forceinline__ static bool live(int it) {
     return (R * V) % NT == 0 || (int)threadIdx.x + it * NT < R * V;
   }
-  __device__ __forceinline__ void fetch(const float* g, int ldg) {
+  __device__ __forceinline__ void fetch(const TS* g, int ldg) {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
       const int idx = threadIdx.x + it * NT;
-      if (live(it)) v[it] = *reinterpret_cast<const float4*>(lane_ptr(g, idx / V, ldg, 4 * (idx % V)));
+      if (live(it)) v[it] = *reinterpret_cast<const Packed4<TS>*>(lane_ptr(g, idx / V, ldg, 4 * (idx % V)));
     }
   }
   // a lower triangular tile: only the 16 x 16 tiles on and below the diagonal are read. The
@@ -604,11 +615,12 @@ struct Regs {
     const int idx = threadIdx.x + it * NT;
     return ((idx % V) >> 2) > ((idx / V) >> 4);
   }
-  __device__ __forceinline__ void fetch_lower(const float* g, int ldg) {
+  __device__ __forceinline__ void fetch_lower(const TS* g, int ldg) {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
       const int idx = threadIdx.x + it * NT, c4 = idx % V;
-      if (live(it)) v[it] = *reinterpret_cast<const float4*>(lane_ptr(g, idx / V, ldg, 4 * (upper(it) ? (c4 & 3) : c4)));
+      if (live(it))
+        v[it] = *reinterpret_cast<const Packed4<TS>*>(lane_ptr(g, idx / V, ldg, 4 * (upper(it) ? (c4 & 3) : c4)));
     }
   }
   __device__ __forceinline__ void put_lds_lower(float* s, int ld) const {
@@ -616,7 +628,12 @@ struct Regs {
     for (int it = 0; it < IT; ++it) {
       if (!live(it)) continue;
       const int idx = threadIdx.x + it * NT;
-      *reinterpret_cast<float4*>(s + (idx / V) * ld + 4 * (idx % V)) = upper(it) ? make_float4(0.f, 0.f, 0.f, 0.f) : v[it];
+      if constexpr (sizeof(TS) == 2) {
+        *reinterpret_cast<float4*>(s + (idx / V) * ld + 4 * (idx % V)) =
+            upper(it) ? make_float4(0.f, 0.f, 0.f, 0.f) : f4_of(v[it]);
+      } else {
+        *reinterpret_cast<float4*>(s + (idx / V) * ld + 4 * (idx % V)) = upper(it) ? make_float4(0.f, 0.f, 0.f, 0.f) : v[it];
+      }
     }
   }
   // op(r, k) = g[r][k] * rs[r] * cst
@@ -627,7 +644,12 @@ struct Regs {
       if (!live(it)) continue;
       const int idx = threadIdx.x + it * NT, r = idx / V, c = 4 * (idx % V);
       const float f = (rs ? rs[r] : 1.f) * cst;
-      op.put4(r, c, v[it].x * f, v[it].y * f, v[it].z * f, v[it].w * f);
+      if constexpr (sizeof(TS) == 2) {
+        const float4 x = f4_of(v[it]);
+        op.put4(r, c, x.x * f, x.y * f, x.z * f, x.w * f);
+      } else {
+        op.put4(r, c, v[it].x * f, v[it].y * f, v[it].z * f, v[it].w * f);
+      }
     }
   }
   // plain fp32 LDS tile with row stride ld
@@ -636,7 +658,11 @@ struct Regs {
     for (int it = 0; it < IT; ++it) {
       if (!live(it)) continue;
       const int idx = threadIdx.x + it * NT;
-      *reinterpret_cast<float4*>(s + (idx / V) * ld + 4 * (idx % V)) = v[it];
+      if constexpr (sizeof(TS) == 2) {
+        *reinterpret_cast<float4*>(s + (idx / V) * ld + 4 * (idx % V)) = f4_of(v[it]);
+      } else {
+        *reinterpret_cast<float4*>(s + (idx / V) * ld + 4 * (idx % V)) = v[it];
+      }
     }
   }
 };
@@ -664,13 +690,13 @@ __device__ __forceinline__ void rotate(const float (&x)[E], int rot, float (&z)[
 // their 4 columns in a rotated order so that the 8 groups of one write instruction fall in
 // distinct LDS banks (bf16 operand rows of (R + 8)/2 words); without ROT (fewer registers)
 // two groups share the banks of each write.
-template <int R, int K, int NT, bool ROT = true>
+template <int R, int K, int NT, bool ROT = true, class TS = float>
 struct RegsT {
   static constexpr int RP = R / 2;
   static constexpr int V = K / 4;
   static constexpr int G = V < 8 ? V : 8;
   static constexpr int IT = (RP * V + NT - 1) / NT;
-  float4 a[IT], b[IT];
+  Packed4<TS> a[IT], b[IT];  // as stored (fp32, or bf16 expanded when put)
   __device__ __forceinline__ static bool live(int it) {
     return (RP * V) % NT == 0 || (int)threadIdx.x + it * NT < RP * V;
   }
@@ -681,21 +707,28 @@ struct RegsT {
     c = 4 * (q + G * (rest / RP));
   }
   // every thread loads (slots past the tile repeat one inside it): no branch around the loads
-  __device__ __forceinline__ void fetch(const float* g, int ldg) {
+  __device__ __forceinline__ void fetch(const TS* g, int ldg) {
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
       int q, j, c;
       slot(it, q, j, c);
-      a[it] = *reinterpret_cast<const float4*>(lane_ptr(g, 2 * j, ldg, c));
-      b[it] = *reinterpret_cast<const float4*>(lane_ptr(g, 2 * j + 1, ldg, c));
+      a[it] = *reinterpret_cast<const Packed4<TS>*>(lane_ptr(g, 2 * j, ldg, c));
+      b[it] = *reinterpret_cast<const Packed4<TS>*>(lane_ptr(g, 2 * j + 1, ldg, c));
     }
   }
   template <int P>
   __device__ __forceinline__ void put(const Op<P>& op, int it, float fa, float fb) const {
     int q, j, c;
     slot(it, q, j, c);
-    const float xa[4] = {a[it].x, a[it].y, a[it].z, a[it].w};
-    const float xb[4] = {b[it].x, b[it].y, b[it].z, b[it].w};
+    float xa[4], xb[4];
+    if constexpr (sizeof(TS) == 2) {
+      const float4 av = f4_of(a[it]), bv = f4_of(b[it]);
+      xa[0] = av.x, xa[1] = av.y, xa[2] = av.z, xa[3] = av.w;
+      xb[0] = bv.x, xb[1] = bv.y, xb[2] = bv.z, xb[3] = bv.w;
+    } else {
+      xa[0] = a[it].x, xa[1] = a[it].y, xa[2] = a[it].z, xa[3] = a[it].w;
+      xb[0] = b[it].x, xb[1] = b[it].y, xb[2] = b[it].z, xb[3] = b[it].w;
+    }
     const int rot = ROT && G == 8 ? 2 * (q / 4) : 0;
     float za[4], zb[4];
     rotate(xa, rot, za);
@@ -731,17 +764,23 @@ struct RegsT {
       if (!live(it)) continue;
       int q, j, c;
       slot(it, q, j, c);
-      op.put4(2 * j, c, a[it].x, a[it].y, a[it].z, a[it].w);
-      op.put4(2 * j + 1, c, b[it].x, b[it].y, b[it].z, b[it].w);
+      if constexpr (sizeof(TS) == 2) {
+        const float4 av = f4_of(a[it]), bv = f4_of(b[it]);
+        op.put4(2 * j, c, av.x, av.y, av.z, av.w);
+        op.put4(2 * j + 1, c, bv.x, bv.y, bv.z, bv.w);
+      } else {
+        op.put4(2 * j, c, a[it].x, a[it].y, a[it].z, a[it].w);
+        op.put4(2 * j + 1, c, b[it].x, b[it].y, b[it].z, b[it].w);
+      }
     }
   }
   // the row pair (2j, 2j+1) this thread holds (put_cols2's rows)
   __device__ __forceinline__ static int pair() { return ((int)threadIdx.x / G) % RP; }
 };
 
-template <int R, int K, int NT, int P>
-__device__ __forceinline__ void stage_rows(const Op<P>& op, const float* g, int ldg, const float* rs = nullptr) {
-  Regs<R, K, NT> t;
+template <int R, int K, int NT, int P, class TS>
+__device__ __forceinline__ void stage_rows(const Op<P>& op, const TS* g, int ldg, const float* rs = nullptr) {
+  Regs<R, K, NT, TS> t;
   t.fetch(g, ldg);
   t.put_rows(op, rs);
 }
@@ -1001,6 +1040,12 @@ struct AccVals {
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) v[t][rr] = *lane_ptr(g, i0 + acc_row(rr), ld, 16 * t + acc_col());
   }
+  __device__ __forceinline__ void fetch(const uint16_t* g, int ld, int i0) {  // bf16, expanded
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) v[t][rr] = bf2f(*lane_ptr(g, i0 + acc_row(rr), ld, 16 * t + acc_col()));
+  }
   __device__ __forceinline__ void clear() {
 #pragma unroll
     for (int t = 0; t < TN; ++t)
@@ -1060,12 +1105,12 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
     if constexpr (!LOAD_T) kk.put_rows(ob);
     rc.fetch(A, y.b, y.h, y.n);
     RegsT<C, D, NT> vc;  // this unit's (v beta)^T source (forward)
-    RegsT<D, D, NT> sc;  // S_before, its strip of k and its v at the accumulator layout (backward)
+    RegsT<D, D, NT, true, StateT<PS>> sc;  // S_before, its strip of k and its v at the accumulator layout (backward)
     StripA<D> ks;
     AccVals<D / 16> va;
     if constexpr (LOAD_T) {
       load_tile<C, C, NT>(sT, LT, tg);
-      sc.fetch(A.states + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * D * D, D);
+      sc.fetch(states_ptr<PS>(A) + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * D * D, D);
       ks.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D, i0);
       va.fetch(A.vv + off, D, i0);
     }
@@ -1097,7 +1142,7 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
           for (int rr = 0; rr < 4; ++rr) lds_st(sT + (i0 + acc_row(rr)) * LT + 16 * t + acc_col(), acc[t][rr]);
       }
       if constexpr (!FWD) {  // in flight during the inverse
-        sc.fetch(A.states + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * D * D, D);
+        sc.fetch(states_ptr<PS>(A) + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * D * D, D);
         ks.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D, i0);
       }
       if constexpr (FWD) {  // k again and v, in flight during the inverse
@@ -1300,12 +1345,17 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_fwd(GdnArgs A) {
     const bool emit = n >= n0;              // the replayed chunk n0 - 1 only rebuilds the state
     if (NW == D / 16 || w < D / 16) {
       const int dk = 16 * w + acc_col();
-      float* sg = A.states + ((size_t)bh * A.N + n) * D * D + (size_t)dk * D + j0 + jl;
+      const size_t so = ((size_t)bh * A.N + n) * D * D + (size_t)dk * D + j0 + jl;
+      StateT<PS>* sg = states_ptr<PS>(A) + so;
 #pragma unroll
       for (int t = 0; t < TJ; ++t) {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) os.put(16 * t + jl + rr, dk, accS[t][rr]);
-        if (emit) *reinterpret_cast<float4*>(sg + 16 * t) = make_float4(accS[t][0], accS[t][1], accS[t][2], accS[t][3]);
+        const float v[4] = {accS[t][0], accS[t][1], accS[t][2], accS[t][3]};
+        if (emit) st4_io(sg + 16 * t, v);
+        if constexpr (sizeof(StateT<PS>) == 2) {  // the final state's fp32 source
+          if (emit && n == A.N - 1 && A.s_last) st4_io(A.s_last + ((size_t)bh * D + dk) * D + j0 + jl + 16 * t, v);
+        }
       }
     }
     const float carry = in.gt.carry();
@@ -1496,15 +1546,22 @@ __global__ __launch_bounds__(512) void k_scan_fwd_split(GdnArgs A) {
     }
   };
   auto store_s = [&](int n) {  // S before chunk n, from sU, where put_u writes next
-    float* sg = A.states + ((size_t)bh * A.N + n) * D * D + j0;
+    StateT<PS>* sg = states_ptr<PS>(A) + ((size_t)bh * A.N + n) * D * D + j0;
 #pragma unroll
     for (int it = 0; it < 3; ++it) {
       const int idx = lt + it * NL;
       if (idx < 1024) {
         const int dk = idx >> 3, c = 4 * (idx & 7);
-        const float4 v = make_float4(sU[(c + 0) * LU + dk], sU[(c + 1) * LU + dk], sU[(c + 2) * LU + dk],
-                                     sU[(c + 3) * LU + dk]);
-        *reinterpret_cast<float4*>(sg + (unsigned)(dk * D + c)) = v;
+        if constexpr (sizeof(StateT<PS>) == 2) {  // and the final state's fp32 source
+          const float v[4] = {sU[(c + 0) * LU + dk], sU[(c + 1) * LU + dk], sU[(c + 2) * LU + dk],
+                              sU[(c + 3) * LU + dk]};
+          st4_io(sg + (unsigned)(dk * D + c), v);
+          if (n == A.N - 1 && A.s_last) st4_io(A.s_last + (size_t)bh * D * D + j0 + (unsigned)(dk * D + c), v);
+        } else {
+          const float4 v = make_float4(sU[(c + 0) * LU + dk], sU[(c + 1) * LU + dk], sU[(c + 2) * LU + dk],
+                                       sU[(c + 3) * LU + dk]);
+          *reinterpret_cast<float4*>(sg + (unsigned)(dk * D + c)) = v;
+        }
       }
     }
   };
@@ -1609,13 +1666,13 @@ __global__ __launch_bounds__(512) void k_scan_fwd_split(GdnArgs A) {
 // S_before, token-major output. Every global input of a unit is held in registers and refilled
 // with the next unit's values right after it has been used, so its loads run during the rest
 // of the unit instead of stalling the next one.
-template <int C, int D, int NT>
+template <int C, int D, int NT, class TS>
 struct OutIn {
   CtxRaw<C> cx;
   Regs<C, D, NT> k;      // k rows: B(d, j) = k[j][d]
   StripA<D> q;           // this wave's q rows (A operand of q k^T and of q_read S)
   RegsT<C, D, NT> v;     // v_new rows, staged as v_new^T
-  RegsT<D, D, NT> st;    // S_before rows, staged as S^T
+  RegsT<D, D, NT, true, TS> st;  // S_before rows, staged as S^T
 };
 
 template <int C, int D, int PI, int PS, class TIO, bool NORM = false>
@@ -1635,14 +1692,14 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
   const Op<PI> ob = TB::at(sB);
   const int ws = wave_strip<C / 16, false>();
   const int total = A.B * A.H * A.N;
-  OutIn<C, D, NT> in;
+  OutIn<C, D, NT, StateT<PS>> in;
   {
     const UnitIx<BY_HEAD> x(A, blockIdx.x);
     in.cx.fetch(A, x.b, x.h, x.n);
     in.k.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D);
     in.q.fetch(A.qn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D, 16 * ws);
     in.v.fetch(A.vnew + hoff(A, x.b, x.h, A.H, x.n, C, D), D);
-    in.st.fetch(A.states + ((size_t)x.b * A.H + x.h) * A.N * D * D + (size_t)x.n * D * D, D);
+    in.st.fetch(states_ptr<PS>(A) + ((size_t)x.b * A.H + x.h) * A.N * D * D + (size_t)x.n * D * D, D);
   }
   for (int u = blockIdx.x; u < total; u += gridDim.x) {
     const int w = opaque_uniform(ws), i0 = 16 * w;  // conditions on w stay in the loop
@@ -1690,7 +1747,7 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
     __syncthreads();
     in.q.template product<PS>(o, ob, 0, D / 16, cx.grow[i0 + (lane() & 15)]);
     in.q.fetch(A.qn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D, i0);
-    in.st.fetch(A.states + ((size_t)y.b * A.H + y.h) * A.N * D * D + (size_t)y.n * D * D, D);
+    in.st.fetch(states_ptr<PS>(A) + ((size_t)y.b * A.H + y.h) * A.N * D * D + (size_t)y.n * D * D, D);
     TIO* out = reinterpret_cast<TIO*>(A.out);
     {  // quad transposes: each lane stores 4 consecutive columns of one row
       float ss = 0.f;
@@ -1761,7 +1818,8 @@ __global__ __launch_bounds__(256) void k_final_state(GdnArgs A) {
   const float carry = sl == before ? expf(gl + ll) : 0.f;
   __syncthreads();
   const int j = threadIdx.x % DT, rg = threadIdx.x / DT;
-  const float* S = A.states + ((size_t)bh * A.N + nl) * D * D + tile * DT + j;
+  const float* S = (A.s_last ? A.s_last + (size_t)bh * D * D
+                              : static_cast<const float*>(A.states) + ((size_t)bh * A.N + nl) * D * D) + tile * DT + j;
   float acc[RPT];
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
@@ -1935,8 +1993,9 @@ struct ScanBwdIn {
   AccVals<DVT / 16> xl;           // X_loc at the strip's accumulator layout
   // Loads without branches (a fixed count of memory operations per wave): waves past the
   // D/16 (C/16) strips load a strip they do not use.
+  template <int PS>
   __device__ __forceinline__ void fetch_sbef(const GdnArgs& A, int bh, int n, int j0) {
-    sbef.fetch(A.states + ((size_t)bh * A.N + n) * D * D + j0, D, 16 * (wave() % (D / 16)));
+    sbef.fetch(states_ptr<PS>(A) + ((size_t)bh * A.N + n) * D * D + j0, D, 16 * (wave() % (D / 16)));
   }
   __device__ __forceinline__ void fetch_do(const GdnArgs& A, int b, int h, int n, int j0) {
     const TIO* dout = reinterpret_cast<const TIO*>(A.d_out);
@@ -2008,7 +2067,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
       in.put_gates(sgate[n & 1]);
       in.gt.fetch(A, b, h, n > n0 ? n - 1 : n, lane() % (C / 2));
     }
-    in.fetch_sbef(A, bh, n, j0);
+    in.template fetch_sbef<PS>(A, bh, n, j0);
     in.fetch_do(A, b, h, n, j0);
     in.fetch_qk(A.qn + hoff(A, b, hk, A.Hk, n, C, D));
     in.fetch_kt(A, b, h, n);
@@ -2033,7 +2092,7 @@ __global__ __launch_bounds__((C > D ? C : D) * 4) void k_scan_bwd(GdnArgs A) {
         }
         if (emit) st_tile(gdst + 16 * w * D + j0 + 16 * t, D, accG[t]);
       }
-      in.fetch_sbef(A, bh, nx, j0);
+      in.template fetch_sbef<PS>(A, bh, nx, j0);
     }
     part = sum64(part);
     if (lane() == 0) red[w] = part;
@@ -2143,7 +2202,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_grads(GdnArgs A) {
   xs.fetch(A.xl + off, D, i0);
   dos.fetch(dout + (((size_t)b * A.T + (size_t)n * C) * A.H + h) * D, A.H * D, i0, A.T - n * C);
   load_ctx<C, NT>(cx, A, b, h, n);
-  stage_rows<D, D, NT>(ob, A.states + ((size_t)bh * A.N + n) * D * D, D);  // S: B(dv, j=dk) = S[dk][dv]
+  stage_rows<D, D, NT>(ob, states_ptr<PS>(A) + ((size_t)bh * A.N + n) * D * D, D);  // S: B(dv, j=dk) = S[dk][dv]
   vn.fetch(A.vnew + off, D, i0);
   __syncthreads();
   f32x4 dkb[TD], dq[TD];

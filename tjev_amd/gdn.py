@@ -80,6 +80,10 @@ class GdnPlan:
         self.chunk_run = min(max(chunk, 16), 128)  # the kernels' chunk (tjev_gdn_params.chunk clamped)
         self.n_chunks = math.ceil(length / self.chunk_run)
         self.states_shape = (batch, value_heads, self.n_chunks, key_dim, value_dim)
+        # the states' storage: bf16 when the state-path products are one bf16 pass, as the
+        # reference's _state_dtypes (pallas_tpu_mega.py:425-426)
+        self.states_dtype = torch.bfloat16 if precision in ("mixed", "bf16") else torch.float32
+        self.states_bytes = self.lib.tjev_gdn_states_bytes(ctypes.byref(self.params))
         self.residual_bytes = self.lib.tjev_gdn_residual_bytes(ctypes.byref(self.params))
         self.fwd_bytes = self.lib.tjev_gdn_workspace_bytes(ctypes.byref(self.params), 0)
         self.bwd_bytes = self.lib.tjev_gdn_workspace_bytes(ctypes.byref(self.params), 1)
@@ -92,12 +96,23 @@ class GdnPlan:
         return torch.empty(self.bwd_bytes if backward else self.fwd_bytes, dtype=torch.uint8, device=device)
 
     def residuals(self, device) -> torch.Tensor:
-        """The forward's residual buffer (fp32): the states first, then what ``residuals`` keeps."""
+        """The forward's residual buffer (4-byte words): the states first, then what ``residuals``
+        keeps, each part 256-byte aligned."""
         return torch.empty(self.residual_bytes // 4, dtype=torch.float32, device=device)
 
     def states_of(self, residuals: torch.Tensor) -> torch.Tensor:
-        """The states [B, H, N, Dk, Dv] part of a residual buffer (a view)."""
-        return residuals[: math.prod(self.states_shape)].view(self.states_shape)
+        """The states [B, H, N, Dk, Dv] part of a residual buffer (a view, ``states_dtype``)."""
+        return residuals.view(torch.uint8)[: self.states_bytes].view(self.states_dtype).view(self.states_shape)
+
+    def tinv_of(self, residuals: torch.Tensor) -> torch.Tensor:
+        """The kept T [B, H, N, C, C] fp32 part of a residual buffer ("tinv" and "all")."""
+        if self.params.residuals == _lib.RESIDUALS["states"]:
+            raise ValueError("residuals='states' keeps no T")
+        start = (self.states_bytes + 255) // 256 * 256
+        b, h, n = self.states_shape[:3]
+        size = b * h * n * self.chunk_run * self.chunk_run * 4
+        return residuals.view(torch.uint8)[start:start + size].view(torch.float32).view(
+            b, h, n, self.chunk_run, self.chunk_run)
 
     def forward(self, qkv, a, b, a_log, dt_bias, conv_w, seg, out, residuals, workspace) -> None:
         status = self.lib.tjev_gdn_mega2_fwd(
