@@ -108,6 +108,26 @@ def test_merged_lora_backward_matches_autograd():
         assert rel(g.double().cpu(), h.double().cpu()) <= 1e-5
 
 
+@pytest.mark.parametrize("k", [16384, 8192 + 4096, 1000])
+def test_split_k_adapter_products(k):
+    """The adapters' token-contracted products (a^T b over K tokens, fp32 accumulation) cut into
+    K parts at long K: equal to one fp32-accumulated product to fp32 rounding, for a contiguous a
+    and for a column slice of a wider a (the split of x A); K = 12288 cuts in 4, 1000 not at all."""
+    from tjev_amd.block import _mm32, _mm32_tn
+
+    gen = torch.Generator().manual_seed(2)
+    wide = torch.randn(k, 256, generator=gen).to(torch.bfloat16).cuda()
+    b = torch.randn(k, 640, generator=gen).to(torch.bfloat16).cuda()
+    exact = (wide.double().t() @ b.double())
+    for a, want in ((wide, exact), (wide[:, 64:128], exact[64:128])):
+        got = _mm32_tn(a, b)
+        plain = _mm32(a.t(), b)
+        assert got.dtype == torch.float32 and got.shape == want.shape
+        err, err_plain = rel(got.double(), want), rel(plain.double(), want)
+        print(f"K={k} {tuple(a.shape)}: split {err:.1e}, plain {err_plain:.1e}", flush=True)
+        assert err <= 1e-5 and err_plain <= 1e-5
+
+
 def test_block_fp32_matches_fp64_oracle():
     blk = _block(torch.float32, "highest", 16, 8, **SMALL)
     x, seg, dy = _inputs(2, 150, SMALL["hidden"], 3, torch.float32)
