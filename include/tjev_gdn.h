@@ -22,7 +22,8 @@
  *                                                   fp32, or bf16 under TJEV_GDN_MIXED and
  *                                                   TJEV_GDN_ONE_PASS_BF16 (the reference's
  *                                                   _state_dtypes, pallas_tpu_mega.py:425-426)
- *                tinv   [B, H, ceil(T/C), C, C]    fp32 (I + L)^-1 of each chunk (gdn_tinv), when
+ *                tinv   [B, H, ceil(T/C), C, C]    (I + L)^-1 of each chunk (gdn_tinv), fp32 (bf16
+ *                                                   under TJEV_GDN_ONE_PASS_BF16), when
  *                                                   residuals >= TJEV_GDN_SAVE_TINV
  *                v_new  [B, H, ceil(T/C)*C, Dv]    fp32 u - w S of each token, when
  *                                                   residuals == TJEV_GDN_SAVE_ALL

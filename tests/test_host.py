@@ -107,9 +107,11 @@ def test_c_abi_sizes():
         assert lib.tjev_gdn_states_bytes(ctypes.byref(q)) == part // 2
         assert lib.tjev_gdn_residual_bytes(ctypes.byref(q)) == part // 2
         assert lib.tjev_gdn_workspace_bytes(ctypes.byref(q), 0) == fwd + 4 * 16 * 128 * 128 * 4
-        assert lib.tjev_gdn_workspace_bytes(ctypes.byref(q), 1) == bwd
-        q.residuals = 1  # T stays fp32 after the bf16 states (256-byte aligned)
-        assert lib.tjev_gdn_residual_bytes(ctypes.byref(q)) == part // 2 + part
+        # under "bf16" T between the backward's first two kernels is bf16 too (the reference's t_dtype)
+        t_part = 4 * 16 * 32 * 128 * 128 * 2
+        assert lib.tjev_gdn_workspace_bytes(ctypes.byref(q), 1) == bwd - (t_part if precision == 2 else 0)
+        q.residuals = 1  # T after the bf16 states (256-byte aligned): bf16 under "bf16" only
+        assert lib.tjev_gdn_residual_bytes(ctypes.byref(q)) == part // 2 + (part // 2 if precision == 2 else part)
     # a ragged T is padded to whole chunks (the last segment's id carried over, as the reference pads)
     p = _params(length=100, chunk=16)
     assert lib.tjev_gdn_states_bytes(ctypes.byref(p)) == 1 * 4 * 7 * 16 * 16 * 4

@@ -103,6 +103,8 @@ size_t up(size_t x) { return (x + 255) & ~size_t(255); }
 size_t state_elem(const tjev_gdn_params* p) {
   return (p->precision == TJEV_GDN_MIXED || p->precision == TJEV_GDN_ONE_PASS_BF16) ? 2 : 4;
 }
+// bytes per element of T: bf16 when the intra-chunk products are one bf16 pass (bf16)
+size_t tinv_elem(const tjev_gdn_params* p) { return p->precision == TJEV_GDN_ONE_PASS_BF16 ? 2 : 4; }
 
 Layout layout(const tjev_gdn_params* p, int backward) {
   const size_t C = kernel_chunk(p), D = p->key_dim;
@@ -136,7 +138,7 @@ Layout layout(const tjev_gdn_params* p, int backward) {
         none;
   } else {
     L.uu = L.ww = L.s_last = none;
-    L.tt = p->residuals == TJEV_GDN_SAVE_STATES ? take(B * H * N * C * C * 4) : none;
+    L.tt = p->residuals == TJEV_GDN_SAVE_STATES ? take(B * H * N * C * C * tinv_elem(p)) : none;
     L.qk = take(B * H * N * C * C * 4);
     L.xl = take(hv);
     L.kt = take(hv);
@@ -172,7 +174,7 @@ Residuals residual_layout(const tjev_gdn_params* p) {
   R.tinv = R.vnew = none;
   if (p->residuals >= TJEV_GDN_SAVE_TINV) {
     R.tinv = o;
-    o += up(B * H * N * C * C * 4);
+    o += up(B * H * N * C * C * tinv_elem(p));
   }
   if (p->residuals == TJEV_GDN_SAVE_ALL) {
     R.vnew = o;

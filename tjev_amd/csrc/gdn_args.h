@@ -73,7 +73,7 @@ struct GdnArgs {
   float* uu;      // [B, H, Tp, D]   u = T v beta            (forward)
   float* ww;      // [B, H, Tp, D]   w = T kbe               (forward)
   float* vnew;    // [B, H, Tp, D]   v_new
-  float* tt;      // [B, H, N, C, C] T = (I+L)^-1           (backward: only the 16 x 16 tiles on and
+  void* tt;       // [B, H, N, C, C] T = (I+L)^-1, fp32 (bf16 under precision bf16) (backward: only the 16 x 16 tiles on and
                   // below the diagonal are written and read)
   float* qk;      // [B, H, N, C/16, C/16, 256] q k^T's 16 x 16 tiles on and below the diagonal, in
                   // accumulator order (backward)

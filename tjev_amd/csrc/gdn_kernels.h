@@ -36,6 +36,15 @@ template <int PS>
 __device__ __forceinline__ StateT<PS>* states_ptr(const GdnArgs& A) {
   return static_cast<StateT<PS>*>(A.states);
 }
+// Storage of T = (I + L)^-1 between kernels and as a residual: bf16 when the intra-chunk products
+// are one bf16 pass (precision bf16, the reference's t_dtype), else fp32. T only ever enters
+// those products.
+template <int PI>
+using TinvT = std::conditional_t<PI == P_BF16, uint16_t, float>;
+template <int PI>
+__device__ __forceinline__ TinvT<PI>* tinv_ptr(const GdnArgs& A) {
+  return static_cast<TinvT<PI>*>(A.tt);
+}
 
 __device__ __forceinline__ size_t hoff(const GdnArgs& A, int b, int head, int heads, int n, int C, int D) {
   return ((size_t)(b * heads + head) * A.Tp + (size_t)n * C) * D;
@@ -235,8 +244,8 @@ struct StripDecay {
 };
 
 // R x D fp32 tile from global (row stride D) into LDS (row stride LD), every load issued first
-template <int R, int D, int NT>
-__device__ __forceinline__ void load_tile(float* s, int LD, const float* g);
+template <int R, int D, int NT, class TS>
+__device__ __forceinline__ void load_tile(float* s, int LD, const TS* g);
 
 // The order in which a persistent kernel walks its units (workgroup i takes units i, i + grid,
 // ...). A kernel's last units are still in the L2 and memory-side caches when the next kernel
@@ -1054,9 +1063,9 @@ struct AccVals {
   }
 };
 
-template <int R, int D, int NT>
-__device__ __forceinline__ void load_tile(float* s, int LD, const float* g) {
-  Regs<R, D, NT> t;
+template <int R, int D, int NT, class TS>
+__device__ __forceinline__ void load_tile(float* s, int LD, const TS* g) {
+  Regs<R, D, NT, TS> t;
   t.fetch(g, D);
   t.put_lds(s, LD);
 }
@@ -1100,7 +1109,7 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
     const UnitIx<CHUNKS_DOWN> x(A, u);
     const UnitIx<CHUNKS_DOWN> y(A, u + gridDim.x < total ? u + gridDim.x : u);  // the next unit (or this one again)
     const size_t off = hoff(A, x.b, x.h, A.H, x.n, C, D);
-    float* tg = A.tt + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * C * C;
+    TinvT<PI>* tg = tinv_ptr<PI>(A) + ((size_t)(x.b * A.H + x.h) * A.N + x.n) * C * C;
     rc.commit(cx);
     if constexpr (!LOAD_T) kk.put_rows(ob);
     rc.fetch(A, y.b, y.h, y.n);
@@ -1180,8 +1189,13 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
           const int r = idx / (C / 4), c = 4 * (idx % (C / 4));
           if ((c >> 4) <= (r >> 4)) {  // the lower triangle (the rest of sT is scratch)
             const float4 t = *reinterpret_cast<const float4*>(sT + r * LT + c);
-            *reinterpret_cast<float4*>(tg + r * C + c) =
-                make_float4(c <= r ? t.x : 0.f, c + 1 <= r ? t.y : 0.f, c + 2 <= r ? t.z : 0.f, c + 3 <= r ? t.w : 0.f);
+            if constexpr (sizeof(TinvT<PI>) == 2) {
+              const float v[4] = {c <= r ? t.x : 0.f, c + 1 <= r ? t.y : 0.f, c + 2 <= r ? t.z : 0.f, c + 3 <= r ? t.w : 0.f};
+              st4_io(tg + r * C + c, v);
+            } else {
+              *reinterpret_cast<float4*>(tg + r * C + c) =
+                  make_float4(c <= r ? t.x : 0.f, c + 1 <= r ? t.y : 0.f, c + 2 <= r ? t.z : 0.f, c + 3 <= r ? t.w : 0.f);
+            }
           }
         }
       }
@@ -1211,7 +1225,7 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
     kk.fetch(A.kn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D);
     if constexpr (STORE_T) {
       for (int idx = threadIdx.x; idx < C * C; idx += NT)  // lower triangle (the rest is scratch)
-        tg[idx] = idx % C <= idx / C ? sT[(idx / C) * LT + idx % C] : 0.f;
+        stf(tg + idx, idx % C <= idx / C ? sT[(idx / C) * LT + idx % C] : 0.f);
     }
 #pragma unroll
     for (int t = 0; t < D / 16; ++t)
@@ -1869,13 +1883,13 @@ __global__ __launch_bounds__(256) void k_conv_state(GdnArgs A) {
 // its stagings: as rows for q k^T, transposed and scaled for k_write^T) are refilled with the
 // next unit's values once used; do and T are loaded at the unit's start and after the product
 // before their use (holding them longer would spill).
-template <int C, int D, int NT, class TIO>
+template <int C, int D, int NT, class TIO, class TT>
 struct LocalIn {
   CtxRaw<C> cx;
   RegsT<C, D, NT> k;          // k rows
   StripA<D> q;                // this wave's q rows (A operand of q k^T)
   RegsIO<C, D, NT, TIO> dov;  // do rows, staged as do^T
-  Regs<C, C, NT> tt;          // T rows
+  Regs<C, C, NT, TT> tt;      // T rows (as stored)
   template <class U>
   __device__ __forceinline__ void fetch_k(const GdnArgs& A, const U& y) {
     k.fetch(A.kn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D);
@@ -1891,7 +1905,7 @@ struct LocalIn {
   }
   template <class U>
   __device__ __forceinline__ void fetch_t(const GdnArgs& A, const U& y) {
-    tt.fetch_lower(A.tt + ((size_t)y.bh * A.N + y.n) * C * C, C);
+    tt.fetch_lower(static_cast<const TT*>(A.tt) + ((size_t)y.bh * A.N + y.n) * C * C, C);
   }
 };
 
@@ -1908,7 +1922,7 @@ __global__ __launch_bounds__(C * 4) void k_bwd_local(GdnArgs A) {
   const Op<PI> ob = TB::at(sB);
   const int ws = wave_strip<C / 16, true>();
   const int total = A.B * A.H * A.N;
-  LocalIn<C, D, NT, TIO> in;
+  LocalIn<C, D, NT, TIO, TinvT<PI>> in;
   {
     const UnitIx<CHUNKS_UP> x(A, blockIdx.x);
     in.cx.fetch(A, x.b, x.h, x.n);

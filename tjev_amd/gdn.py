@@ -83,6 +83,7 @@ class GdnPlan:
         # the states' storage: bf16 when the state-path products are one bf16 pass, as the
         # reference's _state_dtypes (pallas_tpu_mega.py:425-426)
         self.states_dtype = torch.bfloat16 if precision in ("mixed", "bf16") else torch.float32
+        self.tinv_dtype = torch.bfloat16 if precision == "bf16" else torch.float32  # the reference's t_dtype
         self.states_bytes = self.lib.tjev_gdn_states_bytes(ctypes.byref(self.params))
         self.residual_bytes = self.lib.tjev_gdn_residual_bytes(ctypes.byref(self.params))
         self.fwd_bytes = self.lib.tjev_gdn_workspace_bytes(ctypes.byref(self.params), 0)
@@ -105,13 +106,13 @@ class GdnPlan:
         return residuals.view(torch.uint8)[: self.states_bytes].view(self.states_dtype).view(self.states_shape)
 
     def tinv_of(self, residuals: torch.Tensor) -> torch.Tensor:
-        """The kept T [B, H, N, C, C] fp32 part of a residual buffer ("tinv" and "all")."""
+        """The kept T [B, H, N, C, C] part of a residual buffer ("tinv" and "all"; ``tinv_dtype``)."""
         if self.params.residuals == _lib.RESIDUALS["states"]:
             raise ValueError("residuals='states' keeps no T")
         start = (self.states_bytes + 255) // 256 * 256
         b, h, n = self.states_shape[:3]
-        size = b * h * n * self.chunk_run * self.chunk_run * 4
-        return residuals.view(torch.uint8)[start:start + size].view(torch.float32).view(
+        size = b * h * n * self.chunk_run * self.chunk_run * self.tinv_dtype.itemsize
+        return residuals.view(torch.uint8)[start:start + size].view(self.tinv_dtype).view(
             b, h, n, self.chunk_run, self.chunk_run)
 
     def forward(self, qkv, a, b, a_log, dt_bias, conv_w, seg, out, residuals, workspace) -> None:
