@@ -54,11 +54,13 @@ def oracle_outputs(inputs, cot, *, key_heads, key_dim, value_heads, value_dim, c
 
 
 def case_inputs(batch, length, hk, h, d, *, cuts=None, seed=0, dtype=torch.float32, style="reference",
-                trailing_pad=5, segments=None, taps=4):
-    """test_gdn_mega._inputs: 4 random cuts (or ``cuts``) and 5 trailing padding tokens."""
+                trailing_pad=5, segments=None, taps=4, dk=None, dv=None):
+    """test_gdn_mega._inputs: 4 random cuts (or ``cuts``) and 5 trailing padding tokens; head
+    widths d, or dk (q, k) and dv (v)."""
     if segments is None:
         segments = "cuts" if cuts is not None else "random4"
     inputs = gdn_inputs(batch=batch, length=length, key_heads=hk, value_heads=h, dim=d, seed=seed, dtype=dtype,
-                        segments=segments, cuts=cuts, trailing_pad=trailing_pad, style=style, taps=taps)
-    cot = cotangent(batch, length, h, d)
+                        segments=segments, cuts=cuts, trailing_pad=trailing_pad, style=style, taps=taps,
+                        key_dim=dk, value_dim=dv)
+    cot = cotangent(batch, length, h, dv or d)
     return inputs, cot

@@ -486,3 +486,22 @@ def test_chunks_above_128_run_the_128_kernels():
         q = _params(chunk=128, length=600)
         assert lib.tjev_gdn_residual_bytes(ctypes.byref(p)) == lib.tjev_gdn_residual_bytes(ctypes.byref(q))
         assert lib.tjev_gdn_workspace_bytes(ctypes.byref(p), 1) == lib.tjev_gdn_workspace_bytes(ctypes.byref(q), 1)
+
+
+def test_head_dims_run_padded_to_a_compiled_dim():
+    """Head dims the kernels do not hold as they are run zero-padded to the next compiled dim
+    (Dk != Dv, or widths other than 16 .. 128 powers of two, up to 128); the lane layout of
+    qkv round-trips through the padding."""
+    from tjev_amd.gdn import pad_qkv, run_dim, unpad_qkv
+
+    assert [run_dim(d, d) for d in (16, 32, 64, 128)] == [16, 32, 64, 128]
+    assert run_dim(64, 128) == run_dim(128, 64) == 128 and run_dim(48, 48) == 64 and run_dim(32, 96) == 128
+    assert run_dim(8, 8) == 16 and run_dim(256, 256) is None and run_dim(64, 192) is None
+    hk, dk, h, dv = 2, 48, 3, 40
+    x = torch.arange(5 * (2 * hk * dk + h * dv), dtype=torch.float32).reshape(5, -1)
+    padded = pad_qkv(x, hk, dk, h, dv, 64)
+    assert padded.shape == (5, 2 * hk * 64 + h * 64)
+    heads = padded.reshape(5, 2 * hk + h, 64)
+    assert torch.all(heads[..., :dk][:, :2 * hk] == x[:, :2 * hk * dk].reshape(5, 2 * hk, dk))
+    assert torch.all(heads[:, :2 * hk, dk:] == 0) and torch.all(heads[:, 2 * hk:, dv:] == 0)
+    assert torch.equal(unpad_qkv(padded, hk, dk, h, dv, 64), x)

@@ -2,7 +2,8 @@
 // delta rule on given q, k [B,T,Hk,D], v [B,T,H,D], g, beta [B,T,H] -- no conv, no l2norm, no
 // gate functions -- around the same chunk, scan and output kernels as the megakernel. q and k
 // are taken as given (the model passes l2norm(q) * Dk^-1/2 and l2norm(k), gdn.py:90-92); the
-// padded tail (t >= T) is segment 0 with zero inputs (pallas_tpu_v2.py:565-569).
+// padded tail (t >= T) has zero inputs and the last token's segment id (xla.py:198-204; the
+// segment-0 padding of pallas_tpu_v2.py:565-569 gives the same outputs).
 #pragma once
 
 #include "gdn_kernels.h"

@@ -51,6 +51,45 @@ def kernel_inverse(inverse: str) -> str:
 
 
 _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+RUN_DIMS = (16, 32, 64, 128)  # the head dims with compiled kernels (csrc/gdn_shapes.def), Dk = Dv
+NORM_DIMS = (16, 32, 64, 128, 256)  # the gated RMSNorm's kernels
+
+
+def run_dim(key_dim: int, value_dim: int) -> int | None:
+    """The head dim the kernels run a (key_dim, value_dim) problem at: the two equal and compiled
+    run as they are; otherwise both are zero-padded to the smallest compiled dim that holds the
+    larger (None above 128). Zero q/k lanes change no dot product or l2 norm, and zero v lanes
+    only add zero output and state columns, so the padded problem holds the original one."""
+    if key_dim == value_dim and key_dim in RUN_DIMS:
+        return key_dim
+    return next((d for d in RUN_DIMS if d >= max(key_dim, value_dim)), None)
+
+
+def pad_heads(x: torch.Tensor, heads: int, dim: int, run: int) -> torch.Tensor:
+    """[..., heads * dim] -> [..., heads * run]: each head's lanes zero-padded at its end."""
+    if dim == run:
+        return x
+    lead = x.shape[:-1]
+    return torch.nn.functional.pad(x.reshape(*lead, heads, dim), (0, run - dim)).reshape(*lead, heads * run)
+
+
+def pad_qkv(x: torch.Tensor, key_heads: int, key_dim: int, value_heads: int, value_dim: int, run: int):
+    """The q | k | v lanes of x [..., 2 Hk Dk + H Dv] (qkv, the conv weight, conv history) with
+    every head padded to ``run`` lanes."""
+    q, k, v = torch.split(x, [key_heads * key_dim, key_heads * key_dim, value_heads * value_dim], dim=-1)
+    return torch.cat([pad_heads(q, key_heads, key_dim, run), pad_heads(k, key_heads, key_dim, run),
+                      pad_heads(v, value_heads, value_dim, run)], dim=-1)
+
+
+def unpad_qkv(x: torch.Tensor, key_heads: int, key_dim: int, value_heads: int, value_dim: int, run: int):
+    """The inverse of pad_qkv: each head's first lanes."""
+    lead = x.shape[:-1]
+    q, k, v = torch.split(x, [key_heads * run, key_heads * run, value_heads * run], dim=-1)
+
+    def cut(t, heads, dim):
+        return t.reshape(*lead, heads, run)[..., :dim].reshape(*lead, heads * dim)
+
+    return torch.cat([cut(q, key_heads, key_dim), cut(k, key_heads, key_dim), cut(v, value_heads, value_dim)], dim=-1)
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -359,6 +398,15 @@ def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: t
                   conv_weight)
     if not qkv.is_cuda:
         raise RuntimeError("gdn_megakernel runs on the GPU (HIP); got a CPU tensor")
+    run = run_dim(key_dim, value_dim)
+    if run is None:
+        raise ValueError(f"head dims up to 128: this build's kernels cannot hold Dk={key_dim}, Dv={value_dim}")
+    if run != key_dim or run != value_dim:
+        return _padded_megakernel(run, qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, key_heads=key_heads,
+                                  key_dim=key_dim, value_heads=value_heads, value_dim=value_dim, chunk=chunk,
+                                  precision=precision, inverse=inverse, heads_per_step=heads_per_step,
+                                  residuals=residuals, initial_state=initial_state, initial_conv=initial_conv,
+                                  output_final_state=output_final_state)
     plan = GdnPlan(batch=batch, length=length, key_heads=key_heads, key_dim=key_dim, value_heads=value_heads,
                    value_dim=value_dim, taps=0 if conv_weight is None else taps, chunk=chunk,
                    io_dtype=qkv.dtype, gate_dtype=a.dtype, precision=precision, inverse=inverse,
@@ -404,6 +452,12 @@ def gdn_megakernel_normed(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a
         raise ValueError(f"gate must be [{batch}, {length}, {value_heads}, {value_dim}], not {tuple(gate.shape)}")
     if tuple(norm_weight.shape) != (value_dim,):
         raise ValueError(f"norm_weight must be [{value_dim}], not {tuple(norm_weight.shape)}")
+    if not (key_dim == value_dim and key_dim in RUN_DIMS):
+        # padded head dims: the core (padded), then the norm over the Dv lanes on its own
+        out = gdn_megakernel(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, key_heads=key_heads,
+                             key_dim=key_dim, value_heads=value_heads, value_dim=value_dim, chunk=chunk,
+                             precision=precision, inverse=inverse, heads_per_step=heads_per_step, residuals=residuals)
+        return _norm_any_dim(out, gate, norm_weight, eps, segment_ids)
     plan = GdnPlan(batch=batch, length=length, key_heads=key_heads, key_dim=key_dim, value_heads=value_heads,
                    value_dim=value_dim, taps=0 if conv_weight is None else taps, chunk=chunk,
                    io_dtype=qkv.dtype, gate_dtype=a.dtype, precision=precision, inverse=inverse,
@@ -414,6 +468,57 @@ def gdn_megakernel_normed(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a
                              a_log.to(torch.float32).contiguous(), dt_bias.to(torch.float32).contiguous(), conv_w,
                              segment_ids.to(torch.int32).contiguous(), gate.to(qkv.dtype).contiguous(),
                              norm_weight.to(torch.float32).contiguous(), float(eps), shape)
+
+
+def _padded_megakernel(run, qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_heads, key_dim,
+                       value_heads, value_dim, initial_state, initial_conv, output_final_state, **kw):
+    """gdn_megakernel on head dims the kernels do not hold as they are (Dk != Dv, or not a
+    compiled dim): every q, k and v head zero-padded to ``run`` lanes (qkv, the conv weight and
+    history, the initial state) around the kernels at Dk = Dv = run, the outputs cut back. The
+    kernels scale q by run^-1/2; out is linear in q, so it is scaled by (run / Dk)^1/2 to the
+    reference's Dk^-1/2. Gradients flow through the padding (torch's autograd)."""
+    pad = lambda x: pad_qkv(x, key_heads, key_dim, value_heads, value_dim, run)  # noqa: E731
+    init = None
+    if initial_state is not None:
+        if initial_state.shape != (qkv.shape[0], value_heads, key_dim, value_dim):
+            raise ValueError(f"initial_state must be [{qkv.shape[0]}, {value_heads}, {key_dim}, {value_dim}], "
+                             f"not {tuple(initial_state.shape)}")
+        init = torch.nn.functional.pad(initial_state.to(torch.float32), (0, run - value_dim, 0, run - key_dim))
+    if initial_conv is not None and (initial_conv.dim() != 3 or initial_conv.shape[-1] != qkv.shape[-1]):
+        raise ValueError(f"initial_conv must be [B, K-1, {qkv.shape[-1]}], not {tuple(initial_conv.shape)}")
+    res = gdn_megakernel(pad(qkv), a, b, a_log, dt_bias, None if conv_weight is None else pad(conv_weight),
+                         segment_ids, key_heads=key_heads, key_dim=run, value_heads=value_heads, value_dim=run,
+                         initial_state=init, initial_conv=None if initial_conv is None else pad(initial_conv),
+                         output_final_state=output_final_state, **kw)
+    out = res[0] if output_final_state else res
+    out = out[..., :value_dim]
+    if run != key_dim:
+        out = out * math.sqrt(run / key_dim)
+    if not output_final_state:
+        return out
+    _, final, conv_state = res
+    final = final[:, :, :key_dim, :value_dim]
+    if conv_state is not None:
+        conv_state = unpad_qkv(conv_state, key_heads, key_dim, value_heads, value_dim, run)
+    return out, final, conv_state
+
+
+def _norm_any_dim(out, gate, norm_weight, eps, segment_ids):
+    """gated_rmsnorm(out, gate, norm_weight, eps, segment_ids) for any Dv: a dim without norm
+    kernels runs zero-padded to the next one with eps and the weight rescaled so that the mean
+    square over the padded lanes gives the Dv one: mean_P(x^2) + eps Dv/P = (Dv/P)(mean_Dv(x^2)
+    + eps), whose rsqrt carries a factor (P/Dv)^1/2 that the weight takes back."""
+    from .norm import gated_rmsnorm
+
+    dv = out.shape[-1]
+    if dv in NORM_DIMS:
+        return gated_rmsnorm(out, gate, norm_weight, eps, segment_ids=segment_ids)
+    pdim = next(d for d in NORM_DIMS if d >= dv)
+    padding = (0, pdim - dv)
+    w = torch.nn.functional.pad(norm_weight.to(torch.float32) * math.sqrt(dv / pdim), padding)
+    y = gated_rmsnorm(torch.nn.functional.pad(out, padding), torch.nn.functional.pad(gate.to(out.dtype), padding),
+                      w, eps * dv / pdim, segment_ids=segment_ids)
+    return y[..., :dv]
 
 
 def gdn_core_mega(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_heads: int, key_dim: int,

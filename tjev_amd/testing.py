@@ -50,16 +50,17 @@ def cut_segments(length: int, cuts, trailing_pad: int = 0) -> np.ndarray:
 
 def gdn_inputs(*, batch: int, length: int, key_heads: int, value_heads: int, dim: int, taps: int = 4,
                seed: int = 0, dtype=torch.float32, segments="one", cuts=None, trailing_pad: int = 0,
-               style: str = "baseline", device="cpu"):
+               style: str = "baseline", device="cpu", key_dim: int | None = None, value_dim: int | None = None):
     """(qkv, a, b, a_log, dt_bias, conv_w, segment_ids) as torch tensors.
 
     style "baseline" (the benchmark configurations): qkv, a, b, dt_bias ~ N(0,1), A_log ~ U(0, ln 16),
     conv w ~ N(0, 0.5). style "reference" (test_gdn_mega.py:25-41): A_log, dt_bias ~ 0.5 N(0,1).
     ``segments``: "one" (id 1 everywhere), "geometric" (varlen packing), "cuts" (``cuts``,
     plus ``trailing_pad`` segment-0 tokens) or "random4" (4 random cuts per row, as the
-    reference tests draw them). qkv, a and b are cast to ``dtype``; the rest stay fp32."""
+    reference tests draw them). qkv, a and b are cast to ``dtype``; the rest stay fp32.
+    ``key_dim`` / ``value_dim`` (default ``dim``) give the heads' widths in qkv."""
     rng = np.random.default_rng(seed)
-    width = 2 * key_heads * dim + value_heads * dim
+    width = 2 * key_heads * (key_dim or dim) + value_heads * (value_dim or dim)
     qkv = rng.standard_normal((batch, length, width), dtype=np.float32)
     a = rng.standard_normal((batch, length, value_heads), dtype=np.float32)
     b = rng.standard_normal((batch, length, value_heads), dtype=np.float32)

@@ -18,7 +18,7 @@ import ctypes
 import torch
 
 from . import _lib
-from .gdn import INVERSE_BLOCKS, LANES, PRECISIONS, GdnPlan, _ptr, heads_per_block
+from .gdn import INVERSE_BLOCKS, LANES, PRECISIONS, GdnPlan, _ptr, heads_per_block, run_dim
 
 _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
 
@@ -93,12 +93,15 @@ def chunk_gated_delta_rule_v2(q, k, v, g, beta, segment_ids=None, *, chunk: int 
                               residuals: str = "states", initial_state: torch.Tensor | None = None,
                               output_final_state: bool = False):
     """q, k [B,T,Hk,Dk] (Hk divides H), v [B,T,H,Dv], g, beta [B,T,H] -> out [B,T,H,Dv] in v's
-    dtype (pallas_tpu_v2.py:541-582). T is padded to whole chunks with segment-0 tokens.
+    dtype (pallas_tpu_v2.py:541-582). T is padded to whole chunks with zero inputs and the last
+    token's segment id. Head dims the kernels do not hold as they are (Dk != Dv, or not 16, 32,
+    64 or 128; up to 128) run zero-padded to the next compiled dim (q and k are taken as given,
+    so zero lanes change nothing), the outputs cut back.
 
     Beyond the reference's v2 kernel: ``initial_state`` [B, H, Dk, Dv] fp32 continues a sequence
     (xla.py:170-262's ``initial_state``: token 0's segment reads it), and ``output_final_state``
     returns (out, final_state [B, H, Dk, Dv] fp32), the state after token T-1; gradients flow
-    through both (the final state's needs T a multiple of the kernels' chunk)."""
+    through both, for any T."""
     if precision not in PRECISIONS:
         raise ValueError(f"precision in {PRECISIONS}")
     if inverse not in INVERSE_BLOCKS:
@@ -116,6 +119,22 @@ def chunk_gated_delta_rule_v2(q, k, v, g, beta, segment_ids=None, *, chunk: int 
                          f"beta {tuple(beta.shape)} do not agree")
     if not v.is_cuda:
         raise RuntimeError("chunk_gated_delta_rule_v2 runs on the GPU (HIP); got a CPU tensor")
+    run = run_dim(dk, dv)
+    if run is None:
+        raise ValueError(f"head dims up to 128: this build's kernels cannot hold Dk={dk}, Dv={dv}")
+    if run != dk or run != dv:
+        if initial_state is not None and initial_state.shape != (batch, heads, dk, dv):
+            raise ValueError(f"initial_state must be [{batch}, {heads}, {dk}, {dv}], not {tuple(initial_state.shape)}")
+        padk = lambda x: torch.nn.functional.pad(x, (0, run - dk))  # noqa: E731
+        init = None if initial_state is None else torch.nn.functional.pad(
+            initial_state.to(torch.float32), (0, run - dv, 0, run - dk))
+        res = chunk_gated_delta_rule_v2(padk(q), padk(k), torch.nn.functional.pad(v, (0, run - dv)), g, beta,
+                                        segment_ids, chunk=chunk, precision=precision, inverse=inverse,
+                                        heads_per_step=heads_per_step, residuals=residuals, initial_state=init,
+                                        output_final_state=output_final_state)
+        if not output_final_state:
+            return res[..., :dv]
+        return res[0][..., :dv], res[1][:, :, :dk, :dv]
     if segment_ids is None:
         segment_ids = torch.ones((batch, length), dtype=torch.int32, device=v.device)
     qk_dtype = q.dtype if q.dtype in _DTYPES else torch.float32
