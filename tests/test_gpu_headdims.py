@@ -109,3 +109,34 @@ def test_padded_head_dims_v2():
     print("v2 Dk=64 Dv=96:", {k_: f"{v_:.1e}" for k_, v_ in errs.items()}, flush=True)
     for k_, v_ in errs.items():
         assert v_ <= 1e-5, (k_, v_)
+
+
+@pytest.mark.parametrize("shape,inplace", [((2, 64, 4, 128), False), ((1, 48, 2, 48), True)],
+                         ids=["Dk64-Dv128", "Dk48-Dv48-inplace"])
+def test_padded_head_dims_prefill_then_decode(shape, inplace):
+    """Serving at padded head dims: a prefill of T tokens then three decode steps equal the
+    megakernel over T + 3 tokens (fp32), the state updated in place when asked."""
+    from tjev_amd import gdn_megakernel
+    from tjev_amd.serve import gdn_decode_step, gdn_prefill
+
+    hk, dk, h, dv = shape
+    length, extra = 150, 3
+    (qkv, a, b, a_log, dt_bias, w, seg), _ = case_inputs(2, length + extra, hk, h, 0, dk=dk, dv=dv,
+                                                         segments="one", seed=11)
+    qkv, a, b, a_log, dt_bias, w, seg = (x.cuda() for x in (qkv, a, b, a_log, dt_bias, w, seg))
+    kw = dict(key_heads=hk, key_dim=dk, value_heads=h, value_dim=dv)
+    full = gdn_megakernel(qkv, a, b, a_log, dt_bias, w, seg, chunk=64, precision="highest", **kw)
+    _, state, hist = gdn_prefill(qkv[:, :length], a[:, :length], b[:, :length], a_log, dt_bias, w, seg[:, :length],
+                                 chunk=64, precision="highest", **kw)
+    assert state.shape == (2, h, dk, dv) and hist.shape == (2, 3, qkv.shape[-1])
+    outs = []
+    for t in range(length, length + extra):
+        o, hist, st = gdn_decode_step(qkv[:, t], a[:, t], b[:, t], a_log, dt_bias, w, hist, state, inplace=inplace,
+                                      **kw)
+        assert (st.data_ptr() == state.data_ptr()) == inplace
+        state = st
+        outs.append(o)
+    torch.cuda.synchronize()
+    err = rel(torch.stack(outs, 1).double().cpu(), full[:, length:].double().cpu())
+    print(f"prefill + decode Dk={dk} Dv={dv}: {err:.1e}", flush=True)
+    assert err <= 1e-5

@@ -14,11 +14,12 @@ belongs to; a new request starts from a fresh prefill.
 from __future__ import annotations
 
 import ctypes
+import math
 
 import torch
 
 from . import _lib
-from .gdn import GdnPlan, _check, _ptr
+from .gdn import GdnPlan, _check, _ptr, pad_qkv, run_dim, unpad_qkv
 
 _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
 
@@ -35,6 +36,21 @@ def gdn_prefill(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_head
                   conv_weight)
     if not qkv.is_cuda:
         raise RuntimeError("gdn_prefill runs on the GPU (HIP); got a CPU tensor")
+    run = run_dim(key_dim, value_dim)
+    if run is None:
+        raise ValueError(f"head dims up to 128: this build's kernels cannot hold Dk={key_dim}, Dv={value_dim}")
+    if run != key_dim or run != value_dim:  # zero-padded heads (gdn_megakernel's padded route)
+        pad = lambda x: None if x is None else pad_qkv(x, key_heads, key_dim, value_heads, value_dim, run)  # noqa: E731
+        init = None if initial_state is None else torch.nn.functional.pad(
+            initial_state.to(torch.float32), (0, run - value_dim, 0, run - key_dim))
+        out, state, conv_state = gdn_prefill(
+            pad(qkv), a, b, a_log, dt_bias, pad(conv_weight), segment_ids, key_heads=key_heads, key_dim=run,
+            value_heads=value_heads, value_dim=run, chunk=chunk, precision=precision, inverse=inverse,
+            heads_per_step=heads_per_step, initial_state=init, initial_conv=pad(initial_conv))
+        out = out[..., :value_dim] * math.sqrt(run / key_dim) if run != key_dim else out[..., :value_dim]
+        if conv_state is not None:
+            conv_state = unpad_qkv(conv_state, key_heads, key_dim, value_heads, value_dim, run)
+        return out.contiguous(), state[:, :, :key_dim, :value_dim].contiguous(), conv_state
     plan = GdnPlan(batch=batch, length=length, key_heads=key_heads, key_dim=key_dim, value_heads=value_heads,
                    value_dim=value_dim, taps=0 if conv_weight is None else taps, chunk=chunk, io_dtype=qkv.dtype,
                    gate_dtype=a.dtype, precision=precision, inverse=inverse, heads_per_step=heads_per_step)
@@ -83,6 +99,22 @@ def gdn_decode_step(qkv, a, b, a_log, dt_bias, conv_weight, conv_state, state, *
         raise ValueError(f"state must be fp32 [{batch}, {value_heads}, {key_dim}, {value_dim}]")
     if taps > 1 and (conv_state is None or conv_state.shape != (batch, taps - 1, width)):
         raise ValueError(f"conv_state must be [{batch}, {taps - 1}, {width}]")
+    run = run_dim(key_dim, value_dim)
+    if run is None:
+        raise ValueError(f"head dims up to 128: this build's kernels cannot hold Dk={key_dim}, Dv={value_dim}")
+    if run != key_dim or run != value_dim:  # zero-padded heads (gdn_megakernel's padded route)
+        pad = lambda x: None if x is None else pad_qkv(x, key_heads, key_dim, value_heads, value_dim, run)  # noqa: E731
+        out, hist_out, st = gdn_decode_step(
+            pad(qkv), a, b, a_log, dt_bias, pad(conv_weight), pad(conv_state),
+            torch.nn.functional.pad(state, (0, run - value_dim, 0, run - key_dim)), key_heads=key_heads,
+            key_dim=run, value_heads=value_heads, value_dim=run)
+        out = out[..., :value_dim] * math.sqrt(run / key_dim) if run != key_dim else out[..., :value_dim]
+        st = st[:, :, :key_dim, :value_dim]
+        if inplace:
+            state.copy_(st)
+            st = state
+        hist_out = None if hist_out is None else unpad_qkv(hist_out, key_heads, key_dim, value_heads, value_dim, run)
+        return out.contiguous(), hist_out, st.contiguous() if not inplace else st
     lib = _lib.load()
     p = _lib.Params(batch, 1, key_heads, key_dim, value_heads, value_dim, taps, 64, _DTYPES[qkv.dtype],
                     _DTYPES[a.dtype], 1, 0, 0, 0)
