@@ -32,14 +32,14 @@ def _mm32(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return torch.mm(a, b, out_dtype=torch.float32)
 
 
-def _addmm32(c: torch.Tensor, a: torch.Tensor, b: torch.Tensor, alpha: float = 1.0) -> torch.Tensor:
-    """c + alpha a @ b in fp32 (c fp32), the product accumulated in fp32: one GEMM with c as its
-    addend where the backend has the mixed-precision form, else a product and an add."""
+def _addmm32_(c: torch.Tensor, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """c += a @ b in place (c fp32), the product accumulated in fp32: one GEMM with c as its
+    addend and output (an out-of-place addmm first copies c, 168 MB at the 4B block's dx)."""
     if a.dtype == torch.float32:
-        return torch.addmm(c, a, b.to(torch.float32), alpha=alpha)
+        return c.addmm_(a, b.to(torch.float32))
     if a.is_cuda:
-        return torch.addmm(c, a, b, alpha=alpha, out_dtype=torch.float32)
-    return c + alpha * _mm32(a, b)
+        return torch.addmm(c, a, b, out_dtype=torch.float32, out=c)
+    return c.add_(_mm32(a, b))
 
 
 def _mm32_tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
@@ -59,8 +59,12 @@ def _mm32_tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 
 def _merge(w: torch.Tensor, a: torch.Tensor, b: torch.Tensor, s: float, dtype) -> torch.Tensor:
     """W' = (W + s A B) rounded once to ``dtype``, A and B rounded to it first and their product
-    accumulated in fp32 (lora.py:284-295, ``_merge``)."""
-    return _addmm32(w.to(torch.float32), a.to(dtype), b.to(dtype), alpha=s).to(dtype)
+    accumulated in fp32 (lora.py:284-295, ``_merge``): one GEMM whose epilogue adds W in fp32
+    and rounds once (W in ``dtype`` is exact in fp32)."""
+    w, a, b = w.to(dtype), a.to(dtype), b.to(dtype)
+    if dtype == torch.float32 or w.is_cuda:
+        return torch.addmm(w, a, b, alpha=s)
+    return (w.to(torch.float32) + s * _mm32(a, b)).to(dtype)
 
 
 class _MergedLoRA(torch.autograd.Function):
@@ -90,22 +94,28 @@ class _MergedLoRA(torch.autograd.Function):
                else dy.to(dtype).contiguous() for dy, m in zip(dys, merged)]
         # dx = sum_i dy_i W'_i^T, each product and the sum in fp32, rounded once (lora.py:333-338);
         # W'^T read in place. The narrow projections (b, a) as one product over their joined
-        # outputs (a small copy), the wide ones each with the running sum as its addend.
-        wide = [i for i in range(n) if merged[i].shape[1] >= 256]
-        narrow = [i for i in range(n) if merged[i].shape[1] < 256]
-        dx = None
-        if narrow:
-            dyn = dys[narrow[0]] if len(narrow) == 1 else torch.cat([dys[i] for i in narrow], dim=1)
-            mn = merged[narrow[0]] if len(narrow) == 1 else torch.cat([merged[i] for i in narrow], dim=1)
-            dx = _mm32(dyn, mn.t())
-        for i in wide:
-            dx = _mm32(dys[i], merged[i].t()) if dx is None else _addmm32(dx, dys[i], merged[i].t())
-        dx = dx.to(dtype)
+        # outputs (a small copy), the wide ones each added onto the running sum in place. One
+        # projection alone: its product rounded once by the GEMM itself.
+        if n == 1:
+            dx = dys[0] @ merged[0].t()
+        else:
+            wide = [i for i in range(n) if merged[i].shape[1] >= 256]
+            narrow = [i for i in range(n) if merged[i].shape[1] < 256]
+            dx = None
+            if narrow:
+                dyn = dys[narrow[0]] if len(narrow) == 1 else torch.cat([dys[i] for i in narrow], dim=1)
+                mn = merged[narrow[0]] if len(narrow) == 1 else torch.cat([merged[i] for i in narrow], dim=1)
+                dx = _mm32(dyn, mn.t())
+            for i in wide:
+                dx = _mm32(dys[i], merged[i].t()) if dx is None else _addmm32_(dx, dys[i], merged[i].t())
+            dx = dx.to(dtype)
         # the adapters: one pass over x for every A, x^T [s_1 t_1 | s_2 t_2 | ...]
         ranks = [a.shape[1] for a in a_s]
         a_cat = a_s[0].to(dtype) if n == 1 else torch.cat([a.to(dtype) for a in a_s], dim=1)
         xa = x @ a_cat
-        ts = [(s * _mm32(dy, b.to(dtype).t())).to(dtype) for dy, b, s in zip(dys, b_s, scales)]
+        ts = [torch.mul(_mm32(dy, b.to(dtype).t()), s, out=torch.empty((x.shape[0], b.shape[0]), dtype=dtype,
+                                                                         device=x.device))
+              for dy, b, s in zip(dys, b_s, scales)]  # s t_i, rounded once to dtype
         t = ts[0] if n == 1 else torch.cat(ts, dim=1)
         da = torch.split(_mm32_tn(x, t), ranks, dim=1)
         xas = torch.split(xa, ranks, dim=1)
