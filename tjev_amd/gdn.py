@@ -392,7 +392,10 @@ def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: t
     reads them), and ``output_final_state`` returns (out, final_state [B, H, Dk, Dv] fp32,
     conv_state [B, K-1, W] or None), the state after token T-1 and the last K-1 raw rows of its
     segment, which the next piece takes as its initial state and history. Gradients flow through
-    all of them, for any T."""
+    all of them, for any T.
+
+    Head dims: Dk = Dv in (16, 32, 64, 128) run as they are; other widths up to 128, Dk != Dv
+    included, run zero-padded to the next of those (``run_dim``, ``_padded_megakernel``)."""
     batch, length, width = qkv.shape
     taps = _check(precision, inverse, chunk, width, key_heads, key_dim, value_heads, value_dim, heads_per_step,
                   conv_weight)
