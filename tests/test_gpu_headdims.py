@@ -1,7 +1,9 @@
 """Head dims the kernels do not hold as they are (GPU): Dk != Dv, which the reference accepts
-(pallas_tpu_mega.py:597-615, pallas_tpu_v2.py:528-538), and widths other than 16, 32, 64, 128
-(up to 128). The Python operators run them zero-padded to the next compiled dim (run_dim in
-tjev_amd/gdn.py) and cut the outputs back; every output and gradient is held to the fp32 bar
+(pallas_tpu_mega.py:597-615, pallas_tpu_v2.py:528-538), widths other than 16, 32, 64, 128 (up
+to 128), and value heads wider than 128 (the reference's TPU kernels take multiples of 128:
+Dv = 256 with Dk = 128). The Python operators run the first two zero-padded to the next
+compiled dim (run_dim in tjev_amd/gdn.py) and the wide value heads as groups of value columns
+(value_groups), and cut or join the outputs; every output and gradient is held to the fp32 bar
 against the oracle, which computes at the given widths.
 """
 
@@ -19,6 +21,8 @@ SHAPES = [  # (Hk, Dk, H, Dv)
     (2, 128, 4, 64),
     (1, 48, 2, 48),
     (2, 32, 2, 96),
+    (2, 128, 4, 256),  # two groups of 128 value columns
+    (1, 32, 2, 300),   # groups of 128, 128 and 44 (padded)
 ]
 
 
@@ -37,7 +41,8 @@ def test_padded_head_dims_fp32(shape, conv):
             assert errs[k] <= (5e-5 if k in ("A_log", "dt_bias") else 1e-5), (k, errs[k])
 
 
-@pytest.mark.parametrize("shape", [(2, 64, 4, 128), (2, 128, 4, 96)], ids=["Dk64-Dv128", "Dk128-Dv96"])
+@pytest.mark.parametrize("shape", [(2, 64, 4, 128), (2, 128, 4, 96), (2, 64, 4, 256), (1, 128, 2, 192)],
+                         ids=["Dk64-Dv128", "Dk128-Dv96", "Dk64-Dv256", "Dk128-Dv192"])
 def test_padded_head_dims_state_and_norm(shape):
     """The continued sequence (initial state and conv history in, final ones out, gradients
     through all of them) and the normed operator at padded head dims, fp32, against the oracle
@@ -81,13 +86,15 @@ def test_padded_head_dims_state_and_norm(shape):
     assert err <= 1e-5
 
 
-def test_padded_head_dims_v2():
-    """The v2 operator at Dk != Dv with a state: against the fp64 chunked rule."""
+@pytest.mark.parametrize("dv", [96, 200])
+def test_padded_head_dims_v2(dv):
+    """The v2 operator at Dk != Dv with a state (Dv = 200: two groups of value columns, the
+    second padded): against the fp64 chunked rule."""
     from oracle.gdn_oracle import chunk_gated_delta_rule
     from tjev_amd.v2 import chunk_gated_delta_rule as v2_rule
 
     gen = torch.Generator().manual_seed(9)
-    B, T, hk, dk, h, dv = 1, 141, 2, 64, 4, 96
+    B, T, hk, dk, h = 1, 141, 2, 64, 4
     q, k = (torch.nn.functional.normalize(torch.randn((B, T, hk, dk), generator=gen), dim=-1) for _ in range(2))
     q = q * dk ** -0.5
     v = torch.randn((B, T, h, dv), generator=gen)
@@ -106,13 +113,14 @@ def test_padded_head_dims_v2():
     r_grads = torch.autograd.grad((r_out * cot.double()).sum() + (r_fin * d_fin.double()).sum(), ref)
     errs = {"out": rel(out.cpu(), r_out), "final": rel(fin.cpu(), r_fin)}
     errs.update({n: rel(x.cpu(), y) for n, x, y in zip(("q", "k", "v", "g", "beta", "s0"), grads, r_grads)})
-    print("v2 Dk=64 Dv=96:", {k_: f"{v_:.1e}" for k_, v_ in errs.items()}, flush=True)
+    print(f"v2 Dk=64 Dv={dv}:", {k_: f"{v_:.1e}" for k_, v_ in errs.items()}, flush=True)
     for k_, v_ in errs.items():
         assert v_ <= 1e-5, (k_, v_)
 
 
-@pytest.mark.parametrize("shape,inplace", [((2, 64, 4, 128), False), ((1, 48, 2, 48), True)],
-                         ids=["Dk64-Dv128", "Dk48-Dv48-inplace"])
+@pytest.mark.parametrize("shape,inplace", [((2, 64, 4, 128), False), ((1, 48, 2, 48), True),
+                                           ((2, 64, 4, 256), True), ((1, 32, 2, 160), False)],
+                         ids=["Dk64-Dv128", "Dk48-Dv48-inplace", "Dk64-Dv256-inplace", "Dk32-Dv160"])
 def test_padded_head_dims_prefill_then_decode(shape, inplace):
     """Serving at padded head dims: a prefill of T tokens then three decode steps equal the
     megakernel over T + 3 tokens (fp32), the state updated in place when asked."""

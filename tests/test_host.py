@@ -505,3 +505,22 @@ def test_head_dims_run_padded_to_a_compiled_dim():
     assert torch.all(heads[..., :dk][:, :2 * hk] == x[:, :2 * hk * dk].reshape(5, 2 * hk, dk))
     assert torch.all(heads[:, :2 * hk, dk:] == 0) and torch.all(heads[:, 2 * hk:, dv:] == 0)
     assert torch.equal(unpad_qkv(padded, hk, dk, h, dv, 64), x)
+
+
+def test_wide_value_heads_run_as_column_groups():
+    """Value heads wider than 128 (Dk <= 128) run as groups of at most 128 value columns; the
+    lanes of qkv cut into each group's and the conv history joined back round-trip; Dk above 128
+    has no split."""
+    from tjev_amd.gdn import merge_value_cols, value_cols, value_groups
+
+    assert value_groups(128, 128) is None and value_groups(64, 96) is None and value_groups(256, 256) is None
+    assert value_groups(128, 256) == [(0, 128), (128, 128)]
+    assert value_groups(32, 300) == [(0, 128), (128, 128), (256, 44)]
+    hk, dk, h, dv = 2, 16, 3, 300
+    x = torch.arange(4 * (2 * hk * dk + h * dv), dtype=torch.float32).reshape(4, -1)
+    parts = [value_cols(x, hk, dk, h, dv, c, w) for c, w in value_groups(dk, dv)]
+    for (c, w), p in zip(value_groups(dk, dv), parts):
+        assert p.shape == (4, 2 * hk * dk + h * w)
+        assert torch.equal(p[:, :2 * hk * dk], x[:, :2 * hk * dk])
+        assert torch.equal(p[:, 2 * hk * dk:].reshape(4, h, w), x[:, 2 * hk * dk:].reshape(4, h, dv)[..., c:c + w])
+    assert torch.equal(merge_value_cols(parts, hk, dk, h), x)

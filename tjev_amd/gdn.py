@@ -92,6 +92,40 @@ def unpad_qkv(x: torch.Tensor, key_heads: int, key_dim: int, value_heads: int, v
     return torch.cat([cut(q, key_heads, key_dim), cut(k, key_heads, key_dim), cut(v, value_heads, value_dim)], dim=-1)
 
 
+def value_groups(key_dim: int, value_dim: int) -> list[tuple[int, int]] | None:
+    """Value heads wider than the kernels hold (Dv > 128, with Dk <= 128): the value columns cut
+    into groups of at most 128, as (first column, width), each run as a problem of its own
+    (which may in turn be padded, ``run_dim``). In the delta rule every value column of v, of the
+    state and of the output evolves on its own (v_new = v - S^T k, S += beta k v_new^T and
+    o = S^T q act column by column; q, k and the gates are shared), so the groups' outputs and
+    states are the whole problem's columns and its gradients their sums. None when no split is
+    needed, or when Dk itself exceeds 128 (no split holds that)."""
+    top = RUN_DIMS[-1]
+    if key_dim > top or value_dim <= top:
+        return None
+    return [(c, min(top, value_dim - c)) for c in range(0, value_dim, top)]
+
+
+def value_cols(x: torch.Tensor, key_heads: int, key_dim: int, value_heads: int, value_dim: int, first: int,
+               width: int) -> torch.Tensor:
+    """x [..., 2 Hk Dk + H Dv] (qkv's lanes: qkv, the conv weight, the conv history) with each
+    value head cut to its columns first .. first + width - 1; the q and k lanes as they are."""
+    kq = 2 * key_heads * key_dim
+    lead = x.shape[:-1]
+    v = x[..., kq:].reshape(*lead, value_heads, value_dim)[..., first:first + width]
+    return torch.cat([x[..., :kq], v.reshape(*lead, value_heads * width)], dim=-1)
+
+
+def merge_value_cols(parts: list[torch.Tensor], key_heads: int, key_dim: int, value_heads: int) -> torch.Tensor:
+    """The inverse of value_cols over a split's groups for a tensor whose q and k lanes are the
+    same in every group (the conv history): those lanes from the first group, then each value
+    head's columns from the groups in order."""
+    kq = 2 * key_heads * key_dim
+    lead = parts[0].shape[:-1]
+    vs = [p[..., kq:].reshape(*lead, value_heads, -1) for p in parts]
+    return torch.cat([parts[0][..., :kq], torch.cat(vs, dim=-1).reshape(*lead, -1)], dim=-1)
+
+
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -395,15 +429,24 @@ def gdn_megakernel(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a_log: t
     all of them, for any T.
 
     Head dims: Dk = Dv in (16, 32, 64, 128) run as they are; other widths up to 128, Dk != Dv
-    included, run zero-padded to the next of those (``run_dim``, ``_padded_megakernel``)."""
+    included, run zero-padded to the next of those (``run_dim``, ``_padded_megakernel``); value
+    heads wider than 128 (with Dk <= 128) run as groups of value columns (``value_groups``,
+    ``_split_megakernel``). Dk above 128 is refused."""
     batch, length, width = qkv.shape
     taps = _check(precision, inverse, chunk, width, key_heads, key_dim, value_heads, value_dim, heads_per_step,
                   conv_weight)
     if not qkv.is_cuda:
         raise RuntimeError("gdn_megakernel runs on the GPU (HIP); got a CPU tensor")
+    groups = value_groups(key_dim, value_dim)
+    if groups is not None:
+        return _split_megakernel(groups, qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, key_heads=key_heads,
+                                 key_dim=key_dim, value_heads=value_heads, value_dim=value_dim, chunk=chunk,
+                                 precision=precision, inverse=inverse, heads_per_step=heads_per_step,
+                                 residuals=residuals, initial_state=initial_state, initial_conv=initial_conv,
+                                 output_final_state=output_final_state)
     run = run_dim(key_dim, value_dim)
     if run is None:
-        raise ValueError(f"head dims up to 128: this build's kernels cannot hold Dk={key_dim}, Dv={value_dim}")
+        raise ValueError(f"key dims up to 128: this build's kernels cannot hold Dk={key_dim}, Dv={value_dim}")
     if run != key_dim or run != value_dim:
         return _padded_megakernel(run, qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, key_heads=key_heads,
                                   key_dim=key_dim, value_heads=value_heads, value_dim=value_dim, chunk=chunk,
@@ -456,7 +499,10 @@ def gdn_megakernel_normed(qkv: torch.Tensor, a: torch.Tensor, b: torch.Tensor, a
     if tuple(norm_weight.shape) != (value_dim,):
         raise ValueError(f"norm_weight must be [{value_dim}], not {tuple(norm_weight.shape)}")
     if not (key_dim == value_dim and key_dim in RUN_DIMS):
-        # padded head dims: the core (padded), then the norm over the Dv lanes on its own
+        # padded or split head dims: the core (padded or by value columns), then the norm over
+        # the Dv lanes on its own
+        if value_dim > NORM_DIMS[-1]:
+            raise ValueError(f"the gated RMSNorm's kernels hold Dv up to {NORM_DIMS[-1]}, not {value_dim}")
         out = gdn_megakernel(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, key_heads=key_heads,
                              key_dim=key_dim, value_heads=value_heads, value_dim=value_dim, chunk=chunk,
                              precision=precision, inverse=inverse, heads_per_step=heads_per_step, residuals=residuals)
@@ -503,6 +549,33 @@ def _padded_megakernel(run, qkv, a, b, a_log, dt_bias, conv_weight, segment_ids,
     final = final[:, :, :key_dim, :value_dim]
     if conv_state is not None:
         conv_state = unpad_qkv(conv_state, key_heads, key_dim, value_heads, value_dim, run)
+    return out, final, conv_state
+
+
+def _split_megakernel(groups, qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_heads, key_dim,
+                      value_heads, value_dim, initial_state, initial_conv, output_final_state, **kw):
+    """gdn_megakernel on value heads wider than the kernels hold: one call per group of value
+    columns (``value_groups``), each on qkv with every value head cut to the group's columns
+    (the conv weight and history alike, the initial state by its columns); outputs and final
+    states are joined by columns, the conv history takes the q and k lanes from the first group.
+    Gradients of the shared inputs (q and k lanes, gates, A_log, dt_bias, conv weight) sum over
+    the groups through torch's autograd."""
+    if initial_state is not None and initial_state.shape != (qkv.shape[0], value_heads, key_dim, value_dim):
+        raise ValueError(f"initial_state must be [{qkv.shape[0]}, {value_heads}, {key_dim}, {value_dim}], "
+                         f"not {tuple(initial_state.shape)}")
+    if initial_conv is not None and (initial_conv.dim() != 3 or initial_conv.shape[-1] != qkv.shape[-1]):
+        raise ValueError(f"initial_conv must be [B, K-1, {qkv.shape[-1]}], not {tuple(initial_conv.shape)}")
+    cut = lambda x, c, w: None if x is None else value_cols(x, key_heads, key_dim, value_heads, value_dim, c, w)  # noqa: E731
+    res = [gdn_megakernel(cut(qkv, c, w), a, b, a_log, dt_bias, cut(conv_weight, c, w), segment_ids,
+                          key_heads=key_heads, key_dim=key_dim, value_heads=value_heads, value_dim=w,
+                          initial_state=None if initial_state is None else initial_state[..., c:c + w],
+                          initial_conv=cut(initial_conv, c, w), output_final_state=output_final_state, **kw)
+           for c, w in groups]
+    if not output_final_state:
+        return torch.cat(res, dim=-1)
+    out = torch.cat([r[0] for r in res], dim=-1)
+    final = torch.cat([r[1] for r in res], dim=-1)
+    conv_state = None if res[0][2] is None else merge_value_cols([r[2] for r in res], key_heads, key_dim, value_heads)
     return out, final, conv_state
 
 

@@ -19,7 +19,7 @@ import math
 import torch
 
 from . import _lib
-from .gdn import GdnPlan, _check, _ptr, pad_qkv, run_dim, unpad_qkv
+from .gdn import GdnPlan, _check, _ptr, merge_value_cols, pad_qkv, run_dim, unpad_qkv, value_cols, value_groups
 
 _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
 
@@ -36,9 +36,25 @@ def gdn_prefill(qkv, a, b, a_log, dt_bias, conv_weight, segment_ids, *, key_head
                   conv_weight)
     if not qkv.is_cuda:
         raise RuntimeError("gdn_prefill runs on the GPU (HIP); got a CPU tensor")
+    groups = value_groups(key_dim, value_dim)
+    if groups is not None:  # value heads wider than 128: groups of value columns (gdn_megakernel's split)
+        if initial_state is not None and initial_state.shape != (batch, value_heads, key_dim, value_dim):
+            raise ValueError(f"initial_state must be [{batch}, {value_heads}, {key_dim}, {value_dim}], "
+                             f"not {tuple(initial_state.shape)}")
+        cut = lambda x, c, w: None if x is None else value_cols(  # noqa: E731
+            x, key_heads, key_dim, value_heads, value_dim, c, w)
+        res = [gdn_prefill(cut(qkv, c, w), a, b, a_log, dt_bias, cut(conv_weight, c, w), segment_ids,
+                           key_heads=key_heads, key_dim=key_dim, value_heads=value_heads, value_dim=w, chunk=chunk,
+                           precision=precision, inverse=inverse, heads_per_step=heads_per_step,
+                           initial_state=None if initial_state is None else initial_state[..., c:c + w],
+                           initial_conv=cut(initial_conv, c, w))
+               for c, w in groups]
+        conv_state = None if res[0][2] is None else merge_value_cols([r[2] for r in res], key_heads, key_dim,
+                                                                       value_heads)
+        return torch.cat([r[0] for r in res], dim=-1), torch.cat([r[1] for r in res], dim=-1), conv_state
     run = run_dim(key_dim, value_dim)
     if run is None:
-        raise ValueError(f"head dims up to 128: this build's kernels cannot hold Dk={key_dim}, Dv={value_dim}")
+        raise ValueError(f"key dims up to 128: this build's kernels cannot hold Dk={key_dim}, Dv={value_dim}")
     if run != key_dim or run != value_dim:  # zero-padded heads (gdn_megakernel's padded route)
         pad = lambda x: None if x is None else pad_qkv(x, key_heads, key_dim, value_heads, value_dim, run)  # noqa: E731
         init = None if initial_state is None else torch.nn.functional.pad(
@@ -99,9 +115,25 @@ def gdn_decode_step(qkv, a, b, a_log, dt_bias, conv_weight, conv_state, state, *
         raise ValueError(f"state must be fp32 [{batch}, {value_heads}, {key_dim}, {value_dim}]")
     if taps > 1 and (conv_state is None or conv_state.shape != (batch, taps - 1, width)):
         raise ValueError(f"conv_state must be [{batch}, {taps - 1}, {width}]")
+    groups = value_groups(key_dim, value_dim)
+    if groups is not None:  # value heads wider than 128: groups of value columns (gdn_megakernel's split)
+        cut = lambda x, c, w: None if x is None else value_cols(  # noqa: E731
+            x, key_heads, key_dim, value_heads, value_dim, c, w)
+        res = [gdn_decode_step(cut(qkv, c, w), a, b, a_log, dt_bias, cut(conv_weight, c, w), cut(conv_state, c, w),
+                               state[..., c:c + w], key_heads=key_heads, key_dim=key_dim, value_heads=value_heads,
+                               value_dim=w)
+               for c, w in groups]
+        out = torch.cat([r[0] for r in res], dim=-1)
+        hist_out = None if res[0][1] is None else merge_value_cols([r[1] for r in res], key_heads, key_dim,
+                                                                     value_heads)
+        st = torch.cat([r[2] for r in res], dim=-1)
+        if inplace:
+            state.copy_(st)
+            st = state
+        return out, hist_out, st
     run = run_dim(key_dim, value_dim)
     if run is None:
-        raise ValueError(f"head dims up to 128: this build's kernels cannot hold Dk={key_dim}, Dv={value_dim}")
+        raise ValueError(f"key dims up to 128: this build's kernels cannot hold Dk={key_dim}, Dv={value_dim}")
     if run != key_dim or run != value_dim:  # zero-padded heads (gdn_megakernel's padded route)
         pad = lambda x: None if x is None else pad_qkv(x, key_heads, key_dim, value_heads, value_dim, run)  # noqa: E731
         out, hist_out, st = gdn_decode_step(

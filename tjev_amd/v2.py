@@ -18,7 +18,7 @@ import ctypes
 import torch
 
 from . import _lib
-from .gdn import INVERSE_BLOCKS, LANES, PRECISIONS, GdnPlan, _ptr, heads_per_block, run_dim
+from .gdn import INVERSE_BLOCKS, LANES, PRECISIONS, GdnPlan, _ptr, heads_per_block, run_dim, value_groups
 
 _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
 
@@ -96,7 +96,9 @@ def chunk_gated_delta_rule_v2(q, k, v, g, beta, segment_ids=None, *, chunk: int 
     dtype (pallas_tpu_v2.py:541-582). T is padded to whole chunks with zero inputs and the last
     token's segment id. Head dims the kernels do not hold as they are (Dk != Dv, or not 16, 32,
     64 or 128; up to 128) run zero-padded to the next compiled dim (q and k are taken as given,
-    so zero lanes change nothing), the outputs cut back.
+    so zero lanes change nothing), the outputs cut back; value heads wider than 128 (Dk <= 128)
+    run as groups of value columns, each column of v, the state and the output being
+    independent of the others.
 
     Beyond the reference's v2 kernel: ``initial_state`` [B, H, Dk, Dv] fp32 continues a sequence
     (xla.py:170-262's ``initial_state``: token 0's segment reads it), and ``output_final_state``
@@ -119,9 +121,21 @@ def chunk_gated_delta_rule_v2(q, k, v, g, beta, segment_ids=None, *, chunk: int 
                          f"beta {tuple(beta.shape)} do not agree")
     if not v.is_cuda:
         raise RuntimeError("chunk_gated_delta_rule_v2 runs on the GPU (HIP); got a CPU tensor")
+    groups = value_groups(dk, dv)
+    if groups is not None:  # value heads wider than 128: groups of value columns (value_groups)
+        if initial_state is not None and initial_state.shape != (batch, heads, dk, dv):
+            raise ValueError(f"initial_state must be [{batch}, {heads}, {dk}, {dv}], not {tuple(initial_state.shape)}")
+        res = [chunk_gated_delta_rule_v2(q, k, v[..., c:c + w], g, beta, segment_ids, chunk=chunk, precision=precision,
+                                         inverse=inverse, heads_per_step=heads_per_step, residuals=residuals,
+                                         initial_state=None if initial_state is None else initial_state[..., c:c + w],
+                                         output_final_state=output_final_state)
+               for c, w in groups]
+        if not output_final_state:
+            return torch.cat(res, dim=-1)
+        return torch.cat([r[0] for r in res], dim=-1), torch.cat([r[1] for r in res], dim=-1)
     run = run_dim(dk, dv)
     if run is None:
-        raise ValueError(f"head dims up to 128: this build's kernels cannot hold Dk={dk}, Dv={dv}")
+        raise ValueError(f"key dims up to 128: this build's kernels cannot hold Dk={dk}, Dv={dv}")
     if run != dk or run != dv:
         if initial_state is not None and initial_state.shape != (batch, heads, dk, dv):
             raise ValueError(f"initial_state must be [{batch}, {heads}, {dk}, {dv}], not {tuple(initial_state.shape)}")
