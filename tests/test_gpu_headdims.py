@@ -148,3 +148,24 @@ def test_padded_head_dims_prefill_then_decode(shape, inplace):
     err = rel(torch.stack(outs, 1).double().cpu(), full[:, length:].double().cpu())
     print(f"prefill + decode Dk={dk} Dv={dv}: {err:.1e}", flush=True)
     assert err <= 1e-5
+
+
+def test_key_dims_above_128_raise():
+    """Dk above 128 has no padded or split form: every operator refuses it before any launch."""
+    from tjev_amd import gdn_megakernel
+    from tjev_amd.serve import gdn_prefill
+    from tjev_amd.v2 import chunk_gated_delta_rule_v2
+
+    hk, dk, h, dv, T = 1, 256, 1, 256, 16
+    qkv = torch.zeros((1, T, 2 * hk * dk + h * dv), device="cuda")
+    a = b = torch.zeros((1, T, h), device="cuda")
+    a_log = dt_bias = torch.zeros(h, device="cuda")
+    seg = torch.ones((1, T), dtype=torch.int32, device="cuda")
+    kw = dict(key_heads=hk, key_dim=dk, value_heads=h, value_dim=dv)
+    with pytest.raises(ValueError, match="key dims up to 128"):
+        gdn_megakernel(qkv, a, b, a_log, dt_bias, None, seg, **kw)
+    with pytest.raises(ValueError, match="key dims up to 128"):
+        gdn_prefill(qkv, a, b, a_log, dt_bias, None, seg, **kw)
+    q = torch.zeros((1, T, hk, dk), device="cuda")
+    with pytest.raises(ValueError, match="key dims up to 128"):
+        chunk_gated_delta_rule_v2(q, q, torch.zeros((1, T, h, dv), device="cuda"), a, b, seg)
