@@ -1,0 +1,103 @@
+"""The reference's hardware tests of the megakernel (tests/kernels/test_gdn_mega.py:254-337), on
+the GPU: the model's head counts and head dim (16/16 and 16/32 heads of 128, chunks 64 and
+128) on one row of 1,100 tokens with segment starts at [64, 129, 510, 513, 1027] and 5 padding
+tokens, mega2 and mega1.
+
+- fp32 (``highest``) against the fp64 oracle: every output and gradient within the reference's
+  fp32 tolerance (its TPU test allows 10x that against its fp32 path).
+- The training precision (``high``, bf16x3), fp32 or bf16 projections: the megakernel's error
+  against the fp64 oracle on the same projection values is no larger than that of the path it
+  replaces on the same inputs -- the model's XLA glue (conv + SiLU rounded to the projection
+  dtype, l2norm and gates in fp32, v in the projection dtype) around the v2 rule, here the
+  oracle's glue in torch around this build's v2 operator -- by the reference's margins (relative
+  L2 within 1.25x plus a floor, max error within 2x plus a floor).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gdn_cases import NAMES, case_inputs, hip_outputs, oracle_outputs, rel, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+TPU_CASES = [(16, 16, 64), (16, 32, 64), (16, 16, 128)]  # test_gdn_mega.py:254
+CUTS = [64, 129, 510, 513, 1027]
+# test_gdn_mega.py:89-91
+TOL = {"out": 1e-5, "qkv": 1e-5, "a": 1e-5, "b": 1e-5, "A_log": 5e-5, "dt_bias": 5e-5, "w": 1e-5}
+
+
+def _inputs(hk, h):
+    return case_inputs(1, 1100, hk, h, 128, seed=3, cuts=CUTS)
+
+
+@pytest.mark.parametrize("conv", [True, False], ids=["mega2", "mega1"])
+@pytest.mark.parametrize(("hk", "h", "chunk"), TPU_CASES, ids=[f"{c[0]}-{c[1]}-C{c[2]}" for c in TPU_CASES])
+def test_model_heads_fp32_matches_oracle(hk, h, chunk, conv):
+    inputs, cot = _inputs(hk, h)
+    kw = dict(key_heads=hk, key_dim=128, value_heads=h, value_dim=128, conv=conv)
+    print(f"fp32 {hk}/{h} C{chunk} conv={conv}", flush=True)
+    got = hip_outputs(inputs, cot, chunk=chunk, precision="highest", **kw)
+    want = oracle_outputs(inputs, cot, dtype=torch.float64, **kw)
+    errors = {k: rel(got[k], want[k]) for k in got}
+    print("  vs fp64:", {k: f"{v:.1e}" for k, v in errors.items()}, flush=True)
+    assert all(bool(torch.isfinite(v).all()) for v in got.values())
+    bad = {k: v for k, v in errors.items() if v > TOL[k]}
+    assert not bad, errors
+
+
+def _v2_path_outputs(inputs, cot, *, hk, h, d, conv, chunk):
+    """The model's path before the megakernel (test_gdn_mega.py:226-249) with its casts: the
+    glue in torch on the CPU (the oracle's conv and norms), this build's v2 operator on the GPU
+    at ``high``; out and the gradients of sum(out * cot) as float64 CPU tensors."""
+    from oracle.gdn_oracle import gates, l2norm, segmented_causal_conv1d
+    from tjev_amd.v2 import chunk_gated_delta_rule_v2
+
+    qkv, a, b, a_log, dt_bias, w, seg = inputs
+    leaves = [x.detach().clone().requires_grad_(True) for x in (qkv, a, b, a_log, dt_bias)]
+    wl = w.detach().clone().requires_grad_(True) if conv else None
+    qkv_, a_, b_, a_log_, dt_bias_ = leaves
+    batch, length, _ = qkv.shape
+    seg64 = seg.to(torch.int64)
+    x = qkv_
+    if conv:
+        x = segmented_causal_conv1d(qkv_.float(), wl, seg64).to(qkv.dtype)
+        x = torch.where((seg64 > 0)[..., None], torch.nn.functional.silu(x), torch.zeros((), dtype=x.dtype))
+        x = x.to(qkv.dtype)
+    q, k, v = torch.split(x, [hk * d, hk * d, h * d], dim=-1)
+    q = l2norm(q.reshape(batch, length, hk, d).float()) * d ** -0.5
+    k = l2norm(k.reshape(batch, length, hk, d).float())
+    v = v.reshape(batch, length, h, d)
+    g, beta = gates(a_.float(), b_.float(), a_log_, dt_bias_)
+    out = chunk_gated_delta_rule_v2(q.cuda(), k.cuda(), v.cuda(), g.cuda(), beta.cuda(), seg.cuda(), chunk=chunk,
+                                    precision="high").cpu()
+    targets = leaves + ([wl] if conv else [])
+    grads = torch.autograd.grad((out.float() * cot).sum(), targets)
+    res = {"out": out.detach().double()}
+    res.update({n: gr.double() for n, gr in zip(NAMES, grads)})
+    return res
+
+
+def _errors(got, want):
+    return {k: (rel(got[k], want[k]), rel_l2(got[k], want[k])) for k in got}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["float32", "bfloat16"])
+@pytest.mark.parametrize("conv", [True, False], ids=["mega2", "mega1"])
+@pytest.mark.parametrize(("hk", "h", "chunk"), TPU_CASES, ids=[f"{c[0]}-{c[1]}-C{c[2]}" for c in TPU_CASES])
+def test_model_heads_high_no_worse_than_v2_path(hk, h, chunk, conv, dtype):
+    (qkv, a, b, a_log, dt_bias, w, seg), cot = _inputs(hk, h)
+    xs = (qkv.to(dtype), a.to(dtype), b.to(dtype), a_log, dt_bias, w, seg)
+    xs_ref = tuple(x.float() if i < 3 else x for i, x in enumerate(xs))  # the same values in fp32
+    kw = dict(key_heads=hk, key_dim=128, value_heads=h, value_dim=128, conv=conv)
+    print(f"high {dtype} {hk}/{h} C{chunk} conv={conv}", flush=True)
+    want = oracle_outputs(xs_ref, cot, dtype=torch.float64, **kw)
+    mega = _errors(hip_outputs(xs, cot, chunk=chunk, precision="high", **kw), want)
+    v2 = _errors(_v2_path_outputs(xs, cot, hk=hk, h=h, d=128, conv=conv, chunk=chunk), want)
+    fmt = lambda e: {k: f"{m:.1e}/{r:.1e}" for k, (m, r) in e.items()}  # noqa: E731
+    print(f"  (max/l2) mega {fmt(mega)}\n  v2 path {fmt(v2)}", flush=True)
+    floor = 1e-6 if dtype == torch.float32 else 1e-4
+    worse = {k: (mega[k], v2[k]) for k in mega
+             if mega[k][1] > 1.25 * v2[k][1] + floor or mega[k][0] > 2 * v2[k][0] + floor}
+    assert not worse, worse
