@@ -101,3 +101,35 @@ def test_model_heads_high_no_worse_than_v2_path(hk, h, chunk, conv, dtype):
     worse = {k: (mega[k], v2[k]) for k in mega
              if mega[k][1] > 1.25 * v2[k][1] + floor or mega[k][0] > 2 * v2[k][0] + floor}
     assert not worse, worse
+
+
+LAYOUTS = [  # test_gdn_mega.py:187-192: (precision, inverse, chunk, heads_per_step)
+    ("high", "doubling", 64, 0), ("mixed", "doubling", 64, 0), ("bf16", "doubling", 64, 0),
+    ("high", "blocked", 64, 0), ("mixed", "blocked", 128, 0), ("high", "doubling", 64, 16),
+]
+COSINE = {"high": 0.9999, "mixed": 0.999, "bf16": 0.99}
+
+
+@pytest.mark.parametrize("conv", [True, False], ids=["mega2", "mega1"])
+@pytest.mark.parametrize(("precision", "inverse", "chunk", "hb"), LAYOUTS,
+                         ids=[f"{p}-{i}-C{c}-hb{h}" for p, i, c, h in LAYOUTS])
+@pytest.mark.parametrize(("hk", "h"), [(16, 16), (16, 32)], ids=["0.8B", "9B"])
+def test_model_layouts_run_forward_and_backward(hk, h, precision, inverse, chunk, hb, conv):
+    """The reference's lowering test (test_gdn_mega.py:187-215) run instead of lowered: the
+    model's layouts (Dk = Dv = 128, bf16 qkv, gates and conv weight, B = 2, T = 256) under each of
+    its precision / inverse / chunk / heads-per-step combinations, forward and backward through
+    the library: every output and gradient finite and aligned with the fp32 oracle on the same
+    values (cosine at the precision's level)."""
+    from gdn_cases import cosine
+
+    (qkv, a, b, a_log, dt_bias, w, seg), cot = case_inputs(2, 256, hk, h, 128, seed=4, segments="random4")
+    xs = (qkv.bfloat16(), a.bfloat16(), b.bfloat16(), a_log, dt_bias, w.bfloat16(), seg)
+    xs_ref = tuple(x.float() if i in (0, 1, 2, 5) else x for i, x in enumerate(xs))
+    kw = dict(key_heads=hk, key_dim=128, value_heads=h, value_dim=128, conv=conv)
+    print(f"{precision} {inverse} C{chunk} hb{hb} {hk}/{h} conv={conv}", flush=True)
+    got = hip_outputs(xs, cot, chunk=chunk, precision=precision, inverse=inverse, heads_per_step=hb, **kw)
+    want = oracle_outputs(xs_ref, cot, **kw)
+    cos = {k: cosine(got[k], want[k]) for k in got}
+    print("  cosine:", {k: f"{v:.6f}" for k, v in cos.items()}, flush=True)
+    assert all(bool(torch.isfinite(v).all()) for v in got.values())
+    assert min(cos.values()) >= COSINE[precision], cos
