@@ -273,3 +273,30 @@ def test_hip_all_padding_row_fp32():
     errors = {k: rel(got[k], want[k]) for k in got}
     for name, err in errors.items():
         assert err < TOL[name], (name, errors)
+
+
+@pytest.mark.parametrize("conv", [True, False], ids=["mega2", "mega1"])
+def test_hip_packed_rows_equal_segments_alone(conv):
+    """test_gdn_mega.py:135-147: a packed row (segments at [0, 16), [16, 33), [33, 71), [71, 96):
+    boundaries at chunk offsets 0 and 1 and mid-chunk, chunk 16) computes what each segment
+    computes alone (conv taps and the state never cross a boundary). Beyond the reference's
+    forward check: under one cotangent the packed row's gradients of each segment's qkv, a and
+    b equal those of the segment alone, and its A_log, dt_bias and conv-weight gradients the
+    sums over the segments."""
+    (qkv, a, b, a_log, dt_bias, w, _), cot = case_inputs(1, 96, 2, 4, 16, segments="one")
+    cuts = [0, 16, 33, 71, 96]
+    spans = list(zip(cuts[:-1], cuts[1:]))
+    seg = torch.cat([torch.full((e - s,), i + 1, dtype=torch.int32) for i, (s, e) in enumerate(spans)])[None]
+    kw = dict(key_heads=2, key_dim=16, value_heads=4, value_dim=16, chunk=16, precision="highest", conv=conv)
+    packed = hip_outputs((qkv, a, b, a_log, dt_bias, w, seg), cot, **kw)
+    sums = {k: torch.zeros_like(packed[k]) for k in ("A_log", "dt_bias", "w") if k in packed}
+    for s, e in spans:
+        alone = hip_outputs((qkv[:, s:e], a[:, s:e], b[:, s:e], a_log, dt_bias, w,
+                             torch.ones((1, e - s), dtype=torch.int32)), cot[:, s:e], **kw)
+        errs = {k: rel(packed[k][:, s:e], alone[k]) for k in ("out", "qkv", "a", "b")}
+        print(f"span [{s}, {e}) conv={conv}:", {k: f"{v:.1e}" for k, v in errs.items()}, flush=True)
+        assert all(v < 1e-5 for v in errs.values()), (s, e, errs)
+        for k in sums:
+            sums[k] += alone[k]
+    for k, total in sums.items():
+        assert rel(packed[k], total) < 1e-5, (k, rel(packed[k], total))
