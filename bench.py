@@ -53,7 +53,8 @@ def _args(argv=None):
     ap.add_argument("--cpu-rows", type=int, default=0, help="rows of the workload in the CPU baseline (0: all)")
     ap.add_argument("--details", default=None, help="also write the full report to this JSON file")
     ap.add_argument("--no-9b", action="store_true",
-                    help="with the default 0.8B config, skip the 9B config timed after it in the same run")
+                    help="with the default 0.8B config, time it alone: skip the 9B, varlen and 4B-block configs "
+                         "timed after it in the same run")
     return ap.parse_args(argv)
 
 
@@ -409,6 +410,29 @@ def main(argv=None) -> int:
             "roofline": {k: nine["roofline"][k] for k in ("kernel", "bound", "achieved", "peak", "unit", "frac")},
             "kernels_ms": {k: v["ms"] for k, v in nine["kernels"].items()},
             "finite": nine["finite"], "wall_s_timed": nine["wall_s_timed"],
+        }
+        # the other BASELINE configs on one GPU: the packed varlen row and the 4B block
+        del nine
+        torch.cuda.empty_cache()
+        var = _layer_bench(args, "varlen", cpu=False)
+        report["config_varlen"] = {
+            "workload": var["config"]["workload"], "value": var["value"], "unit": "tokens/s",
+            "ms_per_step": var["ms_per_step"], "batch": var["config"]["batch"], "seq_len": var["config"]["seq_len"],
+            "segments": var["config"]["segments"], "operator_roofline_frac": var["operator_roofline"]["frac"],
+            "roofline": {k: var["roofline"][k] for k in ("kernel", "bound", "achieved", "peak", "unit", "frac")},
+            "kernels_ms": {k: v["ms"] for k, v in var["kernels"].items()},
+            "finite": var["finite"], "wall_s_timed": var["wall_s_timed"],
+        }
+        del var
+        torch.cuda.empty_cache()
+        blk = _block_bench(argparse.Namespace(**{**vars(args), "no_cpu_baseline": True}))
+        report["config_4B_block"] = {
+            "workload": blk["config"]["workload"], "value": blk["value"], "unit": "tokens/s",
+            "ms_per_step": blk["ms_per_step"], "batch": blk["config"]["batch"], "seq_len": blk["config"]["seq_len"],
+            "hidden": blk["config"]["hidden"], "lora_rank": blk["config"]["lora_rank"],
+            "peak_activation_bytes": blk["peak_activation_bytes"], "split_ms": blk["split_ms"],
+            "roofline": {k: blk["roofline"][k] for k in ("kernel", "bound", "achieved", "peak", "unit", "frac")},
+            "finite": blk["finite"],
         }
     if args.details:
         with open(args.details, "w") as f:
