@@ -524,3 +524,36 @@ def test_wide_value_heads_run_as_column_groups():
         assert torch.equal(p[:, :2 * hk * dk], x[:, :2 * hk * dk])
         assert torch.equal(p[:, 2 * hk * dk:].reshape(4, h, w), x[:, 2 * hk * dk:].reshape(4, h, dv)[..., c:c + w])
     assert torch.equal(merge_value_cols(parts, hk, dk, h), x)
+
+
+def test_head_layout_round_trips_property():
+    """For any head counts and widths (hypothesis): padding every head of qkv's lanes to a wider
+    dim and cutting it back is the identity, the padded lanes are zero, and cutting qkv's lanes
+    into value-column groups and joining them back is the identity; the groups tile Dv."""
+    from hypothesis import given, settings
+    from hypothesis import strategies as st
+
+    from tjev_amd.gdn import merge_value_cols, pad_qkv, run_dim, unpad_qkv, value_cols, value_groups
+
+    @settings(max_examples=60, deadline=None)
+    @given(hk=st.integers(1, 4), ratio=st.integers(1, 3), dk=st.integers(1, 128), dv=st.integers(1, 400),
+           rows=st.integers(1, 3))
+    def check(hk, ratio, dk, dv, rows):
+        h = hk * ratio
+        x = torch.randn(rows, 2 * hk * dk + h * dv)
+        groups = value_groups(dk, dv)
+        if groups is None:
+            run = run_dim(dk, dv)
+            assert run is not None and run >= max(dk, dv)
+            padded = pad_qkv(x, hk, dk, h, dv, run)
+            assert padded.shape == (rows, (2 * hk + h) * run)
+            assert torch.equal(unpad_qkv(padded, hk, dk, h, dv, run), x)
+            lanes = padded.reshape(rows, 2 * hk + h, run)
+            assert torch.all(lanes[:, :2 * hk, dk:] == 0) and torch.all(lanes[:, 2 * hk:, dv:] == 0)
+        else:
+            assert dv > 128 and sum(w for _, w in groups) == dv
+            assert all(0 < w <= 128 for _, w in groups) and [c for c, _ in groups] == list(range(0, dv, 128))
+            parts = [value_cols(x, hk, dk, h, dv, c, w) for c, w in groups]
+            assert torch.equal(merge_value_cols(parts, hk, dk, h), x)
+
+    check()
