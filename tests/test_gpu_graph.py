@@ -1,5 +1,6 @@
-"""The library under HIP graph capture (GPU): the C ABI allocates nothing, synchronizes nothing
-and launches only kernels on the caller's stream (no memset nodes), so a caller can capture it.
+"""The library under HIP graph capture, and its determinism (GPU): the C ABI allocates nothing,
+synchronizes nothing and launches only kernels on the caller's stream (no memset nodes), so a
+caller can capture it; it uses no atomics, so runs repeat bit for bit.
 
 - A training step (the megakernel's forward and its backward through torch autograd, bf16, the
   0.8B heads) captured once in a torch CUDA graph and replayed three times, with eager work of
@@ -122,3 +123,28 @@ def test_noalloc_prefill_replays_in_a_graph():
             if name == "residuals":
                 x, y = x[:n_states], y[:n_states]
             assert torch.equal(x, y), (replay, name)
+
+
+@pytest.mark.parametrize("hk,h", [(16, 16), (16, 32)], ids=["0.8B-heads", "9B-heads"])
+def test_fwd_bwd_is_deterministic(hk, h):
+    """No atomics and fixed-order reductions (the gate sums and the conv weight's gradient in
+    fp64 over chunks in order): the same inputs give bit-identical outputs and gradients run
+    after run, the conv weight's gradient included, with other work between the runs."""
+    from tjev_amd import gdn_megakernel
+
+    raw, cot = case_inputs(2, 1000, hk, h, 128, dtype=torch.bfloat16, style="baseline", segments="cuts",
+                           cuts=[300, 301, 640], trailing_pad=3, seed=7)
+    qkv, a, b, a_log, dt_bias, w, seg = (x.cuda() for x in raw)
+    kw = dict(key_heads=hk, key_dim=128, value_heads=h, value_dim=128, chunk=128, precision="high")
+
+    def run():
+        xs = [x.clone().requires_grad_(True) for x in (qkv, a, b, a_log, dt_bias, w)]
+        out = gdn_megakernel(*xs[:5], xs[5], seg, **kw)
+        return [out.detach()] + list(torch.autograd.grad((out.float() * cot.cuda()).sum(), xs))
+
+    first = run()
+    for r in range(2):
+        gdn_megakernel(qkv.flip(1), a, b, a_log, dt_bias, w, seg, **kw)  # other work in between
+        again = run()
+        for name, x, y in zip(("out", "qkv", "a", "b", "A_log", "dt_bias", "w"), again, first):
+            assert torch.equal(x, y), (r, name)
