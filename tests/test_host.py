@@ -557,3 +557,16 @@ def test_head_layout_round_trips_property():
             assert torch.equal(merge_value_cols(parts, hk, dk, h), x)
 
     check()
+
+
+def test_integration_python_samples_compile():
+    """The Python bindings INTEGRATION.md shows a maintainer parse as Python (they are compiled,
+    not run: jax is not in this image)."""
+    import re
+    from pathlib import Path
+
+    text = (Path(__file__).resolve().parents[1] / "INTEGRATION.md").read_text()
+    blocks = re.findall(r"```python\n(.*?)```", text, flags=re.S)
+    assert len(blocks) >= 2
+    for i, src in enumerate(blocks):
+        compile(src, f"INTEGRATION.md python block {i}", "exec")
