@@ -139,3 +139,35 @@ def test_fullsize_varlen_segments_are_isolated():
     far = torch.ones(16384, dtype=torch.bool)
     far[first:last] = False
     _same(base["a"][0, far.cuda()], pert["a"][0, far.cuda()], "d_a outside the chunks of the changed segment")
+
+
+def test_row_past_2_32_elements():
+    """The offsets are 64-bit where the problem's size needs them: one row of 2^20 tokens at the
+    0.8B heads (qkv holds 6.4e9 elements, past 2^32; about 140 GB of HBM with the workspace), whose
+    last 16,384 tokens form a segment of their own starting at a chunk boundary: that segment's
+    out, d_qkv, d_a and d_b equal, bit for bit, a standalone run of those tokens. Inputs are
+    drawn on the GPU."""
+    T, tail, hk, h = 1 << 20, 16384, 16, 16
+    W = (2 * hk + h) * D
+    assert T * W > 2 ** 32
+    print(f"one row of {T} tokens, W = {W}: {T * W / 2 ** 31:.2f} x 2^31 elements", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(11)
+    qkv = torch.randn((1, T, W), generator=g, device="cuda", dtype=torch.bfloat16)
+    a = torch.randn((1, T, h), generator=g, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn((1, T, h), generator=g, device="cuda", dtype=torch.bfloat16)
+    a_log = torch.rand(h, generator=g, device="cuda") * float(np.log(16.0))
+    dt_bias = torch.randn(h, generator=g, device="cuda")
+    w = 0.5 * torch.randn((4, W), generator=g, device="cuda")
+    seg = torch.ones((1, T), dtype=torch.int32, device="cuda")
+    seg[:, T - tail:] = 2
+    cot = torch.randn((1, T, h, D), generator=g, device="cuda", dtype=torch.bfloat16)
+    big = _run([qkv, a, b, a_log, dt_bias, w, seg], cot, hk, h)
+    got = {k: v[:, T - tail:].clone() for k, v in big.items()}
+    del big
+    torch.cuda.empty_cache()
+    sl = lambda x: x[:, T - tail:]  # noqa: E731
+    alone = _run([sl(qkv), sl(a), sl(b), a_log, dt_bias, w, torch.ones((1, tail), dtype=torch.int32)], sl(cot),
+                 hk, h)
+    for name in NAMES:
+        assert bool(torch.isfinite(got[name].float()).all()), name
+        assert torch.equal(got[name], alone[name]), (name, float((got[name].float() - alone[name].float()).abs().max()))

@@ -1867,8 +1867,8 @@ __global__ __launch_bounds__(256) void k_conv_state(GdnArgs A) {
   TIO* dst = reinterpret_cast<TIO*>(A.conv_state) + (size_t)b * k1 * A.W;
   const int sl = A.seg[(size_t)b * A.T + last];
   const TIO* hist = reinterpret_cast<const TIO*>(A.init_conv);
-  for (int idx = threadIdx.x; idx < k1 * A.W; idx += 256) {
-    const int r = idx / A.W, c = idx % A.W, t = last - k1 + 1 + r;
+  for (long idx = threadIdx.x; idx < (long)k1 * A.W; idx += 256) {  // k1 W can pass 2^31 (W < 2^30)
+    const int r = (int)(idx / A.W), c = (int)(idx % A.W), t = last - k1 + 1 + r;
     // rows before the row: the history of a continued sequence (token 0's segment)
     const bool keep = A.seg[(size_t)b * A.T + (t >= 0 ? t : 0)] == sl && (t >= 0 || hist);
     dst[idx] = !keep ? TIO(0) : t >= 0 ? x[((size_t)b * A.T + t) * A.W + c] : hist[((size_t)b * k1 + k1 + t) * A.W + c];
