@@ -27,7 +27,8 @@
  *                                                   residuals >= TJEV_GDN_SAVE_TINV
  *                v_new  [B, H, ceil(T/C)*C, Dv]    fp32 u - w S of each token, when
  *                                                   residuals == TJEV_GDN_SAVE_ALL
- *              (C: the chunk the kernels run, max(chunk, 16))
+ *              (C: the chunk the kernels run, min(max(chunk, 16), 128): chunk 8 runs the
+ *              16-token kernels, chunks above 128 the 128-token ones)
  * T need not be a multiple of the chunk: the kernels pad the tail with zero q, k, v and beta,
  * g = 0 and the last token's segment id (xla.py:198-204), so the padding changes no output
  * (pallas_tpu_mega.py:616-621 pads with segment 0: the same outputs) and carries the state after
