@@ -1,0 +1,94 @@
+"""The forward's chunk kernel building v from the raw qkv rows (bf16 I/O, a conv of 1 to 4 taps,
+chunk = head dim = 128; k_prep then skips the v rows) against the same kernels reading v from
+k_prep's rows (TJEV_GDN_UNFUSED_V=1, read by the library on each call), bit for bit (the fused
+run under TJEV_GDN_POISON=1: NaN wherever the kernels read memory they did not write): outputs,
+final state, conv state and every gradient (both routes end in the same backward, whose k_prep
+writes the v rows). The cases are those where the conv's halo crosses a chunk edge: segments
+starting 1, 2 and 3 tokens before a chunk and 1-token segments there, rows continued from an
+initial state and conv history, a padded tail, GQA (value heads past the key heads' channels),
+every conv width, each precision, the blocked inverse with T kept, and the 9B heads.
+"""
+
+from __future__ import annotations
+
+import os
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+CUTS = (1, 2, 125, 126, 127, 128, 129, 253, 254, 256, 257, 384, 511)
+
+
+def _inputs(seed, batch, length, hk, h, taps, cont):
+    gen = torch.Generator().manual_seed(seed)
+    width = (2 * hk + h) * D
+    qkv = torch.randn((batch, length, width), generator=gen).bfloat16()
+    a = torch.randn((batch, length, h), generator=gen).bfloat16()
+    b = torch.randn((batch, length, h), generator=gen).bfloat16()
+    a_log = torch.rand(h, generator=gen)
+    dt_bias = torch.randn(h, generator=gen)
+    w = 0.5 * torch.randn((taps, width), generator=gen)
+    seg = torch.ones((batch, length), dtype=torch.int32)
+    for c in CUTS:
+        if c < length:
+            seg[:, c:] += 1
+    seg[0, length - 7:] = 0  # a padded tail
+    if batch > 1:
+        seg[1, length - 140:] = 0  # a padded chunk and more
+    cot = torch.randn((batch, length, h, D), generator=gen).bfloat16()
+    extra = {}
+    if cont:
+        extra["initial_state"] = 0.1 * torch.randn((batch, h, D, D), generator=gen)
+        if taps > 1:
+            extra["initial_conv"] = torch.randn((batch, taps - 1, width), generator=gen).bfloat16()
+        extra["output_final_state"] = True
+    dev = torch.device("cuda")
+    return ([x.to(dev) for x in (qkv, a, b, a_log, dt_bias, w, seg)], cot.to(dev),
+            {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in extra.items()})
+
+
+def _run(inputs, cot, extra, unfused, **kw):
+    from tjev_amd import gdn_megakernel
+
+    if unfused:
+        os.environ["TJEV_GDN_UNFUSED_V"] = "1"
+    else:  # NaN in the workspace: a read of the v rows k_prep did not write reaches the outputs
+        os.environ["TJEV_GDN_POISON"] = "1"
+    try:
+        leaves = [x.clone().requires_grad_(True) for x in inputs[:6]]
+        res = gdn_megakernel(*leaves[:5], leaves[5], inputs[6], chunk=128, **kw, **extra)
+        out, more = (res[0], [x for x in res[1:] if x is not None]) if isinstance(res, tuple) else (res, [])
+        grads = torch.autograd.grad((out.float() * cot.float()).sum(), leaves)
+        torch.cuda.synchronize()
+    finally:
+        os.environ.pop("TJEV_GDN_UNFUSED_V", None)
+        os.environ.pop("TJEV_GDN_POISON", None)
+    return [out.detach()] + [x.detach() for x in more] + list(grads)
+
+
+CASES = [(taps, cont, "high", {}, (2, 4)) for taps in (1, 2, 3, 4) for cont in (False, True)]
+CASES += [(4, True, p, {}, (2, 4)) for p in ("highest", "mixed", "bf16")]
+CASES += [(4, True, "high", {"inverse": "blocked", "residuals": "tinv"}, (2, 4)),
+          (3, False, "high", {"residuals": "all"}, (2, 4)), (4, True, "high", {}, (16, 32))]
+
+
+@pytest.mark.parametrize(("taps", "cont", "precision", "kw", "heads"), CASES,
+                         ids=[f"K{t}-{'cont' if c else 'fresh'}-{p}{'-' + '-'.join(k.values()) if k else ''}-{h[0]}x{h[1]}"
+                              for t, c, p, k, h in CASES])
+def test_fused_v_equals_k_prep_rows(taps, cont, precision, kw, heads):
+    hk, h = heads
+    length = 700 if hk == 2 else 400
+    inputs, cot, extra = _inputs(taps + 10 * cont, 2, length, hk, h, taps, cont)
+    shape = dict(key_heads=hk, key_dim=D, value_heads=h, value_dim=D, precision=precision, **kw)
+    print(f"fused v: taps={taps} cont={cont} {precision} {kw} heads={heads} T={length}", flush=True)
+    fused = _run(inputs, cot, extra, False, **shape)
+    plain = _run(inputs, cot, extra, True, **shape)
+    names = ["out"] + (["final_state"] + (["conv_state"] if taps > 1 else []) if cont else []) + \
+        ["qkv", "a", "b", "A_log", "dt_bias", "w"]
+    assert len(names) == len(fused) == len(plain)
+    for name, x, y in zip(names, fused, plain):
+        assert bool(torch.isfinite(x.float()).all()), name
+        assert torch.equal(x, y), (name, float((x.float() - y.float()).abs().max()))

@@ -340,12 +340,29 @@ def test_kernel_roofline_takes_the_longer_ideal_time():
     tri = 4 * 16 * 32 * (128 * 127 // 2) * 4  # T: its strictly lower triangle per chunk
     assert kernel_work(batch=4, length=4096, key_heads=16, value_heads=16, dim=128, chunk=128, io_bytes=2,
                        residuals="tinv")["gdn_chunk_fwd"]["bytes"] == 4 * act + ctx + tri
+    # v from the raw rows in the forward's chunk kernel: it reads bf16 raw v for the fp32 v rows,
+    # which the forward's k_prep no longer reads (raw) or writes (fp32)
+    fv = kernel_work(batch=4, length=4096, key_heads=16, value_heads=16, dim=128, chunk=128, io_bytes=2, fused_v=True)
+    assert fv["gdn_chunk_fwd"]["bytes"] == 3 * act + io + ctx
+    assert fv["gdn_prep_fwd"]["bytes"] == w["gdn_prep_fwd"]["bytes"] - io - act
+    assert fv["gdn_prep_bwd"] == w["gdn_prep_bwd"] and fv["gdn_chunk_bwd"] == w["gdn_chunk_bwd"]
     r = kernel_roofline(w["gdn_bwd_grads"], 338e-6, PEAK_BF16_TFLOPS)
     assert r["bound"] == "hbm" and r["unit"] == "GB/s" and abs(r["frac"] - r["hbm_frac"]) < 1e-12
     assert abs(r["achieved"] - w["gdn_bwd_grads"]["bytes"] / 338e-6 / 1e9) < 1e-6
     r = kernel_roofline(w["gdn_bwd_grads"], 338e-6, PEAK_FP32_TFLOPS)
     assert r["bound"] == "mfma" and r["unit"] == "TFLOP/s" and r["frac"] == r["mfma_frac"]
     assert kernel_roofline(w["gdn_post"], 270e-6, PEAK_FP32_TFLOPS)["bound"] == "hbm"
+
+
+def test_fuses_v_follows_the_launch_rule():
+    """The forward's chunk kernel builds v from the raw rows for bf16 I/O through a conv of 1 to 4
+    taps at chunk = head dim = 128 (chunks above 128 run the 128-token kernels), else not."""
+    from tjev_amd.roofline import fuses_v
+
+    assert fuses_v(io_bytes=2, chunk=128, dim=128, taps=4) and fuses_v(io_bytes=2, chunk=256, dim=128, taps=1)
+    assert not fuses_v(io_bytes=4, chunk=128, dim=128, taps=4)
+    assert not fuses_v(io_bytes=2, chunk=64, dim=128, taps=4) and not fuses_v(io_bytes=2, chunk=128, dim=64, taps=4)
+    assert not fuses_v(io_bytes=2, chunk=128, dim=128, taps=0) and not fuses_v(io_bytes=2, chunk=128, dim=128, taps=5)
 
 
 def test_state_entry_points_validate_before_launch():

@@ -12,6 +12,8 @@ struct GdnArgs {
   int parts;   // chunk ranges per (row, head, tile) of the scans, split where a segment resets
   int res;     // residuals kept by the forward: 0 states, 1 and T, 2 and v_new
   int inv;     // the in-chunk inverse: 0 pure doubling, 1 diagonal blocks by substitution + doubling
+  int fuse_v;  // the forward's k_chunk builds v from the raw rows, k_prep skips them (k_chunk's RawV);
+               // the caller's value allows it, the launch sequence decides
   float scale; // Dk^-1/2
   // inputs
   const void* qkv;

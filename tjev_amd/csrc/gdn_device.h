@@ -192,6 +192,10 @@ template <> struct Raw4<float> {
 template <> struct Raw4<uint16_t> {
   uint2 a;
   __device__ __forceinline__ void load(const uint16_t* p) { a = *reinterpret_cast<const uint2*>(p); }
+  __device__ __forceinline__ float elem(int e) const {  // value e (a compile-time index)
+    const uint32_t w = e < 2 ? a.x : a.y;
+    return __uint_as_float(e % 2 ? w & 0xffff0000u : w << 16);
+  }
   __device__ __forceinline__ void get(float (&o)[4]) const {
     o[0] = __uint_as_float(a.x << 16);
     o[1] = __uint_as_float(a.x & 0xffff0000u);

@@ -64,6 +64,14 @@ constexpr int kDVT = GDN_D < 32 ? GDN_D : 32;
   GDN_CHUNK_INV(PI, PS, false)     \
   GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 3, false>(GdnArgs);
 GDN_EACH_PAIR(GDN_CHUNK)
+#if GDN_C == 128 && GDN_D == 128  // and the forward's with v from the raw rows (bf16 I/O)
+#define GDN_CHUNK_FV(PI, PS)                                                        \
+  GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 0, true, true>(GdnArgs);   \
+  GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 0, false, true>(GdnArgs);  \
+  GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 2, true, true>(GdnArgs);   \
+  GDN_KW_1 __global__ void k_chunk<GDN_C, GDN_D, PI, PS, 2, false, true>(GdnArgs);
+GDN_EACH_PAIR(GDN_CHUNK_FV)
+#endif
 // part 2: the scans
 #define GDN_SCAN_BWD(PI, PS, TIO) GDN_KW_2 __global__ void k_scan_bwd<GDN_C, GDN_D, kDVT, PI, PS, TIO>(GdnArgs);
 #if GDN_C == 128 && GDN_D == 128
@@ -123,6 +131,10 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
   parts = parts < 1 ? 1 : (parts > A.N ? A.N : parts);
   GdnArgs L = A;  // the launched arguments
   L.parts = parts;
+  // bf16 I/O through a conv of 1 to 4 taps at C = D = 128: the forward's k_chunk builds the v
+  // rows from the raw ones and k_prep skips them (the backward's k_prep writes them)
+  constexpr bool kFV = C == 128 && D == 128 && std::is_same_v<TIO, uint16_t>;
+  L.fuse_v = A.fuse_v && kFV && !backward && A.taps >= 1 && A.taps <= 4;
   const dim3 tiles(chains * parts);
   const int units = A.B * A.H * A.N, cus = cu_count();
   const dim3 persist(units < cus ? units : cus);
@@ -139,10 +151,20 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
     if (A.taps <= 4) GDN_LAUNCH(K_PREP_FWD, (k_prep<C, D, TIO, TG, 3>), prep, dim3(256));
     else GDN_LAUNCH(K_PREP_FWD, (k_prep<C, D, TIO, TG, 4>), prep, dim3(256));
     if (A.res == 0) {
-      if (A.inv == 0) GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0, true>), persist, dim3(C * 4));
+      if (L.fuse_v) {
+        if constexpr (kFV) {
+          if (A.inv == 0) GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0, true, true>), persist, dim3(C * 4));
+          else GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0, false, true>), persist, dim3(C * 4));
+        }
+      } else if (A.inv == 0) GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0, true>), persist, dim3(C * 4));
       else GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 0, false>), persist, dim3(C * 4));
     } else {  // T kept for the backward
-      if (A.inv == 0) GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 2, true>), persist, dim3(C * 4));
+      if (L.fuse_v) {
+        if constexpr (kFV) {
+          if (A.inv == 0) GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 2, true, true>), persist, dim3(C * 4));
+          else GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 2, false, true>), persist, dim3(C * 4));
+        }
+      } else if (A.inv == 0) GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 2, true>), persist, dim3(C * 4));
       else GDN_LAUNCH(K_CHUNK_FWD, (k_chunk<C, D, PI, PS, 2, false>), persist, dim3(C * 4));
     }
     if constexpr (C == 128 && D == 128) GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd_split<PI, PS>), tiles, dim3(512));
@@ -191,6 +213,7 @@ hipError_t run_v2(const GdnArgs& A, hipStream_t st, int backward, const Timer* t
   parts = parts < 1 ? 1 : (parts > A.N ? A.N : parts);
   GdnArgs L = A;
   L.parts = parts;
+  L.fuse_v = 0;  // v is an input here (k_prep_v2 writes its rows)
   const dim3 tiles(chains * parts);
   const int units = A.B * A.H * A.N, cus = cu_count();
   const dim3 persist(units < cus ? units : cus);

@@ -78,6 +78,7 @@ struct Ctx {
   int seg[C];
   float gam[C], gaml[C], beta[C], grow[C], kws[C], bg[C];
   int before;
+  int hseg[3];  // ids of tokens nC - 1, nC - 2, nC - 3 (token 0's in chunk 0), with CtxRaw's HALO
   float carry;
 };
 
@@ -147,7 +148,7 @@ __device__ __forceinline__ void cross_tile(const f32x4& e, bool diag, float (&rp
 // The per-token inputs of one chunk's context held in registers (thread i < C holds token i):
 // fetch() issues the loads, commit() writes them to the LDS context (derive_ctx then fills in
 // the rest). Needs at least C threads.
-template <int C>
+template <int C, bool HALO = false>
 struct CtxRaw {
   int seg, before;
   float gam, gaml, beta;
@@ -162,7 +163,8 @@ struct CtxRaw {
     gam = A.gam[tok];
     gaml = A.gaml[tok];
     beta = A.bet[tok];
-    before = A.segp[(size_t)b * A.Tp + (n > 0 ? (size_t)n * C - 1 : 0)];
+    // HALO: threads 1 and 2 (and their repeats) load the ids of the two tokens before that one
+    before = A.segp[(size_t)b * A.Tp + (n > 0 ? (size_t)n * C - 1 - (HALO ? (i < 2 ? i : 2) : 0) : 0)];
     first = n == 0 && !A.init_state;
   }
   __device__ __forceinline__ void commit(Ctx<C>& cx) const {
@@ -174,6 +176,7 @@ struct CtxRaw {
       cx.beta[i] = beta;
     }
     if (i == 0) cx.before = first ? -2 : before;
+    if (HALO && i < 3) cx.hseg[i] = before;
   }
 };
 
@@ -473,7 +476,8 @@ __device__ __forceinline__ const TIO* halo_row(const GdnArgs& A, const TIO* x, i
 // grid B*N*(2*Hk + H), 256 threads, the slot fastest: the workgroups of one chunk run together
 // and read its token rows whole. Slot y: q head y (< Hk), k head y - Hk, v head y - 2Hk.
 // Every (token, 8 channels) is independent: D/8 lanes per token row. l2norm of xla.py:42-53.
-// Slot 0 first writes the padded segment ids of the chunk (read by every later kernel).
+// Slot 0 first writes the padded segment ids of the chunk (read by every later kernel). With
+// fuse_v the v slots only compute the gates (k_chunk builds the v rows from the raw ones).
 template <int C, int D, class TIO, class TG, int K1 = 4>
 __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
   static_assert(K1 >= 1 && K1 <= 4, "conv lags 1..K1 (launched with K1 >= taps - 1)");
@@ -501,7 +505,7 @@ __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
   constexpr int RG = C / RPP > 0 ? C / RPP : 1;
   constexpr int HW = 4;  // taps - 1 <= 4 (a halo of 3 for taps <= 4 measured slower here)
   const int r0 = (threadIdx.x / CG) * RG;
-  if (RG * RPP == C || r0 < C) {
+  if ((RG * RPP == C || r0 < C) && !(kind == 2 && A.fuse_v)) {
     Raw8<TIO> raw[RG + HW];
     int sgv[RG + HW];
 #pragma unroll
@@ -1070,6 +1074,74 @@ __device__ __forceinline__ void load_tile(float* s, int LD, const TS* g) {
   t.put_lds(s, LD);
 }
 
+// The forward's (v beta)^T operand built from the raw qkv rows of a bf16 I/O conv of 1 to 4 taps
+// at C = D = 128 (fuse_v: k_prep skips the v rows). Each thread owns tokens 8 jb .. 8 jb + 7 at
+// channels 4m .. 4m + 3, whose conv reads raw rows 8 jb - 3 .. 8 jb + 7: they land during the
+// inverse, and the conv and SiLU run as the operand is put, in k_prep's fp32 arithmetic (the same
+// values k_prep would store), one 16-byte write per channel and plane. Lane l of wave w:
+// m = 16 (w % 2) + 2 (l / 8) + l % 2, jb = 4 (w / 2) + (l / 2) % 4, so that any 16 consecutive
+// lanes write 16 distinct 16-byte bank groups (row stride 272 bytes) and 16 lanes read 128
+// contiguous bytes of a row. The unit's conv weights go through LDS (lag threadIdx.x / D).
+template <int C, int D, int NT>
+struct RawV {
+  static_assert(C == 128 && D == 128 && NT == 512, "the lane map of C = D = 128");
+  Raw4<uint16_t> raw[11];
+  float wt;
+  __device__ __forceinline__ static int chan4() {
+    return 4 * (16 * (wave() & 1) + 2 * (lane() >> 3) + (lane() & 1));
+  }
+  __device__ __forceinline__ static int row0() { return 8 * (4 * (wave() >> 1) + ((lane() >> 1) & 3)); }
+  __device__ __forceinline__ void fetch(const GdnArgs& A, int b, int h, int n) {
+    const uint16_t* x = reinterpret_cast<const uint16_t*>(A.qkv);
+    const int c0 = (2 * A.Hk + h) * D, c = chan4(), r0 = row0();
+#pragma unroll
+    for (int i = 0; i < 11; ++i) raw[i].load(halo_row<uint16_t>(A, x, b, n * C + r0 - 3 + i, c0 + c));
+    const int lag = threadIdx.x / D;  // lags past the taps read lag 0's (a weight of zero when put)
+    wt = A.conv_w[(size_t)(lag < A.taps ? A.taps - 1 - lag : A.taps - 1) * A.W + c0 + threadIdx.x % D];
+  }
+  __device__ __forceinline__ void put_weights(float* sw, const GdnArgs& A) const {
+    sw[threadIdx.x] = (int)threadIdx.x / D < A.taps ? wt : 0.f;
+  }
+  // after put_weights and a barrier
+  template <int P>
+  __device__ __forceinline__ void put_cols(const Op<P>& op, const Ctx<C>& cx, const float* sw, const GdnArgs& A,
+                                           int n) const {
+    const int c = chan4(), r0 = row0();
+    int sr[11];  // ids of rows r0 - 3 .. r0 + 7 (rows before the chunk: the context's halo ids)
+#pragma unroll
+    for (int i = 0; i < 11; ++i) {
+      const int r = r0 - 3 + i;
+      sr[i] = i >= 3 ? cx.seg[r] : *(r >= 0 ? &cx.seg[r] : &cx.hseg[-1 - r]);
+    }
+    bool keep[8][4];  // keep[i][L]: token r0 + i reads row r0 + i - L
+    bool live[8];     // token r0 + i is not padding
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int t = n * C + r0 + i;
+      const int st = t < A.T ? sr[3 + i] : 0;
+      live[i] = st > 0;
+#pragma unroll
+      for (int L = 1; L <= 3; ++L) keep[i][L] = L < A.taps && (t - L >= 0 || A.init_conv) && sr[3 + i - L] == st;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {  // channel c + e, as k_prep: z = sum over lags of keep * x[t-L] * w[K-1-L]
+      float wl[4], x[11], v[8];
+#pragma unroll
+      for (int L = 0; L < 4; ++L) wl[L] = sw[L * D + c + e];
+#pragma unroll
+      for (int i = 0; i < 11; ++i) x[i] = raw[i].elem(e);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float z = x[3 + i] * wl[0];
+#pragma unroll
+        for (int L = 1; L <= 3; ++L) z = keep[i][L] ? z + x[3 + i - L] * wl[L] : z;
+        v[i] = (live[i] ? z * sigmoid_io<uint16_t>(z) : 0.f) * cx.beta[r0 + i];
+      }
+      op.put8(c + e, r0, v);
+    }
+  }
+};
+
 // ---------------------------------------------------------------- k_chunk
 // Persistent over the (row, head, chunk) units as k_out; C/16 waves (one 16-row strip each).
 // MODE 0 (forward): writes w and u; MODE 2: also T (kept as a residual). MODE 1 (backward
@@ -1080,8 +1152,9 @@ __device__ __forceinline__ void load_tile(float* s, int LD, const TS* g) {
 // and k rows are loaded at this unit's start and end; the forward's k (again) and v, and the
 // backward's S and k strip, during the inverse; the backward's v after it (held across the
 // inverse, it would spill). DBL: the inverse's diagonal blocks by doubling (else by substitution;
-// a template argument: both forms in one kernel take 17 more VGPRs and spill in MODE 1).
-template <int C, int D, int PI, int PS, int MODE, bool DBL>
+// a template argument: both forms in one kernel take 17 more VGPRs and spill in MODE 1). FV: the
+// forward's v built from the raw rows (RawV) instead of read from k_prep's rows.
+template <int C, int D, int PI, int PS, int MODE, bool DBL, bool FV = false>
 __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
   constexpr bool FWD = MODE == 0 || MODE == 2;  // writes w and u (else v_new)
   constexpr bool LOAD_T = MODE == 3;            // T from the residuals
@@ -1094,11 +1167,13 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
   __shared__ __align__(16) float sT[C * LT];
   __shared__ __align__(16) char sB[RB];
   __shared__ Ctx<C> cx;
+  __shared__ __align__(16) float sW[FV ? 4 * D : 4];  // FV: the unit's conv weights
+  static_assert(!FV || FWD, "FV: the forward modes");
   GDN_POISON_LDS(sT, sB, cx);
   const int w = wave(), i0 = 16 * w;
   const Op<PI> ob = TB::at(sB);
   const int total = A.B * A.H * A.N;
-  CtxRaw<C> rc;
+  CtxRaw<C, FV> rc;
   RegsT<C, D, NT> kk;  // k: staged as rows (A and B of k k^T), then as kbe^T
   {
     const UnitIx<CHUNKS_DOWN> x(A, blockIdx.x);
@@ -1113,7 +1188,7 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
     rc.commit(cx);
     if constexpr (!LOAD_T) kk.put_rows(ob);
     rc.fetch(A, y.b, y.h, y.n);
-    RegsT<C, D, NT> vc;  // this unit's (v beta)^T source (forward)
+    std::conditional_t<FV, RawV<C, D, NT>, RegsT<C, D, NT>> vc;  // this unit's (v beta)^T source (forward)
     RegsT<D, D, NT, true, StateT<PS>> sc;  // S_before, its strip of k and its v at the accumulator layout (backward)
     StripA<D> ks;
     AccVals<D / 16> va;
@@ -1156,7 +1231,8 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
       }
       if constexpr (FWD) {  // k again and v, in flight during the inverse
         kk.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D);
-        vc.fetch(A.vv + off, D);
+        if constexpr (FV) vc.fetch(A, x.b, x.h, x.n);
+        else vc.fetch(A.vv + off, D);
       }
       __syncthreads();
       invert_unit_lower<C, PI>(sT, LT, reinterpret_cast<float*>(sB), DBL);
@@ -1210,6 +1286,7 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
     zero(aw);
     zero(au);
     kk.put_cols(ob, cx.bg);  // kbe^T
+    if constexpr (FV) vc.put_weights(sW, A);
     __syncthreads();
     strip_mma<PI, C, D / 16>(aw, krow(sT, LT), i0, ob, 0, 0, tri_end<C>(i0));
 #pragma unroll
@@ -1217,7 +1294,8 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) A.ww[off + (size_t)(i0 + acc_row(rr)) * D + 16 * t + acc_col()] = aw[t][rr];
     __syncthreads();
-    vc.put_cols(ob, cx.beta);  // (v beta)^T
+    if constexpr (FV) vc.put_cols(ob, cx, sW, A, x.n);  // (v beta)^T
+    else vc.put_cols(ob, cx.beta);
     __syncthreads();
     strip_mma<PI, C, D / 16>(au, krow(sT, LT), i0, ob, 0, 0, tri_end<C>(i0));
     // the next unit's k before this unit's stores: waiting for it later (vmcnt counts in issue

@@ -19,14 +19,24 @@ PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 
 
+def fuses_v(*, io_bytes: int, chunk: int, dim: int, taps: int) -> bool:
+    """Whether the forward's chunk kernel builds v from the raw rows (k_prep then skips them):
+    bf16 I/O through a conv of 1 to 4 taps at chunk = head dim = 128, as the library's launch
+    sequence decides."""
+    return io_bytes == 2 and min(max(chunk, 16), 128) == 128 and dim == 128 and 1 <= taps <= 4
+
+
 def kernel_work(*, batch: int, length: int, key_heads: int, value_heads: int, dim: int, chunk: int,
-                io_bytes: int, residuals: str = "states", fused_norm: bool = False) -> dict[str, dict]:
+                io_bytes: int, residuals: str = "states", fused_norm: bool = False,
+                fused_v: bool = False) -> dict[str, dict]:
     """Per-launch algorithmic work of each kernel: {"bytes": B, "flops": F}. Bytes are the
     minimal HBM traffic of the kernel's own inputs and outputs (each tensor read or written
     once); FLOPs count the dense chunk contractions once (zero for the elementwise kernels).
     ``residuals`` (states | tinv | all) sets what the forward's chunk kernel writes and what
     the backward's reads, as the library's residual policy does; ``fused_norm``: the output
-    kernel also reads the norm's gate and writes its y."""
+    kernel also reads the norm's gate and writes its y; ``fused_v`` (``fuses_v``): the forward's
+    chunk kernel reads v's raw rows (io dtype) instead of the fp32 v rows, which the forward's
+    k_prep neither reads nor writes."""
     C, D = chunk, dim
     n = -(-length // C)
     tp = n * C
@@ -46,11 +56,14 @@ def kernel_work(*, batch: int, length: int, key_heads: int, value_heads: int, di
     io = tok_h * D * io_bytes                  # out or d out
     ctx = batch * tp * 4 + 3 * tok_h * f32     # segment ids, gamma (hi, lo), beta
     prep = tokens * (width + 2 * value_heads) * io_bytes + (2 * tok_k + tok_h) * D * f32 + 3 * tok_h * f32
+    raw_v = tokens * value_heads * D * io_bytes  # v's raw rows
+    prep_fwd = prep - (raw_v + tok_h * D * f32 if fused_v else 0)
+    v_in = raw_v if fused_v else act_v
     w = {
         # conv + gates + l2norm: read qkv, a, b; write q, k (key heads), v, gamma (hi, lo), beta
-        "gdn_prep_fwd": {"bytes": prep, "flops": 0},
+        "gdn_prep_fwd": {"bytes": prep_fwd, "flops": 0},
         # k, v -> w, u (and T kept for the backward unless only the states are)
-        "gdn_chunk_fwd": {"bytes": act_k + act_v + ctx + 2 * act_v + (tinv if residuals != "states" else 0),
+        "gdn_chunk_fwd": {"bytes": act_k + v_in + ctx + 2 * act_v + (tinv if residuals != "states" else 0),
                           "flops": units * (3 * sq + inv)},
         # w, u, k -> v_new, S before each chunk
         "gdn_scan_fwd": {"bytes": tok_h * D * f32 * 4 + units * D * D * f32, "flops": 0},
