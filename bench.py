@@ -450,8 +450,8 @@ def _layer_bench(args, config: str, cpu: bool = True) -> dict:
     from tjev_amd.gdn import GdnPlan
     from tjev_amd.norm import _params as _norm_params
     from tjev_amd.norm import norm_backward, norm_forward
-    from tjev_amd.roofline import (PEAK_BF16_TFLOPS, PEAK_FP32_TFLOPS, fuses_v, kernel_roofline, kernel_work,
-                                   operator_work)
+    from tjev_amd.roofline import (PEAK_BF16_TFLOPS, PEAK_FP32_TFLOPS, fuses_q, fuses_v, kernel_roofline,
+                                   kernel_work, operator_work)
     from tjev_amd.testing import CONFIGS, cotangent, gdn_inputs
 
     cfg = dict(CONFIGS[config])
@@ -517,8 +517,10 @@ def _layer_bench(args, config: str, cpu: bool = True) -> dict:
     per_kernel = {k: kt.ms[k] / kt.launches[k] for k in kt.ms if kt.launches[k]}
     io_bytes = 2 if dtype == torch.bfloat16 else 4
     shape = dict(batch=B, length=T, key_heads=Hk, value_heads=H, dim=D, chunk=C, io_bytes=io_bytes)
+    taps = int(w.shape[0])
     work = kernel_work(**shape, residuals=args.residuals, fused_norm=fused,
-                       fused_v=fuses_v(io_bytes=io_bytes, chunk=C, dim=D, taps=int(w.shape[0])))
+                       fused_v=fuses_v(io_bytes=io_bytes, chunk=C, dim=D, taps=taps),
+                       fused_q=fuses_q(io_bytes=io_bytes, chunk=C, dim=D, taps=taps, key_heads=Hk, value_heads=H))
     shape["norm"] = norm
     peak_mfma = PEAK_FP32_TFLOPS if precision == "highest" else PEAK_BF16_TFLOPS
     kernels = {name: {"ms": avg_ms, **kernel_roofline(work[name], avg_ms * 1e-3, peak_mfma)}

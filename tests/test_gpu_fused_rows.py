@@ -1,12 +1,14 @@
-"""The forward's chunk kernel building v from the raw qkv rows (bf16 I/O, a conv of 1 to 4 taps,
-chunk = head dim = 128; k_prep then skips the v rows) against the same kernels reading v from
-k_prep's rows (TJEV_GDN_UNFUSED_V=1, read by the library on each call), bit for bit (the fused
-run under TJEV_GDN_POISON=1: NaN wherever the kernels read memory they did not write): outputs,
+"""The forward building q and v from the raw qkv rows (bf16 I/O, a conv of 1 to 4 taps, chunk =
+head dim = 128: v in the chunk kernel, and q in the output kernel when each key head has one
+value head; k_prep then skips those rows) against the same kernels reading q and v from
+k_prep's rows (TJEV_GDN_UNFUSED=1, read by the library on each call), bit for bit (the fused run
+under TJEV_GDN_POISON=1: NaN wherever the kernels read memory they did not write): outputs,
 final state, conv state and every gradient (both routes end in the same backward, whose k_prep
-writes the v rows). The cases are those where the conv's halo crosses a chunk edge: segments
+writes the rows). The cases are those where the conv's halo crosses a chunk edge: segments
 starting 1, 2 and 3 tokens before a chunk and 1-token segments there, rows continued from an
-initial state and conv history, a padded tail, GQA (value heads past the key heads' channels),
-every conv width, each precision, the blocked inverse with T kept, and the 9B heads.
+initial state and conv history, a padded tail, every conv width, each precision, the blocked
+inverse with T kept, the 0.8B heads, and GQA (2 value heads per key head: v only) with the 9B
+heads.
 """
 
 from __future__ import annotations
@@ -54,8 +56,8 @@ def _run(inputs, cot, extra, unfused, **kw):
     from tjev_amd import gdn_megakernel
 
     if unfused:
-        os.environ["TJEV_GDN_UNFUSED_V"] = "1"
-    else:  # NaN in the workspace: a read of the v rows k_prep did not write reaches the outputs
+        os.environ["TJEV_GDN_UNFUSED"] = "1"
+    else:  # NaN in the workspace: a read of the q or v rows k_prep did not write reaches the outputs
         os.environ["TJEV_GDN_POISON"] = "1"
     try:
         leaves = [x.clone().requires_grad_(True) for x in inputs[:6]]
@@ -64,26 +66,27 @@ def _run(inputs, cot, extra, unfused, **kw):
         grads = torch.autograd.grad((out.float() * cot.float()).sum(), leaves)
         torch.cuda.synchronize()
     finally:
-        os.environ.pop("TJEV_GDN_UNFUSED_V", None)
+        os.environ.pop("TJEV_GDN_UNFUSED", None)
         os.environ.pop("TJEV_GDN_POISON", None)
     return [out.detach()] + [x.detach() for x in more] + list(grads)
 
 
-CASES = [(taps, cont, "high", {}, (2, 4)) for taps in (1, 2, 3, 4) for cont in (False, True)]
-CASES += [(4, True, p, {}, (2, 4)) for p in ("highest", "mixed", "bf16")]
-CASES += [(4, True, "high", {"inverse": "blocked", "residuals": "tinv"}, (2, 4)),
-          (3, False, "high", {"residuals": "all"}, (2, 4)), (4, True, "high", {}, (16, 32))]
+CASES = [(taps, cont, "high", {}, (2, 2)) for taps in (1, 2, 3, 4) for cont in (False, True)]
+CASES += [(4, True, p, {}, (2, 2)) for p in ("highest", "mixed", "bf16")]
+CASES += [(4, True, "high", {"inverse": "blocked", "residuals": "tinv"}, (2, 2)),
+          (3, False, "high", {"residuals": "all"}, (2, 2)), (4, True, "high", {}, (16, 16)),
+          (4, True, "high", {}, (2, 4)), (2, False, "mixed", {}, (2, 4)), (4, True, "high", {}, (16, 32))]
 
 
 @pytest.mark.parametrize(("taps", "cont", "precision", "kw", "heads"), CASES,
                          ids=[f"K{t}-{'cont' if c else 'fresh'}-{p}{'-' + '-'.join(k.values()) if k else ''}-{h[0]}x{h[1]}"
                               for t, c, p, k, h in CASES])
-def test_fused_v_equals_k_prep_rows(taps, cont, precision, kw, heads):
+def test_fused_rows_equal_k_prep_rows(taps, cont, precision, kw, heads):
     hk, h = heads
     length = 700 if hk == 2 else 400
     inputs, cot, extra = _inputs(taps + 10 * cont, 2, length, hk, h, taps, cont)
     shape = dict(key_heads=hk, key_dim=D, value_heads=h, value_dim=D, precision=precision, **kw)
-    print(f"fused v: taps={taps} cont={cont} {precision} {kw} heads={heads} T={length}", flush=True)
+    print(f"fused rows: taps={taps} cont={cont} {precision} {kw} heads={heads} T={length}", flush=True)
     fused = _run(inputs, cot, extra, False, **shape)
     plain = _run(inputs, cot, extra, True, **shape)
     names = ["out"] + (["final_state"] + (["conv_state"] if taps > 1 else []) if cont else []) + \

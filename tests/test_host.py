@@ -346,6 +346,11 @@ def test_kernel_roofline_takes_the_longer_ideal_time():
     assert fv["gdn_chunk_fwd"]["bytes"] == 3 * act + io + ctx
     assert fv["gdn_prep_fwd"]["bytes"] == w["gdn_prep_fwd"]["bytes"] - io - act
     assert fv["gdn_prep_bwd"] == w["gdn_prep_bwd"] and fv["gdn_chunk_bwd"] == w["gdn_chunk_bwd"]
+    # and q in the output kernel: bf16 raw q for the fp32 q rows k_prep no longer reads or writes
+    fq = kernel_work(batch=4, length=4096, key_heads=16, value_heads=16, dim=128, chunk=128, io_bytes=2, fused_v=True,
+                     fused_q=True)
+    assert fq["gdn_out"]["bytes"] == w["gdn_out"]["bytes"] - act + io
+    assert fq["gdn_prep_fwd"]["bytes"] == w["gdn_prep_fwd"]["bytes"] - 2 * (io + act)
     r = kernel_roofline(w["gdn_bwd_grads"], 338e-6, PEAK_BF16_TFLOPS)
     assert r["bound"] == "hbm" and r["unit"] == "GB/s" and abs(r["frac"] - r["hbm_frac"]) < 1e-12
     assert abs(r["achieved"] - w["gdn_bwd_grads"]["bytes"] / 338e-6 / 1e9) < 1e-6
@@ -356,8 +361,13 @@ def test_kernel_roofline_takes_the_longer_ideal_time():
 
 def test_fuses_v_follows_the_launch_rule():
     """The forward's chunk kernel builds v from the raw rows for bf16 I/O through a conv of 1 to 4
-    taps at chunk = head dim = 128 (chunks above 128 run the 128-token kernels), else not."""
-    from tjev_amd.roofline import fuses_v
+    taps at chunk = head dim = 128 (chunks above 128 run the 128-token kernels), else not; its
+    output kernel q where, besides, each key head has one value head."""
+    from tjev_amd.roofline import fuses_q, fuses_v
+
+    assert fuses_q(io_bytes=2, chunk=128, dim=128, taps=4, key_heads=16, value_heads=16)
+    assert not fuses_q(io_bytes=2, chunk=128, dim=128, taps=4, key_heads=16, value_heads=32)
+    assert not fuses_q(io_bytes=4, chunk=128, dim=128, taps=4, key_heads=16, value_heads=16)
 
     assert fuses_v(io_bytes=2, chunk=128, dim=128, taps=4) and fuses_v(io_bytes=2, chunk=256, dim=128, taps=1)
     assert not fuses_v(io_bytes=4, chunk=128, dim=128, taps=4)

@@ -189,10 +189,11 @@ T* at(void* ws, size_t off) {
   return off == ~size_t(0) ? nullptr : reinterpret_cast<T*>(static_cast<char*>(ws) + off);
 }
 
-// TJEV_GDN_UNFUSED_V=1 in the environment (read on each call): the forward's chunk kernel reads
-// v from k_prep's rows even where it builds them from the raw rows (the same bits: a check)
-bool unfused_v() {
-  const char* e = getenv("TJEV_GDN_UNFUSED_V");
+// TJEV_GDN_UNFUSED=1 in the environment (read on each call): the forward's chunk and output
+// kernels read v and q from k_prep's rows even where they build them from the raw rows (the
+// same bits: a check)
+bool unfused() {
+  const char* e = getenv("TJEV_GDN_UNFUSED");
   return e && e[0] == '1';
 }
 
@@ -238,7 +239,7 @@ gdn::GdnArgs base_args(const tjev_gdn_params* p, void* ws, const Layout& L) {
   A.dwp = at<float>(ws, L.dwp);
   A.res = p->residuals;
   A.inv = p->inverse;
-  A.fuse_v = !unfused_v();
+  A.fuse_v = !unfused();
   return A;
 }
 

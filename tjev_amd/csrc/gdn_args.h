@@ -12,8 +12,9 @@ struct GdnArgs {
   int parts;   // chunk ranges per (row, head, tile) of the scans, split where a segment resets
   int res;     // residuals kept by the forward: 0 states, 1 and T, 2 and v_new
   int inv;     // the in-chunk inverse: 0 pure doubling, 1 diagonal blocks by substitution + doubling
+  int fuse_q;  // the forward's k_out builds q from the raw rows, k_prep skips them (k_out's RawQ)
   int fuse_v;  // the forward's k_chunk builds v from the raw rows, k_prep skips them (k_chunk's RawV);
-               // the caller's value allows it, the launch sequence decides
+               // the caller's fuse_v allows both, the launch sequence decides each
   float scale; // Dk^-1/2
   // inputs
   const void* qkv;

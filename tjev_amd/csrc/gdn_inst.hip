@@ -89,6 +89,12 @@ GDN_EACH_PAIR(GDN_SCANS)
   GDN_KW_3 __global__ void k_out<GDN_C, GDN_D, PI, PS, TIO, true>(GdnArgs);
 #define GDN_OUT(PI, PS) GDN_EACH_IO(GDN_OUT_IO, PI, PS)
 GDN_EACH_PAIR(GDN_OUT)
+#if GDN_C == 128 && GDN_D == 128  // and with q from the raw rows (bf16 I/O)
+#define GDN_OUT_FQ(PI, PS)                                                                \
+  GDN_KW_3 __global__ void k_out<GDN_C, GDN_D, PI, PS, uint16_t, false, true>(GdnArgs); \
+  GDN_KW_3 __global__ void k_out<GDN_C, GDN_D, PI, PS, uint16_t, true, true>(GdnArgs);
+GDN_EACH_PAIR(GDN_OUT_FQ)
+#endif
 // part 4: k_bwd_local (one A-side precision each: the pairs' first members, once)
 #define GDN_LOCAL_IO(PI, PS, TIO) GDN_KW_4 __global__ void k_bwd_local<GDN_C, GDN_D, PI, TIO>(GdnArgs);
 GDN_EACH_IO(GDN_LOCAL_IO, P_F32, 0)
@@ -132,9 +138,12 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
   GdnArgs L = A;  // the launched arguments
   L.parts = parts;
   // bf16 I/O through a conv of 1 to 4 taps at C = D = 128: the forward's k_chunk builds the v
-  // rows from the raw ones and k_prep skips them (the backward's k_prep writes them)
+  // rows from the raw ones, and with one value head per key head k_out the q rows (with more,
+  // it would build each q row once per value head: measured slower at 9B); k_prep skips them
+  // (the backward's k_prep writes them)
   constexpr bool kFV = C == 128 && D == 128 && std::is_same_v<TIO, uint16_t>;
   L.fuse_v = A.fuse_v && kFV && !backward && A.taps >= 1 && A.taps <= 4;
+  L.fuse_q = L.fuse_v && A.ratio == 1;
   const dim3 tiles(chains * parts);
   const int units = A.B * A.H * A.N, cus = cu_count();
   const dim3 persist(units < cus ? units : cus);
@@ -169,7 +178,12 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
     }
     if constexpr (C == 128 && D == 128) GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd_split<PI, PS>), tiles, dim3(512));
     else GDN_LAUNCH(K_SCAN_FWD, (k_scan_fwd<C, D, DVT, PI, PS>), tiles, dim3(NS));
-    if (A.ny) GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO, true>), persist, dim3(C * 4));
+    if (L.fuse_q) {
+      if constexpr (kFV) {
+        if (A.ny) GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO, true, true>), persist, dim3(C * 4));
+        else GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO, false, true>), persist, dim3(C * 4));
+      }
+    } else if (A.ny) GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO, true>), persist, dim3(C * 4));
     else GDN_LAUNCH(K_OUT, (k_out<C, D, PI, PS, TIO>), persist, dim3(C * 4));
     if (A.final_state) GDN_LAUNCH(K_FINAL_STATE, (k_final_state<C, D>), dim3(A.B * A.H * (D / DVT)), dim3(256));
     if (A.conv_state && A.taps > 1) GDN_LAUNCH(K_FINAL_STATE, (k_conv_state<TIO>), dim3(A.B), dim3(256));
@@ -214,6 +228,7 @@ hipError_t run_v2(const GdnArgs& A, hipStream_t st, int backward, const Timer* t
   GdnArgs L = A;
   L.parts = parts;
   L.fuse_v = 0;  // v is an input here (k_prep_v2 writes its rows)
+  L.fuse_q = 0;
   const dim3 tiles(chains * parts);
   const int units = A.B * A.H * A.N, cus = cu_count();
   const dim3 persist(units < cus ? units : cus);

@@ -477,7 +477,8 @@ __device__ __forceinline__ const TIO* halo_row(const GdnArgs& A, const TIO* x, i
 // and read its token rows whole. Slot y: q head y (< Hk), k head y - Hk, v head y - 2Hk.
 // Every (token, 8 channels) is independent: D/8 lanes per token row. l2norm of xla.py:42-53.
 // Slot 0 first writes the padded segment ids of the chunk (read by every later kernel). With
-// fuse_v the v slots only compute the gates (k_chunk builds the v rows from the raw ones).
+// fuse_v the v slots only compute the gates (k_chunk builds the v rows from the raw ones), with
+// fuse_q the q slots write nothing but slot 0's ids (k_out builds the q rows).
 template <int C, int D, class TIO, class TG, int K1 = 4>
 __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
   static_assert(K1 >= 1 && K1 <= 4, "conv lags 1..K1 (launched with K1 >= taps - 1)");
@@ -505,7 +506,7 @@ __global__ __launch_bounds__(256) void k_prep(GdnArgs A) {
   constexpr int RG = C / RPP > 0 ? C / RPP : 1;
   constexpr int HW = 4;  // taps - 1 <= 4 (a halo of 3 for taps <= 4 measured slower here)
   const int r0 = (threadIdx.x / CG) * RG;
-  if ((RG * RPP == C || r0 < C) && !(kind == 2 && A.fuse_v)) {
+  if ((RG * RPP == C || r0 < C) && !(kind == 2 && A.fuse_v) && !(kind == 0 && A.fuse_q)) {
     Raw8<TIO> raw[RG + HW];
     int sgv[RG + HW];
 #pragma unroll
@@ -1752,31 +1753,125 @@ __global__ __launch_bounds__(512) void k_scan_fwd_split(GdnArgs A) {
   }
 }
 
+// The forward's q strip built from the raw qkv rows of a bf16 I/O conv of 1 to 4 taps at
+// C = D = 128 (fuse_q: k_prep skips the q rows), at StripA's layout: lane l holds row
+// i0 + l % 16 at channel groups 8 (4s + l / 16) .. + 7. Each lane stages its raw row in LDS, the
+// first 48 threads the 3 rows before the chunk (the conv's halo); after a barrier every lane
+// reads its lagged rows from there. The conv, SiLU and l2norm run in k_prep's fp32 arithmetic
+// and summation order (its 16 lane partials of 8 channels summed pairwise: groups c, c ^ 1
+// (lanes l ^ 16), then c ^ 2 (l ^ 32), then within the lane), so the strip holds the values
+// k_prep would store. The unit's conv weights go through LDS.
+template <int C, int K>
+struct RawQ {
+  static_assert(C == 128 && K == 128, "the strip of C = D = 128");
+  static constexpr int KS = K / 32;
+  static constexpr int LDR = 2 * K + 16;        // staged row stride in bytes (16 of padding)
+  static constexpr int BYTES = (C + 3) * LDR;   // rows nC - 3 .. nC + C - 1
+  Raw8<uint16_t> own[KS], halo;
+  float wt;
+  __device__ __forceinline__ void fetch(const GdnArgs& A, int b, int hk, int n, int i0) {
+    const uint16_t* x = reinterpret_cast<const uint16_t*>(A.qkv);
+    const int l = lane(), r = l & 15, kg = (l >> 4) << 3, c0 = hk * K;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) own[s].load(halo_row<uint16_t>(A, x, b, n * C + i0 + r, c0 + 32 * s + kg));
+    const int hi = threadIdx.x < 48 ? threadIdx.x : 0;  // halo row hi / 16, channels 8 (hi % 16) ..
+    halo.load(halo_row<uint16_t>(A, x, b, n * C - 3 + hi / 16, c0 + 8 * (hi % 16)));
+    const int lag = threadIdx.x / K;  // lags past the taps read lag 0's (a weight of zero when put)
+    wt = A.conv_w[(size_t)(lag < A.taps ? A.taps - 1 - lag : A.taps - 1) * A.W + c0 + threadIdx.x % K];
+  }
+  __device__ __forceinline__ void stage(char* sq, float* sw, const GdnArgs& A, int i0) const {
+    const int l = lane(), r = l & 15, kg = (l >> 4) << 3;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) *reinterpret_cast<uint4*>(sq + (i0 + r + 3) * LDR + 2 * (32 * s + kg)) = own[s].a;
+    if (threadIdx.x < 48) *reinterpret_cast<uint4*>(sq + (threadIdx.x / 16) * LDR + 16 * (threadIdx.x % 16)) = halo.a;
+    sw[threadIdx.x] = (int)threadIdx.x / K < A.taps ? wt : 0.f;
+  }
+  // after stage and a barrier (the context committed)
+  __device__ __forceinline__ void convert(const Ctx<C>& cx, const char* sq, const float* sw, const GdnArgs& A, int n,
+                                          int i0, StripA<K>& q) const {
+    const int l = lane(), r = l & 15, kg = (l >> 4) << 3, i = i0 + r, t = n * C + i;
+    const int st = t < A.T ? cx.seg[i] : 0;
+    bool keep[4];
+#pragma unroll
+    for (int L = 1; L <= 3; ++L) {
+      const int j = i - L;
+      const int sj = *(j >= 0 ? &cx.seg[j] : &cx.hseg[-1 - j]);
+      keep[L] = L < A.taps && (t - L >= 0 || A.init_conv) && sj == st;
+    }
+    float part[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      float z[8];
+#pragma unroll
+      for (int L = 0; L <= 3; ++L) {
+        Raw8<uint16_t> lr = own[s];  // lag 0: the lane's own row
+        if (L > 0) lr.a = *reinterpret_cast<const uint4*>(sq + (i + 3 - L) * LDR + 2 * (32 * s + kg));
+        float xl[8];
+        lr.get(xl);
+        const float4 w0 = *reinterpret_cast<const float4*>(sw + L * K + 32 * s + kg);
+        const float4 w1 = *reinterpret_cast<const float4*>(sw + L * K + 32 * s + kg + 4);
+        const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (L == 0) z[e] = xl[e] * w[e];
+          else z[e] = keep[L] ? z[e] + xl[e] * w[e] : z[e];
+        }
+      }
+      float sq2 = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        q.x[s][e] = st > 0 ? z[e] * sigmoid_io<uint16_t>(z[e]) : 0.f;
+        sq2 += q.x[s][e] * q.x[s][e];
+      }
+      part[s] = sq2;
+      __builtin_amdgcn_sched_barrier(0);  // one channel group's loads and arithmetic at a time
+    }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {  // k_prep's pairs: groups c ^ 1, then c ^ 2
+      part[s] += __shfl_xor(part[s], 16);
+      part[s] += __shfl_xor(part[s], 32);
+    }
+    const float sqs = (part[0] + part[1]) + (part[2] + part[3]);
+    float rn = sqs == 0.f ? 0.f : 1.0f / sqrtf(sqs + 1e-6f);
+    rn *= A.scale;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        q.x[s][e] *= rn;
+        asm volatile("" : "+v"(q.x[s][e]));  // rounded as k_prep stores it: not fused into the operand split
+      }
+  }
+};
+
 // ---------------------------------------------------------------- k_out
 // Persistent: one workgroup per CU (grid <= number of units) loops over the (row, head, chunk)
 // units blockIdx.x, + gridDim.x, ...; C/16 waves. Per unit: o = ((q k^T) . D) v_new + q_read
-// S_before, token-major output. Every global input of a unit is held in registers and refilled
+// S_before, token-major output. FQ: q built from the raw rows (RawQ) instead of read from
+// k_prep's rows. Every global input of a unit is held in registers and refilled
 // with the next unit's values right after it has been used, so its loads run during the rest
 // of the unit instead of stalling the next one.
-template <int C, int D, int NT, class TS>
+template <int C, int D, int NT, class TS, bool FQ = false>
 struct OutIn {
-  CtxRaw<C> cx;
+  CtxRaw<C, FQ> cx;
   Regs<C, D, NT> k;      // k rows: B(d, j) = k[j][d]
-  StripA<D> q;           // this wave's q rows (A operand of q k^T and of q_read S)
+  std::conditional_t<FQ, RawQ<C, D>, StripA<D>> q;  // this wave's q rows (A operand of q k^T and of q_read S)
   RegsT<C, D, NT> v;     // v_new rows, staged as v_new^T
   RegsT<D, D, NT, true, TS> st;  // S_before rows, staged as S^T
 };
 
-template <int C, int D, int PI, int PS, class TIO, bool NORM = false>
+template <int C, int D, int PI, int PS, class TIO, bool NORM = false, bool FQ = false>
 __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
   constexpr int NT = C * 4;
   constexpr int LI = C + 4;
   constexpr int M = C > D ? C : D;
   using TB = OpTile<PI, M, M>;
-  __shared__ float sI[C * LI];
+  __shared__ __align__(16) float sI[C * LI];  // also the staged raw q rows (FQ)
   __shared__ __align__(16) char sB[TB::BYTES];
   __shared__ Ctx<C> cx;
   __shared__ __align__(16) float snw[NORM ? D : 1];  // the norm's weight
+  __shared__ __align__(16) float sWq[FQ ? 4 * D : 4];  // FQ: the unit's conv weights of q
+  static_assert(!FQ || (C + 3) * (2 * D + 16) <= C * LI * 4, "FQ: the raw rows staged in sI (RawQ::BYTES)");
   GDN_POISON_LDS(sI, sB, cx, snw);
   if constexpr (NORM) {
     for (int c = threadIdx.x; c < D; c += NT) snw[c] = A.nw[c];
@@ -1784,12 +1879,13 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
   const Op<PI> ob = TB::at(sB);
   const int ws = wave_strip<C / 16, false>();
   const int total = A.B * A.H * A.N;
-  OutIn<C, D, NT, StateT<PS>> in;
+  OutIn<C, D, NT, StateT<PS>, FQ> in;
   {
     const UnitIx<BY_HEAD> x(A, blockIdx.x);
     in.cx.fetch(A, x.b, x.h, x.n);
     in.k.fetch(A.kn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D);
-    in.q.fetch(A.qn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D, 16 * ws);
+    if constexpr (FQ) in.q.fetch(A, x.b, x.hk, x.n, 16 * ws);
+    else in.q.fetch(A.qn + hoff(A, x.b, x.hk, A.Hk, x.n, C, D), D, 16 * ws);
     in.v.fetch(A.vnew + hoff(A, x.b, x.h, A.H, x.n, C, D), D);
     in.st.fetch(states_ptr<PS>(A) + ((size_t)x.b * A.H + x.h) * A.N * D * D + (size_t)x.n * D * D, D);
   }
@@ -1800,13 +1896,17 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
     in.cx.commit(cx);
     in.cx.fetch(A, y.b, y.h, y.n);
     in.k.put_rows(ob);
+    if constexpr (FQ) in.q.stage(reinterpret_cast<char*>(sI), sWq, A, i0);
     __syncthreads();
     derive_ctx<C, NT>(cx);
+    StripA<D> qs;  // FQ: the strip built from the staged raw rows
+    if constexpr (FQ) in.q.convert(cx, reinterpret_cast<const char*>(sI), sWq, A, x.n, i0, qs);
+    else qs = in.q;
     __syncthreads();
     {
       f32x4 acc[C / 16];
       zero(acc);
-      in.q.template product<PI>(acc, ob, 0, w + 1);
+      qs.template product<PI>(acc, ob, 0, w + 1);
       // refills are issued after the product that follows each staging: the staged
       // registers are then not live across that product
       in.k.fetch(A.kn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D);
@@ -1837,8 +1937,9 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
       for (int t = 0; t < D / 16; ++t) zr[t].load(reinterpret_cast<const TIO*>(A.nz) + orow + 16 * t);
     }
     __syncthreads();
-    in.q.template product<PS>(o, ob, 0, D / 16, cx.grow[i0 + (lane() & 15)]);
-    in.q.fetch(A.qn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D, i0);
+    qs.template product<PS>(o, ob, 0, D / 16, cx.grow[i0 + (lane() & 15)]);
+    if constexpr (FQ) in.q.fetch(A, y.b, y.hk, y.n, i0);
+    else in.q.fetch(A.qn + hoff(A, y.b, y.hk, A.Hk, y.n, C, D), D, i0);
     in.st.fetch(states_ptr<PS>(A) + ((size_t)y.b * A.H + y.h) * A.N * D * D + (size_t)y.n * D * D, D);
     TIO* out = reinterpret_cast<TIO*>(A.out);
     {  // quad transposes: each lane stores 4 consecutive columns of one row

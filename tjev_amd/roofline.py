@@ -26,9 +26,15 @@ def fuses_v(*, io_bytes: int, chunk: int, dim: int, taps: int) -> bool:
     return io_bytes == 2 and min(max(chunk, 16), 128) == 128 and dim == 128 and 1 <= taps <= 4
 
 
+def fuses_q(*, io_bytes: int, chunk: int, dim: int, taps: int, key_heads: int, value_heads: int) -> bool:
+    """Whether the forward's output kernel builds q from the raw rows (k_prep then skips them):
+    where v is built from them (``fuses_v``) and each key head has one value head."""
+    return fuses_v(io_bytes=io_bytes, chunk=chunk, dim=dim, taps=taps) and key_heads == value_heads
+
+
 def kernel_work(*, batch: int, length: int, key_heads: int, value_heads: int, dim: int, chunk: int,
                 io_bytes: int, residuals: str = "states", fused_norm: bool = False,
-                fused_v: bool = False) -> dict[str, dict]:
+                fused_v: bool = False, fused_q: bool = False) -> dict[str, dict]:
     """Per-launch algorithmic work of each kernel: {"bytes": B, "flops": F}. Bytes are the
     minimal HBM traffic of the kernel's own inputs and outputs (each tensor read or written
     once); FLOPs count the dense chunk contractions once (zero for the elementwise kernels).
@@ -36,7 +42,8 @@ def kernel_work(*, batch: int, length: int, key_heads: int, value_heads: int, di
     the backward's reads, as the library's residual policy does; ``fused_norm``: the output
     kernel also reads the norm's gate and writes its y; ``fused_v`` (``fuses_v``): the forward's
     chunk kernel reads v's raw rows (io dtype) instead of the fp32 v rows, which the forward's
-    k_prep neither reads nor writes."""
+    k_prep neither reads nor writes; ``fused_q`` (``fuses_q``): the same for q and the output
+    kernel."""
     C, D = chunk, dim
     n = -(-length // C)
     tp = n * C
@@ -57,8 +64,10 @@ def kernel_work(*, batch: int, length: int, key_heads: int, value_heads: int, di
     ctx = batch * tp * 4 + 3 * tok_h * f32     # segment ids, gamma (hi, lo), beta
     prep = tokens * (width + 2 * value_heads) * io_bytes + (2 * tok_k + tok_h) * D * f32 + 3 * tok_h * f32
     raw_v = tokens * value_heads * D * io_bytes  # v's raw rows
-    prep_fwd = prep - (raw_v + tok_h * D * f32 if fused_v else 0)
+    raw_q = tokens * key_heads * D * io_bytes    # q's raw rows
+    prep_fwd = prep - (raw_v + tok_h * D * f32 if fused_v else 0) - (raw_q + act_k if fused_q else 0)
     v_in = raw_v if fused_v else act_v
+    q_in = raw_q if fused_q else act_k
     w = {
         # conv + gates + l2norm: read qkv, a, b; write q, k (key heads), v, gamma (hi, lo), beta
         "gdn_prep_fwd": {"bytes": prep_fwd, "flops": 0},
@@ -68,7 +77,7 @@ def kernel_work(*, batch: int, length: int, key_heads: int, value_heads: int, di
         # w, u, k -> v_new, S before each chunk
         "gdn_scan_fwd": {"bytes": tok_h * D * f32 * 4 + units * D * D * f32, "flops": 0},
         # q, k, v_new, S -> out
-        "gdn_out": {"bytes": 2 * act_k + act_v + mats + ctx + io * (3 if fused_norm else 1),
+        "gdn_out": {"bytes": q_in + act_k + act_v + mats + ctx + io * (3 if fused_norm else 1),
                     "flops": units * (2 * sq + sd)},
         "gdn_prep_bwd": {"bytes": prep, "flops": 0},
         # k, v, S (and T under tinv) -> v_new = T (v beta - kbe S) (and T under states)
