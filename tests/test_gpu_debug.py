@@ -61,6 +61,7 @@ CASES = [
     ((2, 200, 2, 4, 16), 64, None, torch.float32, "high", "tinv"),
     ((1, 300, 2, 2, 64), 64, [63, 65, 130], torch.float32, "mixed", "all"),
     ((1, 400, 2, 4, 128), 128, [100, 177], torch.bfloat16, "high", "states"),
+    ((1, 400, 2, 2, 128), 128, [127, 128, 255], torch.bfloat16, "high", "tinv"),  # q and v from the raw rows
 ]
 
 

@@ -1170,7 +1170,7 @@ __global__ __launch_bounds__(C * 4) void k_chunk(GdnArgs A) {
   __shared__ Ctx<C> cx;
   __shared__ __align__(16) float sW[FV ? 4 * D : 4];  // FV: the unit's conv weights
   static_assert(!FV || FWD, "FV: the forward modes");
-  GDN_POISON_LDS(sT, sB, cx);
+  GDN_POISON_LDS(sT, sB, cx, sW);
   const int w = wave(), i0 = 16 * w;
   const Op<PI> ob = TB::at(sB);
   const int total = A.B * A.H * A.N;
@@ -1872,7 +1872,7 @@ __global__ __launch_bounds__(C * 4) void k_out(GdnArgs A) {
   __shared__ __align__(16) float snw[NORM ? D : 1];  // the norm's weight
   __shared__ __align__(16) float sWq[FQ ? 4 * D : 4];  // FQ: the unit's conv weights of q
   static_assert(!FQ || (C + 3) * (2 * D + 16) <= C * LI * 4, "FQ: the raw rows staged in sI (RawQ::BYTES)");
-  GDN_POISON_LDS(sI, sB, cx, snw);
+  GDN_POISON_LDS(sI, sB, cx, snw, sWq);
   if constexpr (NORM) {
     for (int c = threadIdx.x; c < D; c += NT) snw[c] = A.nw[c];
   }
