@@ -95,3 +95,60 @@ def test_fused_rows_equal_k_prep_rows(taps, cont, precision, kw, heads):
     for name, x, y in zip(names, fused, plain):
         assert bool(torch.isfinite(x.float()).all()), name
         assert torch.equal(x, y), (name, float((x.float() - y.float()).abs().max()))
+
+
+def _random_case(rng):
+    """A row layout drawn at random: length 1 to 600, 1 to 3 rows, 1 to 4 key heads with 1 or 2
+    value heads each, 1 to 4 conv taps, cuts anywhere (chunk edges included) and trailing padding,
+    fresh or continued rows, any precision and residual policy."""
+    batch, length = int(rng.integers(1, 4)), int(rng.integers(1, 601))
+    hk = int(rng.choice([1, 2, 4]))
+    h = hk * int(rng.choice([1, 2]))
+    taps = int(rng.integers(1, 5))
+    cont = bool(rng.integers(0, 2))
+    gen = torch.Generator().manual_seed(int(rng.integers(0, 2**31)))
+    width = (2 * hk + h) * D
+    qkv = torch.randn((batch, length, width), generator=gen).bfloat16()
+    a, b = (torch.randn((batch, length, h), generator=gen).bfloat16() for _ in range(2))
+    a_log, dt_bias = torch.rand(h, generator=gen), torch.randn(h, generator=gen)
+    w = 0.5 * torch.randn((taps, width), generator=gen)
+    seg = torch.ones((batch, length), dtype=torch.int32)
+    for row in range(batch):
+        edges = [c for c in (126, 127, 128, 129, 255, 256, 384) if c < length]
+        cuts = sorted(set(rng.choice(range(1, length), size=min(length - 1, 4), replace=False).tolist() if length > 1
+                          else []) | set(rng.choice(edges, size=min(len(edges), 2), replace=False).tolist() if edges else []))
+        for c in cuts:
+            seg[row, c:] += 1
+        pad = int(rng.integers(0, min(length, 140)))
+        if pad:
+            seg[row, length - pad:] = 0
+    cot = torch.randn((batch, length, h, D), generator=gen).bfloat16()
+    extra = {}
+    if cont:
+        extra["initial_state"] = 0.1 * torch.randn((batch, h, D, D), generator=gen)
+        if taps > 1:
+            extra["initial_conv"] = torch.randn((batch, taps - 1, width), generator=gen).bfloat16()
+        extra["output_final_state"] = True
+    dev = torch.device("cuda")
+    kw = dict(key_heads=hk, key_dim=D, value_heads=h, value_dim=D,
+              precision=str(rng.choice(["high", "highest", "mixed", "bf16"])),
+              residuals=str(rng.choice(["states", "tinv", "all"])), inverse=str(rng.choice(["doubling", "blocked"])))
+    return ([x.to(dev) for x in (qkv, a, b, a_log, dt_bias, w, seg)], cot.to(dev),
+            {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in extra.items()}, kw, taps, cont)
+
+
+@pytest.mark.parametrize("index", range(12))
+def test_fused_rows_random_layouts(index):
+    """12 layouts drawn with seed 2027: fused and unfused runs bit-identical."""
+    import numpy as np
+
+    rng = np.random.default_rng([2027, index])
+    inputs, cot, extra, kw, taps, cont = _random_case(rng)
+    print(f"fused rows random {index}: B={inputs[0].shape[0]} T={inputs[0].shape[1]} taps={taps} cont={cont} {kw}",
+          flush=True)
+    fused = _run(inputs, cot, extra, False, **kw)
+    plain = _run(inputs, cot, extra, True, **kw)
+    assert len(fused) == len(plain)
+    for i, (x, y) in enumerate(zip(fused, plain)):
+        assert bool(torch.isfinite(x.float()).all()), i
+        assert torch.equal(x, y), (i, float((x.float() - y.float()).abs().max()))
