@@ -1,8 +1,10 @@
 """The forward building q and v from the raw qkv rows (bf16 I/O, a conv of 1 to 4 taps, chunk =
 head dim = 128: v in the chunk kernel, and q in the output kernel when each key head has one
-value head; k_prep then skips those rows) against the same kernels reading q and v from
-k_prep's rows (TJEV_GDN_UNFUSED=1, read by the library on each call), bit for bit (the fused run
-under TJEV_GDN_POISON=1: NaN wherever the kernels read memory they did not write): outputs,
+value head; k_prep then skips those rows and the forward's workspace has none) against the
+same kernels reading q and v from k_prep's rows (the LDS-poison debug library, which keeps those
+rows, with TJEV_GDN_UNFUSED=1), bit for bit (the fused run under TJEV_GDN_POISON=1: NaN wherever
+the kernels read memory they did not write; the unfused one with NaN in every LDS array before
+its kernels run): outputs,
 final state, conv state and every gradient (both routes end in the same backward, whose k_prep
 writes the rows). The cases are those where the conv's halo crosses a chunk edge: segments
 starting 1, 2 and 3 tokens before a chunk and 1-token segments there, rows continued from an
@@ -52,23 +54,33 @@ def _inputs(seed, batch, length, hk, h, taps, cont):
             {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in extra.items()})
 
 
-def _run(inputs, cot, extra, unfused, **kw):
+def _call(inputs, cot, extra, **kw):
     from tjev_amd import gdn_megakernel
 
-    if unfused:
-        os.environ["TJEV_GDN_UNFUSED"] = "1"
-    else:  # NaN in the workspace: a read of the q or v rows k_prep did not write reaches the outputs
-        os.environ["TJEV_GDN_POISON"] = "1"
-    try:
-        leaves = [x.clone().requires_grad_(True) for x in inputs[:6]]
-        res = gdn_megakernel(*leaves[:5], leaves[5], inputs[6], chunk=128, **kw, **extra)
-        out, more = (res[0], [x for x in res[1:] if x is not None]) if isinstance(res, tuple) else (res, [])
-        grads = torch.autograd.grad((out.float() * cot.float()).sum(), leaves)
-        torch.cuda.synchronize()
-    finally:
-        os.environ.pop("TJEV_GDN_UNFUSED", None)
-        os.environ.pop("TJEV_GDN_POISON", None)
+    leaves = [x.clone().requires_grad_(True) for x in inputs[:6]]
+    res = gdn_megakernel(*leaves[:5], leaves[5], inputs[6], chunk=128, **kw, **extra)
+    out, more = (res[0], [x for x in res[1:] if x is not None]) if isinstance(res, tuple) else (res, [])
+    grads = torch.autograd.grad((out.float() * cot.float()).sum(), leaves)
+    torch.cuda.synchronize()
     return [out.detach()] + [x.detach() for x in more] + list(grads)
+
+
+def _run(inputs, cot, extra, unfused, **kw):
+    from tjev_amd import _lib
+
+    if unfused:  # the debug library: k_prep's rows kept, and read with TJEV_GDN_UNFUSED=1
+        os.environ["TJEV_GDN_UNFUSED"] = "1"
+        try:
+            with _lib.library(_lib.LDS_POISON_PATH) as lib:
+                assert lib.tjev_gdn_lds_poison() == 1
+                return _call(inputs, cot, extra, **kw)
+        finally:
+            os.environ.pop("TJEV_GDN_UNFUSED", None)
+    os.environ["TJEV_GDN_POISON"] = "1"  # NaN in the workspace: a read of rows no kernel wrote shows
+    try:
+        return _call(inputs, cot, extra, **kw)
+    finally:
+        os.environ.pop("TJEV_GDN_POISON", None)
 
 
 CASES = [(taps, cont, "high", {}, (2, 2)) for taps in (1, 2, 3, 4) for cont in (False, True)]

@@ -112,6 +112,23 @@ def test_c_abi_sizes():
         assert lib.tjev_gdn_workspace_bytes(ctypes.byref(q), 1) == bwd - (t_part if precision == 2 else 0)
         q.residuals = 1  # T after the bf16 states (256-byte aligned): bf16 under "bf16" only
         assert lib.tjev_gdn_residual_bytes(ctypes.byref(q)) == part // 2 + (part // 2 if precision == 2 else part)
+    # a forward that builds v (bf16 I/O, 1 to 4 taps, chunk and head dim 128) and, with one value
+    # head per key head, q from the raw rows has no fp32 rows of them in its workspace; the
+    # backward's are unchanged
+    rows = 4 * 16 * 4096 * 128 * 4
+    for hv in (16, 32):
+        f32, b16 = (_params(batch=4, length=4096, key_heads=16, key_dim=128, value_heads=hv, value_dim=128, chunk=128,
+                            io_dtype=io, gate_dtype=io) for io in (0, 1))
+        gap = lib.tjev_gdn_workspace_bytes(ctypes.byref(f32), 0) - lib.tjev_gdn_workspace_bytes(ctypes.byref(b16), 0)
+        assert gap == 2 * rows, (hv, gap)  # 16 value heads: q and v rows; 32 (GQA): v rows of 32 heads
+        assert lib.tjev_gdn_workspace_bytes(ctypes.byref(f32), 1) == lib.tjev_gdn_workspace_bytes(ctypes.byref(b16), 1)
+    for kw in (dict(taps=5), dict(taps=0), dict(chunk=64), dict(key_dim=64, value_dim=64)):
+        f32, b16 = (_params(batch=4, length=4096, key_heads=16, key_dim=128, value_heads=16, value_dim=128, chunk=128,
+                            io_dtype=io, gate_dtype=io) for io in (0, 1))
+        for x in (f32, b16):
+            for k, v in kw.items():
+                setattr(x, k, v)
+        assert lib.tjev_gdn_workspace_bytes(ctypes.byref(f32), 0) == lib.tjev_gdn_workspace_bytes(ctypes.byref(b16), 0), kw
     # a ragged T is padded to whole chunks (the last segment's id carried over, as the reference pads)
     p = _params(length=100, chunk=16)
     assert lib.tjev_gdn_states_bytes(ctypes.byref(p)) == 1 * 4 * 7 * 16 * 16 * 4

@@ -106,6 +106,27 @@ size_t state_elem(const tjev_gdn_params* p) {
 // bytes per element of T: bf16 when the intra-chunk products are one bf16 pass (bf16)
 size_t tinv_elem(const tjev_gdn_params* p) { return p->precision == TJEV_GDN_ONE_PASS_BF16 ? 2 : 4; }
 
+// Whether the forward's kernels build v (k_chunk) and, with one value head per key head, q
+// (k_out) from the raw rows: bf16 I/O, a conv of 1 to 4 taps and the 128-token kernels at head
+// dim 128, the launch sequence's rule (gdn_inst.hip). Such a forward's workspace holds no fp32 v
+// (q) rows. The LDS-poison debug library keeps them and builds them in k_chunk and k_out unless
+// TJEV_GDN_UNFUSED=1 is set (read on each call): the route through k_prep's rows, the fused
+// route's bitwise reference.
+bool fwd_fuses_v(const tjev_gdn_params* p) {
+  return p->io_dtype == TJEV_GDN_BF16 && kernel_chunk(p) == 128 && p->key_dim == 128 && p->value_dim == 128 &&
+         p->taps >= 1 && p->taps <= 4;
+}
+bool fwd_fuses_q(const tjev_gdn_params* p) { return fwd_fuses_v(p) && p->value_heads == p->key_heads; }
+#ifdef GDN_LDS_POISON
+constexpr bool kKeepRows = true;
+bool unfused() {
+  const char* e = getenv("TJEV_GDN_UNFUSED");
+  return e && e[0] == '1';
+}
+#else
+constexpr bool kKeepRows = false;
+#endif
+
 Layout layout(const tjev_gdn_params* p, int backward) {
   const size_t C = kernel_chunk(p), D = p->key_dim;
   const size_t B = p->batch, H = p->value_heads, Hk = p->key_heads;
@@ -121,10 +142,11 @@ Layout layout(const tjev_gdn_params* p, int backward) {
     return at;
   };
   const size_t none = ~size_t(0);
+  const bool drop_q = !backward && !kKeepRows && fwd_fuses_q(p), drop_v = !backward && !kKeepRows && fwd_fuses_v(p);
   L.segp = take(B * Tp * 4);
-  L.qn = take(hkv);
+  L.qn = drop_q ? none : take(hkv);
   L.kn = take(hkv);
-  L.vv = take(hv);
+  L.vv = drop_v ? none : take(hv);
   L.gam = take(tok);
   L.gaml = take(tok);
   L.bet = take(tok);
@@ -189,14 +211,6 @@ T* at(void* ws, size_t off) {
   return off == ~size_t(0) ? nullptr : reinterpret_cast<T*>(static_cast<char*>(ws) + off);
 }
 
-// TJEV_GDN_UNFUSED=1 in the environment (read on each call): the forward's chunk and output
-// kernels read v and q from k_prep's rows even where they build them from the raw rows (the
-// same bits: a check)
-bool unfused() {
-  const char* e = getenv("TJEV_GDN_UNFUSED");
-  return e && e[0] == '1';
-}
-
 gdn::GdnArgs base_args(const tjev_gdn_params* p, void* ws, const Layout& L) {
   gdn::GdnArgs A{};
   const int C = kernel_chunk(p), D = p->key_dim;
@@ -239,7 +253,11 @@ gdn::GdnArgs base_args(const tjev_gdn_params* p, void* ws, const Layout& L) {
   A.dwp = at<float>(ws, L.dwp);
   A.res = p->residuals;
   A.inv = p->inverse;
+#ifdef GDN_LDS_POISON
   A.fuse_v = !unfused();
+#else
+  A.fuse_v = 1;
+#endif
   return A;
 }
 

@@ -14,7 +14,8 @@ struct GdnArgs {
   int inv;     // the in-chunk inverse: 0 pure doubling, 1 diagonal blocks by substitution + doubling
   int fuse_q;  // the forward's k_out builds q from the raw rows, k_prep skips them (k_out's RawQ)
   int fuse_v;  // the forward's k_chunk builds v from the raw rows, k_prep skips them (k_chunk's RawV);
-               // the caller's fuse_v allows both, the launch sequence decides each
+               // the caller's fuse_v allows both, the launch sequence decides each (the
+               // forward's workspace then has no fp32 rows of what is built)
   float scale; // Dk^-1/2
   // inputs
   const void* qkv;

@@ -144,6 +144,9 @@ hipError_t run(const GdnArgs& A, hipStream_t st, int backward, const Timer* tm) 
   constexpr bool kFV = C == 128 && D == 128 && std::is_same_v<TIO, uint16_t>;
   L.fuse_v = A.fuse_v && kFV && !backward && A.taps >= 1 && A.taps <= 4;
   L.fuse_q = L.fuse_v && A.ratio == 1;
+  // a workspace without fp32 q or v rows (gdn_api.hip's layout: the same rule) needs these
+  // kernels to build them: fail rather than let k_prep write through a null pointer
+  if (!backward && ((!L.fuse_v && !A.vv) || (!L.fuse_q && !A.qn))) return hipErrorInvalidValue;
   const dim3 tiles(chains * parts);
   const int units = A.B * A.H * A.N, cus = cu_count();
   const dim3 persist(units < cus ? units : cus);
