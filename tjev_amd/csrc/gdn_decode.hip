@@ -4,12 +4,13 @@
 // megakernel's inputs, with the conv over the K-1 kept raw rows and the new one (HF
 // causal_conv1d_update), SiLU, the q/k l2norm and the gates as k_prep computes them.
 //
-// One workgroup per (row, value head, Dv tile of 32): it rebuilds its q and k head and its
-// v tile from the raw rows, then updates its D x 32 slice of the state: s = s e^g,
-// delta = (v - s^T k) beta, s += k delta^T, o = s^T q. Each thread holds 4 adjacent columns
-// of D/32 rows (16-byte accesses); the two column sums go through lane shuffles and LDS. The state is read and written once (in place
-// allowed: each slice belongs to one workgroup); the new conv history goes to a separate
-// buffer, copied in 16-byte pieces by all the workgroups of each row.
+// One workgroup per (row, value head, tile of tile_cols<D>() value columns: the whole head, one
+// q and k build per head): it rebuilds its q and k head and its v columns from the raw rows,
+// then updates its D x tile slice of the state: s = s e^g, delta = (v - s^T k) beta,
+// s += k delta^T, o = s^T q. Each thread holds 4 adjacent columns of several rows (16-byte
+// accesses); the two column sums go through lane shuffles and LDS. The state is read and
+// written once (in place allowed: each slice belongs to one workgroup); the new conv history
+// goes to a separate buffer, copied in 16-byte pieces by all the workgroups of each row.
 #include <hip/hip_runtime.h>
 
 #include <string>
@@ -38,6 +39,11 @@ struct DecodeArgs {
 };
 
 constexpr int kThreads = 256;
+// value columns per workgroup: the whole head (measured at the 0.8B heads, 64 rows: 27.5-28.9
+// against 29.4-30.2 us per step with tiles of 32, 28.2-28.7 with 64, 46 with 16; 512 threads
+// per workgroup with whole heads: no faster)
+template <int D>
+constexpr int tile_cols() { return D; }
 
 // channel c's raw values for its activation: the new row and the K-1 kept rows with their conv
 // weights, loaded as soon as the workgroup starts
@@ -89,7 +95,7 @@ __device__ __forceinline__ float2 block_sum2(float a, float b, float (*red)[kThr
 
 template <int D, class TIO, class TG>
 __global__ __launch_bounds__(kThreads) void k_decode(DecodeArgs A) {
-  constexpr int DT = D < 32 ? D : 32;
+  constexpr int DT = tile_cols<D>();
   constexpr int NTL = D / DT;
   constexpr int QPR = DT / 4;                 // column quads of a tile (one per thread)
   constexpr int RG = kThreads / QPR;          // row groups
@@ -209,7 +215,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeArgs A) {
 
 template <int D>
 hipError_t launch(const DecodeArgs& A, int io, int gate, hipStream_t st) {
-  const dim3 grid(A.B * A.H * (D / (D < 32 ? D : 32)));
+  const dim3 grid(A.B * A.H * (D / tile_cols<D>()));
   if (io == TJEV_GDN_BF16 && gate == TJEV_GDN_BF16) hipLaunchKernelGGL((k_decode<D, uint16_t, uint16_t>), grid, dim3(kThreads), 0, st, A);
   if (io == TJEV_GDN_BF16 && gate == TJEV_GDN_F32) hipLaunchKernelGGL((k_decode<D, uint16_t, float>), grid, dim3(kThreads), 0, st, A);
   if (io == TJEV_GDN_F32 && gate == TJEV_GDN_BF16) hipLaunchKernelGGL((k_decode<D, float, uint16_t>), grid, dim3(kThreads), 0, st, A);
