@@ -164,3 +164,16 @@ def test_fused_rows_random_layouts(index):
     for i, (x, y) in enumerate(zip(fused, plain)):
         assert bool(torch.isfinite(x.float()).all()), i
         assert torch.equal(x, y), (i, float((x.float() - y.float()).abs().max()))
+
+
+def test_fused_rows_at_the_08b_shape():
+    """The 0.8B layer shape (4 rows of 4096 tokens, 16 key and value heads) with packed segments
+    and a continued first row's history: fused and unfused bit for bit."""
+    inputs, cot, extra = _inputs(42, 4, 4096, 16, 16, 4, True)
+    kw = dict(key_heads=16, key_dim=D, value_heads=16, value_dim=D, precision="high")
+    print("fused rows at the 0.8B shape", flush=True)
+    fused = _run(inputs, cot, extra, False, **kw)
+    plain = _run(inputs, cot, extra, True, **kw)
+    for i, (x, y) in enumerate(zip(fused, plain)):
+        assert bool(torch.isfinite(x.float()).all()), i
+        assert torch.equal(x, y), (i, float((x.float() - y.float()).abs().max()))
